@@ -1,0 +1,162 @@
+/*
+ * qimg_hot.h — C ABI of the MI355X (gfx950) quantized-linear and
+ * SageAttention hot path of the qwen-image MMDiT.
+ *
+ * Plain pointers, sizes and a hipStream_t (passed as void*; NULL = the null
+ * stream). Every entry point validates its arguments on the host before any
+ * HIP call and returns a qimg_status; qimg_last_error() gives the message of
+ * the last failure on the calling thread. Device pointers must be 16-byte
+ * aligned. Calls are asynchronous on `stream` unless stated otherwise.
+ *
+ * Each function names the reference interface it replaces (file:line in the
+ * qwen-image.cu tree).
+ */
+#ifndef QIMG_HOT_H
+#define QIMG_HOT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    QIMG_OK = 0,
+    QIMG_ERR_INVALID_ARG = 1,  /* null pointer, bad size, bad enum */
+    QIMG_ERR_UNSUPPORTED = 2,  /* valid request this build does not implement */
+    QIMG_ERR_SCRATCH = 3,      /* caller scratch smaller than required */
+    QIMG_ERR_HIP = 4           /* a HIP runtime call failed */
+} qimg_status;
+
+/* Element types. Replaces DType (tensor.h:39) plus FP16 and FP8_E4M3. */
+typedef enum {
+    QIMG_FP32 = 0,
+    QIMG_BF16 = 1,
+    QIMG_FP16 = 2,
+    QIMG_INT8 = 3,
+    QIMG_INT32 = 4,
+    QIMG_FP8_E4M3 = 5  /* OCP E4M3FN: max 448, no inf */
+} qimg_dtype;
+
+/* Quantization modes. Replaces QuantMode::INT8_HADAMARD
+ * (cuda_kernels.cuh:183); FP8_HADAMARD is new (same Hadamard front end,
+ * e4m3 values, scale = amax/448). */
+typedef enum {
+    QIMG_QM_INT8_HADAMARD = 0,
+    QIMG_QM_FP8_HADAMARD = 1
+} qimg_quant_mode;
+
+const char* qimg_status_string(int status);
+/* Message of the last failing call on this thread ("" if none). */
+const char* qimg_last_error(void);
+/* Library version string. */
+const char* qimg_version(void);
+
+/* ---- sizing helpers --------------------------------------------------- */
+
+/* hadamard_block_size (cuda_kernels.cuh:253): K & -K. */
+int qimg_hadamard_block_size(int K);
+
+/* int8_scratch_bytes (cuda_kernels.cuh:311-319), same formula:
+ * align256(max(M*K, M*N)*4) + align256(M*K) + align256(4*M).
+ * qimg_linear needs only align256(M*K) + align256(4*M) of it (the int32 GEMM
+ * result is never materialised), so any buffer sized by this formula works. */
+int64_t qimg_int8_scratch_bytes(int M, int K, int N);
+
+/* ---- Hadamard + quantization ----------------------------------------- */
+
+/* fwht_inplace (cuda_kernels.cuh:250, cuda_kernels.cu:2209-2254): in-place
+ * normalised block-diagonal FWHT of each row of data[M,K] (fp32),
+ * hbs a power of two dividing K, hbs <= 32768. */
+int qimg_fwht_inplace(float* data, int M, int K, int hbs, void* stream);
+
+/* quantize_per_row_fp32 (cuda_kernels.cuh:260-261, cuda_kernels.cu:2385-2416):
+ * per-row symmetric int8, scale = amax/127. */
+int qimg_quantize_per_row_fp32(const float* x, int8_t* out, float* scales, int M, int K,
+                               void* stream);
+
+/* quantize_activation_int8_hadamard_{fp32,bf16} (cuda_kernels.cuh:277-280,
+ * cuda_kernels.cu:2493-2619), fused FWHT + per-token quantization.
+ *   x        [M,K], x_dtype QIMG_FP32 or QIMG_BF16
+ *   hbs      Hadamard block (1 = no rotation), power of two dividing K
+ *   mode     QIMG_QM_INT8_HADAMARD (int8 out, scale amax/127) or
+ *            QIMG_QM_FP8_HADAMARD (e4m3 out, scale amax/448)
+ *   q_out    [M,K] int8 or e4m3 bytes; scales_out [M] fp32 */
+int qimg_quantize_activation(const void* x, int x_dtype, int M, int K, int hbs, int mode,
+                             void* q_out, float* scales_out, void* stream);
+
+/* quantize_weight_tensor (cuda_kernels.cuh:308, cuda_kernels.cu:2830-2862):
+ * w [N,K] bf16 (or fp32) -> FWHT with hbs = K & -K -> per-row quantization.
+ * Writes q_out [N,K], scales_out [N] and *hbs_out (host int, may be NULL).
+ * Synchronous: returns after the device work has finished, as the
+ * reference does (cudaDeviceSynchronize at :2860). */
+int qimg_quantize_weight(const void* w, int w_dtype, int N, int K, int mode,
+                         void* q_out, float* scales_out, int* hbs_out, void* stream);
+
+/* ---- quantized linear ------------------------------------------------- */
+
+/* linear_forward_int8_prequantized (cuda_kernels.cuh:297-300,
+ * cuda_kernels.cu:2734-2773) with the dequant epilogue fused into the GEMM:
+ *   out[m,n] = act_scale[m] * w_scale[n] * sum_k act_q[m,k] w_q[n,k]
+ *              + bias[n]  (then GELU-tanh if gelu != 0)
+ * act_q [M,K], w_q [N,K] in `mode`'s element type; bias bf16 [N] or NULL;
+ * out [M,N] with out_dtype QIMG_FP32 (the reference's type) or QIMG_BF16.
+ * No scratch is needed. */
+int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
+                             const void* w_q, const float* w_scales, int N, int mode,
+                             const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
+                             void* stream);
+
+/* linear_forward_int8 / linear_forward_int8_bf16in (cuda_kernels.cuh:294-296,
+ * 303-305; cuda_kernels.cu:2674-2732, 2776-2827): activation FWHT+quant into
+ * `scratch`, then qimg_linear_prequantized. scratch_bytes must be at least
+ * align256(M*K) + align256(4*M) (qimg_int8_scratch_bytes also suffices). */
+int qimg_linear(const void* x, int x_dtype, int M, int K,
+                const void* w_q, const float* w_scales, int N, int hbs, int mode,
+                const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
+                void* scratch, int64_t scratch_bytes, void* stream);
+
+/* ---- SageAttention ---------------------------------------------------- */
+
+/* Scratch needed by qimg_sage_attention for BH heads of S tokens, head dim D:
+ * Q/K int8, V re-laid for the PV product, scales and the K mean. */
+int64_t qimg_sage_scratch_bytes(int BH, int S, int D);
+
+/* sageattention_k_mean_kernel (sageattention_sm80.cu:759-773): k fp16
+ * [BH,S,D] -> mean fp32 [BH,D], sequential fp32 sum over s / max(S,1). */
+int qimg_sage_k_mean(const uint16_t* k_f16, float* mean, int BH, int S, int D, void* stream);
+
+/* sageattention_query_per_thread_int8_kernel (sageattention_sm80.cu:775-824):
+ * q fp16 [BH,S,D] -> int8 [BH,S,D] + scales fp32 [BH, ceil(S/128)*32]. */
+int qimg_sage_quant_q(const uint16_t* q_f16, int8_t* q_out, float* q_scale, int BH, int S,
+                      int D, void* stream);
+
+/* sageattention_key_per_thread_int8_kernel (sageattention_sm80.cu:826-886):
+ * (k - mean) fp16 [BH,S,D] -> int8 [BH,S,D] + scales fp32 [BH, ceil(S/64)*4]. */
+int qimg_sage_quant_k(const uint16_t* k_f16, const float* mean, int8_t* k_out, float* k_scale,
+                      int BH, int S, int D, void* stream);
+
+/* qk_int_sv_f16_attn_kernel via sageattention_launch_accum_f32
+ * (sageattention_sm80.cu:47-674, 896-961): attention on pre-quantized
+ * Q/K (scales laid out as above) and fp16 V [BH,S,D]. out [BH,S,D] in
+ * out_dtype QIMG_FP16, QIMG_FP32 (fp16-rounded, as the reference) or
+ * QIMG_BF16. D must be 64 or 128. `scratch` receives the re-laid V
+ * (qimg_sage_scratch_bytes covers it). */
+int qimg_sage_attn_quantized(const int8_t* q, const int8_t* k, const uint16_t* v_f16,
+                             const float* q_scale, const float* k_scale, void* out,
+                             int out_dtype, int BH, int S, int D, float sm_scale, int causal,
+                             void* scratch, int64_t scratch_bytes, void* stream);
+
+/* attention_forward_sage_sm80_fp16io (cuda_kernels.cuh:560-562,
+ * sageattention_sm80.cu:965-1027): fp16 q,k,v [BH,S,D] -> out [BH,S,D]
+ * (out_dtype as above; the reference writes QIMG_FP32). Uses caller scratch
+ * of qimg_sage_scratch_bytes(BH,S,D) bytes instead of a hidden static
+ * workspace. */
+int qimg_sage_attention(const uint16_t* q_f16, const uint16_t* k_f16, const uint16_t* v_f16,
+                        void* out, int out_dtype, float sm_scale, int BH, int S, int D,
+                        int causal, void* scratch, int64_t scratch_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QIMG_HOT_H */

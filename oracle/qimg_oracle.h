@@ -1,0 +1,116 @@
+/*
+ * qimg_oracle.h — CPU restatement of qwen-image.cu's quantized-linear and
+ * SageAttention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke
+ * check and the bench's CPU-baseline leg call it to produce expected values.
+ * No product code path links or calls it.
+ *
+ * Every function states the reference file:line it restates. Arithmetic is
+ * IEEE-754 fp32 in the same operation order as the reference, except where
+ * the reference relies on nvcc --use_fast_math approximations (rsqrtf, `/`,
+ * tanhf, ex2.approx, rcp.approx): there the oracle uses the correctly
+ * rounded operation.
+ *
+ * Pinning status (which independent check fixes each function) is listed in
+ * oracle/README.md.
+ */
+#ifndef QIMG_ORACLE_H
+#define QIMG_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar conversions (bit-level, round-to-nearest-even) ------------ */
+float    or_bf16_to_f32(uint16_t h);
+uint16_t or_f32_to_bf16(float f);
+float    or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);
+/* OCP FP8 E4M3FN (no inf, max 448), RNE, saturating to +-448; NaN -> 0x7f. */
+uint8_t  or_f32_to_e4m3(float f);
+float    or_e4m3_to_f32(uint8_t b);
+
+/* a1: cuda_kernels.cuh:253  hadamard_block_size(K) = K & -K */
+int   or_hadamard_block_size(int K);
+/* Normalisation factor 1/sqrt(hbs), correctly rounded to fp32.
+ * Reference: rsqrtf((float)block_size), cuda_kernels.cu:2243, 2538. */
+float or_fwht_norm(int hbs);
+
+/* a2: cuda_kernels.cu:2209-2254 fwht_inplace_kernel. Row-wise block-diagonal
+ * FWHT, stages half = 1,2,...,hbs/2 in that order, (a,b) <- (a+b, a-b),
+ * then multiply by or_fwht_norm(hbs). In place on x[M,K]. */
+void or_fwht_rows(float* x, int64_t M, int K, int hbs);
+
+/* a3: cuda_kernels.cu:2385-2416 quantize_per_row_fp32_kernel.
+ * amax = max|row|; scale = amax/127; inv = amax>0 ? 127/amax : 0;
+ * q = clamp(rne(v*inv), -128, 127). */
+void or_quant_rows_int8(const float* x, int64_t M, int K, int8_t* q, float* scales);
+
+/* a4: cuda_kernels.cu:2830-2862 quantize_weight_tensor. BF16 [N,K] ->
+ * FP32 -> FWHT(hbs = K & -K, if > 1) -> a3. Returns hbs. */
+int or_quantize_weight_bf16(const uint16_t* w, int N, int K, int8_t* q, float* scales);
+
+/* a5/a6: cuda_kernels.cu:2493-2619 fwht_quantize_kernel<T> and
+ * quantize_activation_per_token_*: per token FWHT (hbs > 1) then a3.
+ * x_is_bf16 selects the input type (else fp32). */
+void or_quantize_activation(const void* x, int x_is_bf16, int64_t M, int K, int hbs,
+                            int8_t* q, float* scales);
+
+/* a7: cuda_kernels.cu:2711-2721 cublasGemmEx s8*s8->s32, C[m,n] = sum_k
+ * A[m,k] * W[n,k], exact. Rows [m0, m1) only (use 0, M for all). */
+void or_gemm_s8s8s32(const int8_t* A, const int8_t* W, int64_t M, int N, int K,
+                     int64_t m0, int64_t m1, int32_t* C);
+
+/* a8: cuda_kernels.cu:2623-2668 dequantize_and_bias / dequantize_bias_gelu.
+ * v = ((float)acc * as[m]) * ws[n]; v += bf16 bias[n]; optional GELU-tanh
+ * 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))). bias may be NULL. */
+void or_dequant_epilogue(const int32_t* C, const float* as, const float* ws,
+                         const uint16_t* bias_bf16, int64_t M, int N, int gelu, float* out);
+
+/* ---- fp8-e4m3 mode (no reference counterpart: new mode) -------------- */
+/* Same shape as a3 with the e4m3 range: scale = amax/448,
+ * inv = amax>0 ? 448/amax : 0, q = e4m3_rne_sat(v*inv). */
+void or_quant_rows_fp8(const float* x, int64_t M, int K, uint8_t* q, float* scales);
+/* fp8 analogue of a7 + a8: C[m,n] = sum_k e4m3(A[m,k]) e4m3(W[n,k]) in
+ * double, then the a8 epilogue on the (rounded to fp32) sum. */
+void or_gemm_fp8_epilogue(const uint8_t* A, const uint8_t* W, const float* as, const float* ws,
+                          const uint16_t* bias_bf16, int64_t M, int N, int K,
+                          int64_t m0, int64_t m1, int gelu, float* out);
+
+/* ---- SageAttention (sageattention_sm80.cu) --------------------------- */
+/* a12: :759-773 sageattention_k_mean_kernel. mean[h,d] = (sequential fp32
+ * sum over s of k[h,s,d]) / max(S,1). */
+void or_sage_k_mean(const uint16_t* k_f16, int BH, int S, int D, float* mean);
+/* a13: :775-824. Per (head, 128-token block b, warp w, lane group g): tokens
+ * b*128 + w*32 + g + 8i, i = 0..3. amax starts at 1e-7; scale = amax/127 +
+ * 1e-7; q = sat_rne(v * (1/scale)). Scales [BH, ceil(S/128)*32]. */
+void or_sage_quant_q(const uint16_t* q_f16, int BH, int S, int D, int8_t* q_out, float* q_scale);
+/* a14: :826-886. Per (head, 64-token block b, group g in 0..3): tokens
+ * b*64 + 2g + {0,1} + 8i, i = 0..7, values k - mean[h,d]. Scales
+ * [BH, ceil(S/64)*4]. */
+void or_sage_quant_k(const uint16_t* k_f16, const float* mean, int BH, int S, int D,
+                     int8_t* k_out, float* k_scale);
+/* a15/a16: :47-674 qk_int_sv_f16_attn_kernel with CTA_Q=128, CTA_K=64,
+ * per-thread Q/K scales, fp32 PV accumulation, fp16 output. Online softmax in
+ * base 2 over 64-key tiles, m0 = -5e6, d0 = 1, P rounded to fp16 before the
+ * row sum and before PV, O/d rounded to fp16. Query rows [q0, q1) of every
+ * head are computed (0, S for all); out is fp16 [BH, S, D]. */
+void or_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v_f16,
+                  const float* q_scale, const float* k_scale, int BH, int S, int D,
+                  float sm_scale, int causal, int q0, int q1, uint16_t* out_f16);
+/* Full a17 composition: fp16 q,k,v -> k-mean -> quant -> attention. */
+void or_sage_attention_fp16io(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              int BH, int S, int D, float sm_scale, int causal,
+                              uint16_t* out_f16);
+
+/* Threads used by the parallel loops (OpenMP); <= 0 leaves the default. */
+void or_set_threads(int n);
+int  or_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,283 @@
+// capi.hip — the extern "C" boundary (include/qimg_hot.h).
+//
+// Every entry point validates its arguments on the host before any HIP call
+// (the reference aborts via assert/exit instead, cuda_kernels.cu:2681-2686,
+// sageattention_sm80.cu:975-978) and returns a qimg_status. The message of the
+// last failure is kept per thread for qimg_last_error().
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "qimg_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int hip_status(hipError_t e, const char* where) {
+    if (e == hipSuccess) return QIMG_OK;
+    return fail(QIMG_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int64_t align256(int64_t v) { return (v + 255) & ~static_cast<int64_t>(255); }
+
+constexpr int kMaxRowK = 32768;  // the fused row kernels keep one row in LDS
+
+#define QIMG_REQUIRE(cond, ...)                                  \
+    do {                                                         \
+        if (!(cond)) return fail(QIMG_ERR_INVALID_ARG, __VA_ARGS__); \
+    } while (0)
+
+int check_rows(const char* fn, int M, int K, int hbs) {
+    QIMG_REQUIRE(M >= 0 && K > 0, "%s: need M >= 0 and K > 0 (M=%d K=%d)", fn, M, K);
+    QIMG_REQUIRE(is_pow2(hbs), "%s: hbs=%d is not a power of two", fn, hbs);
+    QIMG_REQUIRE(K % hbs == 0, "%s: K=%d is not a multiple of hbs=%d", fn, K, hbs);
+    if (K > kMaxRowK)
+        return fail(QIMG_ERR_UNSUPPORTED, "%s: K=%d exceeds the fused row limit %d", fn, K, kMaxRowK);
+    return QIMG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qimg_status_string(int status) {
+    switch (status) {
+        case QIMG_OK: return "ok";
+        case QIMG_ERR_INVALID_ARG: return "invalid argument";
+        case QIMG_ERR_UNSUPPORTED: return "unsupported";
+        case QIMG_ERR_SCRATCH: return "scratch too small";
+        case QIMG_ERR_HIP: return "HIP error";
+        default: return "unknown status";
+    }
+}
+
+const char* qimg_last_error(void) { return g_err; }
+
+const char* qimg_version(void) { return "qimg-hot 0.1 gfx950"; }
+
+int qimg_hadamard_block_size(int K) { return K & (-K); }
+
+int64_t qimg_int8_scratch_bytes(int M, int K, int N) {
+    const int64_t mk = static_cast<int64_t>(M) * K;
+    const int64_t mn = static_cast<int64_t>(M) * N;
+    return align256((mk > mn ? mk : mn) * 4) + align256(mk) + align256(static_cast<int64_t>(M) * 4);
+}
+
+int qimg_fwht_inplace(float* data, int M, int K, int hbs, void* stream) {
+    int st = check_rows("qimg_fwht_inplace", M, K, hbs);
+    if (st) return st;
+    QIMG_REQUIRE(data || M == 0, "qimg_fwht_inplace: data is null");
+    return hip_status(qimg::launch_fwht_inplace(data, M, K, hbs, static_cast<hipStream_t>(stream)),
+                      "qimg_fwht_inplace");
+}
+
+int qimg_quantize_per_row_fp32(const float* x, int8_t* out, float* scales, int M, int K,
+                               void* stream) {
+    int st = check_rows("qimg_quantize_per_row_fp32", M, K, 1);
+    if (st) return st;
+    QIMG_REQUIRE(M == 0 || (x && out && scales), "qimg_quantize_per_row_fp32: null pointer");
+    return hip_status(qimg::launch_fwht_quant(x, QIMG_FP32, M, K, 1, QIMG_QM_INT8_HADAMARD, out, scales,
+                                              static_cast<hipStream_t>(stream)),
+                      "qimg_quantize_per_row_fp32");
+}
+
+int qimg_quantize_activation(const void* x, int x_dtype, int M, int K, int hbs, int mode,
+                             void* q_out, float* scales_out, void* stream) {
+    const char* fn = "qimg_quantize_activation";
+    QIMG_REQUIRE(x_dtype == QIMG_FP32 || x_dtype == QIMG_BF16, "%s: x_dtype %d must be FP32 or BF16", fn,
+                 x_dtype);
+    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
+    int st = check_rows(fn, M, K, hbs);
+    if (st) return st;
+    QIMG_REQUIRE(M == 0 || (x && q_out && scales_out), "%s: null pointer", fn);
+    return hip_status(qimg::launch_fwht_quant(x, x_dtype, M, K, hbs, mode, q_out, scales_out,
+                                              static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+int qimg_quantize_weight(const void* w, int w_dtype, int N, int K, int mode, void* q_out,
+                         float* scales_out, int* hbs_out, void* stream) {
+    const char* fn = "qimg_quantize_weight";
+    QIMG_REQUIRE(w_dtype == QIMG_FP32 || w_dtype == QIMG_BF16, "%s: w_dtype %d must be BF16 or FP32", fn,
+                 w_dtype);
+    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
+    QIMG_REQUIRE(N > 0 && K > 0, "%s: need N > 0 and K > 0 (N=%d K=%d)", fn, N, K);
+    const int hbs = K & (-K);
+    int st = check_rows(fn, N, K, hbs);
+    if (st) return st;
+    QIMG_REQUIRE(w && q_out && scales_out, "%s: null pointer", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    st = hip_status(qimg::launch_fwht_quant(w, w_dtype, N, K, hbs, mode, q_out, scales_out, s), fn);
+    if (st) return st;
+    st = hip_status(hipStreamSynchronize(s), fn);
+    if (st) return st;
+    if (hbs_out) *hbs_out = hbs;
+    return QIMG_OK;
+}
+
+int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
+                             const void* w_q, const float* w_scales, int N, int mode,
+                             const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
+                             void* stream) {
+    const char* fn = "qimg_linear_prequantized";
+    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
+    QIMG_REQUIRE(out_dtype == QIMG_FP32 || out_dtype == QIMG_BF16, "%s: out_dtype %d must be FP32 or BF16",
+                 fn, out_dtype);
+    QIMG_REQUIRE(M >= 0 && N >= 0 && K > 0, "%s: bad sizes M=%d N=%d K=%d", fn, M, N, K);
+    if (M == 0 || N == 0) return QIMG_OK;
+    QIMG_REQUIRE(act_q && act_scales && w_q && w_scales && out, "%s: null pointer", fn);
+    if (K % 64 != 0) {
+        if (mode == QIMG_QM_FP8_HADAMARD)
+            return fail(QIMG_ERR_UNSUPPORTED, "%s: e4m3 mode needs K %% 64 == 0 (K=%d)", fn, K);
+    } else {
+        QIMG_REQUIRE(aligned16(act_q) && aligned16(w_q), "%s: operands must be 16-byte aligned", fn);
+    }
+    return hip_status(qimg::launch_linear_prequantized(act_q, act_scales, M, K, w_q, w_scales, N, mode,
+                                                       bias_bf16, out, out_dtype, gelu,
+                                                       static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+int qimg_linear(const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales, int N,
+                int hbs, int mode, const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
+                void* scratch, int64_t scratch_bytes, void* stream) {
+    const char* fn = "qimg_linear";
+    QIMG_REQUIRE(x_dtype == QIMG_FP32 || x_dtype == QIMG_BF16, "%s: x_dtype %d must be FP32 or BF16", fn,
+                 x_dtype);
+    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
+    QIMG_REQUIRE(out_dtype == QIMG_FP32 || out_dtype == QIMG_BF16, "%s: out_dtype %d must be FP32 or BF16",
+                 fn, out_dtype);
+    int st = check_rows(fn, M, K, hbs);
+    if (st) return st;
+    QIMG_REQUIRE(N >= 0, "%s: bad N=%d", fn, N);
+    if (M == 0 || N == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && w_q && w_scales && out, "%s: null pointer", fn);
+    if (mode == QIMG_QM_FP8_HADAMARD && K % 64 != 0)
+        return fail(QIMG_ERR_UNSUPPORTED, "%s: e4m3 mode needs K %% 64 == 0 (K=%d)", fn, K);
+    const int64_t act_bytes = align256(static_cast<int64_t>(M) * K);
+    const int64_t need = act_bytes + align256(static_cast<int64_t>(M) * 4);
+    if (!scratch || scratch_bytes < need)
+        return fail(QIMG_ERR_SCRATCH, "%s: scratch %lld bytes < required %lld", fn,
+                    static_cast<long long>(scratch_bytes), static_cast<long long>(need));
+    QIMG_REQUIRE(aligned16(scratch), "%s: scratch must be 16-byte aligned", fn);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t* qa = static_cast<uint8_t*>(scratch);
+    float* sa = reinterpret_cast<float*>(qa + act_bytes);
+    st = hip_status(qimg::launch_fwht_quant(x, x_dtype, M, K, hbs, mode, qa, sa, s), fn);
+    if (st) return st;
+    return hip_status(qimg::launch_linear_prequantized(qa, sa, M, K, w_q, w_scales, N, mode, bias_bf16, out,
+                                                       out_dtype, gelu, s),
+                      fn);
+}
+
+int64_t qimg_sage_scratch_bytes(int BH, int S, int D) {
+    if (BH <= 0 || S <= 0 || D <= 0) return 0;
+    return qimg::sage_scratch_layout(BH, S, D, nullptr, nullptr);
+}
+
+static int check_sage(const char* fn, int BH, int S, int D) {
+    QIMG_REQUIRE(BH > 0 && S > 0, "%s: need BH > 0 and S > 0 (BH=%d S=%d)", fn, BH, S);
+    if (D != 64 && D != 128)
+        return fail(QIMG_ERR_UNSUPPORTED, "%s: head_dim %d not supported (64 or 128)", fn, D);
+    QIMG_REQUIRE(static_cast<int64_t>(BH) * S * D < (static_cast<int64_t>(1) << 31),
+                 "%s: BH*S*D must be < 2^31", fn);
+    return QIMG_OK;
+}
+
+int qimg_sage_k_mean(const uint16_t* k_f16, float* mean, int BH, int S, int D, void* stream) {
+    const char* fn = "qimg_sage_k_mean";
+    int st = check_sage(fn, BH, S, D);
+    if (st) return st;
+    QIMG_REQUIRE(k_f16 && mean, "%s: null pointer", fn);
+    return hip_status(qimg::launch_sage_k_mean(k_f16, mean, BH, S, D, static_cast<hipStream_t>(stream)), fn);
+}
+
+int qimg_sage_quant_q(const uint16_t* q_f16, int8_t* q_out, float* q_scale, int BH, int S, int D,
+                      void* stream) {
+    const char* fn = "qimg_sage_quant_q";
+    int st = check_sage(fn, BH, S, D);
+    if (st) return st;
+    QIMG_REQUIRE(q_f16 && q_out && q_scale, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(q_f16) && aligned16(q_out), "%s: q and q_out must be 16-byte aligned", fn);
+    return hip_status(qimg::launch_sage_quant_q(q_f16, q_out, q_scale, BH, S, D, static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+int qimg_sage_quant_k(const uint16_t* k_f16, const float* mean, int8_t* k_out, float* k_scale, int BH, int S,
+                      int D, void* stream) {
+    const char* fn = "qimg_sage_quant_k";
+    int st = check_sage(fn, BH, S, D);
+    if (st) return st;
+    QIMG_REQUIRE(k_f16 && mean && k_out && k_scale, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(k_f16) && aligned16(k_out), "%s: k and k_out must be 16-byte aligned", fn);
+    return hip_status(
+        qimg::launch_sage_quant_k(k_f16, mean, k_out, k_scale, BH, S, D, static_cast<hipStream_t>(stream)), fn);
+}
+
+int qimg_sage_attn_quantized(const int8_t* q, const int8_t* k, const uint16_t* v_f16, const float* q_scale,
+                             const float* k_scale, void* out, int out_dtype, int BH, int S, int D,
+                             float sm_scale, int causal, void* scratch, int64_t scratch_bytes,
+                             void* stream) {
+    const char* fn = "qimg_sage_attn_quantized";
+    int st = check_sage(fn, BH, S, D);
+    if (st) return st;
+    QIMG_REQUIRE(out_dtype == QIMG_FP16 || out_dtype == QIMG_FP32 || out_dtype == QIMG_BF16,
+                 "%s: out_dtype %d must be FP16, FP32 or BF16", fn, out_dtype);
+    QIMG_REQUIRE(q && k && v_f16 && q_scale && k_scale && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v_f16) && aligned16(out) && aligned16(k_scale),
+                 "%s: buffers must be 16-byte aligned", fn);
+    const int64_t need = qimg::sage_vt_bytes(BH, S, D);
+    if (!scratch || scratch_bytes < need)
+        return fail(QIMG_ERR_SCRATCH, "%s: scratch %lld bytes < required %lld", fn,
+                    static_cast<long long>(scratch_bytes), static_cast<long long>(need));
+    QIMG_REQUIRE(aligned16(scratch), "%s: scratch must be 16-byte aligned", fn);
+    return hip_status(qimg::launch_sage_attn(q, k, v_f16, q_scale, k_scale, out, out_dtype, BH, S, D, sm_scale,
+                                             causal, static_cast<uint16_t*>(scratch),
+                                             static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+int qimg_sage_attention(const uint16_t* q_f16, const uint16_t* k_f16, const uint16_t* v_f16, void* out,
+                        int out_dtype, float sm_scale, int BH, int S, int D, int causal, void* scratch,
+                        int64_t scratch_bytes, void* stream) {
+    const char* fn = "qimg_sage_attention";
+    int st = check_sage(fn, BH, S, D);
+    if (st) return st;
+    QIMG_REQUIRE(out_dtype == QIMG_FP16 || out_dtype == QIMG_FP32 || out_dtype == QIMG_BF16,
+                 "%s: out_dtype %d must be FP16, FP32 or BF16", fn, out_dtype);
+    QIMG_REQUIRE(q_f16 && k_f16 && v_f16 && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(q_f16) && aligned16(k_f16) && aligned16(v_f16) && aligned16(out),
+                 "%s: buffers must be 16-byte aligned", fn);
+    const int64_t need = qimg::sage_scratch_layout(BH, S, D, nullptr, nullptr);
+    if (!scratch || scratch_bytes < need)
+        return fail(QIMG_ERR_SCRATCH, "%s: scratch %lld bytes < required %lld", fn,
+                    static_cast<long long>(scratch_bytes), static_cast<long long>(need));
+    QIMG_REQUIRE(aligned16(scratch), "%s: scratch must be 16-byte aligned", fn);
+    qimg::SageScratch ws;
+    qimg::sage_scratch_layout(BH, S, D, scratch, &ws);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    st = hip_status(qimg::launch_sage_k_mean(k_f16, ws.k_mean, BH, S, D, s), fn);
+    if (st) return st;
+    st = hip_status(qimg::launch_sage_quant_q(q_f16, ws.q_i8, ws.q_scale, BH, S, D, s), fn);
+    if (st) return st;
+    st = hip_status(qimg::launch_sage_quant_k(k_f16, ws.k_mean, ws.k_i8, ws.k_scale, BH, S, D, s), fn);
+    if (st) return st;
+    return hip_status(qimg::launch_sage_attn(ws.q_i8, ws.k_i8, v_f16, ws.q_scale, ws.k_scale, out, out_dtype,
+                                             BH, S, D, sm_scale, causal, ws.v_t, s),
+                      fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,269 @@
+// hadamard_quant.hip — fused block-diagonal Walsh-Hadamard transform +
+// per-row quantization for gfx950.
+//
+// Semantics follow qwen-image.cu:
+//   fwht_inplace_kernel        cuda_kernels.cu:2209-2254   (weights, in place)
+//   quantize_per_row_fp32      cuda_kernels.cu:2385-2416
+//   fwht_quantize_kernel<T>    cuda_kernels.cu:2493-2577   (activations)
+//   quantize_weight_tensor     cuda_kernels.cu:2830-2862
+// Every output element sees the same fp32 operation sequence as the
+// reference: butterfly stages half = 1, 2, ..., hbs/2 in that order with
+// (a, b) <- (a + b, a - b), then one multiply by 1/sqrt(hbs). The
+// reference runs each stage as a separate shared-memory sweep; here a
+// thread applies up to four consecutive stages to 16 elements held in
+// registers (a radix-16 pass), so a 1024-point transform takes three LDS
+// sweeps instead of ten, and the first sweep comes straight from the
+// global load. The per-element arithmetic, and therefore the result, is
+// unchanged.
+//
+// One workgroup owns one row: the row lives in LDS (K fp32 plus one pad
+// word per 16, which makes the strided radix passes bank-conflict free).
+#include "qimg_device.h"
+#include "qimg_internal.h"
+
+namespace qimg {
+
+enum class RowOut { Int8 = 0, Fp8 = 1, Fp32 = 2 };
+
+__device__ __forceinline__ int lds_pad(int i) { return i + (i >> 4); }
+
+// Butterfly stages on a register array: stage s pairs v[i], v[i + 2^s].
+template <int RB>
+__device__ __forceinline__ void butterfly(float* v) {
+    constexpr int R = 1 << RB;
+#pragma unroll
+    for (int s = 0; s < RB; ++s) {
+        const int h = 1 << s;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if ((i & h) == 0) {
+                float a = v[i];
+                float b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+        }
+    }
+}
+
+// One radix-2^RB sweep over the row in LDS covering bits [lo, lo + RB) of
+// the index inside each Hadamard block.
+template <int RB>
+__device__ __forceinline__ void lds_pass(float* lds, int K, int lo, bool last, float norm,
+                                         float& amax) {
+    constexpr int R = 1 << RB;
+    const int ngroups = K >> RB;
+    const int lomask = (1 << lo) - 1;
+    for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+        const int base = (g & lomask) + ((g >> lo) << (lo + RB));
+        float v[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) v[i] = lds[lds_pad(base + (i << lo))];
+        butterfly<RB>(v);
+        if (last) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                v[i] = v[i] * norm;
+                amax = fmaxf(amax, fabsf(v[i]));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; ++i) lds[lds_pad(base + (i << lo))] = v[i];
+    }
+}
+
+__device__ __forceinline__ void lds_pass_dispatch(int rb, float* lds, int K, int lo, bool last,
+                                                  float norm, float& amax) {
+    switch (rb) {
+        case 1: lds_pass<1>(lds, K, lo, last, norm, amax); break;
+        case 2: lds_pass<2>(lds, K, lo, last, norm, amax); break;
+        case 3: lds_pass<3>(lds, K, lo, last, norm, amax); break;
+        default: lds_pass<4>(lds, K, lo, last, norm, amax); break;
+    }
+}
+
+template <typename InT>
+__device__ __forceinline__ void load16(const InT* p, float* v);
+
+template <>
+__device__ __forceinline__ void load16<float>(const float* p, float* v) {
+    const v4f* q = reinterpret_cast<const v4f*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v4f t = q[j];
+        v[4 * j + 0] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+    }
+}
+
+template <>
+__device__ __forceinline__ void load16<uint16_t>(const uint16_t* p, float* v) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        u32x4 t = q[j];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[8 * j + 2 * c + 0] = __uint_as_float(t[c] << 16);
+            v[8 * j + 2 * c + 1] = __uint_as_float(t[c] & 0xffff0000u);
+        }
+    }
+}
+
+template <typename InT>
+__device__ __forceinline__ float load1(const InT* p);
+template <>
+__device__ __forceinline__ float load1<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load1<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+
+// grid.x = rows, blockDim.x = 64..256 (multiple of 64).
+// hbs_log2 = log2(hbs) (0 = no transform). K % 16 == 0 and hbs >= 16 take
+// the vector path (first 4 stages in registers straight from global).
+template <typename InT, RowOut OUT>
+__global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
+    const InT* x, void* out, float* __restrict__ scales, int M, int K,
+    int hbs_log2, float norm) {
+    extern __shared__ float lds[];
+    float* red = lds + lds_pad(K) + 1;  // 4 floats for the cross-wave max
+    const int row = blockIdx.x;
+    if (row >= M) return;
+    const InT* xin = x + static_cast<int64_t>(row) * K;
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+
+    const bool vec = (hbs_log2 >= 4) && ((K & 15) == 0);
+    float amax = 0.0f;
+    int lo;  // first stage bit still to do
+
+    if (vec) {
+        const bool only = (hbs_log2 == 4);
+        for (int c = tid; c < (K >> 4); c += nthr) {
+            float v[16];
+            load16<InT>(xin + 16 * c, v);
+            butterfly<4>(v);
+            if (only) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    v[i] = v[i] * norm;
+                    amax = fmaxf(amax, fabsf(v[i]));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lds[lds_pad(16 * c + i)] = v[i];
+        }
+        lo = 4;
+    } else {
+        for (int i = tid; i < K; i += nthr) {
+            float v = load1<InT>(xin + i);
+            if (hbs_log2 == 0) amax = fmaxf(amax, fabsf(v));
+            lds[lds_pad(i)] = v;
+        }
+        lo = 0;
+    }
+    __syncthreads();
+
+    while (lo < hbs_log2) {
+        const int rem = hbs_log2 - lo;
+        const int rb = rem >= 8 ? 4 : (rem > 4 ? (rem + 1) / 2 : rem);
+        const bool last = (lo + rb == hbs_log2);
+        lds_pass_dispatch(rb, lds, K, lo, last, norm, amax);
+        lo += rb;
+        __syncthreads();
+    }
+
+    if constexpr (OUT == RowOut::Fp32) {
+        float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(row) * K;
+        for (int i = tid; i < K; i += nthr) o[i] = lds[lds_pad(i)];
+        return;
+    } else {
+        amax = wave_max(amax);
+        if ((tid & (kWave - 1)) == 0) red[tid / kWave] = amax;
+        __syncthreads();
+        amax = red[0];
+        for (int w = 1; w < nthr / kWave; ++w) amax = fmaxf(amax, red[w]);
+        constexpr float QMAX = (OUT == RowOut::Int8) ? 127.0f : 448.0f;
+        if (tid == 0) scales[row] = amax / QMAX;
+        const float inv = (amax > 0.0f) ? QMAX / amax : 0.0f;
+
+        uint8_t* o = reinterpret_cast<uint8_t*>(out) + static_cast<int64_t>(row) * K;
+        if ((K & 15) == 0) {
+            for (int c = tid; c < (K >> 4); c += nthr) {
+                u32x4 pk;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        float v = lds[lds_pad(16 * c + 4 * w + b)] * inv;
+                        uint32_t byte;
+                        if constexpr (OUT == RowOut::Int8)
+                            byte = static_cast<uint8_t>(sat_rne_i8(v));
+                        else
+                            byte = f32_to_e4m3(v);
+                        word |= byte << (8 * b);
+                    }
+                    pk[w] = word;
+                }
+                *reinterpret_cast<u32x4*>(o + 16 * c) = pk;
+            }
+        } else {
+            for (int i = tid; i < K; i += nthr) {
+                float v = lds[lds_pad(i)] * inv;
+                if constexpr (OUT == RowOut::Int8)
+                    o[i] = static_cast<uint8_t>(sat_rne_i8(v));
+                else
+                    o[i] = static_cast<uint8_t>(f32_to_e4m3(v));
+            }
+        }
+    }
+}
+
+static int ilog2(int v) {
+    int r = 0;
+    while ((1 << r) < v) ++r;
+    return r;
+}
+
+size_t rows_lds_bytes(int K) { return sizeof(float) * (static_cast<size_t>(K) + K / 16 + 1 + 8); }
+
+template <typename InT, RowOut OUT>
+static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int K, int hbs,
+                              hipStream_t stream) {
+    if (M == 0) return hipSuccess;
+    int chunks = (K + 15) / 16;
+    int threads = ((chunks + kWave - 1) / kWave) * kWave;
+    threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
+    const size_t lds = rows_lds_bytes(K);
+    auto kern = fwht_quant_rows_kernel<InT, OUT>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    hipLaunchKernelGGL(kern, dim3(M), dim3(threads), lds, stream, x, out, scales, M, K, ilog2(hbs),
+                       norm);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, int mode,
+                             void* q_out, float* scales, hipStream_t stream) {
+    const bool fp8 = (mode == QIMG_QM_FP8_HADAMARD);
+    if (x_dtype == QIMG_BF16) {
+        const uint16_t* xi = static_cast<const uint16_t*>(x);
+        return fp8 ? launch_rows<uint16_t, RowOut::Fp8>(xi, q_out, scales, M, K, hbs, stream)
+                   : launch_rows<uint16_t, RowOut::Int8>(xi, q_out, scales, M, K, hbs, stream);
+    }
+    const float* xf = static_cast<const float*>(x);
+    return fp8 ? launch_rows<float, RowOut::Fp8>(xf, q_out, scales, M, K, hbs, stream)
+               : launch_rows<float, RowOut::Int8>(xf, q_out, scales, M, K, hbs, stream);
+}
+
+hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t stream) {
+    // Rows are transformed through LDS, so in place is safe: each workgroup
+    // reads its whole row before writing it back.
+    return launch_rows<float, RowOut::Fp32>(data, data, nullptr, M, K, hbs, stream);
+}
+
+}  // namespace qimg

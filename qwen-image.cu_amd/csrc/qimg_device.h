@@ -1,0 +1,99 @@
+// qimg_device.h — device-side helpers shared by the gfx950 kernels:
+// element conversions with explicit rounding, wave-64 reductions, and
+// small vector types for 16-byte memory traffic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qimg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    _Float16 x;
+    __builtin_memcpy(&x, &h, 2);
+    return static_cast<float>(x);
+}
+
+// fp32 -> fp16 bits with the IEEE default rounding (nearest even).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    _Float16 x = static_cast<_Float16>(f);
+    uint16_t h;
+    __builtin_memcpy(&h, &x, 2);
+    return h;
+}
+
+// Saturating round-half-to-even to int8 (the reference's
+// __float2int_rn + clamp and cvt.rni.sat.s8.f32). NaN maps to 0.
+__device__ __forceinline__ int8_t sat_rne_i8(float v) {
+    float r = __builtin_rintf(v);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return static_cast<int8_t>(static_cast<int>(r));
+}
+
+// fp32 -> OCP E4M3FN bits, round to nearest even, saturating to +-448.
+// Integer-only so the result does not depend on conversion-instruction modes.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t s = (u >> 24) & 0x80u;
+    float a = fabsf(f);
+    if (a != a) return 0x7fu;
+    if (a >= 448.0f) return s | 0x7eu;
+    if (a < 0.015625f) {  // subnormal quantum 2^-9
+        float r = __builtin_rintf(a * 512.0f);
+        return s | static_cast<uint32_t>(r);
+    }
+    uint32_t au = __float_as_uint(a);
+    uint32_t e = (au >> 23) - 120u;  // rebias 127 -> 7
+    uint32_t m = au & 0x7fffffu;
+    uint32_t hm = m >> 20;
+    uint32_t rem = m & 0xfffffu;
+    uint32_t out = (e << 3) | hm;
+    out += (rem > 0x80000u || (rem == 0x80000u && (hm & 1u))) ? 1u : 0u;
+    out = out > 0x7eu ? 0x7eu : out;
+    return s | out;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float v) {
+    const float c = 0.7978845608f;
+    float inner = c * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+}  // namespace qimg

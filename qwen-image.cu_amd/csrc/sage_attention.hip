@@ -1,0 +1,592 @@
+// sage_attention.hip — SageAttention-style joint attention for gfx950.
+//
+// Semantics follow the kernels qwen-image.cu vendors from SageAttention
+// (sageattention_sm80.cu):
+//   k mean                 :759-773  sequential fp32 sum over tokens / max(S,1)
+//   Q int8, per 4 tokens   :775-824  tokens b*128 + w*32 + g + 8i, i < 4
+//   K int8, per 16 tokens  :826-886  tokens b*64 + 2g + {0,1} + 8i, i < 8,
+//                                    values k - mean
+//   attention              :47-674   int8 QK^T, base-2 online softmax over
+//                                    64-key tiles, P rounded to fp16, fp16 PV
+//                                    with fp32 accumulation, O/d -> fp16
+// The quantized values and scales are bit-identical to the reference's
+// formulas (scale = amax/127 + 1e-7, q = rne_sat(v * (1/scale))).
+//
+// MI355X design of the attention kernel:
+//  * A workgroup is 4 waves; each wave owns 32 queries (128 per workgroup,
+//    so each wave's queries are exactly one of the reference's per-thread Q
+//    scale groups' 32-token windows).
+//  * Scores are computed transposed, S^T = K Q^T, with
+//    v_mfma_i32_32x32x32_i8: lane l then holds ONE query (l % 32) and 32 of
+//    the tile's 64 keys, so the softmax row max / row sum are lane-local
+//    plus one exchange with lane l ^ 32. No 4-lane shuffles per row.
+//  * O is accumulated transposed too, O^T = V^T P^T with
+//    v_mfma_f32_32x32x16_f16: the P^T registers produced by the score MFMA
+//    are already the B operand, and the output keeps one query per lane, so
+//    the online-softmax rescale is a per-lane scalar.
+//  * V is re-laid once per call into [head][64-key tile][d][64 keys] with a
+//    fixed permutation of each 16-key group that makes a lane's 8 keys of a
+//    PV fragment contiguous (one ds_read_b128).
+//  * K (int8) and V (fp16) tiles stream through a double-buffered LDS ring
+//    with rows padded to 144 bytes (bank-conflict-free 16-byte fragment
+//    reads); Q stays in registers for the whole kernel.
+#include "qimg_device.h"
+#include "qimg_internal.h"
+
+namespace qimg {
+
+namespace {
+
+constexpr int KTILE = 64;
+constexpr int QBLK = 128;
+
+__host__ __device__ constexpr int div_up(int a, int b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- k mean
+// One thread per (head, d); the fp32 sum runs token by token in order,
+// exactly as the reference's single-thread loop, so the mean is bit-equal.
+__global__ void k_mean_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean, int BH,
+                              int S, int D) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= BH * D) return;
+    const int h = idx / D;
+    const int d = idx % D;
+    const uint16_t* p = k + static_cast<int64_t>(h) * S * D + d;
+    float sum = 0.0f;
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = f16_to_f32(p[static_cast<int64_t>(s + u) * D]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += v[u];
+    }
+    for (; s < S; ++s) sum += f16_to_f32(p[static_cast<int64_t>(s) * D]);
+    mean[idx] = sum / fmaxf(static_cast<float>(S), 1.0f);
+}
+
+// ---------------------------------------------------------------- Q quant
+// Block = 256 threads for one (head, 128-token block). Thread t holds token
+// t/2, half t%2 of the head dim (D/2 values).
+template <int D>
+__global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict__ q,
+                                                      int8_t* __restrict__ q_out,
+                                                      float* __restrict__ q_scale, int S) {
+    constexpr int HD = D / 2;
+    __shared__ float red[QBLK][2];
+    __shared__ float inv_s[32];
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int tok = b * QBLK + (tid >> 1);
+    const int part = tid & 1;
+    const bool valid = tok < S;
+    const uint16_t* src = q + (static_cast<int64_t>(h) * S + tok) * D + part * HD;
+    uint32_t raw[HD / 2];
+    float amax = 0.0f;
+    if (valid) {
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) {
+            u32x4 t = reinterpret_cast<const u32x4*>(src)[c];
+            raw[4 * c + 0] = t.x; raw[4 * c + 1] = t.y; raw[4 * c + 2] = t.z; raw[4 * c + 3] = t.w;
+        }
+#pragma unroll
+        for (int i = 0; i < HD / 2; ++i) {
+            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] & 0xffffu))));
+            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] >> 16))));
+        }
+    }
+    red[tid >> 1][part] = amax;
+    __syncthreads();
+    if (tid < 32) {
+        const int w = tid >> 3, g = tid & 7;
+        float a = 1e-7f;  // the reference starts its max at 1e-7
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int lt = w * 32 + g + 8 * i;
+            a = fmaxf(a, fmaxf(red[lt][0], red[lt][1]));
+        }
+        const float scale = a / 127.0f + 1e-7f;
+        const int nq = div_up(S, QBLK) * 32;
+        q_scale[static_cast<int64_t>(h) * nq + b * 32 + w * 8 + g] = scale;
+        inv_s[tid] = 1.0f / scale;
+    }
+    __syncthreads();
+    if (!valid) return;
+    const int lt = tid >> 1;
+    const float inv = inv_s[((lt % QBLK) / 32) * 8 + (lt & 7)];
+    int8_t* dst = q_out + (static_cast<int64_t>(h) * S + tok) * D + part * HD;
+#pragma unroll
+    for (int c = 0; c < HD / 16; ++c) {
+        u32x4 pk;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const uint32_t r = raw[8 * c + 2 * wd + bb];
+                const uint32_t lo = static_cast<uint8_t>(sat_rne_i8(f16_to_f32(static_cast<uint16_t>(r & 0xffffu)) * inv));
+                const uint32_t hi = static_cast<uint8_t>(sat_rne_i8(f16_to_f32(static_cast<uint16_t>(r >> 16)) * inv));
+                word |= (lo | (hi << 8)) << (16 * bb);
+            }
+            pk[wd] = word;
+        }
+        reinterpret_cast<u32x4*>(dst)[c] = pk;
+    }
+}
+
+// ---------------------------------------------------------------- K quant
+// Block = 128 threads for one (head, 64-token block); thread t holds token
+// t/2, half t%2 of the head dim, values k - mean.
+template <int D>
+__global__ __launch_bounds__(128) void quant_k_kernel(const uint16_t* __restrict__ k,
+                                                      const float* __restrict__ mean,
+                                                      int8_t* __restrict__ k_out,
+                                                      float* __restrict__ k_scale, int S) {
+    constexpr int HD = D / 2;
+    __shared__ float red[KTILE][2];
+    __shared__ float inv_s[4];
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int tok = b * KTILE + (tid >> 1);
+    const int part = tid & 1;
+    const bool valid = tok < S;
+    const uint16_t* src = k + (static_cast<int64_t>(h) * S + tok) * D + part * HD;
+    const float* mu = mean + static_cast<int64_t>(h) * D + part * HD;
+    float v[HD];
+    float amax = 0.0f;
+    if (valid) {
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) {
+            u32x4 t = reinterpret_cast<const u32x4*>(src)[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[8 * c + 2 * e + 0] = f16_to_f32(static_cast<uint16_t>(t[e] & 0xffffu)) - mu[8 * c + 2 * e + 0];
+                v[8 * c + 2 * e + 1] = f16_to_f32(static_cast<uint16_t>(t[e] >> 16)) - mu[8 * c + 2 * e + 1];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < HD; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    }
+    red[tid >> 1][part] = amax;
+    __syncthreads();
+    if (tid < 4) {
+        float a = 1e-7f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int lt = 2 * tid + j + 8 * i;
+                a = fmaxf(a, fmaxf(red[lt][0], red[lt][1]));
+            }
+        const float scale = a / 127.0f + 1e-7f;
+        const int nk = div_up(S, KTILE) * 4;
+        k_scale[static_cast<int64_t>(h) * nk + b * 4 + tid] = scale;
+        inv_s[tid] = 1.0f / scale;
+    }
+    __syncthreads();
+    if (!valid) return;
+    const float inv = inv_s[((tid >> 1) & 7) >> 1];
+    int8_t* dst = k_out + (static_cast<int64_t>(h) * S + tok) * D + part * HD;
+#pragma unroll
+    for (int c = 0; c < HD / 16; ++c) {
+        u32x4 pk;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+                word |= static_cast<uint32_t>(static_cast<uint8_t>(sat_rne_i8(v[16 * c + 4 * wd + bb] * inv))) << (8 * bb);
+            pk[wd] = word;
+        }
+        reinterpret_cast<u32x4*>(dst)[c] = pk;
+    }
+}
+
+// ------------------------------------------------------------ V re-layout
+// V fp16 [BH][S][D] -> Vt [BH][ceil(S/64)][D][64]: for each 64-key tile the
+// head dim becomes rows, and inside each 16-key group position p holds key
+// 8*((p%8)/4) + 4*(p/8) + p%4. Keys past S are zero.
+__device__ __forceinline__ int vt_key_of_pos(int p) {
+    const int g = p >> 4, r = p & 15;
+    return g * 16 + 8 * ((r & 7) >> 2) + 4 * (r >> 3) + (r & 3);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restrict__ v,
+                                                         uint16_t* __restrict__ vt, int S) {
+    __shared__ uint16_t tile[KTILE][D + 2];
+    const int kt = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const uint16_t* src = v + static_cast<int64_t>(h) * S * D;
+    // load 64 x D, 16 bytes per piece
+    constexpr int PIECES = KTILE * D / 8;
+    for (int pc = tid; pc < PIECES; pc += 256) {
+        const int key = pc / (D / 8);
+        const int c = pc % (D / 8);
+        const int tok = kt * KTILE + key;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (tok < S) val = reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(tok) * D)[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            tile[key][8 * c + 2 * e + 0] = static_cast<uint16_t>(val[e] & 0xffffu);
+            tile[key][8 * c + 2 * e + 1] = static_cast<uint16_t>(val[e] >> 16);
+        }
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (static_cast<int64_t>(h) * div_up(S, KTILE) + kt) * D * KTILE;
+    for (int pc = tid; pc < PIECES; pc += 256) {
+        const int d = pc / 8;
+        const int c = pc % 8;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = tile[vt_key_of_pos(8 * c + 2 * e)][d];
+            const uint32_t hi = tile[vt_key_of_pos(8 * c + 2 * e + 1)][d];
+            o[e] = lo | (hi << 16);
+        }
+        reinterpret_cast<u32x4*>(dst + d * KTILE)[c] = o;
+    }
+}
+
+// ------------------------------------------------------------ attention
+template <int D>
+struct AttnCfg {
+    static constexpr int KROW = D + 16;            // padded int8 K row (bytes)
+    static constexpr int VROW = 2 * KTILE + 16;    // padded fp16 V^T row (bytes)
+    static constexpr int K_BYTES = KTILE * KROW;
+    static constexpr int V_BYTES = D * VROW;
+    static constexpr int STAGE = K_BYTES + V_BYTES;
+    static constexpr int KSTEPS = D / 32;          // int8 MFMA k-steps
+    static constexpr int DT = D / 32;              // 32-row d tiles of O^T
+    static constexpr int K_PIECES = KTILE * D / 16;      // 16-byte pieces per K tile
+    static constexpr int V_PIECES = D * KTILE * 2 / 16;  // per V tile
+    static constexpr int K_PER_THR = K_PIECES / 256;
+    static constexpr int V_PER_THR = V_PIECES / 256;
+};
+
+template <int D, bool CAUSAL, int OUT_DT>
+__global__ __launch_bounds__(256, 2) void sage_attn_kernel(
+    const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const uint16_t* __restrict__ Vt,
+    const float* __restrict__ q_scale, const float* __restrict__ k_scale, void* __restrict__ out,
+    int S, float sm_log2) {
+    // Every rounding step is spelled out (explicit fmaf where fused), so all
+    // output-type instantiations compute identical values.
+#pragma clang fp contract(off)
+    using C = AttnCfg<D>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE];
+
+    const int qb = blockIdx.x;
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int half = lane >> 5;
+    const int nkt = div_up(S, KTILE);
+    const int q_idx = qb * QBLK + wave * 32 + l32;
+
+    // Q fragments: lane's query row, bytes [half*D/2, half*D/2 + D/2).
+    v4i qf[C::KSTEPS];
+    {
+        const int qr = q_idx < S ? q_idx : S - 1;
+        const int8_t* qp = Q + (static_cast<int64_t>(h) * S + qr) * D + half * (D / 2);
+#pragma unroll
+        for (int s = 0; s < C::KSTEPS; ++s) qf[s] = reinterpret_cast<const v4i*>(qp)[s];
+    }
+    const int nq = div_up(S, QBLK) * 32;
+    const float qsc = q_scale[static_cast<int64_t>(h) * nq + (q_idx / QBLK) * 32 +
+                              ((q_idx % QBLK) / 32) * 8 + (q_idx & 7)];
+    const float* ksh = k_scale + static_cast<int64_t>(h) * (nkt * 4);
+
+    int kt_end = nkt;
+    if (CAUSAL) {
+        const int lim = (qb + 1) * QBLK < S ? (qb + 1) * QBLK : S;
+        kt_end = div_up(lim, KTILE);
+    }
+
+    const int8_t* Kh = K + static_cast<int64_t>(h) * S * D;
+    const uint16_t* Vh = Vt + static_cast<int64_t>(h) * nkt * D * KTILE;
+
+    // cooperative tile copies (global -> registers -> LDS)
+    v4i kreg[C::K_PER_THR], vreg[C::V_PER_THR];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < C::K_PER_THR; ++i) {
+            const int pc = tid + 256 * i;
+            const int key = pc / (D / 16);
+            const int c = pc % (D / 16);
+            const int tok = kt * KTILE + key;
+            kreg[i] = (v4i){0, 0, 0, 0};
+            if (tok < S) kreg[i] = reinterpret_cast<const v4i*>(Kh + static_cast<int64_t>(tok) * D)[c];
+        }
+        const v4i* vsrc = reinterpret_cast<const v4i*>(Vh + static_cast<int64_t>(kt) * D * KTILE);
+#pragma unroll
+        for (int i = 0; i < C::V_PER_THR; ++i) vreg[i] = vsrc[tid + 256 * i];
+    };
+    auto store_tile = [&](int buf) {
+        uint8_t* base = lds + buf * C::STAGE;
+#pragma unroll
+        for (int i = 0; i < C::K_PER_THR; ++i) {
+            const int pc = tid + 256 * i;
+            const int key = pc / (D / 16);
+            const int c = pc % (D / 16);
+            *reinterpret_cast<v4i*>(base + key * C::KROW + c * 16) = kreg[i];
+        }
+        uint8_t* vb = base + C::K_BYTES;
+#pragma unroll
+        for (int i = 0; i < C::V_PER_THR; ++i) {
+            const int pc = tid + 256 * i;
+            const int d = pc / 8;
+            const int c = pc % 8;
+            *reinterpret_cast<v4i*>(vb + d * C::VROW + c * 16) = vreg[i];
+        }
+    };
+
+    v16f o[C::DT];
+#pragma unroll
+    for (int t = 0; t < C::DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+    float m = -5000000.0f;  // running max (base-2 scaled), as the reference
+    float dsum = 0.0f;      // this lane-half's share of the row sum
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < kt_end; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < kt_end;
+        if (more) load_tile(kt + 1);
+
+        const uint8_t* kb_lds = lds + cur * C::STAGE;
+        const uint8_t* vb_lds = kb_lds + C::K_BYTES;
+
+        // S^T blocks: keys 32*kb + (8*(r/4) + 4*half + r%4), query l32.
+        v16i sacc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0;
+            const uint8_t* krow = kb_lds + (kb * 32 + l32) * C::KROW + half * (D / 2);
+#pragma unroll
+            for (int s = 0; s < C::KSTEPS; ++s) {
+                const v4i kf = *reinterpret_cast<const v4i*>(krow + 16 * s);
+                sacc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[s], sacc[kb], 0, 0, 0);
+            }
+        }
+
+        // Per-lane multipliers: key group g = (key % 8) / 2 = 2*half + (r%4)/2.
+        const float4 ks4 = *reinterpret_cast<const float4*>(ksh + kt * 4);
+        const float ks_lo = half ? ks4.z : ks4.x;
+        const float ks_hi = half ? ks4.w : ks4.y;
+        const float mul_lo = sm_log2 * (qsc * ks_lo);
+        const float mul_hi = sm_log2 * (qsc * ks_hi);
+
+        // validity of each key slot (tail tile / causal diagonal)
+        const int kbase = kt * KTILE;
+        const bool need_mask = (kbase + KTILE > S) || (CAUSAL && kbase + KTILE - 1 > qb * QBLK);
+        auto key_ok = [&](int kb, int r) {
+            const int key = kbase + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            bool ok = key < S;
+            if (CAUSAL) ok = ok && key <= q_idx;
+            return ok;
+        };
+
+        // tile max: integer max per scale group, then one multiply each
+        // (max of fl(acc*c) equals fl(max(acc)*c) for c > 0).
+        int mx_lo = INT32_MIN, mx_hi = INT32_MIN;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int a = sacc[kb][r];
+                if (need_mask && !key_ok(kb, r)) a = INT32_MIN;
+                if ((r & 2) == 0) mx_lo = max(mx_lo, a);
+                else mx_hi = max(mx_hi, a);
+            }
+        float mt = -5000000.0f;
+        if (mx_lo != INT32_MIN) mt = fmaxf(mt, static_cast<float>(mx_lo) * mul_lo);
+        if (mx_hi != INT32_MIN) mt = fmaxf(mt, static_cast<float>(mx_hi) * mul_hi);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m, mt);
+        const float o_scale = __builtin_amdgcn_exp2f(m - m_new);
+        m = m_new;
+        dsum *= o_scale;
+#pragma unroll
+        for (int t = 0; t < C::DT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[t][r] *= o_scale;
+
+        // P = exp2(acc * mult - m) -> fp16, as PV B-operand fragments.
+        const float neg_m = -m_new;
+        v8h pf[4];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float mul = (r & 2) ? mul_hi : mul_lo;
+                float p = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(sacc[kb][r]), mul, neg_m));
+                if (need_mask && !key_ok(kb, r)) p = 0.0f;
+                pf[2 * kb + (r >> 3)][r & 7] = static_cast<_Float16>(p);
+            }
+        // row-sum share of the fp16-rounded P (fp32 accumulate)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float part = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part += static_cast<float>(pf[t][e]);
+            dsum += part;
+        }
+
+        // O^T += V^T P^T over the tile's four 16-key groups.
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) {
+                const v8h vf = *reinterpret_cast<const v8h*>(vb_lds + (dt * 32 + l32) * C::VROW +
+                                                              (16 * t + 8 * half) * 2);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], o[dt], 0, 0, 0);
+            }
+        }
+
+        if (more) store_tile(cur ^ 1);
+        __syncthreads();
+    }
+
+    // combine the two lane-halves' row sums, normalise, store.
+    const float dtot = dsum + __shfl_xor(dsum, 32, 64);
+    if (q_idx >= S) return;
+    const float rcp = 1.0f / dtot;
+    const int64_t orow = (static_cast<int64_t>(h) * S + q_idx) * D;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = dt * 32 + 8 * g + 4 * half;
+            uint16_t hv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                // O * (1/d) is rounded to fp32 and then to fp16, as the
+                // reference does; the empty asm keeps the compiler from
+                // fusing both roundings into one v_fma_mix.
+                float t = o[dt][4 * g + c] * rcp;
+                asm volatile("" : "+v"(t));
+                hv[c] = f32_to_f16(t);
+            }
+            if (OUT_DT == QIMG_FP16) {
+                uint16_t* op = reinterpret_cast<uint16_t*>(out) + orow + d0;
+                *reinterpret_cast<uint2*>(op) = make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16),
+                                                           hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
+            } else if (OUT_DT == QIMG_FP32) {
+                float* op = reinterpret_cast<float*>(out) + orow + d0;
+                *reinterpret_cast<v4f*>(op) = (v4f){f16_to_f32(hv[0]), f16_to_f32(hv[1]),
+                                                    f16_to_f32(hv[2]), f16_to_f32(hv[3])};
+            } else {
+                uint16_t* op = reinterpret_cast<uint16_t*>(out) + orow + d0;
+                uint16_t b[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) b[c] = f32_to_bf16(f16_to_f32(hv[c]));
+                *reinterpret_cast<uint2*>(op) = make_uint2(b[0] | (static_cast<uint32_t>(b[1]) << 16),
+                                                           b[2] | (static_cast<uint32_t>(b[3]) << 16));
+            }
+        }
+    }
+}
+
+template <int D, bool CAUSAL>
+hipError_t launch_attn_dt(const int8_t* q, const int8_t* k, const uint16_t* vt, const float* qs,
+                          const float* ks, void* out, int out_dt, int BH, int S, float sm_log2,
+                          hipStream_t stream) {
+    dim3 grid(div_up(S, QBLK), BH);
+    if (out_dt == QIMG_FP16)
+        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_FP16>), grid, dim3(256), 0, stream, q, k,
+                           vt, qs, ks, out, S, sm_log2);
+    else if (out_dt == QIMG_FP32)
+        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_FP32>), grid, dim3(256), 0, stream, q, k,
+                           vt, qs, ks, out, S, sm_log2);
+    else
+        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_BF16>), grid, dim3(256), 0, stream, q, k,
+                           vt, qs, ks, out, S, sm_log2);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int64_t sage_vt_bytes(int BH, int S, int D) {
+    return static_cast<int64_t>(BH) * div_up(S, KTILE) * KTILE * D * 2;
+}
+
+static int64_t align256(int64_t v) { return (v + 255) & ~static_cast<int64_t>(255); }
+
+int64_t sage_scratch_layout(int BH, int S, int D, void* base, SageScratch* out) {
+    const int64_t nqkv = static_cast<int64_t>(BH) * S * D;
+    const int64_t o_q = 0;
+    const int64_t o_k = o_q + align256(nqkv);
+    const int64_t o_vt = o_k + align256(nqkv);
+    const int64_t o_qs = o_vt + align256(sage_vt_bytes(BH, S, D));
+    const int64_t o_ks = o_qs + align256(static_cast<int64_t>(BH) * div_up(S, QBLK) * 32 * 4);
+    const int64_t o_mu = o_ks + align256(static_cast<int64_t>(BH) * div_up(S, KTILE) * 4 * 4);
+    const int64_t total = o_mu + align256(static_cast<int64_t>(BH) * D * 4);
+    if (out && base) {
+        char* b = static_cast<char*>(base);
+        out->q_i8 = reinterpret_cast<int8_t*>(b + o_q);
+        out->k_i8 = reinterpret_cast<int8_t*>(b + o_k);
+        out->v_t = reinterpret_cast<uint16_t*>(b + o_vt);
+        out->q_scale = reinterpret_cast<float*>(b + o_qs);
+        out->k_scale = reinterpret_cast<float*>(b + o_ks);
+        out->k_mean = reinterpret_cast<float*>(b + o_mu);
+    }
+    return total;
+}
+
+hipError_t launch_sage_k_mean(const uint16_t* k, float* mean, int BH, int S, int D,
+                              hipStream_t stream) {
+    const int n = BH * D;
+    hipLaunchKernelGGL(k_mean_kernel, dim3(div_up(n, 64)), dim3(64), 0, stream, k, mean, BH, S, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_sage_quant_q(const uint16_t* q, int8_t* q_out, float* q_scale, int BH, int S,
+                               int D, hipStream_t stream) {
+    dim3 grid(div_up(S, QBLK), BH);
+    if (D == 128)
+        hipLaunchKernelGGL(quant_q_kernel<128>, grid, dim3(256), 0, stream, q, q_out, q_scale, S);
+    else
+        hipLaunchKernelGGL(quant_q_kernel<64>, grid, dim3(256), 0, stream, q, q_out, q_scale, S);
+    return hipGetLastError();
+}
+
+hipError_t launch_sage_quant_k(const uint16_t* k, const float* mean, int8_t* k_out,
+                               float* k_scale, int BH, int S, int D, hipStream_t stream) {
+    dim3 grid(div_up(S, KTILE), BH);
+    if (D == 128)
+        hipLaunchKernelGGL(quant_k_kernel<128>, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
+    else
+        hipLaunchKernelGGL(quant_k_kernel<64>, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
+    return hipGetLastError();
+}
+
+hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
+                            const float* q_scale, const float* k_scale, void* out, int out_dtype,
+                            int BH, int S, int D, float sm_scale, int causal, uint16_t* v_t,
+                            hipStream_t stream) {
+    dim3 vgrid(div_up(S, KTILE), BH);
+    if (D == 128)
+        hipLaunchKernelGGL(v_relayout_kernel<128>, vgrid, dim3(256), 0, stream, v, v_t, S);
+    else
+        hipLaunchKernelGGL(v_relayout_kernel<64>, vgrid, dim3(256), 0, stream, v, v_t, S);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const float sm_log2 = sm_scale * 1.44269504088896340736f;
+    if (D == 128)
+        return causal ? launch_attn_dt<128, true>(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, sm_log2, stream)
+                      : launch_attn_dt<128, false>(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, sm_log2, stream);
+    return causal ? launch_attn_dt<64, true>(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, sm_log2, stream)
+                  : launch_attn_dt<64, false>(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, sm_log2, stream);
+}
+
+}  // namespace qimg

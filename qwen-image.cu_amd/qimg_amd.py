@@ -1,0 +1,272 @@
+"""Python binding of the gfx950 hot-path library (lib/libqimg_hot.so).
+
+Mirrors the reference's operator surface (cuda_kernels.cuh) on torch device
+tensors: names, argument meaning and error behaviour follow the reference,
+except that failures raise QimgError instead of aborting the process.
+
+There is no CPU fallback: every operator runs the HIP kernels, and importing
+this module fails loudly when the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libqimg_hot.so")
+
+QIMG_OK, QIMG_ERR_INVALID_ARG, QIMG_ERR_UNSUPPORTED, QIMG_ERR_SCRATCH, QIMG_ERR_HIP = range(5)
+FP32, BF16, FP16, INT8, INT32, FP8_E4M3 = range(6)
+INT8_HADAMARD, FP8_HADAMARD = 0, 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+_SIGS = {
+    "qimg_status_string": (ctypes.c_char_p, [_I]),
+    "qimg_last_error": (ctypes.c_char_p, []),
+    "qimg_version": (ctypes.c_char_p, []),
+    "qimg_hadamard_block_size": (_I, [_I]),
+    "qimg_int8_scratch_bytes": (_I64, [_I, _I, _I]),
+    "qimg_fwht_inplace": (_I, [_P, _I, _I, _I, _P]),
+    "qimg_quantize_per_row_fp32": (_I, [_P, _P, _P, _I, _I, _P]),
+    "qimg_quantize_activation": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "qimg_quantize_weight": (_I, [_P, _I, _I, _I, _I, _P, _P, ctypes.POINTER(_I), _P]),
+    "qimg_linear_prequantized": (_I, [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P]),
+    "qimg_linear": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I64, _P]),
+    "qimg_sage_scratch_bytes": (_I64, [_I, _I, _I]),
+    "qimg_sage_k_mean": (_I, [_P, _P, _I, _I, _I, _P]),
+    "qimg_sage_quant_q": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "qimg_sage_quant_k": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "qimg_sage_attn_quantized": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P, _I64, _P]),
+    "qimg_sage_attention": (_I, [_P, _P, _P, _P, _I, _F, _I, _I, _I, _I, _P, _I64, _P]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+class QimgError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with qwen-image.cu_amd/build.py "
+                          "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = load_library()
+
+
+def lib() -> ctypes.CDLL:
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != QIMG_OK:
+        raise QimgError(status, _lib.qimg_last_error().decode())
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_DT = {torch.float32: FP32, torch.bfloat16: BF16, torch.float16: FP16, torch.int8: INT8,
+       torch.int32: INT32, torch.float8_e4m3fn: FP8_E4M3, torch.uint8: FP8_E4M3}
+_TORCH = {FP32: torch.float32, BF16: torch.bfloat16, FP16: torch.float16}
+
+
+def _dev(t: torch.Tensor, name: str):
+    if not t.is_cuda:
+        raise QimgError(QIMG_ERR_INVALID_ARG, f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise QimgError(QIMG_ERR_INVALID_ARG, f"{name} must be contiguous")
+
+
+# --------------------------------------------------------------- helpers
+def hadamard_block_size(K: int) -> int:
+    """cuda_kernels.cuh:253"""
+    return int(_lib.qimg_hadamard_block_size(int(K)))
+
+
+def int8_scratch_bytes(M: int, K: int, N: int) -> int:
+    """cuda_kernels.cuh:311-319"""
+    return int(_lib.qimg_int8_scratch_bytes(int(M), int(K), int(N)))
+
+
+@dataclass
+class QuantizedWeight:
+    """cuda_kernels.cuh:187-245 (the INT8/FP8 fields)."""
+    data: torch.Tensor       # [N, K] int8 (INT8_HADAMARD) or uint8 e4m3 bits (FP8_HADAMARD)
+    scales: torch.Tensor     # [N] fp32
+    had_block_size: int
+    mode: int = INT8_HADAMARD
+
+
+# --------------------------------------------------------- quantization
+def fwht_inplace(data: torch.Tensor, had_block_size: int) -> torch.Tensor:
+    """cuda_kernels.cu:2209-2254 on fp32 [M, K] rows, in place."""
+    _dev(data, "data")
+    M, K = data.shape
+    _check(_lib.qimg_fwht_inplace(_ptr(data), M, K, int(had_block_size), _stream()))
+    return data
+
+
+def quantize_per_row_fp32(x: torch.Tensor):
+    """cuda_kernels.cu:2385-2416 -> (int8 [M,K], fp32 [M])."""
+    _dev(x, "x")
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _check(_lib.qimg_quantize_per_row_fp32(_ptr(x), _ptr(q), _ptr(s), M, K, _stream()))
+    return q, s
+
+
+def quantize_activation_hadamard(x: torch.Tensor, had_block_size: int, mode: int = INT8_HADAMARD):
+    """quantize_activation_int8_hadamard_{fp32,bf16} (cuda_kernels.cu:2603-2619);
+    FP8_HADAMARD gives e4m3 bytes (uint8) with scale amax/448."""
+    _dev(x, "x")
+    M, K = x.shape
+    qdt = torch.int8 if mode == INT8_HADAMARD else torch.uint8
+    q = torch.empty((M, K), dtype=qdt, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _check(_lib.qimg_quantize_activation(_ptr(x), _DT[x.dtype], M, K, int(had_block_size), int(mode),
+                                         _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def quantize_weight_tensor(w: torch.Tensor, mode: int = INT8_HADAMARD) -> QuantizedWeight:
+    """cuda_kernels.cu:2830-2862: bf16 [N,K] -> FWHT(K & -K) -> per-row quant."""
+    _dev(w, "weight")
+    N, K = w.shape
+    qdt = torch.int8 if mode == INT8_HADAMARD else torch.uint8
+    q = torch.empty((N, K), dtype=qdt, device=w.device)
+    s = torch.empty((N,), dtype=torch.float32, device=w.device)
+    hbs = _I(0)
+    _check(_lib.qimg_quantize_weight(_ptr(w), _DT[w.dtype], N, K, int(mode), _ptr(q), _ptr(s),
+                                     ctypes.byref(hbs), _stream()))
+    return QuantizedWeight(q, s, int(hbs.value), mode)
+
+
+# ---------------------------------------------------------------- linear
+def linear_forward_prequantized(act_q: torch.Tensor, act_scales: torch.Tensor, weight: QuantizedWeight,
+                                bias: torch.Tensor | None = None, apply_gelu: bool = False,
+                                out: torch.Tensor | None = None, out_dtype=torch.float32) -> torch.Tensor:
+    """linear_forward_int8_prequantized (cuda_kernels.cu:2734-2773), epilogue fused."""
+    _dev(act_q, "act_q")
+    M, K = act_q.shape
+    N = weight.data.shape[0]
+    if weight.data.shape[1] != K:
+        raise QimgError(QIMG_ERR_INVALID_ARG, f"weight K {weight.data.shape[1]} != activation K {K}")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=act_q.device)
+    _check(_lib.qimg_linear_prequantized(_ptr(act_q), _ptr(act_scales), M, K, _ptr(weight.data),
+                                         _ptr(weight.scales), N, int(weight.mode), _ptr(bias), _ptr(out),
+                                         _DT[out.dtype], int(bool(apply_gelu)), _stream()))
+    return out
+
+
+def linear_forward_quantized(x: torch.Tensor, weight: QuantizedWeight, bias: torch.Tensor | None = None,
+                             out: torch.Tensor | None = None, scratch: torch.Tensor | None = None,
+                             apply_gelu: bool = False, out_dtype=torch.float32) -> torch.Tensor:
+    """linear_forward_quantized / _bf16in (cuda_kernels.cu:4599-4635) for the
+    INT8/FP8 Hadamard modes: x fp32 or bf16 [M,K] -> out [M,N]."""
+    _dev(x, "x")
+    M, K = x.shape
+    N = weight.data.shape[0]
+    if weight.data.shape[1] != K:
+        raise QimgError(QIMG_ERR_INVALID_ARG, f"weight K {weight.data.shape[1]} != activation K {K}")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if scratch is None:
+        scratch = torch.empty((int8_scratch_bytes(M, K, N),), dtype=torch.uint8, device=x.device)
+    _check(_lib.qimg_linear(_ptr(x), _DT[x.dtype], M, K, _ptr(weight.data), _ptr(weight.scales), N,
+                            int(weight.had_block_size), int(weight.mode), _ptr(bias), _ptr(out),
+                            _DT[out.dtype], int(bool(apply_gelu)), _ptr(scratch), scratch.numel(),
+                            _stream()))
+    return out
+
+
+# ---------------------------------------------------------- SageAttention
+def sage_scratch_bytes(BH: int, S: int, D: int) -> int:
+    return int(_lib.qimg_sage_scratch_bytes(BH, S, D))
+
+
+def sage_k_mean(k: torch.Tensor) -> torch.Tensor:
+    """sageattention_sm80.cu:759-773"""
+    _dev(k, "k")
+    BH, S, D = k.shape
+    mean = torch.empty((BH, D), dtype=torch.float32, device=k.device)
+    _check(_lib.qimg_sage_k_mean(_ptr(k), _ptr(mean), BH, S, D, _stream()))
+    return mean
+
+
+def sage_quant_q(q: torch.Tensor):
+    """sageattention_sm80.cu:775-824"""
+    _dev(q, "q")
+    BH, S, D = q.shape
+    qi = torch.empty((BH, S, D), dtype=torch.int8, device=q.device)
+    qs = torch.empty((BH, (S + 127) // 128 * 32), dtype=torch.float32, device=q.device)
+    _check(_lib.qimg_sage_quant_q(_ptr(q), _ptr(qi), _ptr(qs), BH, S, D, _stream()))
+    return qi, qs
+
+
+def sage_quant_k(k: torch.Tensor, mean: torch.Tensor):
+    """sageattention_sm80.cu:826-886"""
+    _dev(k, "k")
+    BH, S, D = k.shape
+    ki = torch.empty((BH, S, D), dtype=torch.int8, device=k.device)
+    ks = torch.empty((BH, (S + 63) // 64 * 4), dtype=torch.float32, device=k.device)
+    _check(_lib.qimg_sage_quant_k(_ptr(k), _ptr(mean), _ptr(ki), _ptr(ks), BH, S, D, _stream()))
+    return ki, ks
+
+
+def sage_attn_quantized(q_i8, k_i8, v, q_scale, k_scale, sm_scale, causal=False, out_dtype=torch.float16,
+                        scratch=None):
+    """qk_int_sv_f16_attn_kernel (sageattention_sm80.cu:47-674) on pre-quantized Q/K."""
+    BH, S, D = q_i8.shape
+    out = torch.empty((BH, S, D), dtype=out_dtype, device=q_i8.device)
+    if scratch is None:
+        scratch = torch.empty((sage_scratch_bytes(BH, S, D),), dtype=torch.uint8, device=q_i8.device)
+    _check(_lib.qimg_sage_attn_quantized(_ptr(q_i8), _ptr(k_i8), _ptr(v), _ptr(q_scale), _ptr(k_scale),
+                                         _ptr(out), _DT[out_dtype], BH, S, D, float(sm_scale),
+                                         int(bool(causal)), _ptr(scratch), scratch.numel(), _stream()))
+    return out
+
+
+def attention_forward_sage_fp16io(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                                  causal: bool = False, out: torch.Tensor | None = None,
+                                  out_dtype=torch.float32, scratch: torch.Tensor | None = None):
+    """attention_forward_sage_sm80_fp16io (sageattention_sm80.cu:965-1027):
+    fp16 [BH,S,D] q,k,v -> out [BH,S,D] (fp32 by default, as the reference)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dev(t, n)
+        if t.dtype != torch.float16:
+            raise QimgError(QIMG_ERR_INVALID_ARG, f"{n} must be float16")
+    BH, S, D = q.shape
+    if out is None:
+        out = torch.empty((BH, S, D), dtype=out_dtype, device=q.device)
+    if scratch is None:
+        scratch = torch.empty((max(sage_scratch_bytes(BH, S, D), 1),), dtype=torch.uint8, device=q.device)
+    _check(_lib.qimg_sage_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _DT[out.dtype], float(scale),
+                                    BH, S, D, int(bool(causal)), _ptr(scratch), scratch.numel(), _stream()))
+    return out

@@ -1,0 +1,168 @@
+"""GPU parity: the fused quantized linear against the oracle.
+
+* The integer product is checked exactly: with unit scales and no bias the
+  fp32 output is fl(acc), the correctly rounded int32 dot product.
+* The dequant epilogue (no GELU) follows the reference's operation order
+  without contraction, so it is compared bit for bit as well.
+* GELU (tanhf), bf16 outputs and e4m3 accumulation order are checked against
+  tolerances: max|a-b|/max|b| <= 2e-2 and cosine >= 0.999 (the stated bar),
+  plus much tighter bounds where the arithmetic allows.
+* At the full layer shapes the oracle runs on a sample of rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _metrics(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    rel = np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30)
+    cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+    return rel, cos
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _bf16_dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(DEV).view(torch.bfloat16)
+
+
+def _qw(qimg, q, s, hbs, mode=0):
+    return qimg.QuantizedWeight(_dev(q), _dev(s), hbs, mode)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (256, 256, 64), (1, 64, 64), (7, 300, 192), (300, 7, 128), (513, 520, 3072),
+    (257, 255, 1024), (64, 3072, 3072), (4096, 3072, 3072),
+])
+def test_int8_gemm_exact(qimg, oracle, M, N, K):
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    ones_m = np.ones(M, np.float32)
+    ones_n = np.ones(N, np.float32)
+    rows = (0, M) if M * N * K <= 2 ** 31 else None
+    out = qimg.linear_forward_prequantized(_dev(a), _dev(ones_m), _qw(qimg, w, ones_n, 1))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    if rows is None:  # full-size: check a sample of rows
+        idx = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 62)]))
+        ref = (a[idx].astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+        np.testing.assert_array_equal(got[idx], ref)
+    else:
+        ref = oracle.gemm_s8s8s32(a, w).astype(np.float32)
+        np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,N,K,with_bias", [(300, 320, 3072, True), (64, 256, 12288, True),
+                                             (130, 200, 256, False), (5, 96, 100, True)])
+def test_int8_linear_fp32_bit_exact(qimg, oracle, M, N, K, with_bias):
+    rng = np.random.default_rng(M * N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32)) if with_bias else None
+    wq, ws, hbs = oracle.quantize_weight_bf16(w_bits)
+    ref = oracle.linear_w8a8(x, wq, ws, hbs, b_bits)
+    out = qimg.linear_forward_quantized(_dev(x), _qw(qimg, wq, ws, hbs),
+                                        None if b_bits is None else _bf16_dev(b_bits))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+def test_int8_linear_gelu_and_bf16_out(qimg, oracle):
+    rng = np.random.default_rng(21)
+    M, N, K = 320, 512, 3072
+    x_bits = oracle.bf16_bits_from_f32(rng.standard_normal((M, K)).astype(np.float32))
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    wq, ws, hbs = oracle.quantize_weight_bf16(w_bits)
+    qw = _qw(qimg, wq, ws, hbs)
+    ref_g = oracle.linear_w8a8(x_bits, wq, ws, hbs, b_bits, gelu=True)
+    ref = oracle.linear_w8a8(x_bits, wq, ws, hbs, b_bits, gelu=False)
+    xd, bd = _bf16_dev(x_bits), _bf16_dev(b_bits)
+    g = qimg.linear_forward_quantized(xd, qw, bd, apply_gelu=True)
+    o16 = qimg.linear_forward_quantized(xd, qw, bd, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(g.cpu().numpy(), ref_g, rtol=2e-6, atol=2e-6)
+    np.testing.assert_array_equal(o16.float().cpu().numpy(),
+                                  oracle.bf16_bits_to_f32(oracle.bf16_bits_from_f32(ref)).reshape(M, N))
+    # end to end against the unquantized product (the stated tolerance)
+    xf = oracle.bf16_bits_to_f32(x_bits).reshape(M, K).astype(np.float64)
+    wf = oracle.bf16_bits_to_f32(w_bits).reshape(N, K).astype(np.float64)
+    exact = xf @ wf.T + oracle.bf16_bits_to_f32(b_bits)
+    rel, cos = _metrics(o16.float().cpu().numpy(), exact)
+    assert rel <= 2e-2 and cos >= 0.999, (rel, cos)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 3072), (100, 300, 12288), (4352, 512, 3072)])
+def test_fp8_linear(qimg, oracle, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    wq, ws, hbs = oracle.quantize_weight_fp8(w_bits)
+    xq, xs = oracle.quantize_activation_fp8(x, hbs)
+    rows = (0, min(M, 256))
+    ref = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, rows=rows)[rows[0]:rows[1]]
+    qw = _qw(qimg, wq, ws, hbs, mode=qimg.FP8_HADAMARD)
+    out = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()[rows[0]:rows[1]]
+    # fp32 accumulation order differs from the float64 oracle sum only
+    scale = np.abs(ref).max()
+    assert np.max(np.abs(got - ref)) <= 1e-5 * scale * np.sqrt(K / 64), np.max(np.abs(got - ref))
+    exact = x[rows[0]:rows[1]].astype(np.float64) @ oracle.bf16_bits_to_f32(w_bits).reshape(N, K).astype(np.float64).T \
+        + oracle.bf16_bits_to_f32(b_bits)
+    rel, cos = _metrics(got, exact)
+    assert rel <= 5e-2 and cos >= 0.999, (rel, cos)
+
+
+@pytest.mark.slow
+def test_mlp_pair_full_size_sampled(qimg, oracle):
+    """MMDiT MLP at M=4352: fc1 (3072->12288, GELU) -> FWHT(4096)+quant -> fc2,
+    checked on sampled rows against the oracle chain and the float64 MLP."""
+    rng = np.random.default_rng(0)
+    M, D, H = 4352, 3072, 12288
+    x_bits = oracle.bf16_bits_from_f32(rng.standard_normal((M, D)).astype(np.float32))
+    w1 = oracle.bf16_bits_from_f32((rng.standard_normal((H, D)) * 0.02).astype(np.float32))
+    w2 = oracle.bf16_bits_from_f32((rng.standard_normal((D, H)) * 0.02).astype(np.float32))
+    b1 = oracle.bf16_bits_from_f32((rng.standard_normal(H) * 0.01).astype(np.float32))
+    b2 = oracle.bf16_bits_from_f32((rng.standard_normal(D) * 0.01).astype(np.float32))
+    qw1 = qimg.quantize_weight_tensor(_bf16_dev(w1))
+    qw2 = qimg.quantize_weight_tensor(_bf16_dev(w2))
+    h = qimg.linear_forward_quantized(_bf16_dev(x_bits), qw1, _bf16_dev(b1), apply_gelu=True)
+    y = qimg.linear_forward_quantized(h, qw2, _bf16_dev(b2), out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    idx = np.unique(np.concatenate([[0, 4095, 4096, M - 1], rng.integers(0, M, 28)]))
+    w1q, w1s, _ = oracle.quantize_weight_bf16(w1)
+    w2q, w2s, _ = oracle.quantize_weight_bf16(w2)
+    np.testing.assert_array_equal(qw1.data.cpu().numpy(), w1q)
+    np.testing.assert_array_equal(qw2.scales.cpu().numpy(), w2s)
+    h_ref = oracle.linear_w8a8(x_bits[idx], w1q, w1s, 1024, b1, gelu=True)
+    h_got = h.cpu().numpy()[idx]
+    np.testing.assert_allclose(h_got, h_ref, rtol=2e-6, atol=2e-6)
+    y_ref = oracle.linear_w8a8(h_got, w2q, w2s, 4096, b2)
+    y_got = y.float().cpu().numpy()[idx]
+    rel, cos = _metrics(y_got, y_ref)
+    assert rel <= 1e-2 and cos >= 0.99999, (rel, cos)
+    xf = oracle.bf16_bits_to_f32(x_bits).reshape(M, D)[idx].astype(np.float64)
+    w1f = oracle.bf16_bits_to_f32(w1).reshape(H, D).astype(np.float64)
+    w2f = oracle.bf16_bits_to_f32(w2).reshape(D, H).astype(np.float64)
+    t = xf @ w1f.T + oracle.bf16_bits_to_f32(b1)
+    t = 0.5 * t * (1 + np.tanh(0.7978845608 * (t + 0.044715 * t ** 3)))
+    exact = t @ w2f.T + oracle.bf16_bits_to_f32(b2)
+    # The reference algorithm itself is ~6% max-rel from exact math here: the
+    # FWHT folds the GELU output's positive mean into one coefficient per
+    # 4096-block, which then sets the per-token int8 scale of fc2's input.
+    # The GPU must be as close to exact math as the oracle chain is.
+    y_chain = oracle.linear_w8a8(h_ref, w2q, w2s, 4096, b2)
+    rel_o, cos_o = _metrics(y_chain, exact)
+    rel, cos = _metrics(y_got, exact)
+    assert rel <= rel_o * 1.05 + 1e-3 and cos >= cos_o - 1e-4, (rel, cos, rel_o, cos_o)
+    assert cos_o >= 0.99

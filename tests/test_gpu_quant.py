@@ -1,0 +1,108 @@
+"""GPU parity: fused FWHT + quantization kernels against the oracle.
+Quantized values and scales must be bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _bf16_dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(DEV).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,K,in_bf16", [
+    (4096, 3072, True),      # C1 img activations (bf16 in)
+    (256, 3072, False),      # txt activations, fp32 in (the reference's path)
+    (64, 12288, False),      # fc2 input, hbs 4096
+    (1, 3072, False),        # modulation / timestep row
+    (33, 256, True),         # K = 256 (timestep linear_1)
+    (5, 3584, True),         # hbs 512 (odd power of two: non-exact norm)
+    (3, 96, False),          # hbs 32
+    (7, 24, False),          # hbs 8: scalar path
+    (4, 17, True),           # hbs 1: plain per-token quantization
+])
+def test_activation_quant_int8_bit_exact(qimg, oracle, M, K, in_bf16):
+    rng = np.random.default_rng(M * 131 + K)
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
+    hbs = K & -K
+    if in_bf16:
+        bits = oracle.bf16_bits_from_f32(x)
+        q_ref, s_ref = oracle.quantize_activation(bits, hbs, is_bf16=True)
+        xd = _bf16_dev(bits)
+    else:
+        q_ref, s_ref = oracle.quantize_activation(x, hbs, is_bf16=False)
+        xd = torch.from_numpy(x).to(DEV)
+    q, s = qimg.quantize_activation_hadamard(xd, hbs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("M,K", [(128, 3072), (16, 12288), (3, 64)])
+def test_activation_quant_fp8_bit_exact(qimg, oracle, M, K):
+    rng = np.random.default_rng(K + 7)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    hbs = K & -K
+    q_ref, s_ref = oracle.quantize_activation_fp8(x, hbs)
+    q, s = qimg.quantize_activation_hadamard(torch.from_numpy(x).to(DEV), hbs, mode=qimg.FP8_HADAMARD)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_activation_quant_special_rows(qimg, oracle):
+    K = 3072
+    x = np.zeros((4, K), np.float32)
+    x[1, 17] = 3.0
+    x[2, :] = -1.0
+    x[3, ::7] = 1e-30
+    q_ref, s_ref = oracle.quantize_activation(x, 1024, is_bf16=False)
+    q, s = qimg.quantize_activation_hadamard(torch.from_numpy(x).to(DEV), 1024)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    assert s_ref[0] == 0 and not q_ref[0].any()
+
+
+@pytest.mark.parametrize("N,K,mode", [(3072, 3072, 0), (12288, 3072, 0), (3072, 12288, 0),
+                                      (18432, 3072, 0), (512, 3072, 1), (256, 12288, 1)])
+def test_weight_quant_bit_exact(qimg, oracle, N, K, mode):
+    rng = np.random.default_rng(N + K + mode)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    bits = oracle.bf16_bits_from_f32(w)
+    if mode == 0:
+        q_ref, s_ref, hbs_ref = oracle.quantize_weight_bf16(bits)
+    else:
+        q_ref, s_ref, hbs_ref = oracle.quantize_weight_fp8(bits)
+    qw = qimg.quantize_weight_tensor(_bf16_dev(bits), mode=mode)
+    assert qw.had_block_size == hbs_ref
+    np.testing.assert_array_equal(qw.scales.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(qw.data.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
+
+
+def test_fwht_inplace_and_per_row(qimg, oracle):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((300, 3072)).astype(np.float32)
+    xd = torch.from_numpy(x).to(DEV)
+    qimg.fwht_inplace(xd, 1024)
+    torch.cuda.synchronize()
+    ref = oracle.fwht_rows(x, 1024)
+    np.testing.assert_array_equal(xd.cpu().numpy(), ref)
+    q, s = qimg.quantize_per_row_fp32(xd)
+    q_ref, s_ref = oracle.quant_rows_int8(ref)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_quant_repeatable_and_empty(qimg):
+    x = torch.randn(64, 3072, device=DEV)
+    a = qimg.quantize_activation_hadamard(x, 1024)
+    b = qimg.quantize_activation_hadamard(x, 1024)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    e = qimg.quantize_activation_hadamard(torch.empty(0, 3072, device=DEV), 1024)
+    assert e[0].shape == (0, 3072)

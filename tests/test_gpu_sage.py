@@ -1,0 +1,115 @@
+"""GPU parity: SageAttention. K mean, Q/K int8 values and scales must be
+bit-exact against the oracle; the attention output is compared with the
+oracle (same quantized inputs; differences come only from exp2/rcp ulps and
+fp32 summation order inside the MFMAs) and with float64 attention on the
+unquantized inputs at the stated tolerance."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _metrics(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    rel = np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30)
+    cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+    return rel, cos
+
+
+def _inputs(BH, S, D, seed, kshift=0.5):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((BH, S, D)).astype(np.float16)
+    k = (rng.standard_normal((BH, S, D)) + kshift).astype(np.float16)
+    v = rng.standard_normal((BH, S, D)).astype(np.float16)
+    return q, k, v
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+@pytest.mark.parametrize("BH,S,D", [(2, 300, 128), (3, 64, 64), (1, 1, 128), (24, 4352, 128), (2, 129, 64)])
+def test_sage_quant_bit_exact(qimg, oracle, BH, S, D):
+    q, k, v = _inputs(BH, S, D, BH * S + D)
+    mean_ref = oracle.sage_k_mean(k)
+    qi_ref, qs_ref = oracle.sage_quant_q(q)
+    ki_ref, ks_ref = oracle.sage_quant_k(k, mean_ref)
+    kd = _dev(k)
+    mean = qimg.sage_k_mean(kd)
+    qi, qs = qimg.sage_quant_q(_dev(q))
+    ki, ks = qimg.sage_quant_k(kd, mean)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(mean.cpu().numpy(), mean_ref)
+    np.testing.assert_array_equal(qs.cpu().numpy(), qs_ref)
+    np.testing.assert_array_equal(ks.cpu().numpy(), ks_ref)
+    np.testing.assert_array_equal(qi.cpu().numpy(), qi_ref)
+    np.testing.assert_array_equal(ki.cpu().numpy(), ki_ref)
+
+
+def _attn64(q, k, v, scale, causal):
+    s = np.einsum("hqd,hkd->hqk", q, k) * scale
+    if causal:
+        S = q.shape[1]
+        s = np.where(np.tril(np.ones((S, S), bool))[None], s, -np.inf)
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    return np.einsum("hqk,hkd->hqd", p / p.sum(-1, keepdims=True), v)
+
+
+@pytest.mark.parametrize("BH,S,D,causal", [
+    (2, 300, 128, False), (2, 64, 128, False), (1, 1, 128, False), (2, 200, 64, False),
+    (2, 333, 128, True), (1, 130, 64, True), (2, 1000, 128, False),
+])
+def test_sage_attention_vs_oracle(qimg, oracle, BH, S, D, causal):
+    q, k, v = _inputs(BH, S, D, S * D + causal)
+    scale = 1.0 / math.sqrt(D)
+    ref = oracle.sage_attention_fp16io(q, k, v, scale, causal).astype(np.float32)
+    out = qimg.attention_forward_sage_fp16io(_dev(q), _dev(k), _dev(v), scale, causal=causal)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    # same quantized operands: only ulp-level exp2/rcp and summation-order
+    # differences, amplified at most by one fp16 rounding of P and of O
+    assert np.max(np.abs(got - ref)) <= 2e-3 * np.max(np.abs(ref)) + 2e-3, np.max(np.abs(got - ref))
+    rel, cos = _metrics(got, ref)
+    assert cos >= 0.99999, cos
+    exact = _attn64(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), scale, causal)
+    rel, cos = _metrics(got, exact)
+    assert cos >= 0.999, (rel, cos)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_sage_output_dtypes(qimg, dt):
+    rng = np.random.default_rng(5)
+    q, k, v = _inputs(2, 256, 128, 5)
+    o32 = qimg.attention_forward_sage_fp16io(_dev(q), _dev(k), _dev(v), 0.0883883, out_dtype=torch.float32)
+    o32b = qimg.attention_forward_sage_fp16io(_dev(q), _dev(k), _dev(v), 0.0883883, out_dtype=torch.float32)
+    o = qimg.attention_forward_sage_fp16io(_dev(q), _dev(k), _dev(v), 0.0883883, out_dtype=dt)
+    torch.cuda.synchronize()
+    assert torch.equal(o32, o32b), "attention is not run-to-run deterministic"
+    # fp32 output is the fp16 result widened (the reference's half_to_float)
+    assert torch.equal(o32.half().float(), o32)
+    assert torch.equal(o.float(), o32.to(dt).float())
+
+
+@pytest.mark.slow
+def test_sage_joint_attention_full_size_sampled(qimg, oracle):
+    """Config: 24 heads, S = 4352 (256 txt + 4096 img), D = 128, sampled rows."""
+    BH, S, D = 24, 4352, 128
+    q, k, v = _inputs(BH, S, D, 0, kshift=0.3)
+    scale = 1.0 / math.sqrt(128.0)
+    out = qimg.attention_forward_sage_fp16io(_dev(q), _dev(k), _dev(v), scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    mean = oracle.sage_k_mean(k)
+    qi, qs = oracle.sage_quant_q(q)
+    ki, ks = oracle.sage_quant_k(k, mean)
+    for r0 in (0, 2048, 4224):
+        ref = oracle.sage_attn(qi, ki, v, qs, ks, scale, rows=(r0, r0 + 128))[:, r0:r0 + 128].astype(np.float32)
+        g = got[:, r0:r0 + 128]
+        assert np.max(np.abs(g - ref)) <= 2e-3 * np.max(np.abs(ref)) + 2e-3
