@@ -1,0 +1,289 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Workload (one "step"): the MMDiT MLP pair at M = 4352 tokens (4096 image +
+256 text, processed as one matrix):
+    x bf16 [4352, 3072] --FWHT(1024)+int8--> fc1 3072->12288 (+bias, GELU-tanh,
+    fp32 out, as the reference writes it) --FWHT(4096)+int8--> fc2 12288->3072
+    (+bias, bf16 out)
+with random N(0, 0.02) weights quantized by the library (W8A8 + Hadamard).
+Inputs are resident in HBM before timing. value = 2*M*N*K summed over both
+GEMMs (657.13 GOP) / measured time, in TFLOP/s (int8 ops).
+
+Also printed in the same JSON line:
+  roofline     the dominant kernel's achieved rate vs the int8 MFMA peak,
+               from HIP events recorded around each launch in the timed steps
+  cpu_baseline the CPU oracle (oracle/qimg_oracle.c, OpenMP) running the same
+               MLP pair on the host cores
+  extra        single linear (M=4096, 3072x3072), SageAttention (24 heads,
+               S=4352, D=128) and activation-quant bandwidth
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "qwen-image.cu_amd"))
+
+METRIC = "quant-GEMM TFLOP/s (% MFMA peak); ms/MMDiT block @4096 img tokens"
+PEAK_INT8_TOPS = 5033.0     # MI355X dense int8 MFMA
+PEAK_FP16_TFLOPS = 2517.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def _traffic_from_profiles(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, copy-kernel calibrated), kept in profiles/<name>.txt as a
+    'traffic_bytes_per_launch: N' line. None if not measured."""
+    p = os.path.join(ROOT, "profiles", name + ".txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1])
+            except ValueError:
+                return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import qimg_amd as q
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    M, D, H = 4352, 3072, 12288
+
+    # ---- synthetic inputs (seeded), weights quantized by the library
+    x = torch.randn(M, D, generator=g).to(torch.bfloat16).to(dev)
+    w1 = (torch.randn(H, D, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(D, H, generator=g) * 0.02).to(torch.bfloat16)
+    b1 = (torch.randn(H, generator=g) * 0.01).to(torch.bfloat16)
+    b2 = (torch.randn(D, generator=g) * 0.01).to(torch.bfloat16)
+    qw1 = q.quantize_weight_tensor(w1.to(dev))
+    qw2 = q.quantize_weight_tensor(w2.to(dev))
+    b1d, b2d = b1.to(dev), b2.to(dev)
+    h = torch.empty(M, H, dtype=torch.float32, device=dev)
+    y = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    a1 = torch.empty(M, D, dtype=torch.int8, device=dev)
+    s1 = torch.empty(M, dtype=torch.float32, device=dev)
+    a2 = torch.empty(M, H, dtype=torch.int8, device=dev)
+    s2 = torch.empty(M, dtype=torch.float32, device=dev)
+    L = q.lib()
+    stream = torch.cuda.current_stream(dev)
+    sp = q._stream(dev)
+    P = q._ptr
+
+    def quant(src, dt, K, hbs, dst, sc):
+        q._check(L.qimg_quantize_activation(P(src), dt, M, K, hbs, q.INT8_HADAMARD, P(dst), P(sc), sp))
+
+    def gemm(act, sc, w, bias, out, out_dt, gelu):
+        q._check(L.qimg_linear_prequantized(P(act), P(sc), M, act.shape[1], P(w.data), P(w.scales),
+                                            w.data.shape[0], q.INT8_HADAMARD, P(bias), P(out), out_dt,
+                                            gelu, sp))
+
+    names = ["quant_fc1_in", "gemm_fc1", "quant_fc2_in", "gemm_fc2"]
+    launches = [
+        lambda: quant(x, q.BF16, D, 1024, a1, s1),
+        lambda: gemm(a1, s1, qw1, b1d, h, q.FP32, 1),
+        lambda: quant(h, q.FP32, H, 4096, a2, s2),
+        lambda: gemm(a2, s2, qw2, b2d, y, q.BF16, 0),
+    ]
+
+    for _ in range(args.warmup):
+        for f in launches:
+            f()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)] for _ in range(K)]
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(K):
+        ev[i][0].record(stream)
+        for j, f in enumerate(launches):
+            f()
+            ev[i][j + 1].record(stream)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(stop)
+    ms_step = total_ms / K
+    per_kernel_ms = {n: float(np.mean([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K)]))
+                     for j, n in enumerate(names)}
+    gemm_ops = 2.0 * M * D * H
+    total_ops = 2 * gemm_ops
+    value = total_ops / (ms_step * 1e-3) / 1e12
+
+    # ---- roofline of the dominant kernel
+    dom = max(per_kernel_ms, key=per_kernel_ms.get)
+    if dom.startswith("gemm"):
+        achieved = gemm_ops / (per_kernel_ms[dom] * 1e-3) / 1e12
+        traffic = _traffic_from_profiles(f"gemm_w8a8_{dom[5:]}_mlp4352")
+        roof = {"kernel": f"gemm_w8a8_kernel ({dom})", "bound": "mfma", "achieved": round(achieved, 1),
+                "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                "traffic": traffic, "ops_per_launch": gemm_ops,
+                "avg_launch_ms": round(per_kernel_ms[dom], 4)}
+    else:
+        Kd = D if dom == "quant_fc1_in" else H
+        nbytes = M * Kd * (2 if dom == "quant_fc1_in" else 4) + M * Kd + 4 * M
+        achieved = nbytes / (per_kernel_ms[dom] * 1e-3) / 1e9
+        roof = {"kernel": f"fwht_quant_rows_kernel ({dom})", "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": _traffic_from_profiles(f"fwht_quant_{dom}_mlp4352"), "bytes_per_launch": nbytes,
+                "avg_launch_ms": round(per_kernel_ms[dom], 4)}
+
+    # ---- parity spot check of this run's output (oracle on 4 rows)
+    from oracle import oracle as o
+    rows = [0, 1234, 4095, 4351]
+    xb = x[rows].view(torch.int16).cpu().numpy().view(np.uint16)
+    w1b = w1.view(torch.int16).numpy().view(np.uint16)
+    w2b = w2.view(torch.int16).numpy().view(np.uint16)
+    b1b = b1.view(torch.int16).numpy().view(np.uint16)
+    b2b = b2.view(torch.int16).numpy().view(np.uint16)
+    w1q, w1s, _ = o.quantize_weight_bf16(w1b)
+    w2q, w2s, _ = o.quantize_weight_bf16(w2b)
+    h_ref = o.linear_w8a8(xb, w1q, w1s, 1024, b1b, gelu=True)
+    y_ref = o.linear_w8a8(h_ref, w2q, w2s, 4096, b2b)
+    y_got = y[rows].float().cpu().numpy()
+    parity_rel = float(np.max(np.abs(y_got - y_ref)) / np.max(np.abs(y_ref)))
+
+    extra = {"per_kernel_ms": {k: round(v, 4) for k, v in per_kernel_ms.items()},
+             "wall_s_timed": round(wall, 3), "parity_max_rel_vs_oracle_4rows": parity_rel}
+    if not args.no_extra:
+        extra.update(_extra(q, torch, dev))
+
+    # ---- CPU baseline: the oracle on the same MLP pair
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_baseline(o, np, x, w1q, w1s, w2q, w2s, b1b, b2b, M, D, H)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "MMDiT MLP pair, M=4352 tokens: FWHT1024+int8 quant, fc1 3072->12288 "
+                               "+bias+GELU-tanh (fp32), FWHT4096+int8 quant, fc2 12288->3072 +bias (bf16)",
+                   "M": M, "hidden": D, "mlp": H, "weights": "N(0,0.02) -> W8A8 + Hadamard",
+                   "frac_of_int8_peak": round(value / PEAK_INT8_TOPS, 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+def _time(torch, fn, iters=10, warm=3):
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    ts = []
+    for _ in range(iters):
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return float(sorted(ts)[len(ts) // 2])
+
+
+def _extra(q, torch, dev):
+    out = {}
+    g = torch.Generator(device="cpu").manual_seed(0)
+    # C1: single linear, M=4096, 3072x3072 (bf16 in, fp32 out as the reference)
+    M, K, N = 4096, 3072, 3072
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    b = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    qw = q.quantize_weight_tensor(w)
+    o32 = torch.empty(M, N, device=dev)
+    scratch = torch.empty(q.int8_scratch_bytes(M, K, N), dtype=torch.uint8, device=dev)
+    aq, asc = q.quantize_activation_hadamard(x, 1024)
+    ms_lin = _time(torch, lambda: q.linear_forward_quantized(x, qw, b, out=o32, scratch=scratch))
+    ms_gemm = _time(torch, lambda: q.linear_forward_prequantized(aq, asc, qw, b, out=o32))
+    ops = 2.0 * M * N * K
+    out["linear_c1_ms"] = round(ms_lin, 4)
+    out["linear_c1_tflops"] = round(ops / ms_lin / 1e9, 1)
+    out["linear_c1_gemm_only_tflops"] = round(ops / ms_gemm / 1e9, 1)
+    ms_q = _time(torch, lambda: q.quantize_activation_hadamard(x, 1024))
+    out["act_quant_c1_gbs"] = round((M * K * 3 + 4 * M) / ms_q / 1e6, 1)
+    # C3: SageAttention, 24 heads, S = 4352, D = 128
+    BH, S, Dh = 24, 4352, 128
+    qh = torch.randn(BH, S, Dh, generator=g).to(torch.float16).to(dev)
+    kh = torch.randn(BH, S, Dh, generator=g).to(torch.float16).to(dev)
+    vh = torch.randn(BH, S, Dh, generator=g).to(torch.float16).to(dev)
+    ao = torch.empty(BH, S, Dh, dtype=torch.float32, device=dev)
+    sscr = torch.empty(q.sage_scratch_bytes(BH, S, Dh), dtype=torch.uint8, device=dev)
+    sc = 1.0 / math.sqrt(128.0)
+    ms_att = _time(torch, lambda: q.attention_forward_sage_fp16io(qh, kh, vh, sc, out=ao, scratch=sscr))
+    qi, qs = q.sage_quant_q(qh)
+    km = q.sage_k_mean(kh)
+    ki, ks = q.sage_quant_k(kh, km)
+    ms_core = _time(torch, lambda: q.sage_attn_quantized(qi, ki, vh, qs, ks, sc, scratch=sscr))
+    flops = 4.0 * BH * S * S * Dh
+    out["sage_c3_ms"] = round(ms_att, 4)
+    out["sage_c3_tflops"] = round(flops / ms_att / 1e9, 1)
+    out["sage_c3_attn_kernel_tflops"] = round(flops / ms_core / 1e9, 1)
+    out["sage_c3_frac_of_mixed_peak"] = round(flops / ms_att / 1e9 / 3355.0, 4)
+    return out
+
+
+def _cpu_baseline(o, np, x, w1q, w1s, w2q, w2s, b1b, b2b, M, D, H):
+    """The oracle (C, OpenMP over rows) computing the same MLP pair on the
+    host: FWHT+quant, exact int32 GEMM, dequant+bias+GELU, FWHT(4096)+quant,
+    GEMM, dequant+bias. The sample is the whole workload, run once."""
+    threads = o.get_threads()
+    xb = x.view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+    t0 = time.perf_counter()
+    hq, hs = o.quantize_activation(xb, 1024)
+    c1 = o.gemm_s8s8s32(hq, w1q)
+    hh = o.dequant_epilogue(c1, hs, w1s, b1b, gelu=True)
+    del c1
+    q2, s2 = o.quantize_activation(hh, 4096)
+    c2 = o.gemm_s8s8s32(q2, w2q)
+    o.dequant_epilogue(c2, s2, w2s, b2b, gelu=False)
+    dt = time.perf_counter() - t0
+    ops = 2 * 2.0 * M * D * H
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(ops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"full MLP pair (M={M}) once through the C oracle, {dt:.2f} s", "cpu": cpu_model}
+
+
+if __name__ == "__main__":
+    main()
