@@ -11,17 +11,27 @@
 // Tiling (CDNA4, wave64): a 256-thread workgroup owns a 256x256 output tile,
 // four waves in a 2x2 arrangement each own 128x128 = 4x4 MFMA 32x32 blocks
 // (v_mfma_i32_32x32x32_i8 for int8, v_mfma_scale_f32_32x32x64_f8f6f4 with
-// unit scales for e4m3). Both operands are K-major [rows, K] as the
-// reference stores them (TN GEMM). K advances 64 bytes per stage through a
-// double-buffered LDS ring (2 x 32 KB); the next stage's global loads are
-// issued before the current stage's MFMAs so HBM/L2 latency hides behind
-// matrix work. LDS rows are 64 bytes with the 16-byte chunk index XOR-
-// swizzled by ((row>>1) ^ (row>>3)) & 3, so MFMA fragment reads of 8 or 16
-// consecutive rows touch distinct banks.
+// unit scales for e4m3); the 256 accumulator registers live in AGPRs. Both
+// operands are K-major [rows, K] as the reference stores them (TN GEMM).
 //
-// The k ordering inside a 64-byte stage is the same for both operands, so
-// the dot product is exact for int8 regardless of how the instruction
-// consumes bytes within a lane.
+// K advances 64 bytes per stage through a three-slot LDS ring (3 x 32 KB),
+// so two stages are in flight while one is consumed. Stages are filled by
+// direct global->LDS DMA (global_load_lds_dwordx4): no VGPR staging and no
+// ds_write instructions. Each DMA instruction writes 1 KB = 16 LDS rows of
+// 64 bytes; lane i fetches the global chunk that the row's XOR swizzle
+// places at physical chunk i%4, with swizzle(row) = ((row>>1) ^ (row>>3)) & 3,
+// so MFMA fragment reads of 8 or 16 consecutive rows at one logical chunk hit
+// distinct LDS banks. Stage hand-off uses s_waitcnt vmcnt(<stages still in
+// flight>) + s_barrier rather than __syncthreads(), whose workgroup fence
+// would drain every outstanding DMA.
+//
+// The tile's activation scales, weight scales and bias are copied into LDS
+// at kernel start, so the epilogue reads them without global latency.
+//
+// K ordering: within a stage, lane half h of a fragment holds logical
+// chunks 2h, 2h+1; int8 k-step s uses chunk 2h+s (16 bytes), e4m3 uses both
+// (32 bytes, one k-step). Both operands use the same assignment, so each dot
+// product covers every k exactly once and the int8 result is exact.
 #include "qimg_device.h"
 #include "qimg_internal.h"
 
@@ -31,16 +41,33 @@ namespace {
 
 constexpr int BM = 256;
 constexpr int BN = 256;
-constexpr int BK = 64;  // bytes of K per stage
+constexpr int BK = 64;     // bytes of K per stage
+constexpr int NSLOT = 3;   // LDS ring depth
 constexpr int NTHR = 256;
 constexpr int WTM = 128;  // wave tile
 constexpr int WTN = 128;
 constexpr int TM = WTM / 32;  // 32x32 blocks per wave
 constexpr int TN = WTN / 32;
-constexpr int STAGE_BYTES = (BM + BN) * BK;
+constexpr int STAGE_BYTES = (BM + BN) * BK;   // 32 KB
+constexpr int DMA_ROWS = 1024 / BK;           // rows per DMA instruction
+constexpr int NDMA = BM / (4 * DMA_ROWS);     // DMA instructions per operand per wave per stage
+constexpr int SCALE_OFF = NSLOT * STAGE_BYTES;
+constexpr int LDS_BYTES = SCALE_OFF + 3 * 256 * 4;
 
-__device__ __forceinline__ int swz(int row, int chunk) {
-    return row * BK + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+
+__device__ __forceinline__ int swz_row(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+__device__ __forceinline__ int lds_addr(int row, int chunk) {
+    return row * BK + ((chunk ^ swz_row(row)) << 4);
+}
+
+// s_waitcnt with vmcnt = n (0..63) and the other counters left alone.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((0x0f70 & ~0xc00f) | (n & 15) | ((n >> 4) << 14));
 }
 
 // Map the hardware workgroup id so that each XCD (workgroups are dispatched
@@ -70,7 +97,10 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
     int N, int K) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+    float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
+    float* s_ws = s_as + 256;
+    float* s_bias = s_ws + 256;
 
     const int tiles_m = (M + BM - 1) / BM;
     const int tiles_n = (N + BN - 1) / BN;
@@ -84,26 +114,36 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1;
     const int wn = wave & 1;
+    const bool has_bias = bias != nullptr;
 
-    // Global->LDS copy assignment: thread t moves rows t/4 + 64 i, chunk t%4.
-    const int ld_row = tid >> 2;
-    const int ld_chunk = tid & 3;
-    const uint8_t* a_src[4];
-    const uint8_t* w_src[4];
-    int lds_off[4];
+    // epilogue operands for this tile (clamped indices; only stored
+    // outputs use them)
+    // (loaded now, written to LDS after the main loop; the bias load is
+    // branch-free so it stays in flight behind the DMA stream)
+    const int e_n = n0 + tid < N ? n0 + tid : N - 1;
+    const float e_as = as[m0 + tid < M ? m0 + tid : M - 1];
+    const float e_ws = ws[e_n];
+    const uint16_t* bsrc = has_bias ? bias : reinterpret_cast<const uint16_t*>(ws);
+    const uint16_t e_braw = bsrc[e_n];
+
+    // DMA assignment: wave w, instruction i fills LDS rows
+    // DMA_ROWS*(4*i + w) .. +DMA_ROWS of the A tile (and the same rows of
+    // the W tile); lane -> row +lane/4, physical chunk lane%4.
+    const uint8_t* a_src[NDMA];
+    const uint8_t* w_src[NDMA];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = ld_row + 64 * i;
+    for (int i = 0; i < NDMA; ++i) {
+        const int r = DMA_ROWS * (4 * i + wave) + (lane >> 2);
+        const int c = (lane & 3) ^ swz_row(r);
         int gm = m0 + r;
         gm = gm < M ? gm : M - 1;  // clamp: rows past M are computed, never stored
         int gn = n0 + r;
         gn = gn < N ? gn : N - 1;
-        a_src[i] = A + static_cast<int64_t>(gm) * K + ld_chunk * 16;
-        w_src[i] = W + static_cast<int64_t>(gn) * K + ld_chunk * 16;
-        lds_off[i] = swz(r, ld_chunk);
+        a_src[i] = A + static_cast<int64_t>(gm) * K + c * 16;
+        w_src[i] = W + static_cast<int64_t>(gn) * K + c * 16;
     }
 
     typedef typename Acc<FP8>::type acc_t;
@@ -115,96 +155,117 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-    v4i ga[4], gw[4];
     const int KT = K / BK;
 
-    // prologue: stage 0
+    auto issue_stage = [&](int kt, int slot) {
+        kt = kt < KT ? kt : KT - 1;  // past the end: refetch a valid stage into an idle slot
+        const int koff = kt * BK;
+        uint8_t* base = lds + slot * STAGE_BYTES;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ga[i] = *reinterpret_cast<const v4i*>(a_src[i]);
-        gw[i] = *reinterpret_cast<const v4i*>(w_src[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<v4i*>(lds + lds_off[i]) = ga[i];
-        *reinterpret_cast<v4i*>(lds + BM * BK + lds_off[i]) = gw[i];
-    }
-    __syncthreads();
+        for (int i = 0; i < NDMA; ++i) {
+            const int rowblk = DMA_ROWS * (4 * i + wave);
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(a_src[i] + koff),
+                                             (lds_ptr_t)(base + rowblk * BK), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(w_src[i] + koff),
+                                             (lds_ptr_t)(base + BM * BK + rowblk * BK), 16, 0, 0);
+        }
+    };
 
     const int frag_row = lane & 31;
     const int half = lane >> 5;
+    int arow[TM], wrow[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) arow[i] = wm * WTM + i * 32 + frag_row;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) wrow[j] = wn * WTN + j * 32 + frag_row;
 
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        const bool more = (kt + 1) < KT;
-        if (more) {
-            const int koff = (kt + 1) * BK;
+    // prologue: stages 0 .. NSLOT-2 in flight; the epilogue operands go to
+    // LDS once their (earlier) loads return.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ga[i] = *reinterpret_cast<const v4i*>(a_src[i] + koff);
-                gw[i] = *reinterpret_cast<const v4i*>(w_src[i] + koff);
-            }
-        }
-        const uint8_t* la = lds + cur * STAGE_BYTES;
-        const uint8_t* lw = la + BM * BK;
-        if constexpr (!FP8) {
+    for (int p = 0; p < NSLOT - 1; ++p) issue_stage(p, p);
+    constexpr int KEEP = (NSLOT - 2) * 2 * NDMA;  // DMA instructions allowed in flight at a hand-off
+    wait_vmcnt<KEEP>();
+    __builtin_amdgcn_s_barrier();
+
+    if constexpr (!FP8) {
+        v4i fa[2][TM], fw[2][TN];
+        auto read_frags = [&](int slot, int ks, int fb) {
+            const uint8_t* la = lds + slot * STAGE_BYTES;
+            const uint8_t* lw = la + BM * BK;
+            const int chunk = 2 * half + ks;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int chunk = 2 * ks + half;
-                v4i fa[TM], fw[TN];
+            for (int i = 0; i < TM; ++i) fa[fb][i] = *reinterpret_cast<const v4i*>(la + lds_addr(arow[i], chunk));
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
-                    fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * WTM + i * 32 + frag_row, chunk));
+            for (int j = 0; j < TN; ++j) fw[fb][j] = *reinterpret_cast<const v4i*>(lw + lds_addr(wrow[j], chunk));
+        };
+        read_frags(0, 0, 0);
+        for (int kt = 0; kt < KT; ++kt) {
+            const int slot = kt % NSLOT;
+            issue_stage(kt + NSLOT - 1, (kt + NSLOT - 1) % NSLOT);
+            read_frags(slot, 1, 1);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    fw[j] = *reinterpret_cast<const v4i*>(lw + swz(wn * WTN + j * 32 + frag_row, chunk));
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[0][j], fa[0][i], acc[i][j], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
-            }
-        } else {
-            v8i fa[TM], fw[TN];
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[1][j], fa[1][i], acc[i][j], 0, 0, 0);
+            wait_vmcnt<KEEP>();  // stage kt+1 has landed
+            __builtin_amdgcn_s_barrier();
+            read_frags((kt + 1) % NSLOT, 0, 0);
+        }
+    } else {
+        v8i fa[TM], fw[TN];
+        auto read_frags = [&](int slot) {
+            const uint8_t* la = lds + slot * STAGE_BYTES;
+            const uint8_t* lw = la + BM * BK;
+            const int c0 = 2 * half;
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                const int r = wm * WTM + i * 32 + frag_row;
-                v4i lo4 = *reinterpret_cast<const v4i*>(la + swz(r, 2 * half));
-                v4i hi4 = *reinterpret_cast<const v4i*>(la + swz(r, 2 * half + 1));
+                const v4i lo4 = *reinterpret_cast<const v4i*>(la + lds_addr(arow[i], c0));
+                const v4i hi4 = *reinterpret_cast<const v4i*>(la + lds_addr(arow[i], c0 + 1));
                 fa[i] = (v8i){lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
             }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int r = wn * WTN + j * 32 + frag_row;
-                v4i lo4 = *reinterpret_cast<const v4i*>(lw + swz(r, 2 * half));
-                v4i hi4 = *reinterpret_cast<const v4i*>(lw + swz(r, 2 * half + 1));
+                const v4i lo4 = *reinterpret_cast<const v4i*>(lw + lds_addr(wrow[j], c0));
+                const v4i hi4 = *reinterpret_cast<const v4i*>(lw + lds_addr(wrow[j], c0 + 1));
                 fw[j] = (v8i){lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
             }
+        };
+        read_frags(0);
+        for (int kt = 0; kt < KT; ++kt) {
+            issue_stage(kt + NSLOT - 1, (kt + NSLOT - 1) % NSLOT);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                         fw[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+            wait_vmcnt<KEEP>();
+            __builtin_amdgcn_s_barrier();
+            read_frags((kt + 1) % NSLOT);
         }
-        if (more) {
-            uint8_t* nxt = lds + (cur ^ 1) * STAGE_BYTES;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                *reinterpret_cast<v4i*>(nxt + lds_off[i]) = ga[i];
-                *reinterpret_cast<v4i*>(nxt + BM * BK + lds_off[i]) = gw[i];
-            }
-        }
-        __syncthreads();
     }
+
+    // The last iterations re-fetched a valid stage into idle slots; drain
+    // them, then publish the epilogue operands.
+    wait_vmcnt<0>();
+    s_as[tid] = e_as;
+    s_ws[tid] = e_ws;
+    s_bias[tid] = has_bias ? bf16_to_f32(e_braw) : 0.0f;
+    __syncthreads();
 
     // Epilogue. The MFMA was issued as D = W_frag x A_frag, so the 32x32
     // block is indexed [n][m]: lane holds m = lane%32 and n rows
     // 8*(r/4) + 4*(lane/32) + r%4. Each lane therefore owns one output row
     // per block and 16 columns in four runs of 4 consecutive n, stored as
-    // one 16-byte (fp32) or 8-byte (bf16) write per run.
-    const bool has_bias = bias != nullptr;
-    const bool vec_ok = (N & 3) == 0;
+    // one 16-byte (fp32) or 8-byte (bf16) write per run. Interior tiles
+    // (the common case) take a path with no per-element bounds checks.
+    const bool interior = (m0 + BM <= M) && (n0 + BN <= N) && ((N & 3) == 0);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int nj = n0 + wn * WTN + j * 32 + 4 * half;
@@ -213,16 +274,15 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
         for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                int n = nj + 8 * g + c;
-                n = n < N ? n : N - 1;
-                wsv[4 * g + c] = ws[n];
-                bv[4 * g + c] = has_bias ? bf16_to_f32(bias[n]) : 0.0f;
+                const int nl = nj - n0 + 8 * g + c;
+                wsv[4 * g + c] = s_ws[nl];
+                bv[4 * g + c] = s_bias[nl];
             }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int m = m0 + wm * WTM + i * 32 + (lane & 31);
-            if (m >= M) continue;
-            const float sa = as[m];
+            if (!interior && m >= M) continue;
+            const float sa = s_as[m - m0];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int nb = nj + 8 * g;
@@ -235,12 +295,12 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
                         t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[4 * g + c];
                         if (has_bias) t = t + bv[4 * g + c];
                     }
-                    if (GELU) t = gelu_tanh(t);
+                    if (GELU) t = gelu_tanh_fast(t);
                     v[c] = t;
                 }
                 if (OUT_DT == QIMG_FP32) {
                     float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(m) * N + nb;
-                    if (vec_ok && nb + 3 < N) {
+                    if (interior) {
                         *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
                     } else {
 #pragma unroll
@@ -249,10 +309,8 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
                     }
                 } else {
                     uint16_t* o = reinterpret_cast<uint16_t*>(out) + static_cast<int64_t>(m) * N + nb;
-                    if (vec_ok && nb + 3 < N) {
-                        uint32_t lo = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-                        uint32_t hi = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
-                        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+                    if (interior) {
+                        *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     } else {
 #pragma unroll
                         for (int c = 0; c < 4; ++c)

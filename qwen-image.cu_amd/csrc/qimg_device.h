@@ -90,6 +90,26 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// Two fp32 values -> packed bf16x2 bits with the hardware RNE conversion
+// (v_cvt_pk_bf16_f32); same result as f32_to_bf16 on each.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+}
+
+// GELU with tanh(u) = 1 - 2 / (exp(2u) + 1) on the hardware exp2/rcp
+// (about 2e-7 absolute error in tanh; the reference evaluates tanhf under
+// fast-math approximation as well).
+__device__ __forceinline__ float gelu_tanh_fast(float v) {
+    const float c = 0.7978845608f;
+    const float u = c * (v + 0.044715f * v * v * v);
+    const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // exp(2u)
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    return 0.5f * v * (1.0f + t);
+}
+
 __device__ __forceinline__ float gelu_tanh(float v) {
     const float c = 0.7978845608f;
     float inner = c * (v + 0.044715f * v * v * v);

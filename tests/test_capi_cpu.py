@@ -70,7 +70,7 @@ def test_prequantized_rejects_bad_arguments(qimg):
     L = qimg.lib()
     assert L.qimg_linear_prequantized(None, FAKE, 4, 64, FAKE, FAKE, 8, 0, None, FAKE, 0, 0, None) == 1
     assert L.qimg_linear_prequantized(FAKE, FAKE, -1, 64, FAKE, FAKE, 8, 0, None, FAKE, 0, 0, None) == 1
-    assert L.qimg_linear_prequantized(ctypes.c_void_p(0x10004), FAKE, 4, 64, FAKE, FAKE, 8, 0, None, FAKE,
+    assert L.qimg_linear_prequantized(ctypes.c_void_p(0x10004), FAKE, 4, 128, FAKE, FAKE, 8, 0, None, FAKE,
                                       0, 0, None) == 1
     assert "aligned" in _err(qimg)
     assert L.qimg_linear_prequantized(FAKE, FAKE, 4, 96, FAKE, FAKE, 8, 1, None, FAKE, 0, 0, None) == 2

@@ -38,7 +38,8 @@ def _qw(qimg, q, s, hbs, mode=0):
 
 
 @pytest.mark.parametrize("M,N,K", [
-    (256, 256, 64), (1, 64, 64), (7, 300, 192), (300, 7, 128), (513, 520, 3072),
+    (256, 256, 64), (1, 64, 64), (7, 300, 192), (300, 7, 128), (256, 256, 128), (129, 384, 384),
+    (513, 520, 3072),
     (257, 255, 1024), (64, 3072, 3072), (4096, 3072, 3072),
 ])
 def test_int8_gemm_exact(qimg, oracle, M, N, K):
