@@ -6,7 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#include "../../include/qimg_hot.h"
+#include "qimg_hot.h"
 
 namespace qimg {
 
