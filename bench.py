@@ -60,6 +60,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -70,6 +72,10 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.calib_copy:
+        _calib_copy(torch)
+        return
 
     import qimg_amd as q
 
@@ -198,6 +204,18 @@ def main():
         "extra": extra,
     }
     print(json.dumps(line))
+
+
+def _calib_copy(torch):
+    """A plain device-to-device copy of 256 MiB, five times: the known-size
+    reference that FETCH_SIZE / WRITE_SIZE readings are scaled by."""
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes": n, "copies": 5}))
 
 
 def _time(torch, fn, iters=10, warm=3):
