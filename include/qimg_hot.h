@@ -107,6 +107,15 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
                              const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                              void* stream);
 
+/* dequantize_and_bias / dequantize_bias_gelu (cuda_kernels.cuh:282-291,
+ * cuda_kernels.cu:2623-2668): out[m,n] = acc[m,n] * act_scale[m] * w_scale[n]
+ * + bias[n] (then GELU-tanh if gelu != 0), acc int32 [M,N], out fp32 [M,N],
+ * bias bf16 [N] or NULL. The same arithmetic as the fused epilogue of
+ * qimg_linear_prequantized. */
+int qimg_dequantize_bias(const int32_t* acc, const float* act_scales, const float* w_scales,
+                         const uint16_t* bias_bf16, float* out, int M, int N, int gelu,
+                         void* stream);
+
 /* linear_forward_int8 / linear_forward_int8_bf16in (cuda_kernels.cuh:294-296,
  * 303-305; cuda_kernels.cu:2674-2732, 2776-2827): activation FWHT+quant into
  * `scratch`, then qimg_linear_prequantized. scratch_bytes must be at least

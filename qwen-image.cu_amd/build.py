@@ -1,12 +1,16 @@
-"""Build recipe for the gfx950 hot-path library.
+"""Build recipe for the gfx950 hot-path libraries.
 
-Compiles every HIP source under csrc/ with hipcc for gfx950 only and links
-them into `qwen-image.cu_amd/lib/libqimg_hot.so` (the C ABI declared in
-include/qimg_hot.h). The C++ reference-signature host layer (host/) is built
-into `lib/libqimg_host.so` on top of it.
+    lib/libqimg_hot.so   the kernels + C ABI (include/qimg_hot.h), from csrc/
+    lib/libqimg_host.so  the reference-signature C++ layer (host/kernels.h)
+                         over the C ABI
+    tests/cpp/_build/test_host_api
+                         the C++ layer's parity test program (links the CPU
+                         oracle, so it is built only after oracle/ is)
 
-    python qwen-image.cu_amd/build.py            # build both
-    python qwen-image.cu_amd/build.py --jobs 4
+Everything is compiled with hipcc for gfx950 only.
+
+    python qwen-image.cu_amd/build.py            # libraries
+    python qwen-image.cu_amd/build.py --tests    # libraries + test program
 """
 from __future__ import annotations
 
@@ -24,6 +28,9 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib")
 HOT_SO = os.path.join(LIB, "libqimg_hot.so")
 HOST_SO = os.path.join(LIB, "libqimg_host.so")
+TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host_api.cpp")
+TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host_api")
+ORACLE_DIR = os.path.join(ROOT, "oracle")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -55,34 +62,49 @@ def _compile(src: str, out: str, extra=()):
 def build(jobs: int = 4, verbose: bool = True) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB, exist_ok=True)
-    objs = []
+    hot_objs, host_objs = [], []
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = []
         for s in SOURCES:
             o = os.path.join(OBJ, os.path.splitext(s)[0] + ".o")
             futs.append(ex.submit(_compile, os.path.join(CSRC, s), o))
-            objs.append(o)
+            hot_objs.append(o)
         for s in HOST_SOURCES:
-            p = os.path.join(HOST, s)
-            if os.path.exists(p):
-                o = os.path.join(OBJ, "host_" + os.path.splitext(s)[0] + ".o")
-                futs.append(ex.submit(_compile, p, o, ("-x", "hip", "-I", HOST)))
+            o = os.path.join(OBJ, "host_" + os.path.splitext(s)[0] + ".o")
+            futs.append(ex.submit(_compile, os.path.join(HOST, s), o, ("-x", "hip", "-I", HOST)))
+            host_objs.append(o)
         for f in futs:
             f.result()
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", HOT_SO, *objs])
-    host_objs = [os.path.join(OBJ, "host_" + os.path.splitext(s)[0] + ".o") for s in HOST_SOURCES
-                 if os.path.exists(os.path.join(HOST, s))]
-    if host_objs:
-        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", HOST_SO, *host_objs,
-              "-L", LIB, "-lqimg_hot", "-Wl,-rpath,$ORIGIN"])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", HOT_SO, *hot_objs])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", HOST_SO, *host_objs,
+          "-L", LIB, "-lqimg_hot", "-Wl,-rpath,$ORIGIN"])
     if verbose:
-        print(f"built {HOT_SO}")
+        print(f"built {HOT_SO} and {HOST_SO}")
     return HOT_SO
+
+
+def build_tests(verbose: bool = True) -> str:
+    """The C++ layer's test program; needs oracle/_build/libqimg_oracle.so."""
+    oracle_lib = os.path.join(ORACLE_DIR, "_build")
+    if not os.path.exists(os.path.join(oracle_lib, "libqimg_oracle.so")):
+        raise RuntimeError("build the oracle first: make -C oracle")
+    os.makedirs(os.path.dirname(TEST_BIN), exist_ok=True)
+    rel_lib = os.path.relpath(LIB, os.path.dirname(TEST_BIN))
+    rel_oracle = os.path.relpath(oracle_lib, os.path.dirname(TEST_BIN))
+    _run([HIPCC, *HIP_FLAGS, "-x", "hip", "-I", HOST, "-I", os.path.join(ROOT, "include"), "-I", ORACLE_DIR,
+          TEST_SRC, "-o", TEST_BIN, "-L", LIB, "-lqimg_host", "-lqimg_hot", "-L", oracle_lib, "-lqimg_oracle",
+          f"-Wl,-rpath,$ORIGIN/{rel_lib}:$ORIGIN/{rel_oracle}"])
+    if verbose:
+        print(f"built {TEST_BIN}")
+    return TEST_BIN
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--tests", action="store_true")
     a = ap.parse_args()
     build(a.jobs)
+    if a.tests:
+        build_tests()
     sys.exit(0)

@@ -151,6 +151,17 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
                       fn);
 }
 
+int qimg_dequantize_bias(const int32_t* acc, const float* act_scales, const float* w_scales,
+                         const uint16_t* bias_bf16, float* out, int M, int N, int gelu, void* stream) {
+    const char* fn = "qimg_dequantize_bias";
+    QIMG_REQUIRE(M >= 0 && N >= 0, "%s: bad sizes M=%d N=%d", fn, M, N);
+    if (M == 0 || N == 0) return QIMG_OK;
+    QIMG_REQUIRE(acc && act_scales && w_scales && out, "%s: null pointer", fn);
+    return hip_status(qimg::launch_dequant_bias(acc, act_scales, w_scales, bias_bf16, out, M, N, gelu,
+                                                static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
 int qimg_linear(const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales, int N,
                 int hbs, int mode, const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                 void* scratch, int64_t scratch_bytes, void* stream) {

@@ -494,6 +494,32 @@ __global__ void gemm_i8_simple_kernel(const int8_t* __restrict__ A, const int8_t
         reinterpret_cast<uint16_t*>(out)[idx] = f32_to_bf16(t);
 }
 
+// Stand-alone dequant epilogue for an int32 product held in memory
+// (dequantize_and_bias / dequantize_bias_gelu, cuda_kernels.cu:2623-2668):
+// the same per-element arithmetic as the fused epilogue above, so a caller
+// that runs its own integer GEMM gets bit-identical output.
+__global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __restrict__ acc,
+                                                           const float* __restrict__ as,
+                                                           const float* __restrict__ ws,
+                                                           const uint16_t* __restrict__ bias,
+                                                           float* __restrict__ out, int M, int N,
+                                                           int gelu) {
+    const int64_t total = static_cast<int64_t>(M) * N;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int m = static_cast<int>(i / N);
+        const int n = static_cast<int>(i - static_cast<int64_t>(m) * N);
+        float t;
+        {
+#pragma clang fp contract(off)
+            t = static_cast<float>(acc[i]) * as[m] * ws[n];
+            if (bias) t = t + bf16_to_f32(bias[n]);
+        }
+        if (gelu) t = gelu_tanh_fast(t);
+        out[i] = t;
+    }
+}
+
 template <bool FP8, int OUT_DT, bool GELU>
 hipError_t launch_tiled(const void* a, const float* as, int M, int K, const void* w,
                         const float* ws, int N, const uint16_t* bias, void* out,
@@ -517,6 +543,17 @@ hipError_t dispatch_tiled(const void* a, const float* as, int M, int K, const vo
 }
 
 }  // namespace
+
+hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
+                              float* out, int M, int N, int gelu, hipStream_t stream) {
+    const int64_t total = static_cast<int64_t>(M) * N;
+    if (total == 0) return hipSuccess;
+    const int64_t want = (total + 255) / 256;
+    const int blocks = static_cast<int>(want < 16384 ? want : 16384);
+    hipLaunchKernelGGL(dequant_bias_kernel, dim3(blocks), dim3(256), 0, stream, acc, as, ws, bias, out, M, N,
+                       gelu);
+    return hipGetLastError();
+}
 
 hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
                                       const void* w_q, const float* w_scales, int N, int mode,

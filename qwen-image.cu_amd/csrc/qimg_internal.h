@@ -21,6 +21,8 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
                                       const void* w_q, const float* w_scales, int N, int mode,
                                       const uint16_t* bias, void* out, int out_dtype, int gelu,
                                       hipStream_t stream);
+hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
+                              float* out, int M, int N, int gelu, hipStream_t stream);
 
 // sage_attention.hip
 struct SageScratch {

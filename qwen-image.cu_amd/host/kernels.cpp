@@ -1,0 +1,265 @@
+// kernels.cpp — the reference-signature C++ operators (kernels.h) on top of
+// the C ABI of libqimg_hot.so. Shape/dtype checks mirror the reference's
+// asserts (cuda_kernels.cu:2681-2686, 2744-2748, 2783-2785, 2831-2832); the
+// C ABI repeats the numeric checks and its message is reported on failure.
+#include "kernels.h"
+
+#include <cstdarg>
+#include <mutex>
+#include <vector>
+
+#include "qimg_hot.h"
+
+namespace {
+
+[[noreturn]] void die(const char* fn, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    fprintf(stderr, "qimg: %s: ", fn);
+    vfprintf(stderr, fmt, ap);
+    fprintf(stderr, "\n");
+    va_end(ap);
+    exit(1);
+}
+
+void check(int status, const char* fn) {
+    if (status != QIMG_OK) die(fn, "%s (%s)", qimg_last_error(), qimg_status_string(status));
+}
+
+#define REQUIRE(cond, fn, ...) \
+    do {                       \
+        if (!(cond)) die(fn, __VA_ARGS__); \
+    } while (0)
+
+int qmode(QuantMode m, const char* fn) {
+    switch (m) {
+        case QuantMode::INT8_HADAMARD: return QIMG_QM_INT8_HADAMARD;
+        case QuantMode::FP8_HADAMARD: return QIMG_QM_FP8_HADAMARD;
+        case QuantMode::INT4_SVD: die(fn, "QuantMode::INT4_SVD is not part of this library");
+        case QuantMode::INT4_AWQ: die(fn, "QuantMode::INT4_AWQ is not part of this library");
+        case QuantMode::BF16: die(fn, "QuantMode::BF16 is not part of this library");
+    }
+    die(fn, "unknown QuantMode");
+}
+
+DType qdtype(QuantMode m) { return m == QuantMode::FP8_HADAMARD ? DType::FP8_E4M3 : DType::INT8; }
+
+int out_code(const Tensor& out, const char* fn) {
+    if (out.dtype == DType::FP32) return QIMG_FP32;
+    if (out.dtype == DType::BF16) return QIMG_BF16;
+    die(fn, "out must be FP32 or BF16 (got %s)", dtype_name(out.dtype));
+}
+
+const uint16_t* bias_ptr(const Tensor* bias, int N, const char* fn) {
+    if (!bias) return nullptr;
+    REQUIRE(bias->dtype == DType::BF16, fn, "bias must be BF16 (got %s)", dtype_name(bias->dtype));
+    REQUIRE(bias->numel() == N, fn, "bias has %lld elements, expected N=%d", (long long)bias->numel(), N);
+    return static_cast<const uint16_t*>(bias->data);
+}
+
+void check_weight(const QuantizedWeight& w, int K, const char* fn) {
+    REQUIRE(w.data.ndim == 2, fn, "weight.data must be 2-D [N, K]");
+    REQUIRE(w.data.dtype == qdtype(w.mode), fn, "weight.data is %s, mode expects %s", dtype_name(w.data.dtype),
+            dtype_name(qdtype(w.mode)));
+    REQUIRE(w.scales.dtype == DType::FP32 && w.scales.numel() == w.data.shape[0], fn,
+            "weight.scales must be FP32 [N]");
+    REQUIRE(w.data.shape[1] == K, fn, "weight K=%lld != input K=%d", (long long)w.data.shape[1], K);
+}
+
+void check_out(const Tensor& out, int M, int N, const char* fn) {
+    REQUIRE(out.ndim == 2 && out.shape[0] == M && out.shape[1] == N, fn, "out is %s, expected [%d, %d]",
+            out.shape_str().c_str(), M, N);
+}
+
+void linear_common(const Tensor& x, DType want, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                   Tensor& scratch, bool apply_gelu, const char* fn) {
+    REQUIRE(x.ndim == 2, fn, "x must be 2-D [M, K] (got %s)", x.shape_str().c_str());
+    REQUIRE(x.dtype == want, fn, "x must be %s (got %s)", dtype_name(want), dtype_name(x.dtype));
+    const int M = static_cast<int>(x.shape[0]);
+    const int K = static_cast<int>(x.shape[1]);
+    const int mode = qmode(weight.mode, fn);
+    check_weight(weight, K, fn);
+    const int N = static_cast<int>(weight.data.shape[0]);
+    check_out(out, M, N, fn);
+    check(qimg_linear(x.data, want == DType::BF16 ? QIMG_BF16 : QIMG_FP32, M, K, weight.data.data,
+                      static_cast<const float*>(weight.scales.data), N, weight.had_block_size, mode,
+                      bias_ptr(bias, N, fn), out.data, out_code(out, fn), apply_gelu ? 1 : 0, scratch.data,
+                      static_cast<int64_t>(scratch.nbytes()), nullptr),
+          fn);
+}
+
+QuantizedWeight quantize_weight_common(const Tensor& w, QuantMode mode, const char* fn) {
+    REQUIRE(w.dtype == DType::BF16, fn, "weight must be BF16 (got %s)", dtype_name(w.dtype));
+    REQUIRE(w.ndim == 2, fn, "weight must be 2-D [N, K]");
+    const int N = static_cast<int>(w.shape[0]);
+    const int K = static_cast<int>(w.shape[1]);
+    QuantizedWeight qw;
+    qw.mode = mode;
+    qw.data = Tensor::alloc({static_cast<int64_t>(N), static_cast<int64_t>(K)}, qdtype(mode));
+    qw.scales = Tensor::alloc({static_cast<int64_t>(N)}, DType::FP32);
+    int hbs = 0;
+    check(qimg_quantize_weight(w.data, QIMG_BF16, N, K, qmode(mode, fn), qw.data.data,
+                               static_cast<float*>(qw.scales.data), &hbs, nullptr),
+          fn);
+    qw.had_block_size = hbs;
+    return qw;
+}
+
+// Per-device SageAttention workspace, grown on demand (the reference keeps
+// a static SageAttentionWorkspace, sageattention_sm80.cu:679-757).
+struct SageWorkspace {
+    std::mutex mu;
+    std::vector<void*> buf;
+    std::vector<int64_t> bytes;
+};
+
+SageWorkspace& sage_ws() {
+    static SageWorkspace ws;
+    return ws;
+}
+
+}  // namespace
+
+void fwht_inplace(float* data, int M, int K, int had_block_size, hipStream_t stream) {
+    check(qimg_fwht_inplace(data, M, K, had_block_size, stream), "fwht_inplace");
+}
+
+void quantize_per_row_fp32(const float* x, int8_t* out, float* scales, int M, int K, hipStream_t stream) {
+    check(qimg_quantize_per_row_fp32(x, out, scales, M, K, stream), "quantize_per_row_fp32");
+}
+
+void quantize_activation_per_token_fp32(const float* x, int8_t* out, float* scales, int M, int K,
+                                        hipStream_t stream) {
+    check(qimg_quantize_activation(x, QIMG_FP32, M, K, 1, QIMG_QM_INT8_HADAMARD, out, scales, stream),
+          "quantize_activation_per_token_fp32");
+}
+
+void quantize_activation_per_token_bf16(const __hip_bfloat16* x, int8_t* out, float* scales, int M, int K,
+                                        hipStream_t stream) {
+    check(qimg_quantize_activation(x, QIMG_BF16, M, K, 1, QIMG_QM_INT8_HADAMARD, out, scales, stream),
+          "quantize_activation_per_token_bf16");
+}
+
+void fwht_quantize_fp32(const float* input, int8_t* output, float* scales, int M, int K, int had_block_size,
+                        hipStream_t stream) {
+    check(qimg_quantize_activation(input, QIMG_FP32, M, K, had_block_size, QIMG_QM_INT8_HADAMARD, output,
+                                   scales, stream),
+          "fwht_quantize_fp32");
+}
+
+void fwht_quantize_bf16(const __hip_bfloat16* input, int8_t* output, float* scales, int M, int K,
+                        int had_block_size, hipStream_t stream) {
+    check(qimg_quantize_activation(input, QIMG_BF16, M, K, had_block_size, QIMG_QM_INT8_HADAMARD, output,
+                                   scales, stream),
+          "fwht_quantize_bf16");
+}
+
+void quantize_activation_int8_hadamard_fp32(const float* input, int8_t* output, float* scales, int M, int K,
+                                            int had_block_size, hipStream_t stream) {
+    check(qimg_quantize_activation(input, QIMG_FP32, M, K, had_block_size, QIMG_QM_INT8_HADAMARD, output,
+                                   scales, stream),
+          "quantize_activation_int8_hadamard_fp32");
+}
+
+void quantize_activation_int8_hadamard_bf16(const __hip_bfloat16* input, int8_t* output, float* scales, int M,
+                                            int K, int had_block_size, hipStream_t stream) {
+    check(qimg_quantize_activation(input, QIMG_BF16, M, K, had_block_size, QIMG_QM_INT8_HADAMARD, output,
+                                   scales, stream),
+          "quantize_activation_int8_hadamard_bf16");
+}
+
+void dequantize_and_bias(const int32_t* gemm_out, const float* act_scales, const float* w_scales,
+                         const __hip_bfloat16* bias, float* out, int M, int N, hipStream_t stream) {
+    check(qimg_dequantize_bias(gemm_out, act_scales, w_scales, reinterpret_cast<const uint16_t*>(bias), out, M, N,
+                               0, stream),
+          "dequantize_and_bias");
+}
+
+void dequantize_bias_gelu(const int32_t* gemm_out, const float* act_scales, const float* w_scales,
+                          const __hip_bfloat16* bias, float* out, int M, int N, hipStream_t stream) {
+    check(qimg_dequantize_bias(gemm_out, act_scales, w_scales, reinterpret_cast<const uint16_t*>(bias), out, M, N,
+                               1, stream),
+          "dequantize_bias_gelu");
+}
+
+void linear_forward_int8(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                         Tensor& scratch, bool apply_gelu) {
+    REQUIRE(weight.mode == QuantMode::INT8_HADAMARD, "linear_forward_int8", "weight.mode must be INT8_HADAMARD");
+    linear_common(x, DType::FP32, weight, bias, out, scratch, apply_gelu, "linear_forward_int8");
+}
+
+void linear_forward_int8_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                                Tensor& scratch, bool apply_gelu) {
+    REQUIRE(weight.mode == QuantMode::INT8_HADAMARD, "linear_forward_int8_bf16in",
+            "weight.mode must be INT8_HADAMARD");
+    linear_common(x, DType::BF16, weight, bias, out, scratch, apply_gelu, "linear_forward_int8_bf16in");
+}
+
+void linear_forward_int8_prequantized(const int8_t* act_int8, const float* act_scales, int M, int K,
+                                      const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                                      Tensor& /*scratch: the fused kernel needs none*/, bool apply_gelu) {
+    const char* fn = "linear_forward_int8_prequantized";
+    const int mode = qmode(weight.mode, fn);
+    check_weight(weight, K, fn);
+    const int N = static_cast<int>(weight.data.shape[0]);
+    check_out(out, M, N, fn);
+    check(qimg_linear_prequantized(act_int8, act_scales, M, K, weight.data.data,
+                                   static_cast<const float*>(weight.scales.data), N, mode, bias_ptr(bias, N, fn),
+                                   out.data, out_code(out, fn), apply_gelu ? 1 : 0, nullptr),
+          fn);
+}
+
+QuantizedWeight quantize_weight_tensor(const Tensor& bf16_weight) {
+    return quantize_weight_common(bf16_weight, QuantMode::INT8_HADAMARD, "quantize_weight_tensor");
+}
+
+QuantizedWeight quantize_weight_tensor_fp8(const Tensor& bf16_weight) {
+    return quantize_weight_common(bf16_weight, QuantMode::FP8_HADAMARD, "quantize_weight_tensor_fp8");
+}
+
+void linear_forward_quantized(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                              Tensor& scratch, bool apply_gelu) {
+    const char* fn = "linear_forward_quantized";
+    qmode(weight.mode, fn);  // INT4 / BF16 modes are reported here
+    linear_common(x, DType::FP32, weight, bias, out, scratch, apply_gelu, fn);
+}
+
+void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
+                                     Tensor& out, Tensor& scratch) {
+    const char* fn = "linear_forward_quantized_bf16in";
+    qmode(weight.mode, fn);
+    linear_common(x, DType::BF16, weight, bias, out, scratch, false, fn);
+}
+
+void attention_forward_sage_sm80_fp16io(const __half* q, const __half* k, const __half* v, float* out,
+                                        float scale, int BH, int S, int D, bool causal, hipStream_t stream) {
+    const char* fn = "attention_forward_sage_sm80_fp16io";
+    // sageattention_sm80.cu:975-978 rejects other head dims; checked here
+    // before the workspace is touched
+    REQUIRE(D == 64 || D == 128, fn, "head_dim %d not supported (64 or 128)", D);
+    REQUIRE(BH > 0 && S > 0, fn, "need BH > 0 and S > 0 (BH=%d S=%d)", BH, S);
+    const int64_t need = qimg_sage_scratch_bytes(BH, S, D);
+    void* ws = nullptr;
+    if (need > 0) {
+        int dev = 0;
+        HIP_CHECK(hipGetDevice(&dev));
+        SageWorkspace& w = sage_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        if (static_cast<int>(w.buf.size()) <= dev) {
+            w.buf.resize(dev + 1, nullptr);
+            w.bytes.resize(dev + 1, 0);
+        }
+        if (w.bytes[dev] < need) {
+            // the previous buffer may still be read by work queued earlier
+            HIP_CHECK(hipDeviceSynchronize());
+            if (w.buf[dev]) HIP_CHECK(hipFree(w.buf[dev]));
+            HIP_CHECK(hipMalloc(&w.buf[dev], need));
+            w.bytes[dev] = need;
+        }
+        ws = w.buf[dev];
+    }
+    check(qimg_sage_attention(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
+                              reinterpret_cast<const uint16_t*>(v), out, QIMG_FP32, scale, BH, S, D, causal ? 1 : 0,
+                              ws, need, stream),
+          fn);
+}

@@ -1,0 +1,107 @@
+// kernels.h — the quantized-linear and SageAttention operators of the
+// qwen-image MMDiT forward pass, with the reference's C++ call surface
+// (qwen-image.cu cuda_kernels.cuh:177-320, 415-424, 555-562) on the HIP
+// runtime. Every operator runs the gfx950 kernels of libqimg_hot.so through
+// its C ABI (include/qimg_hot.h); there is no host fallback.
+//
+// Differences from the reference surface, all additive:
+//   * QuantMode::FP8_HADAMARD: the same Hadamard front end with OCP e4m3
+//     weights/activations (scale = amax/448); QuantizedWeight::data is then
+//     DType::FP8_E4M3.
+//   * `out` may be FP32 (the reference's type) or BF16.
+//   * The INT4 / BF16 modes of the reference are not part of this library:
+//     dispatching one reports the mode and exits, like any other failed check.
+//
+// Error behaviour follows the reference (assert / CUDA_CHECK -> exit(1)): a
+// rejected argument or failed HIP call prints "qimg: <function>: <reason>"
+// to stderr and exits with status 1.
+#pragma once
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "tensor.h"
+
+enum class QuantMode { INT8_HADAMARD, INT4_SVD, BF16, INT4_AWQ, FP8_HADAMARD };
+
+// cuda_kernels.cuh:187-245, INT8 fields (plus the e4m3 mode).
+struct QuantizedWeight {
+    QuantMode mode = QuantMode::INT8_HADAMARD;
+    Tensor data;             // [N, K] INT8, or FP8_E4M3 for FP8_HADAMARD
+    Tensor scales;           // [N] FP32
+    int had_block_size = 0;  // Hadamard block size (power of 2)
+
+    QuantizedWeight() = default;
+    QuantizedWeight(QuantizedWeight&&) = default;
+    QuantizedWeight& operator=(QuantizedWeight&&) = default;
+
+    void free_data() {
+        data.free_data();
+        scales.free_data();
+    }
+};
+
+// ---- Hadamard + quantization (cuda_kernels.cuh:247-280) ----------------
+void fwht_inplace(float* data, int M, int K, int had_block_size, hipStream_t stream = 0);
+inline int hadamard_block_size(int K) { return K & (-K); }
+void quantize_per_row_fp32(const float* x, int8_t* out, float* scales, int M, int K,
+                           hipStream_t stream = 0);
+void quantize_activation_per_token_fp32(const float* x, int8_t* out, float* scales, int M, int K,
+                                        hipStream_t stream = 0);
+void quantize_activation_per_token_bf16(const __hip_bfloat16* x, int8_t* out, float* scales, int M,
+                                        int K, hipStream_t stream = 0);
+void fwht_quantize_fp32(const float* input, int8_t* output, float* scales, int M, int K,
+                        int had_block_size, hipStream_t stream = 0);
+void fwht_quantize_bf16(const __hip_bfloat16* input, int8_t* output, float* scales, int M, int K,
+                        int had_block_size, hipStream_t stream = 0);
+void quantize_activation_int8_hadamard_fp32(const float* input, int8_t* output, float* scales, int M,
+                                            int K, int had_block_size, hipStream_t stream = 0);
+void quantize_activation_int8_hadamard_bf16(const __hip_bfloat16* input, int8_t* output,
+                                            float* scales, int M, int K, int had_block_size,
+                                            hipStream_t stream = 0);
+
+// ---- dequant epilogue as a separate pass (cuda_kernels.cuh:282-291) ----
+void dequantize_and_bias(const int32_t* gemm_out, const float* act_scales, const float* w_scales,
+                         const __hip_bfloat16* bias, float* out, int M, int N, hipStream_t stream = 0);
+void dequantize_bias_gelu(const int32_t* gemm_out, const float* act_scales, const float* w_scales,
+                          const __hip_bfloat16* bias, float* out, int M, int N, hipStream_t stream = 0);
+
+// ---- quantized linears (cuda_kernels.cuh:293-319, 420-424) -------------
+// out[M,N] = dequant(quant(FWHT(x)) * W^T) + bias, optional GELU-tanh.
+void linear_forward_int8(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                         Tensor& scratch, bool apply_gelu = false);
+void linear_forward_int8_prequantized(const int8_t* act_int8, const float* act_scales, int M, int K,
+                                      const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                                      Tensor& scratch, bool apply_gelu = false);
+void linear_forward_int8_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
+                                Tensor& out, Tensor& scratch, bool apply_gelu = false);
+
+// BF16 [N,K] -> FWHT(K & -K) -> per-row quantization; synchronous, as the
+// reference (cuda_kernels.cu:2830-2862). quantize_weight_tensor_fp8 is the
+// e4m3 twin (mode FP8_HADAMARD).
+QuantizedWeight quantize_weight_tensor(const Tensor& bf16_weight);
+QuantizedWeight quantize_weight_tensor_fp8(const Tensor& bf16_weight);
+
+inline int64_t int8_scratch_bytes(int M, int K, int N) {
+    const int64_t regionA = ((std::max(static_cast<int64_t>(M) * K, static_cast<int64_t>(M) * N) * 4 + 255) & ~255LL);
+    const int64_t act = ((static_cast<int64_t>(M) * K + 255) & ~255LL);
+    const int64_t scales = ((static_cast<int64_t>(M) * 4 + 255) & ~255LL);
+    return regionA + act + scales;
+}
+
+// Dispatch on weight.mode (cuda_kernels.cu:4599-4635): x FP32 resp. BF16.
+void linear_forward_quantized(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
+                              Tensor& out, Tensor& scratch, bool apply_gelu = false);
+void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
+                                     Tensor& out, Tensor& scratch);
+
+// ---- SageAttention (cuda_kernels.cuh:558-562) --------------------------
+// FP16 q, k, v [BH, S, D] -> FP32 out [BH, S, D] (values rounded through
+// FP16, as the reference). D in {64, 128}. Uses a per-device workspace the
+// library grows on demand (the reference's SageAttentionWorkspace).
+void attention_forward_sage_sm80_fp16io(const __half* q, const __half* k, const __half* v, float* out,
+                                        float scale, int BH, int S, int D, bool causal = false,
+                                        hipStream_t stream = 0);

@@ -38,6 +38,7 @@ _SIGS = {
     "qimg_quantize_activation": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "qimg_quantize_weight": (_I, [_P, _I, _I, _I, _I, _P, _P, ctypes.POINTER(_I), _P]),
     "qimg_linear_prequantized": (_I, [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P]),
+    "qimg_dequantize_bias": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "qimg_linear": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I64, _P]),
     "qimg_sage_scratch_bytes": (_I64, [_I, _I, _I]),
     "qimg_sage_k_mean": (_I, [_P, _P, _I, _I, _I, _P]),
@@ -182,6 +183,18 @@ def linear_forward_prequantized(act_q: torch.Tensor, act_scales: torch.Tensor, w
     _check(_lib.qimg_linear_prequantized(_ptr(act_q), _ptr(act_scales), M, K, _ptr(weight.data),
                                          _ptr(weight.scales), N, int(weight.mode), _ptr(bias), _ptr(out),
                                          _DT[out.dtype], int(bool(apply_gelu)), _stream()))
+    return out
+
+
+def dequantize_and_bias(acc: torch.Tensor, act_scales: torch.Tensor, w_scales: torch.Tensor,
+                        bias: torch.Tensor | None = None, apply_gelu: bool = False) -> torch.Tensor:
+    """dequantize_and_bias / dequantize_bias_gelu (cuda_kernels.cu:2623-2668):
+    int32 [M,N] -> fp32 [M,N]."""
+    _dev(acc, "acc")
+    M, N = acc.shape
+    out = torch.empty((M, N), dtype=torch.float32, device=acc.device)
+    _check(_lib.qimg_dequantize_bias(_ptr(acc), _ptr(act_scales), _ptr(w_scales), _ptr(bias), _ptr(out), M, N,
+                                     int(bool(apply_gelu)), _stream()))
     return out
 
 

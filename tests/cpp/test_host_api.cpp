@@ -1,0 +1,341 @@
+// test_host_api.cpp — exercises the reference-signature C++ layer
+// (qwen-image.cu_amd/host/kernels.h) the way the reference's forward pass
+// calls it (transformer.cu:563-606, 680-689, 785-807), and checks every
+// result against the CPU oracle (oracle/qimg_oracle.h, the checker).
+//
+//   test_host_api                    GPU parity cases; exit 0 when all pass
+//   test_host_api --expect-error C   run case C, which must be rejected by the
+//                                    host-side checks before any HIP call (the
+//                                    process then exits 1 with a message, as
+//                                    the reference's asserts do); no GPU needed
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "qimg_oracle.h"
+
+namespace {
+
+int g_fail = 0;
+
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed * 0x9E3779B97F4A7C15ull + 1) {}
+    uint32_t next() {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        return static_cast<uint32_t>(s >> 32);
+    }
+    float uniform() { return (next() + 0.5f) * (1.0f / 4294967296.0f); }
+    float normal() {
+        const float u = uniform(), v = uniform();
+        return std::sqrt(-2.0f * std::log(u)) * std::cos(6.2831853f * v);
+    }
+};
+
+std::vector<uint16_t> bf16_normal(Rng& r, size_t n, float sigma) {
+    std::vector<uint16_t> v(n);
+    for (auto& x : v) x = or_f32_to_bf16(r.normal() * sigma);
+    return v;
+}
+
+std::vector<float> f32_normal(Rng& r, size_t n, float sigma) {
+    std::vector<float> v(n);
+    for (auto& x : v) x = r.normal() * sigma;
+    return v;
+}
+
+template <typename T>
+Tensor upload(const std::vector<T>& h, std::vector<int64_t> dims, DType dt) {
+    Tensor t = Tensor::alloc(dims, dt);
+    t.from_host(h.data(), h.size() * sizeof(T));
+    return t;
+}
+
+template <typename T>
+std::vector<T> download(const Tensor& t) {
+    std::vector<T> h(t.nbytes() / sizeof(T));
+    t.to_host(h.data());
+    return h;
+}
+
+void report(const char* name, bool ok, const std::string& detail = "") {
+    printf("%s %s %s\n", ok ? "ok  " : "FAIL", name, detail.c_str());
+    fflush(stdout);
+    if (!ok) ++g_fail;
+}
+
+// Oracle chain a5 -> a7 -> a8 (fp32 or bf16 input) -> fp32 [M,N].
+std::vector<float> oracle_linear(const void* x, bool bf16, int M, int K, const std::vector<int8_t>& wq,
+                                 const std::vector<float>& ws, int N, int hbs, const uint16_t* bias, bool gelu) {
+    std::vector<int8_t> q(static_cast<size_t>(M) * K);
+    std::vector<float> s(M);
+    or_quantize_activation(x, bf16 ? 1 : 0, M, K, hbs, q.data(), s.data());
+    std::vector<int32_t> c(static_cast<size_t>(M) * N);
+    or_gemm_s8s8s32(q.data(), wq.data(), M, N, K, 0, M, c.data());
+    std::vector<float> out(static_cast<size_t>(M) * N);
+    or_dequant_epilogue(c.data(), s.data(), ws.data(), bias, M, N, gelu ? 1 : 0, out.data());
+    return out;
+}
+
+double max_abs_diff(const std::vector<float>& a, const std::vector<float>& b) {
+    double m = 0;
+    for (size_t i = 0; i < a.size(); ++i) m = std::fmax(m, std::fabs(static_cast<double>(a[i]) - b[i]));
+    return m;
+}
+
+double max_abs(const std::vector<float>& a) {
+    double m = 0;
+    for (float v : a) m = std::fmax(m, std::fabs(v));
+    return m;
+}
+
+void case_tensor_api() {
+    Rng r(1);
+    std::vector<float> h = f32_normal(r, 6 * 5, 1.0f);
+    Tensor t = upload(h, {6, 5}, DType::FP32);
+    Tensor c = t.clone();
+    Tensor s = c.slice(2, 4);
+    Tensor v = s.view({10});
+    std::vector<float> got = download<float>(v);
+    bool ok = got.size() == 10 && std::memcmp(got.data(), h.data() + 10, 40) == 0 && t.numel() == 30 &&
+              s.shape[0] == 2 && s.shape[1] == 5 && !s.owns_data && c.owns_data;
+    Tensor moved = std::move(c);
+    ok = ok && moved.owns_data && c.data == nullptr;
+    report("tensor_api", ok);
+}
+
+void case_weight_quant(QuantMode mode, int N, int K) {
+    Rng r(N + K);
+    std::vector<uint16_t> w = bf16_normal(r, static_cast<size_t>(N) * K, 0.02f);
+    Tensor wt = upload(w, {N, K}, DType::BF16);
+    QuantizedWeight qw = mode == QuantMode::INT8_HADAMARD ? quantize_weight_tensor(wt) : quantize_weight_tensor_fp8(wt);
+    std::vector<uint8_t> gq = download<uint8_t>(qw.data);
+    std::vector<float> gs = download<float>(qw.scales);
+    std::vector<uint8_t> rq(static_cast<size_t>(N) * K);
+    std::vector<float> rs(N);
+    int hbs = 0;
+    if (mode == QuantMode::INT8_HADAMARD) {
+        hbs = or_quantize_weight_bf16(w.data(), N, K, reinterpret_cast<int8_t*>(rq.data()), rs.data());
+    } else {
+        std::vector<float> wf(w.size());
+        for (size_t i = 0; i < w.size(); ++i) wf[i] = or_bf16_to_f32(w[i]);
+        hbs = or_hadamard_block_size(K);
+        or_fwht_rows(wf.data(), N, K, hbs);
+        or_quant_rows_fp8(wf.data(), N, K, rq.data(), rs.data());
+    }
+    const bool ok = qw.had_block_size == hbs && gq == rq && gs == rs &&
+                    qw.data.dtype == (mode == QuantMode::INT8_HADAMARD ? DType::INT8 : DType::FP8_E4M3);
+    report(mode == QuantMode::INT8_HADAMARD ? "quantize_weight_tensor" : "quantize_weight_tensor_fp8", ok);
+}
+
+void case_linear(bool bf16_in, int M, int N, int K, bool with_bias, bool gelu) {
+    Rng r(M * 7 + N * 3 + K);
+    std::vector<uint16_t> w = bf16_normal(r, static_cast<size_t>(N) * K, 0.02f);
+    std::vector<uint16_t> b = bf16_normal(r, N, 0.01f);
+    std::vector<float> xf = f32_normal(r, static_cast<size_t>(M) * K, 1.0f);
+    std::vector<uint16_t> xb(xf.size());
+    for (size_t i = 0; i < xf.size(); ++i) xb[i] = or_f32_to_bf16(xf[i]);
+
+    Tensor wt = upload(w, {N, K}, DType::BF16);
+    QuantizedWeight qw = quantize_weight_tensor(wt);
+    Tensor bias = upload(b, {N}, DType::BF16);
+    Tensor x = bf16_in ? upload(xb, {M, K}, DType::BF16) : upload(xf, {M, K}, DType::FP32);
+    Tensor out = Tensor::alloc({M, N}, DType::FP32);
+    Tensor scratch = Tensor::alloc({int8_scratch_bytes(M, K, N)}, DType::UINT8);
+    if (bf16_in)
+        linear_forward_int8_bf16in(x, qw, with_bias ? &bias : nullptr, out, scratch, gelu);
+    else
+        linear_forward_quantized(x, qw, with_bias ? &bias : nullptr, out, scratch, gelu);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> got = download<float>(out);
+
+    std::vector<int8_t> wq(static_cast<size_t>(N) * K);
+    std::vector<float> ws(N);
+    const int hbs = or_quantize_weight_bf16(w.data(), N, K, wq.data(), ws.data());
+    std::vector<float> ref = oracle_linear(bf16_in ? static_cast<const void*>(xb.data()) : xf.data(), bf16_in, M, K,
+                                           wq, ws, N, hbs, with_bias ? b.data() : nullptr, gelu);
+    char name[128];
+    snprintf(name, sizeof(name), "linear %s M=%d N=%d K=%d bias=%d gelu=%d", bf16_in ? "bf16in" : "fp32in", M, N, K,
+             with_bias, gelu);
+    // No GELU: the epilogue is the reference's operation order, bit-exact.
+    // GELU: tanh evaluated through exp2/rcp on the GPU, ~1e-6 relative.
+    const double d = max_abs_diff(got, ref);
+    const bool ok = gelu ? d <= 2e-6 * (max_abs(ref) + 1.0) : d == 0.0;
+    char det[64];
+    snprintf(det, sizeof(det), "max|diff|=%.3g", d);
+    report(name, ok, det);
+}
+
+void case_prequantized_and_dequant() {
+    const int M = 129, N = 384, K = 3072;
+    Rng r(99);
+    std::vector<uint16_t> w = bf16_normal(r, static_cast<size_t>(N) * K, 0.02f);
+    std::vector<uint16_t> b = bf16_normal(r, N, 0.01f);
+    std::vector<float> xf = f32_normal(r, static_cast<size_t>(M) * K, 1.0f);
+    Tensor qwt = upload(w, {N, K}, DType::BF16);
+    QuantizedWeight qw = quantize_weight_tensor(qwt);
+    Tensor x = upload(xf, {M, K}, DType::FP32);
+    Tensor qa = Tensor::alloc({M, K}, DType::INT8);
+    Tensor sa = Tensor::alloc({M}, DType::FP32);
+    quantize_activation_int8_hadamard_fp32(static_cast<const float*>(x.data), static_cast<int8_t*>(qa.data),
+                                           static_cast<float*>(sa.data), M, K, qw.had_block_size);
+    Tensor bias = upload(b, {N}, DType::BF16);
+    Tensor out = Tensor::alloc({M, N}, DType::FP32);
+    Tensor scratch;
+    linear_forward_int8_prequantized(static_cast<const int8_t*>(qa.data), static_cast<const float*>(sa.data), M, K,
+                                     qw, &bias, out, scratch, false);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> got = download<float>(out);
+    std::vector<int8_t> wq(static_cast<size_t>(N) * K);
+    std::vector<float> ws(N);
+    const int hbs = or_quantize_weight_bf16(w.data(), N, K, wq.data(), ws.data());
+    std::vector<float> ref = oracle_linear(xf.data(), false, M, K, wq, ws, N, hbs, b.data(), false);
+    report("linear_forward_int8_prequantized", max_abs_diff(got, ref) == 0.0);
+
+    // separate dequant pass on an oracle int32 product
+    std::vector<int8_t> q(static_cast<size_t>(M) * K);
+    std::vector<float> s(M);
+    or_quantize_activation(xf.data(), 0, M, K, hbs, q.data(), s.data());
+    std::vector<int32_t> c(static_cast<size_t>(M) * N);
+    or_gemm_s8s8s32(q.data(), wq.data(), M, N, K, 0, M, c.data());
+    Tensor ct = upload(c, {M, N}, DType::INT32);
+    Tensor st = upload(s, {M}, DType::FP32);
+    Tensor wst = upload(ws, {N}, DType::FP32);
+    Tensor o2 = Tensor::alloc({M, N}, DType::FP32);
+    dequantize_and_bias(static_cast<const int32_t*>(ct.data), static_cast<const float*>(st.data),
+                        static_cast<const float*>(wst.data), static_cast<const __hip_bfloat16*>(bias.data),
+                        static_cast<float*>(o2.data), M, N);
+    HIP_CHECK(hipDeviceSynchronize());
+    report("dequantize_and_bias", max_abs_diff(download<float>(o2), ref) == 0.0);
+}
+
+void case_fp8_linear() {
+    const int M = 200, N = 256, K = 3072;
+    Rng r(5);
+    std::vector<uint16_t> w = bf16_normal(r, static_cast<size_t>(N) * K, 0.02f);
+    std::vector<uint16_t> xb = bf16_normal(r, static_cast<size_t>(M) * K, 1.0f);
+    Tensor wt = upload(w, {N, K}, DType::BF16);
+    QuantizedWeight qw = quantize_weight_tensor_fp8(wt);
+    Tensor x = upload(xb, {M, K}, DType::BF16);
+    Tensor out = Tensor::alloc({M, N}, DType::FP32);
+    Tensor scratch = Tensor::alloc({int8_scratch_bytes(M, K, N)}, DType::UINT8);
+    linear_forward_quantized_bf16in(x, qw, nullptr, out, scratch);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> got = download<float>(out);
+    // float64 product of the unquantized operands (H orthonormal, so the
+    // rotation cancels): the e4m3 path must stay within the stated bar.
+    double num = 0, den = 0, dot = 0, na = 0, nb = 0, mx = 0;
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double e = 0;
+            for (int k = 0; k < K; ++k)
+                e += static_cast<double>(or_bf16_to_f32(xb[static_cast<size_t>(m) * K + k])) *
+                     or_bf16_to_f32(w[static_cast<size_t>(n) * K + k]);
+            const double g = got[static_cast<size_t>(m) * N + n];
+            num = std::fmax(num, std::fabs(g - e));
+            mx = std::fmax(mx, std::fabs(e));
+            dot += g * e;
+            na += g * g;
+            nb += e * e;
+        }
+    (void)den;
+    const double rel = num / mx, cos = dot / std::sqrt(na * nb);
+    char det[96];
+    snprintf(det, sizeof(det), "max-rel=%.3g cos=%.6f", rel, cos);
+    report("linear fp8 bf16in vs float64", rel <= 5e-2 && cos >= 0.999, det);
+}
+
+void case_sage(int BH, int S, int D, bool causal) {
+    Rng r(BH * S + D);
+    const size_t n = static_cast<size_t>(BH) * S * D;
+    std::vector<uint16_t> q(n), k(n), v(n);
+    for (size_t i = 0; i < n; ++i) {
+        q[i] = or_f32_to_f16(r.normal());
+        k[i] = or_f32_to_f16(r.normal() + 0.5f);
+        v[i] = or_f32_to_f16(r.normal());
+    }
+    Tensor qt = upload(q, {BH, S, D}, DType::FP16), kt = upload(k, {BH, S, D}, DType::FP16),
+           vt = upload(v, {BH, S, D}, DType::FP16);
+    Tensor ot = Tensor::alloc({BH, S, D}, DType::FP32);
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+    attention_forward_sage_sm80_fp16io(static_cast<const __half*>(qt.data), static_cast<const __half*>(kt.data),
+                                       static_cast<const __half*>(vt.data), static_cast<float*>(ot.data), scale, BH,
+                                       S, D, causal);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> got = download<float>(ot);
+    std::vector<uint16_t> ref16(n);
+    or_sage_attention_fp16io(q.data(), k.data(), v.data(), BH, S, D, scale, causal ? 1 : 0, ref16.data());
+    std::vector<float> ref(n);
+    for (size_t i = 0; i < n; ++i) ref[i] = or_f16_to_f32(ref16[i]);
+    const double d = max_abs_diff(got, ref);
+    char name[96], det[64];
+    snprintf(name, sizeof(name), "attention_forward_sage_sm80_fp16io BH=%d S=%d D=%d causal=%d", BH, S, D, causal);
+    snprintf(det, sizeof(det), "max|diff|=%.3g", d);
+    report(name, d <= 2e-3 * max_abs(ref) + 2e-3, det);
+}
+
+// Host-side rejections: fake device pointers that must never be touched.
+int expect_error(const std::string& c) {
+    void* fake = reinterpret_cast<void*>(0x10000);
+    Tensor x = Tensor::wrap(fake, {4, 64}, DType::FP32);
+    Tensor out = Tensor::wrap(fake, {4, 8}, DType::FP32);
+    Tensor scratch = Tensor::wrap(fake, {1 << 20}, DType::UINT8);
+    QuantizedWeight w;
+    w.data = Tensor::wrap(fake, {8, 64}, DType::INT8);
+    w.scales = Tensor::wrap(fake, {8}, DType::FP32);
+    w.had_block_size = 64;
+    if (c == "out_shape") {
+        Tensor bad = Tensor::wrap(fake, {4, 9}, DType::FP32);
+        linear_forward_int8(x, w, nullptr, bad, scratch);
+    } else if (c == "x_dtype") {
+        Tensor xb = Tensor::wrap(fake, {4, 64}, DType::BF16);
+        linear_forward_int8(xb, w, nullptr, out, scratch);
+    } else if (c == "weight_k") {
+        Tensor x2 = Tensor::wrap(fake, {4, 128}, DType::FP32);
+        linear_forward_quantized(x2, w, nullptr, out, scratch);
+    } else if (c == "mode_int4") {
+        w.mode = QuantMode::INT4_SVD;
+        linear_forward_quantized(x, w, nullptr, out, scratch);
+    } else if (c == "scratch") {
+        Tensor small = Tensor::wrap(fake, {16}, DType::UINT8);
+        linear_forward_int8(x, w, nullptr, out, small);
+    } else if (c == "hbs") {
+        w.had_block_size = 48;
+        linear_forward_int8(x, w, nullptr, out, scratch);
+    } else if (c == "sage_head_dim") {
+        attention_forward_sage_sm80_fp16io(static_cast<const __half*>(fake), static_cast<const __half*>(fake),
+                                           static_cast<const __half*>(fake), static_cast<float*>(fake), 0.1f, 2, 64,
+                                           96);
+    } else {
+        fprintf(stderr, "unknown case %s\n", c.c_str());
+        return 2;
+    }
+    fprintf(stderr, "case %s was not rejected\n", c.c_str());
+    return 3;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc == 3 && std::string(argv[1]) == "--expect-error") return expect_error(argv[2]);
+    case_tensor_api();
+    case_weight_quant(QuantMode::INT8_HADAMARD, 3072, 3072);
+    case_weight_quant(QuantMode::INT8_HADAMARD, 256, 12288);
+    case_weight_quant(QuantMode::FP8_HADAMARD, 512, 3072);
+    case_linear(false, 300, 320, 3072, true, false);
+    case_linear(true, 64, 256, 12288, true, false);
+    case_linear(true, 257, 255, 1024, false, false);
+    case_linear(false, 96, 512, 3072, true, true);
+    case_linear(true, 1, 18432 / 8, 3072, true, false);
+    case_prequantized_and_dequant();
+    case_fp8_linear();
+    case_sage(2, 300, 128, false);
+    case_sage(3, 129, 64, true);
+    printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "PASSED", g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -167,3 +167,26 @@ def test_mlp_pair_full_size_sampled(qimg, oracle):
     rel, cos = _metrics(y_got, exact)
     assert rel <= rel_o * 1.05 + 1e-3 and cos >= cos_o - 1e-4, (rel, cos, rel_o, cos_o)
     assert cos_o >= 0.99
+
+
+def test_dequantize_and_bias_matches_oracle_and_fused(qimg, oracle):
+    """The stand-alone epilogue (dequantize_and_bias / dequantize_bias_gelu)
+    on an oracle int32 product: bit-exact without GELU, and identical to the
+    fused GEMM epilogue with GELU."""
+    rng = np.random.default_rng(31)
+    M, N, K = 200, 264, 3072
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    wq, ws, hbs = oracle.quantize_weight_bf16(w_bits)
+    q, s = oracle.quantize_activation(x, hbs)
+    c = oracle.gemm_s8s8s32(q, wq)
+    got = qimg.dequantize_and_bias(_dev(c), _dev(s), _dev(ws), _bf16_dev(b_bits))
+    got_g = qimg.dequantize_and_bias(_dev(c), _dev(s), _dev(ws), _bf16_dev(b_bits), apply_gelu=True)
+    fused_g = qimg.linear_forward_prequantized(_dev(q), _dev(s), _qw(qimg, wq, ws, hbs), _bf16_dev(b_bits),
+                                               apply_gelu=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle.dequant_epilogue(c, s, ws, b_bits))
+    np.testing.assert_array_equal(got_g.cpu().numpy(), fused_g.cpu().numpy())
+    np.testing.assert_allclose(got_g.cpu().numpy(), oracle.dequant_epilogue(c, s, ws, b_bits, gelu=True),
+                               rtol=2e-6, atol=2e-6)
