@@ -12,8 +12,12 @@
  * tanhf, ex2.approx, rcp.approx): there the oracle uses the correctly
  * rounded operation.
  *
- * Pinning status (which independent check fixes each function) is listed in
- * oracle/README.md.
+ * Each function is pinned by checks independent of its own code (closed
+ * forms, explicit Hadamard matrices, numpy/torch conversions, brute-force
+ * integer products, hand-derived known answers, float64 attention) in
+ * tests/test_oracle_pins.py, and frozen by the fixtures of tests/golden/.
+ * No function is left unpinned. What no check here can pin is the reference
+ * binary's fast-math rounding on exact ties (see tests/test_oracle_pins.py).
  */
 #ifndef QIMG_ORACLE_H
 #define QIMG_ORACLE_H

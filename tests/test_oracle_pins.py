@@ -5,6 +5,13 @@ stage order and scale-group layout, and float64 attention/linear algebra.
 
 No reference source is executed: the reference is CUDA and cannot be built
 here, and it ships no golden vectors for this path.
+
+What these checks cannot pin: the reference binary is compiled with
+--use_fast_math (Makefile:11), so its `127.0f / amax`, `1.0f / scale`,
+rsqrtf, tanhf and ex2.approx are approximations. The oracle (and the GPU
+path) use correctly rounded division and rsqrt, so a value that lands exactly
+on an int8 rounding tie can round differently from a CUDA run of the
+reference. Nothing in the reference's tree records such a run.
 """
 import math
 
