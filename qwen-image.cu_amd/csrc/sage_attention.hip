@@ -43,26 +43,90 @@ constexpr int QBLK = 128;
 __host__ __device__ constexpr int div_up(int a, int b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------- k mean
-// One thread per (head, d); the fp32 sum runs token by token in order,
-// exactly as the reference's single-thread loop, so the mean is bit-equal.
-__global__ void k_mean_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean, int BH,
-                              int S, int D) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= BH * D) return;
-    const int h = idx / D;
-    const int d = idx % D;
-    const uint16_t* p = k + static_cast<int64_t>(h) * S * D + d;
+// mean[h,d] = (sum over s of k[h,s,d], left to right in fp32) / max(S,1),
+// bit-equal to the reference's one-thread-per-(h,d) loop. The sum must stay
+// sequential, so the work is arranged to keep memory latency off that chain:
+// a 256-thread workgroup owns 64 (h,d) chains. Wave 0 only sums; waves 1-3
+// stream 512-token chunks of k[h, :, d0:d0+64] into LDS (16-byte coalesced
+// loads), stored transposed as [d][s] so the summing lane reads 8 consecutive
+// tokens of its chain with one ds_read_b128. Chunks are double-buffered: the
+// loads of chunk c+1 overlap the sums of chunk c, which take about as long as
+// one memory round trip.
+constexpr int KM_CHUNK = 512;                 // tokens per chunk
+constexpr int KM_PITCH = KM_CHUNK + 8;        // fp16 per LDS row (1040 B: 16-byte aligned rows)
+constexpr int KM_PIECES = KM_CHUNK * 8;       // 16-byte pieces per chunk (64 fp16 per token)
+constexpr int KM_LOADERS = 192;               // threads of waves 1-3
+constexpr int KM_BATCH = 22;                  // loads in flight per loader lane: a whole chunk
+static_assert(KM_BATCH * KM_LOADERS >= KM_PIECES, "one batch covers a chunk");
+
+__global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean,
+                                                     int S, int D) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[2][64][KM_PITCH];
+    const int slices = D / 64;
+    const int h = blockIdx.x / slices;
+    const int d0 = (blockIdx.x % slices) * 64;
+    const int tid = threadIdx.x;
+    const uint16_t* src = k + static_cast<int64_t>(h) * S * D + d0;
+    const int nchunk = div_up(S, KM_CHUNK);
+
+    // loader piece p: token p / 8 of the chunk, fp16 columns 8 * (p % 8) .. +8
+    auto load_chunk = [&](int c, int buf) {
+        const int lt = tid - 64;
+        {
+            constexpr int b = 0;
+            u32x4 v[KM_BATCH];
+#pragma unroll
+            for (int j = 0; j < KM_BATCH; ++j) {
+                const int p = (b * KM_BATCH + j) * KM_LOADERS + lt;
+                const int s = c * KM_CHUNK + (p >> 3);
+                v[j] = (u32x4){0u, 0u, 0u, 0u};
+                if (p < KM_PIECES && s < S)
+                    v[j] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(s) * D + (p & 7) * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < KM_BATCH; ++j) {
+                const int p = (b * KM_BATCH + j) * KM_LOADERS + lt;
+                if (p >= KM_PIECES) continue;
+                const int sl = p >> 3;
+                const int col = (p & 7) * 8;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    tile[buf][col + 2 * e][sl] = static_cast<uint16_t>(v[j][e] & 0xffffu);
+                    tile[buf][col + 2 * e + 1][sl] = static_cast<uint16_t>(v[j][e] >> 16);
+                }
+            }
+        }
+    };
+
     float sum = 0.0f;
-    int s = 0;
-    for (; s + 8 <= S; s += 8) {
-        float v[8];
+    if (tid >= 64) load_chunk(0, 0);
+    __syncthreads();
+    for (int c = 0; c < nchunk; ++c) {
+        const int buf = c & 1;
+        if (tid >= 64) {
+            if (c + 1 < nchunk) load_chunk(c + 1, buf ^ 1);
+        } else {
+            const int n = min(KM_CHUNK, S - c * KM_CHUNK);
+            const uint16_t* row = &tile[buf][tid][0];
+            int s = 0;
+            // four 16-byte reads in flight ahead of the add chain
+            for (; s + 32 <= n; s += 32) {
+                u32x4 v[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = f16_to_f32(p[static_cast<int64_t>(s + u) * D]);
+                for (int r = 0; r < 4; ++r) v[r] = *reinterpret_cast<const u32x4*>(row + s + 8 * r);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) sum += v[u];
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sum += f16_to_f32(static_cast<uint16_t>(v[r][e] & 0xffffu));
+                        sum += f16_to_f32(static_cast<uint16_t>(v[r][e] >> 16));
+                    }
+            }
+            for (; s < n; ++s) sum += f16_to_f32(row[s]);
+        }
+        __syncthreads();
     }
-    for (; s < S; ++s) sum += f16_to_f32(p[static_cast<int64_t>(s) * D]);
-    mean[idx] = sum / fmaxf(static_cast<float>(S), 1.0f);
+    if (tid < 64) mean[static_cast<int64_t>(h) * D + d0 + tid] = sum / fmaxf(static_cast<float>(S), 1.0f);
 }
 
 // ---------------------------------------------------------------- Q quant
@@ -545,8 +609,7 @@ int64_t sage_scratch_layout(int BH, int S, int D, void* base, SageScratch* out) 
 
 hipError_t launch_sage_k_mean(const uint16_t* k, float* mean, int BH, int S, int D,
                               hipStream_t stream) {
-    const int n = BH * D;
-    hipLaunchKernelGGL(k_mean_kernel, dim3(div_up(n, 64)), dim3(64), 0, stream, k, mean, BH, S, D);
+    hipLaunchKernelGGL(k_mean_kernel, dim3(BH * (D / 64)), dim3(256), 0, stream, k, mean, S, D);
     return hipGetLastError();
 }
 
