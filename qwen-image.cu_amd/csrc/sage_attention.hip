@@ -9,13 +9,14 @@
 //   attention              :47-674   int8 QK^T, base-2 online softmax over
 //                                    64-key tiles, P rounded to fp16, fp16 PV
 //                                    with fp32 accumulation, O/d -> fp16
+//                                    (the running max here moves lazily; see
+//                                    kRescaleSlack)
 // The quantized values and scales are bit-identical to the reference's
 // formulas (scale = amax/127 + 1e-7, q = rne_sat(v * (1/scale))).
 //
 // MI355X design of the attention kernel:
-//  * A workgroup is 4 waves; each wave owns 32 queries (128 per workgroup,
-//    so each wave's queries are exactly one of the reference's per-thread Q
-//    scale groups' 32-token windows).
+//  * Each wave owns 32 queries, exactly one of the reference's per-thread Q
+//    scale groups' 32-token windows.
 //  * Scores are computed transposed, S^T = K Q^T, with
 //    v_mfma_i32_32x32x32_i8: lane l then holds ONE query (l % 32) and 32 of
 //    the tile's 64 keys, so the softmax row max / row sum are lane-local
@@ -27,9 +28,12 @@
 //  * V is re-laid once per call into [head][64-key tile][d][64 keys] with a
 //    fixed permutation of each 16-key group that makes a lane's 8 keys of a
 //    PV fragment contiguous (one ds_read_b128).
-//  * K (int8) and V (fp16) tiles stream through a double-buffered LDS ring
-//    with rows padded to 144 bytes (bank-conflict-free 16-byte fragment
-//    reads); Q stays in registers for the whole kernel.
+//  * A workgroup is 8 waves over 256 queries; K (int8) and V (fp16) tiles
+//    stream through a 4-slot LDS ring filled by direct global->LDS DMA, with
+//    an XOR swizzle for bank-conflict-free 16-byte fragment reads; Q stays in
+//    registers for the whole kernel.
+#include <type_traits>
+
 #include "qimg_device.h"
 #include "qimg_internal.h"
 
@@ -316,41 +320,87 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
 }
 
 // ------------------------------------------------------------ attention
+// A workgroup is 8 waves (two per SIMD) over AQ = 256 queries; wave w owns
+// queries 32w .. 32w+31 of the block. K (int8 [64][D]) and V^T (fp16
+// [D][64]) tiles stream through a 4-slot LDS ring filled by direct
+// global->LDS DMA (global_load_lds_dwordx4), three tiles ahead of the
+// compute, so each 64-key tile is fetched once for 256 queries. Rows are
+// unpadded; a per-row XOR swizzle of the 16-byte chunks keeps the fragment
+// reads of 8 consecutive rows on distinct LDS banks (the DMA source address
+// of each lane applies the same swizzle).
+constexpr int AQ = 256;          // queries per workgroup
+constexpr float kRescaleSlack = 8.0f;  // lazy-rescale threshold of the running max (log2 units)
+constexpr int AWAVES = AQ / 32;  // 8
+constexpr int ANSLOT = 4;        // LDS ring depth (tiles)
+
 template <int D>
 struct AttnCfg {
-    static constexpr int KROW = D + 16;            // padded int8 K row (bytes)
-    static constexpr int VROW = 2 * KTILE + 16;    // padded fp16 V^T row (bytes)
-    static constexpr int K_BYTES = KTILE * KROW;
-    static constexpr int V_BYTES = D * VROW;
+    static constexpr int K_BYTES = KTILE * D;             // int8 K tile
+    static constexpr int V_BYTES = D * KTILE * 2;         // fp16 V^T tile (rows of 128 B)
     static constexpr int STAGE = K_BYTES + V_BYTES;
-    static constexpr int KSTEPS = D / 32;          // int8 MFMA k-steps
-    static constexpr int DT = D / 32;              // 32-row d tiles of O^T
-    static constexpr int K_PIECES = KTILE * D / 16;      // 16-byte pieces per K tile
-    static constexpr int V_PIECES = D * KTILE * 2 / 16;  // per V tile
-    static constexpr int K_PER_THR = K_PIECES / 256;
-    static constexpr int V_PER_THR = V_PIECES / 256;
+    static constexpr int KSTEPS = D / 32;                 // int8 MFMA k-steps
+    static constexpr int DT = D / 32;                     // 32-row d tiles of O^T
+    static constexpr int K_CPR = D / 16;                  // 16-byte chunks per K row
+    static constexpr int K_INSTR = K_BYTES / 1024;        // 1 KB DMA instructions per tile
+    static constexpr int V_INSTR = V_BYTES / 1024;
+    static constexpr int NI = K_INSTR + V_INSTR;
+    static constexpr int PER_WAVE = (NI + AWAVES - 1) / AWAVES;
+    static constexpr int KEEP = (ANSLOT - 2) * PER_WAVE;  // DMA instructions in flight at a hand-off
 };
 
+// physical 16-byte chunk of logical chunk c in row `row` (involution)
+template <int CPR>
+__device__ __forceinline__ int swz_chunk(int row, int c) {
+    if constexpr (CPR == 8) return c ^ (row & 7);
+    else return c ^ ((row >> 1) & 3);
+}
+
+// s_waitcnt vmcnt(n) (other counters untouched), and vmcnt(n) + lgkmcnt(0)
+template <int n>
+__device__ __forceinline__ void attn_wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((0x0f70 & ~0xc00f) | (n & 15) | ((n >> 4) << 14));
+}
+template <int n>
+__device__ __forceinline__ void attn_wait_vmcnt_lgkm0() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0070 | (n & 15) | ((n >> 4) << 14));
+}
+
+typedef __attribute__((address_space(3))) void* attn_lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* attn_gbl_ptr_t;
+
 template <int D, bool CAUSAL, int OUT_DT>
-__global__ __launch_bounds__(256, 2) void sage_attn_kernel(
+__global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     const int8_t* __restrict__ Q, const int8_t* __restrict__ K, const uint16_t* __restrict__ Vt,
     const float* __restrict__ q_scale, const float* __restrict__ k_scale, void* __restrict__ out,
-    int S, float sm_log2) {
+    int S, int BH, float sm_log2) {
     // Every rounding step is spelled out (explicit fmaf where fused), so all
     // output-type instantiations compute identical values.
 #pragma clang fp contract(off)
     using C = AttnCfg<D>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[ANSLOT * C::STAGE];
 
-    const int qb = blockIdx.x;
-    const int h = blockIdx.y;
+    // Heads are laid out XCD-contiguously: workgroups are dispatched
+    // round-robin over the 8 XCDs, and all query blocks of a head run on one
+    // XCD, so that head's K/V tiles are shared in one L2.
+    const int nqb = div_up(S, AQ);
+    const int nwg = nqb * BH;
+    int logical;
+    {
+        const int bid = blockIdx.x, xcd = bid & 7, local = bid >> 3, per = nwg >> 3, extra = nwg & 7;
+        logical = (xcd < extra) ? xcd * (per + 1) + local : extra * (per + 1) + (xcd - extra) * per + local;
+    }
+    const int h = logical / nqb;
+    const int qb = logical % nqb;
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int half = lane >> 5;
     const int nkt = div_up(S, KTILE);
-    const int q_idx = qb * QBLK + wave * 32 + l32;
+    const int q_idx = qb * AQ + wave * 32 + l32;
 
     // Q fragments: lane's query row, bytes [half*D/2, half*D/2 + D/2).
     v4i qf[C::KSTEPS];
@@ -360,52 +410,49 @@ __global__ __launch_bounds__(256, 2) void sage_attn_kernel(
 #pragma unroll
         for (int s = 0; s < C::KSTEPS; ++s) qf[s] = reinterpret_cast<const v4i*>(qp)[s];
     }
+    // Q scale of the reference's per-thread group (128-token blocks of 32 groups)
     const int nq = div_up(S, QBLK) * 32;
-    const float qsc = q_scale[static_cast<int64_t>(h) * nq + (q_idx / QBLK) * 32 +
-                              ((q_idx % QBLK) / 32) * 8 + (q_idx & 7)];
+    const int qs_idx = q_idx < S ? q_idx : S - 1;
+    const float qsc = q_scale[static_cast<int64_t>(h) * nq + (qs_idx / QBLK) * 32 +
+                              ((qs_idx % QBLK) / 32) * 8 + (qs_idx & 7)];
     const float* ksh = k_scale + static_cast<int64_t>(h) * (nkt * 4);
 
     int kt_end = nkt;
     if (CAUSAL) {
-        const int lim = (qb + 1) * QBLK < S ? (qb + 1) * QBLK : S;
+        const int lim = (qb + 1) * AQ < S ? (qb + 1) * AQ : S;
         kt_end = div_up(lim, KTILE);
     }
 
     const int8_t* Kh = K + static_cast<int64_t>(h) * S * D;
     const uint16_t* Vh = Vt + static_cast<int64_t>(h) * nkt * D * KTILE;
 
-    // cooperative tile copies (global -> registers -> LDS)
-    v4i kreg[C::K_PER_THR], vreg[C::V_PER_THR];
-    auto load_tile = [&](int kt) {
+    // DMA of tile kt into ring slot `slot`: instruction j of the tile (1 KB)
+    // is issued by wave j % 8; tiles past the end re-fetch the last tile
+    // into an idle slot, so every wave issues the same count per tile.
+    auto issue_tile = [&](int kt, int slot) {
+        kt = kt < kt_end ? kt : kt_end - 1;
+        uint8_t* base = lds + slot * C::STAGE;
 #pragma unroll
-        for (int i = 0; i < C::K_PER_THR; ++i) {
-            const int pc = tid + 256 * i;
-            const int key = pc / (D / 16);
-            const int c = pc % (D / 16);
-            const int tok = kt * KTILE + key;
-            kreg[i] = (v4i){0, 0, 0, 0};
-            if (tok < S) kreg[i] = reinterpret_cast<const v4i*>(Kh + static_cast<int64_t>(tok) * D)[c];
-        }
-        const v4i* vsrc = reinterpret_cast<const v4i*>(Vh + static_cast<int64_t>(kt) * D * KTILE);
-#pragma unroll
-        for (int i = 0; i < C::V_PER_THR; ++i) vreg[i] = vsrc[tid + 256 * i];
-    };
-    auto store_tile = [&](int buf) {
-        uint8_t* base = lds + buf * C::STAGE;
-#pragma unroll
-        for (int i = 0; i < C::K_PER_THR; ++i) {
-            const int pc = tid + 256 * i;
-            const int key = pc / (D / 16);
-            const int c = pc % (D / 16);
-            *reinterpret_cast<v4i*>(base + key * C::KROW + c * 16) = kreg[i];
-        }
-        uint8_t* vb = base + C::K_BYTES;
-#pragma unroll
-        for (int i = 0; i < C::V_PER_THR; ++i) {
-            const int pc = tid + 256 * i;
-            const int d = pc / 8;
-            const int c = pc % 8;
-            *reinterpret_cast<v4i*>(vb + d * C::VROW + c * 16) = vreg[i];
+        for (int i = 0; i < C::PER_WAVE; ++i) {
+            int j = wave + AWAVES * i;
+            j = j < C::NI ? j : j - AWAVES;  // a duplicate of this wave's previous piece
+            if (j < C::K_INSTR) {
+                constexpr int RPI = 1024 / D;  // K rows per instruction
+                const int row = j * RPI + lane / C::K_CPR;
+                const int chunk = swz_chunk<C::K_CPR>(row, lane % C::K_CPR);
+                int tok = kt * KTILE + row;
+                tok = tok < S ? tok : S - 1;  // rows past S are loaded but masked
+                __builtin_amdgcn_global_load_lds(
+                    (attn_gbl_ptr_t)(Kh + static_cast<int64_t>(tok) * D + chunk * 16),
+                    (attn_lds_ptr_t)(base + j * 1024), 16, 0, 0);
+            } else {
+                const int jj = j - C::K_INSTR;
+                const int row = jj * 8 + (lane >> 3);  // d row of V^T
+                const int chunk = swz_chunk<8>(row, lane & 7);
+                __builtin_amdgcn_global_load_lds(
+                    (attn_gbl_ptr_t)(Vh + (static_cast<int64_t>(kt) * D + row) * KTILE + chunk * 8),
+                    (attn_lds_ptr_t)(base + C::K_BYTES + jj * 1024), 16, 0, 0);
+            }
         }
     };
 
@@ -417,49 +464,72 @@ __global__ __launch_bounds__(256, 2) void sage_attn_kernel(
     float m = -5000000.0f;  // running max (base-2 scaled), as the reference
     float dsum = 0.0f;      // this lane-half's share of the row sum
 
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < ANSLOT - 1; ++p) issue_tile(p, p);
+    attn_wait_vmcnt<C::KEEP>();  // tile 0 has landed
+    __builtin_amdgcn_s_barrier();
 
-    for (int kt = 0; kt < kt_end; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < kt_end;
-        if (more) load_tile(kt + 1);
-
-        const uint8_t* kb_lds = lds + cur * C::STAGE;
+    // One 64-key tile. Fragment reads are issued in batches ahead of the
+    // MFMAs that use them (sched_barrier fences keep each batch together,
+    // so an MFMA waits on a read issued several MFMAs earlier rather than on
+    // the one just before it), and P of group t+1 is computed on the VALU
+    // while the PV MFMAs of group t run. MASKED tiles (the tail past S, and
+    // for causal the tiles that reach the block's diagonal) evaluate the
+    // per-key validity; the others skip it.
+    auto step = [&](int kt, auto masked_c) {
+        constexpr bool MASKED = decltype(masked_c)::value;
+        issue_tile(kt + ANSLOT - 1, (kt + ANSLOT - 1) % ANSLOT);
+        const uint8_t* kb_lds = lds + (kt % ANSLOT) * C::STAGE;
         const uint8_t* vb_lds = kb_lds + C::K_BYTES;
+        __builtin_amdgcn_sched_barrier(0);
 
-        // S^T blocks: keys 32*kb + (8*(r/4) + 4*half + r%4), query l32.
+        // ---- S^T = K Q^T: blocks of keys 32*kb + (8*(r/4) + 4*half + r%4), query l32
+        v4i kf[2 * C::KSTEPS];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int row = kb * 32 + l32;
+#pragma unroll
+            for (int s = 0; s < C::KSTEPS; ++s) {
+                const int chunk = swz_chunk<C::K_CPR>(row, half * C::KSTEPS + s);
+                kf[kb * C::KSTEPS + s] = *reinterpret_cast<const v4i*>(kb_lds + row * D + chunk * 16);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
         v16i sacc[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0;
-            const uint8_t* krow = kb_lds + (kb * 32 + l32) * C::KROW + half * (D / 2);
 #pragma unroll
-            for (int s = 0; s < C::KSTEPS; ++s) {
-                const v4i kf = *reinterpret_cast<const v4i*>(krow + 16 * s);
-                sacc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[s], sacc[kb], 0, 0, 0);
-            }
+            for (int s = 0; s < C::KSTEPS; ++s)
+                sacc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[kb * C::KSTEPS + s], qf[s], sacc[kb], 0, 0, 0);
         }
+        // first V fragments (groups 0 and 1) are read while QK^T runs
+        v8h vf[2][C::DT];
+        auto read_v = [&](int t, v8h* dst) {
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) {
+                const int row = dt * 32 + l32;
+                const int chunk = swz_chunk<8>(row, 2 * t + half);
+                dst[dt] = *reinterpret_cast<const v8h*>(vb_lds + row * (2 * KTILE) + chunk * 16);
+            }
+        };
+        read_v(0, vf[0]);
+        read_v(1, vf[1]);
 
-        // Per-lane multipliers: key group g = (key % 8) / 2 = 2*half + (r%4)/2.
+        // ---- softmax statistics of the tile
         const float4 ks4 = *reinterpret_cast<const float4*>(ksh + kt * 4);
         const float ks_lo = half ? ks4.z : ks4.x;
         const float ks_hi = half ? ks4.w : ks4.y;
         const float mul_lo = sm_log2 * (qsc * ks_lo);
         const float mul_hi = sm_log2 * (qsc * ks_hi);
-
-        // validity of each key slot (tail tile / causal diagonal)
         const int kbase = kt * KTILE;
-        const bool need_mask = (kbase + KTILE > S) || (CAUSAL && kbase + KTILE - 1 > qb * QBLK);
         auto key_ok = [&](int kb, int r) {
             const int key = kbase + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
             bool ok = key < S;
             if (CAUSAL) ok = ok && key <= q_idx;
             return ok;
         };
-
         // tile max: integer max per scale group, then one multiply each
         // (max of fl(acc*c) equals fl(max(acc)*c) for c > 0).
         int mx_lo = INT32_MIN, mx_hi = INT32_MIN;
@@ -468,7 +538,9 @@ __global__ __launch_bounds__(256, 2) void sage_attn_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 int a = sacc[kb][r];
-                if (need_mask && !key_ok(kb, r)) a = INT32_MIN;
+                if constexpr (MASKED) {
+                    if (!key_ok(kb, r)) a = INT32_MIN;
+                }
                 if ((r & 2) == 0) mx_lo = max(mx_lo, a);
                 else mx_hi = max(mx_hi, a);
             }
@@ -476,50 +548,79 @@ __global__ __launch_bounds__(256, 2) void sage_attn_kernel(
         if (mx_lo != INT32_MIN) mt = fmaxf(mt, static_cast<float>(mx_lo) * mul_lo);
         if (mx_hi != INT32_MIN) mt = fmaxf(mt, static_cast<float>(mx_hi) * mul_hi);
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float m_new = fmaxf(m, mt);
+        // Lazy rescale: the reference max m moves (and O, d are rescaled) only
+        // when the tile max exceeds it by more than kRescaleSlack (log2
+        // units). Otherwise P = exp2(s - m) <= 2^kRescaleSlack, exact in fp16
+        // range; O and d use the same m, so O/d is unchanged in exact
+        // arithmetic and only the fp16 rounding points of P shift.
+        const bool bump = mt > m + kRescaleSlack;
+        const float m_new = bump ? mt : m;
         const float o_scale = __builtin_amdgcn_exp2f(m - m_new);
         m = m_new;
-        dsum *= o_scale;
+        // Lanes that did not move multiply by exactly 1.
+        if (__ballot(bump)) {
+            dsum *= o_scale;
 #pragma unroll
-        for (int t = 0; t < C::DT; ++t)
+            for (int t = 0; t < C::DT; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[t][r] *= o_scale;
+                for (int r = 0; r < 16; ++r) o[t][r] *= o_scale;
+        }
 
-        // P = exp2(acc * mult - m) -> fp16, as PV B-operand fragments.
+        // ---- P = exp2(acc * mult - m) -> fp16 (round to nearest, in pairs)
+        // per 16-key group t, and O^T += V^T P^T for that group. The row sum
+        // of the fp16 P is accumulated in fp32 with v_dot2_f32_f16.
         const float neg_m = -m_new;
-        v8h pf[4];
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+        auto make_p = [&](int t) {
+            const int kb = t >> 1;
+            v8h pt;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
+            for (int e = 0; e < 8; e += 2) {
+                const int r = 8 * (t & 1) + e;
                 const float mul = (r & 2) ? mul_hi : mul_lo;
-                float p = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(sacc[kb][r]), mul, neg_m));
-                if (need_mask && !key_ok(kb, r)) p = 0.0f;
-                pf[2 * kb + (r >> 3)][r & 7] = static_cast<_Float16>(p);
+                float p0 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(sacc[kb][r]), mul, neg_m));
+                float p1 = __builtin_amdgcn_exp2f(fmaf(static_cast<float>(sacc[kb][r + 1]), mul, neg_m));
+                if constexpr (MASKED) {
+                    if (!key_ok(kb, r)) p0 = 0.0f;
+                    if (!key_ok(kb, r + 1)) p1 = 0.0f;
+                }
+                const h2 ph = __builtin_convertvector((f2){p0, p1}, h2);
+                pt[e] = ph.x;
+                pt[e + 1] = ph.y;
+                dsum = __builtin_amdgcn_fdot2(ph, ones, dsum, false);
             }
-        // row-sum share of the fp16-rounded P (fp32 accumulate)
+            return pt;
+        };
+        v8h p_cur = make_p(0);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            float part = 0.0f;
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) part += static_cast<float>(pf[t][e]);
-            dsum += part;
+            for (int dt = 0; dt < C::DT; ++dt)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t & 1][dt], p_cur, o[dt], 0, 0, 0);
+            if (t + 2 < 4) read_v(t + 2, vf[t & 1]);
+            if (t + 1 < 4) p_cur = make_p(t + 1);
         }
+        __builtin_amdgcn_sched_barrier(0);
 
-        // O^T += V^T P^T over the tile's four 16-key groups.
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int dt = 0; dt < C::DT; ++dt) {
-                const v8h vf = *reinterpret_cast<const v8h*>(vb_lds + (dt * 32 + l32) * C::VROW +
-                                                              (16 * t + 8 * half) * 2);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[t], o[dt], 0, 0, 0);
-            }
-        }
+        // hand-off: this wave's reads of slot kt are done and its share of
+        // tile kt+1 has landed; the barrier makes every wave's share visible
+        // and frees slot kt for the DMA issued at the start of step kt+1.
+        attn_wait_vmcnt_lgkm0<C::KEEP>();
+        __builtin_amdgcn_s_barrier();
+    };
 
-        if (more) store_tile(cur ^ 1);
-        __syncthreads();
-    }
+    // Tiles wholly inside [0, S) (and, for causal, wholly below the block's
+    // first query) need no masking.
+    int kt_full = S / KTILE;
+    if (CAUSAL) kt_full = min(kt_full, (qb * AQ) / KTILE);
+    kt_full = min(kt_full, kt_end);
+    int kt = 0;
+    for (; kt < kt_full; ++kt) step(kt, std::false_type{});
+    for (; kt < kt_end; ++kt) step(kt, std::true_type{});
+    attn_wait_vmcnt<0>();  // drain the re-fetches issued by the last steps
 
     // combine the two lane-halves' row sums, normalise, store.
     const float dtot = dsum + __shfl_xor(dsum, 32, 64);
@@ -565,16 +666,17 @@ template <int D, bool CAUSAL>
 hipError_t launch_attn_dt(const int8_t* q, const int8_t* k, const uint16_t* vt, const float* qs,
                           const float* ks, void* out, int out_dt, int BH, int S, float sm_log2,
                           hipStream_t stream) {
-    dim3 grid(div_up(S, QBLK), BH);
+    const dim3 grid(div_up(S, AQ) * BH);
+    const dim3 block(AQ * 2);
     if (out_dt == QIMG_FP16)
-        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_FP16>), grid, dim3(256), 0, stream, q, k,
-                           vt, qs, ks, out, S, sm_log2);
+        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_FP16>), grid, block, 0, stream, q, k, vt, qs, ks,
+                           out, S, BH, sm_log2);
     else if (out_dt == QIMG_FP32)
-        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_FP32>), grid, dim3(256), 0, stream, q, k,
-                           vt, qs, ks, out, S, sm_log2);
+        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_FP32>), grid, block, 0, stream, q, k, vt, qs, ks,
+                           out, S, BH, sm_log2);
     else
-        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_BF16>), grid, dim3(256), 0, stream, q, k,
-                           vt, qs, ks, out, S, sm_log2);
+        hipLaunchKernelGGL((sage_attn_kernel<D, CAUSAL, QIMG_BF16>), grid, block, 0, stream, q, k, vt, qs, ks,
+                           out, S, BH, sm_log2);
     return hipGetLastError();
 }
 
