@@ -190,3 +190,21 @@ def test_dequantize_and_bias_matches_oracle_and_fused(qimg, oracle):
     np.testing.assert_array_equal(got_g.cpu().numpy(), fused_g.cpu().numpy())
     np.testing.assert_allclose(got_g.cpu().numpy(), oracle.dequant_epilogue(c, s, ws, b_bits, gelu=True),
                                rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("M,N,K", [(3328, 2560, 128), (3328, 2560, 320), (4352, 3072, 1024)])
+def test_int8_gemm_partial_round_shapes_exact(qimg, oracle, M, N, K):
+    """Tile counts that do not fill whole rounds of the 256 CUs (130 and 204
+    tiles), with short and long K: exact, and identical on repeated calls."""
+    rng = np.random.default_rng(M + N + K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    qw = _qw(qimg, w, np.ones(N, np.float32), 1)
+    ad, ones_m = _dev(a), _dev(np.ones(M, np.float32))
+    out1 = qimg.linear_forward_prequantized(ad, ones_m, qw)
+    out2 = qimg.linear_forward_prequantized(ad, ones_m, qw)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    idx = np.unique(np.concatenate([[0, M - 1], np.arange(0, M, 97), rng.integers(0, M, 40)]))
+    ref = (a[idx].astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    np.testing.assert_array_equal(out1.cpu().numpy()[idx], ref)
