@@ -16,7 +16,8 @@ Also printed in the same JSON line:
   cpu_baseline the CPU oracle (oracle/qimg_oracle.c, OpenMP) running the same
                MLP pair on the host cores
   extra        single linear (M=4096, 3072x3072), SageAttention (24 heads,
-               S=4352, D=128) and activation-quant bandwidth
+               S=4352, D=128), activation-quant bandwidth, and the small-M
+               linears (modulation M=1/2 as HBM GB/s, text-stream M=256)
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -228,6 +229,27 @@ def _time(torch, fn, iters=10, warm=3):
     return float(sorted(ts)[len(ts) // 2])
 
 
+def _time_cycle(torch, fns, iters=10, warm=2):
+    """Median per-call time of `fns` run back to back in turn (one event pair
+    around each full cycle), so that calls of a few microseconds are not
+    dominated by event overhead."""
+    for _ in range(warm):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    ts = []
+    for _ in range(iters):
+        e0.record()
+        for f in fns:
+            f()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) / len(fns))
+    return float(sorted(ts)[len(ts) // 2])
+
+
 def _extra(q, torch, dev):
     out = {}
     g = torch.Generator(device="cpu").manual_seed(0)
@@ -266,6 +288,44 @@ def _extra(q, torch, dev):
     out["sage_c3_tflops"] = round(flops / ms_att / 1e9, 1)
     out["sage_c3_attn_kernel_tflops"] = round(flops / ms_core / 1e9, 1)
     out["sage_c3_frac_of_mixed_peak"] = round(flops / ms_att / 1e9 / 3355.0, 4)
+    # Small M: modulation (M = 1, and 2 rows for a CFG pair; 18432 x 3072)
+    # and text-stream linears (M = 256). HBM bytes = int8 weights + scales +
+    # bias + activations + fp32 outputs, each once. Each call uses the next
+    # of several weight copies (> 600 MB in all), so weights come from HBM
+    # and not from the 256 MB last-level cache, as in a forward pass.
+    for tag, (M, N, K, gelu) in {"mod_m1": (1, 18432, 3072, False), "mod_m2": (2, 18432, 3072, False),
+                                 "txt_qkv_m256": (256, 3072, 3072, False),
+                                 "txt_fc1_m256": (256, 12288, 3072, True),
+                                 "txt_fc2_m256": (256, 3072, 12288, False)}.items():
+        x = torch.randn(M, K, generator=g).to(dev)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        b = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+        qw0 = q.quantize_weight_tensor(w)
+        del w
+        copies = max(2, -(-600_000_000 // (N * K)))
+        qws = [q.QuantizedWeight(qw0.data.clone(), qw0.scales.clone(), qw0.had_block_size, qw0.mode)
+               for _ in range(copies)]
+        o32 = torch.empty(M, N, device=dev)
+        scratch = torch.empty(q.int8_scratch_bytes(M, K, N), dtype=torch.uint8, device=dev)
+        aq, asc = q.quantize_activation_hadamard(x, qw0.had_block_size)
+
+        def gemm(qw):
+            return lambda: q.linear_forward_prequantized(aq, asc, qw, b, apply_gelu=gelu, out=o32)
+
+        def lin(qw):
+            return lambda: q.linear_forward_quantized(x, qw, b, out=o32, scratch=scratch, apply_gelu=gelu)
+
+        ms_g = _time_cycle(torch, [gemm(w_) for w_ in qws])
+        ms_l = _time_cycle(torch, [lin(w_) for w_ in qws])
+        with q.linear_kernel(q.LINEAR_LARGE_TILE):
+            ms_big = _time_cycle(torch, [gemm(w_) for w_ in qws])
+        nbytes = N * K + 4 * N + 2 * N + M * K + 4 * M + 4 * M * N
+        out[f"{tag}_gemm_us"] = round(ms_g * 1e3, 2)
+        out[f"{tag}_gemm_gbs"] = round(nbytes / ms_g / 1e6, 1)
+        out[f"{tag}_gemm_tops"] = round(2.0 * M * N * K / ms_g / 1e9, 1)
+        out[f"{tag}_linear_us"] = round(ms_l * 1e3, 2)
+        out[f"{tag}_large_tile_gemm_us"] = round(ms_big * 1e3, 2)
+        del qws, qw0
     return out
 
 

@@ -107,6 +107,22 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
                              const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                              void* stream);
 
+/* Kernel selection for qimg_linear_prequantized / qimg_linear when K is a
+ * multiple of 64. No counterpart in the reference (cuBLAS picks its own
+ * algorithm); it exists for tests and tuning, which compare the kernels on
+ * one shape. AUTO (the default) takes 32x32 tiles for M <= 32, 64x64 tiles
+ * when fewer than 128 tiles of 256x256 would cover the output, and 256x256
+ * tiles otherwise. Process-wide; returns QIMG_OK, or QIMG_ERR_INVALID_ARG for
+ * an unknown value. All choices give identical int8 results. */
+enum {
+    QIMG_LINEAR_AUTO = 0,
+    QIMG_LINEAR_LARGE_TILE = 1,
+    QIMG_LINEAR_SMALL_32 = 2,
+    QIMG_LINEAR_SMALL_64 = 3
+};
+int qimg_set_linear_kernel(int which);
+int qimg_get_linear_kernel(void);
+
 /* dequantize_and_bias / dequantize_bias_gelu (cuda_kernels.cuh:282-291,
  * cuda_kernels.cu:2623-2668): out[m,n] = acc[m,n] * act_scale[m] * w_scale[n]
  * + bias[n] (then GELU-tanh if gelu != 0), acc int32 [M,N], out fp32 [M,N],

@@ -162,6 +162,17 @@ int qimg_dequantize_bias(const int32_t* acc, const float* act_scales, const floa
                       fn);
 }
 
+int qimg_set_linear_kernel(int which) {
+    QIMG_REQUIRE(which >= QIMG_LINEAR_AUTO && which <= QIMG_LINEAR_SMALL_64,
+                 "qimg_set_linear_kernel: unknown kernel choice %d", which);
+    qimg::set_linear_kernel(which);
+    return QIMG_OK;
+}
+
+int qimg_get_linear_kernel(void) {
+    return qimg::get_linear_kernel();
+}
+
 int qimg_linear(const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales, int N,
                 int hbs, int mode, const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                 void* scratch, int64_t scratch_bytes, void* stream) {

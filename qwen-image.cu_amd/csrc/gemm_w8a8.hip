@@ -36,6 +36,8 @@
 // chunks 2h, 2h+1; int8 k-step s uses chunk 2h+s (16 bytes), e4m3 uses both
 // (32 bytes, one k-step). Both operands use the same assignment, so each dot
 // product covers every k exactly once and the int8 result is exact.
+#include <atomic>
+
 #include "qimg_device.h"
 #include "qimg_internal.h"
 
@@ -87,17 +89,6 @@ template <int n>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(n >= 0 && n < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((0x0f70 & ~0xc00f) | (n & 15) | ((n >> 4) << 14));
-}
-
-// Map the hardware workgroup id so that each XCD (workgroups are dispatched
-// round-robin over 8 XCDs) receives a contiguous range of logical tiles,
-// which keeps the tiles that share operand rows in one L2.
-__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
-    const int xcd = bid & 7;
-    const int local = bid >> 3;
-    const int per = nwg >> 3;
-    const int extra = nwg & 7;
-    return (xcd < extra) ? xcd * (per + 1) + local : extra * (per + 1) + (xcd - extra) * per + local;
 }
 
 template <bool FP8>
@@ -544,6 +535,11 @@ hipError_t dispatch_tiled(const void* a, const float* as, int M, int K, const vo
 
 }  // namespace
 
+static std::atomic<int> g_linear_kernel{QIMG_LINEAR_AUTO};
+
+int set_linear_kernel(int which) { return g_linear_kernel.exchange(which); }
+int get_linear_kernel() { return g_linear_kernel.load(); }
+
 hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
                               float* out, int M, int N, int gelu, hipStream_t stream) {
     const int64_t total = static_cast<int64_t>(M) * N;
@@ -561,6 +557,13 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
                                       hipStream_t stream) {
     if (M == 0 || N == 0) return hipSuccess;
     const bool fp8 = (mode == QIMG_QM_FP8_HADAMARD);
+    const int choice = g_linear_kernel.load(std::memory_order_relaxed);
+    int small = small_m_variant(M, N, K);
+    if ((K % BK) == 0 && choice != QIMG_LINEAR_AUTO)
+        small = choice == QIMG_LINEAR_SMALL_32 ? 1 : choice == QIMG_LINEAR_SMALL_64 ? 2 : 0;
+    if (small != 0)
+        return launch_linear_small_m(act_q, act_scales, M, K, w_q, w_scales, N, mode, bias, out, out_dtype, gelu,
+                                     small, stream);
     if ((K % BK) == 0) {
         return fp8 ? dispatch_tiled<true>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
                                           out_dtype, gelu, stream)

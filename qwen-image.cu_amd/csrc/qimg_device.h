@@ -76,6 +76,17 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
     return s | out;
 }
 
+// Map the hardware workgroup id so that each XCD (workgroups are dispatched
+// round-robin over 8 XCDs) receives a contiguous range of logical tiles,
+// which keeps the tiles that share operand rows in one L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
+    const int xcd = bid & 7;
+    const int local = bid >> 3;
+    const int per = nwg >> 3;
+    const int extra = nwg & 7;
+    return (xcd < extra) ? xcd * (per + 1) + local : extra * (per + 1) + (xcd - extra) * per + local;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll
@@ -114,6 +125,21 @@ __device__ __forceinline__ float gelu_tanh(float v) {
     const float c = 0.7978845608f;
     float inner = c * (v + 0.044715f * v * v * v);
     return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+// Dequant epilogue of one output element, in the reference's order
+// (cuda_kernels.cu:2623-2668): acc * act_scale * w_scale, then + bias, each
+// step rounded (no contraction), then GELU-tanh.
+template <bool GELU>
+__device__ __forceinline__ float dequant_elem(float acc, float sa, float sw, bool has_bias, float b) {
+    float t;
+    {
+#pragma clang fp contract(off)
+        t = acc * sa * sw;
+        if (has_bias) t = t + b;
+    }
+    if (GELU) t = gelu_tanh_fast(t);
+    return t;
 }
 
 }  // namespace qimg

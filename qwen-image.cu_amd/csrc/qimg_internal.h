@@ -24,6 +24,18 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
 hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
                               float* out, int M, int N, int gelu, hipStream_t stream);
 
+// Kernel selection override for the quantized linear (QIMG_LINEAR_*);
+// returns the previous setting.
+int set_linear_kernel(int which);
+int get_linear_kernel();
+
+// gemm_small_m.hip: 0 = use the large-tile kernel, 1 = 32x32 tiles
+// (M <= 32), 2 = 64x64 tiles (few large tiles)
+int small_m_variant(int M, int N, int K);
+hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int M, int K, const void* w_q,
+                                 const float* w_scales, int N, int mode, const uint16_t* bias, void* out,
+                                 int out_dtype, int gelu, int variant, hipStream_t stream);
+
 // sage_attention.hip
 struct SageScratch {
     int8_t* q_i8;

@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libqimg_hot.so")
 QIMG_OK, QIMG_ERR_INVALID_ARG, QIMG_ERR_UNSUPPORTED, QIMG_ERR_SCRATCH, QIMG_ERR_HIP = range(5)
 FP32, BF16, FP16, INT8, INT32, FP8_E4M3 = range(6)
 INT8_HADAMARD, FP8_HADAMARD = 0, 1
+LINEAR_AUTO, LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64 = range(4)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -39,6 +40,8 @@ _SIGS = {
     "qimg_quantize_weight": (_I, [_P, _I, _I, _I, _I, _P, _P, ctypes.POINTER(_I), _P]),
     "qimg_linear_prequantized": (_I, [_P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _I, _P]),
     "qimg_dequantize_bias": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "qimg_set_linear_kernel": (_I, [_I]),
+    "qimg_get_linear_kernel": (_I, []),
     "qimg_linear": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I64, _P]),
     "qimg_sage_scratch_bytes": (_I64, [_I, _I, _I]),
     "qimg_sage_k_mean": (_I, [_P, _P, _I, _I, _I, _P]),
@@ -184,6 +187,31 @@ def linear_forward_prequantized(act_q: torch.Tensor, act_scales: torch.Tensor, w
                                          _ptr(weight.scales), N, int(weight.mode), _ptr(bias), _ptr(out),
                                          _DT[out.dtype], int(bool(apply_gelu)), _stream()))
     return out
+
+
+def set_linear_kernel(which: int) -> int:
+    """Select the quantized-linear kernel process-wide (LINEAR_AUTO,
+    LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64); returns the
+    previous choice. Every choice gives the same int8 results."""
+    prev = int(_lib.qimg_get_linear_kernel())
+    _check(_lib.qimg_set_linear_kernel(int(which)))
+    return prev
+
+
+class linear_kernel:
+    """Context manager: run the enclosed linears with one kernel choice."""
+
+    def __init__(self, which: int):
+        self.which = which
+        self.prev = None
+
+    def __enter__(self):
+        self.prev = set_linear_kernel(self.which)
+        return self
+
+    def __exit__(self, *exc):
+        set_linear_kernel(self.prev)
+        return False
 
 
 def dequantize_and_bias(acc: torch.Tensor, act_scales: torch.Tensor, w_scales: torch.Tensor,

@@ -37,19 +37,28 @@ def _qw(qimg, q, s, hbs, mode=0):
     return qimg.QuantizedWeight(_dev(q), _dev(s), hbs, mode)
 
 
+KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3}
+
+
+@pytest.mark.parametrize("kernel", list(KERNELS))
 @pytest.mark.parametrize("M,N,K", [
     (256, 256, 64), (1, 64, 64), (7, 300, 192), (300, 7, 128), (256, 256, 128), (129, 384, 384),
     (513, 520, 3072),
     (257, 255, 1024), (64, 3072, 3072), (4096, 3072, 3072),
 ])
-def test_int8_gemm_exact(qimg, oracle, M, N, K):
+def test_int8_gemm_exact(qimg, oracle, M, N, K, kernel):
+    """Every kernel choice gives the exact int32 product (fp32 out with unit
+    scales is fl(acc))."""
+    if kernel == "small32" and M * N > 2 ** 22:
+        pytest.skip("32x32 tiles at this size only repeat the small-shape cases")
     rng = np.random.default_rng(M + 3 * N + 7 * K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
     w = rng.integers(-128, 128, (N, K), dtype=np.int8)
     ones_m = np.ones(M, np.float32)
     ones_n = np.ones(N, np.float32)
     rows = (0, M) if M * N * K <= 2 ** 31 else None
-    out = qimg.linear_forward_prequantized(_dev(a), _dev(ones_m), _qw(qimg, w, ones_n, 1))
+    with qimg.linear_kernel(KERNELS[kernel]):
+        out = qimg.linear_forward_prequantized(_dev(a), _dev(ones_m), _qw(qimg, w, ones_n, 1))
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     if rows is None:  # full-size: check a sample of rows
@@ -208,3 +217,71 @@ def test_int8_gemm_partial_round_shapes_exact(qimg, oracle, M, N, K):
     idx = np.unique(np.concatenate([[0, M - 1], np.arange(0, M, 97), rng.integers(0, M, 40)]))
     ref = (a[idx].astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
     np.testing.assert_array_equal(out1.cpu().numpy()[idx], ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 18432, 3072), (1, 3072, 256), (2, 18432, 3072), (17, 3072, 3072),
+                                   (256, 3072, 3072), (256, 12288, 3072), (256, 3072, 12288)])
+def test_small_m_shapes_exact(qimg, oracle, M, N, K):
+    """The step-level and text-stream shapes: modulation (M = 1 or 2 CFG rows,
+    N = 18432), the timestep MLP (K = 256), text linears (M = 256). The int32
+    product is exact against float64 (|acc| < 2^53) under the automatic
+    choice and under the large-tile kernel."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    ref = (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+    ad, wd = _dev(a), _qw(qimg, w, np.ones(N, np.float32), 1)
+    sd = _dev(np.ones(M, np.float32))
+    got_auto = qimg.linear_forward_prequantized(ad, sd, wd)
+    with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
+        got_large = qimg.linear_forward_prequantized(ad, sd, wd)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got_auto.cpu().numpy(), ref)
+    np.testing.assert_array_equal(got_large.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,gelu", [(1, 18432, 3072, False), (1, 3072, 256, True), (256, 3072, 3072, False),
+                                        (256, 12288, 3072, True), (40, 200, 12288, False)])
+def test_small_m_linear_matches_oracle(qimg, oracle, M, N, K, gelu):
+    """Full linear (activation FWHT + quant, GEMM, dequant epilogue) at the
+    small-M shapes: fp32 out bit-exact against the oracle without GELU and
+    within 2e-6 with it; bf16 out is the RNE rounding of the fp32 out."""
+    rng = np.random.default_rng(M + N * 3 + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    wq, ws, hbs = oracle.quantize_weight_bf16(w_bits)
+    ref = oracle.linear_w8a8(x, wq, ws, hbs, b_bits, gelu=gelu)
+    qw = _qw(qimg, wq, ws, hbs)
+    out = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits), apply_gelu=gelu)
+    o16 = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits), apply_gelu=gelu, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    if gelu:
+        np.testing.assert_allclose(got, ref, rtol=2e-6, atol=2e-6)
+    else:
+        np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(o16.float().cpu().numpy(),
+                                  oracle.bf16_bits_to_f32(oracle.bf16_bits_from_f32(got)).reshape(M, N))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 18432, 3072), (256, 3072, 3072), (9, 100, 12288)])
+def test_small_m_fp8(qimg, oracle, M, N, K):
+    """e4m3 at small M: the oracle's float64 sum of the exact e4m3 products,
+    within the fp32 accumulation-order bound; the small and large kernels
+    agree to the same bound."""
+    rng = np.random.default_rng(M + N + K + 5)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    wq, ws, hbs = oracle.quantize_weight_fp8(w_bits)
+    xq, xs = oracle.quantize_activation_fp8(x, hbs)
+    ref = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, rows=(0, M))
+    qw = _qw(qimg, wq, ws, hbs, mode=qimg.FP8_HADAMARD)
+    got = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits))
+    with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
+        got_l = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits))
+    torch.cuda.synchronize()
+    bound = 1e-5 * np.abs(ref).max() * np.sqrt(K / 64)
+    assert np.max(np.abs(got.cpu().numpy() - ref)) <= bound
+    assert np.max(np.abs(got_l.cpu().numpy() - ref)) <= bound
