@@ -213,41 +213,40 @@ def _calib_copy(torch):
     print(json.dumps({"calib_copy_bytes": n, "copies": 5}))
 
 
-def _time(torch, fn, iters=10, warm=3):
-    for _ in range(warm):
-        fn()
+def _time_cycle(torch, fns, iters=10, min_calls=20):
+    """Median GPU time per call of `fns` (run in turn): the calls are captured
+    into one HIP graph (at least `min_calls` calls) and the graph is replayed
+    between two events, so host launch overhead is not part of the figure."""
+    reps = max(1, -(-min_calls // len(fns)))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            for f in fns:
+                f()
+    graph.replay()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     ts = []
     for _ in range(iters):
         e0.record()
-        fn()
+        graph.replay()
         e1.record()
         e1.synchronize()
-        ts.append(e0.elapsed_time(e1))
+        ts.append(e0.elapsed_time(e1) / (reps * len(fns)))
+    del graph
     return float(sorted(ts)[len(ts) // 2])
 
 
-def _time_cycle(torch, fns, iters=10, warm=2):
-    """Median per-call time of `fns` run back to back in turn (one event pair
-    around each full cycle), so that calls of a few microseconds are not
-    dominated by event overhead."""
-    for _ in range(warm):
-        for f in fns:
-            f()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    ts = []
-    for _ in range(iters):
-        e0.record()
-        for f in fns:
-            f()
-        e1.record()
-        e1.synchronize()
-        ts.append(e0.elapsed_time(e1) / len(fns))
-    return float(sorted(ts)[len(ts) // 2])
+def _time(torch, fn, iters=10):
+    return _time_cycle(torch, [fn], iters=iters)
 
 
 def _extra(q, torch, dev):
@@ -319,6 +318,9 @@ def _extra(q, torch, dev):
         ms_l = _time_cycle(torch, [lin(w_) for w_ in qws])
         with q.linear_kernel(q.LINEAR_LARGE_TILE):
             ms_big = _time_cycle(torch, [gemm(w_) for w_ in qws])
+        if M <= 32:
+            with q.linear_kernel(q.LINEAR_SMALL_32):
+                out[f"{tag}_mfma32_gemm_us"] = round(_time_cycle(torch, [gemm(w_) for w_ in qws]) * 1e3, 2)
         nbytes = N * K + 4 * N + 2 * N + M * K + 4 * M + 4 * M * N
         out[f"{tag}_gemm_us"] = round(ms_g * 1e3, 2)
         out[f"{tag}_gemm_gbs"] = round(nbytes / ms_g / 1e6, 1)

@@ -17,7 +17,8 @@
 //    lane (row r = lane%32, half h = lane/32) of a 32-row block reads the 32
 //    contiguous bytes [64*kb + 32*h, +32) of its row for 64-byte K block kb.
 //    No LDS staging and no barriers in the main loop; each wave keeps DEPTH
-//    K blocks of loads in flight.
+//    K blocks of loads in flight. Buffer loads with out-of-range offsets
+//    stand in for every bounds check (rows past M or N, blocks past K).
 //  - int8: two v_mfma_i32_32x32x32_i8 per K block (16 bytes each); e4m3: one
 //    v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales (32 bytes). Both
 //    operands use the same K assignment, so each dot product covers every k
@@ -27,7 +28,8 @@
 //    is applied as the tile is stored, with the arithmetic of the large-tile
 //    kernel, so both give identical outputs.
 //
-// Rows past M and columns past N are clamped on load and never stored.
+// Rows past M and columns past N read as zero and are never stored. The
+// byte sizes M*K and N*K must be below 2^31 (buffer offsets are 32-bit).
 #include "qimg_device.h"
 #include "qimg_internal.h"
 
@@ -37,6 +39,8 @@ namespace {
 
 constexpr int SM_THR = 256;  // four waves, one K quarter each
 constexpr int SM_KB = 64;    // bytes of K per block
+// Buffer resource word 3 for gfx9-family raw (unswizzled, unformatted) buffers.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 template <bool FP8>
 struct SmAcc;
@@ -72,23 +76,56 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
     const int r = lane & 31;
     const int h = lane >> 5;
 
-    const int nkb = K / SM_KB;
-    const int kb0 = (nkb * wave) >> 2;
-    const int kb1 = (nkb * (wave + 1)) >> 2;
+    // Epilogue operands of the (row, 4-column run) groups this thread stores
+    // (same mapping as the epilogue below), loaded now so their latency hides
+    // behind the operand stream: clamped indices, and a branch-free bias load
+    // (from ws when there is no bias) so the loads issue together.
+    const bool has_bias = bias != nullptr;
+    const uint16_t* bsrc = has_bias ? bias : reinterpret_cast<const uint16_t*>(ws);
+    float e_as[NBLK], e_ws[NBLK][4];
+    uint16_t e_b[NBLK][4];
+#pragma unroll
+    for (int q = 0; q < NBLK; ++q) {
+        const int idx = threadIdx.x + SM_THR * q;
+        const int blk = idx >> 8;
+        const int m = m0 + 32 * (blk / TNW) + (idx & 31);
+        const int nb = n0 + 32 * (blk % TNW) + 8 * ((idx >> 6) & 3) + 4 * ((idx >> 5) & 1);
+        e_as[q] = as[m < M ? m : M - 1];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int n = nb + c < N ? nb + c : N - 1;
+            e_ws[q][c] = ws[n];
+            e_b[q][c] = bsrc[n];
+        }
+    }
 
-    const uint8_t* pa[TMW];
-    const uint8_t* pw[TNW];
+    // K blocks are dealt round-robin to the waves (block 4t + wave), so the
+    // four waves read adjacent 64-byte pieces of the same rows at the same
+    // time. Operands are read with buffer loads: a lane whose row is past
+    // M or N, or a block past K, gets an offset outside the buffer, which
+    // returns zeros without touching memory. The main loop therefore has no
+    // branches, every wave runs the same number of blocks, and the loads of
+    // DEPTH blocks stay in flight while older blocks are consumed.
+    const int nkb = K / SM_KB;
+    const int T = (nkb + 3) >> 2;
+    const int Tp = ((T + DEPTH - 1) / DEPTH) * DEPTH;
+    constexpr uint32_t kOob = 0x80000000u;  // >= num_records: reads as zero
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(A), 0, M * K, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), 0, N * K, kBufferRsrcWord3);
+    // Row offsets with the out-of-range bit or-ed in for rows past the end
+    // (valid offsets are below 2^31, so the bit alone decides).
+    uint32_t oa[TMW], ow[TNW];
 #pragma unroll
     for (int i = 0; i < TMW; ++i) {
-        int gm = m0 + 32 * i + r;
-        gm = gm < M ? gm : M - 1;
-        pa[i] = A + static_cast<int64_t>(gm) * K + 32 * h;
+        const int gm = m0 + 32 * i + r;
+        oa[i] = (static_cast<uint32_t>(gm) * K + 32 * h) | (gm < M ? 0u : kOob);
     }
 #pragma unroll
     for (int j = 0; j < TNW; ++j) {
-        int gn = n0 + 32 * j + r;
-        gn = gn < N ? gn : N - 1;
-        pw[j] = W + static_cast<int64_t>(gn) * K + 32 * h;
+        const int gn = n0 + 32 * j + r;
+        ow[j] = (static_cast<uint32_t>(gn) * K + 32 * h) | (gn < N ? 0u : kOob);
     }
 
     typedef typename SmAcc<FP8>::type acc_t;
@@ -102,16 +139,24 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
 
     v4i ba[DEPTH][TMW][2];
     v4i bw[DEPTH][TNW][2];
-    auto load = [&](int d, int kb) {
-        const int off = kb * SM_KB;
+    auto load = [&](int d, int t) {
+        const int kb = 4 * t + wave;
+        // block past K: the out-of-range bit (branch-free, wave-uniform)
+        const uint32_t koff = (static_cast<uint32_t>(kb) * SM_KB) | (kb < nkb ? 0u : kOob);
 #pragma unroll
-        for (int i = 0; i < TMW; ++i)
+        for (int i = 0; i < TMW; ++i) {
+            const uint32_t o = (oa[i] + koff) | (oa[i] & kOob) | (koff & kOob);
 #pragma unroll
-            for (int s = 0; s < 2; ++s) ba[d][i][s] = *reinterpret_cast<const v4i*>(pa[i] + off + 16 * s);
+            for (int s = 0; s < 2; ++s)
+                ba[d][i][s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, o + 16 * s, 0, 0));
+        }
 #pragma unroll
-        for (int j = 0; j < TNW; ++j)
+        for (int j = 0; j < TNW; ++j) {
+            const uint32_t o = (ow[j] + koff) | (ow[j] & kOob) | (koff & kOob);
 #pragma unroll
-            for (int s = 0; s < 2; ++s) bw[d][j][s] = *reinterpret_cast<const v4i*>(pw[j] + off + 16 * s);
+            for (int s = 0; s < 2; ++s)
+                bw[d][j][s] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, o + 16 * s, 0, 0));
+        }
     };
     auto compute = [&](int d) {
 #pragma unroll
@@ -134,18 +179,22 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
             }
     };
 
-    // Software pipeline over this wave's K blocks: block kb+d is consumed
-    // from register set d, which is then refilled with block kb+d+DEPTH.
+    // Block t is consumed from register set t % DEPTH, which is then refilled
+    // with block t + DEPTH (past the end: zero-returning loads).
+    // (sched_barrier keeps the prologue in block order: the scheduler would
+    // otherwise issue block 0 last, next to its first use, and the first
+    // wait would then drain every load.)
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-        if (kb0 + d < kb1) load(d, kb0 + d);
-    for (int kb = kb0; kb < kb1; kb += DEPTH) {
+    for (int d = 0; d < DEPTH; ++d) {
+        load(d, d);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int t0 = 0; t0 < Tp; t0 += DEPTH) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            if (kb + d < kb1) {
-                compute(d);
-                if (kb + d + DEPTH < kb1) load(d, kb + d + DEPTH);
-            }
+            compute(d);
+            load(d, t0 + d + DEPTH);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -170,7 +219,6 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
             }
     __syncthreads();
 
-    const bool has_bias = bias != nullptr;
     const bool vec_ok = (N & 3) == 0;
 #pragma unroll
     for (int q = 0; q < NBLK; ++q) {
@@ -197,12 +245,9 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
 #pragma unroll
             for (int c = 0; c < 4; ++c) v[c] = s[c];
         }
-        const float sa = as[m];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int n = nb + c < N ? nb + c : N - 1;
-            v[c] = dequant_elem<GELU>(v[c], sa, ws[n], has_bias, has_bias ? bf16_to_f32(bias[n]) : 0.0f);
-        }
+        for (int c = 0; c < 4; ++c)
+            v[c] = dequant_elem<GELU>(v[c], e_as[q], e_ws[q][c], has_bias, bf16_to_f32(e_b[q][c]));
         if (OUT_DT == QIMG_FP32) {
             float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(m) * N + nb;
             if (vec_ok) {
@@ -249,10 +294,182 @@ hipError_t launch_small(const void* a, const float* as, int M, int K, const void
     return hipGetLastError();
 }
 
+
+// int8 rows of A at most GV_MAXM: a weight-streaming GEMV on the vector ALU.
+// Each wave owns RW consecutive weight rows and reads them front to back,
+// 1 KB per load instruction (lane i takes bytes 16i.. of each 1 KB piece),
+// so the wave streams one contiguous RW*K-byte range of W; every lane also
+// loads the matching 16 bytes of the MR activation rows (cache hits after
+// the first wave). v_dot4_i32_i8 accumulates per lane, a wave reduction
+// gives each (m, n) dot product, exact in int32. Out-of-range rows and
+// chunks read as zero through buffer loads, as in the MFMA kernel.
+constexpr int GV_MAXM = 4;
+
+// ONE: the whole row fits in IU chunks per lane (K <= IU*1024): all loads
+// are issued at once and nothing is loaded past K; otherwise steps of IU
+// chunks alternate between two register sets.
+template <int MR, int RW, int IU, bool ONE, int OUT_DT, bool GELU>
+__global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
+    int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = (blockIdx.x * (SM_THR / 64) + wave) * RW;
+    if (n0 >= N) return;  // wave-uniform; no barriers below
+    constexpr uint32_t kOob = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(A), 0, M * K, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), 0, N * K, kBufferRsrcWord3);
+    const int KC = K >> 4;              // 16-byte chunks per row
+    const int I = (KC + 63) >> 6;       // chunks per lane
+    const int S = (I + 2 * IU - 1) / (2 * IU) * 2;  // steps of IU chunks, even
+    uint32_t arow[MR], wrow[RW];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) arow[m] = m < M ? static_cast<uint32_t>(m) * K : kOob;
+#pragma unroll
+    for (int q = 0; q < RW; ++q) wrow[q] = n0 + q < N ? static_cast<uint32_t>(n0 + q) * K : kOob;
+
+    // Lane l < MR*RW stores output (m = l / RW, n = n0 + l % RW); its scales
+    // and bias are loaded now (clamped, branch-free) so their latency hides
+    // behind the weight stream.
+    const bool has_bias = bias != nullptr;
+    const int e_m = lane / RW;
+    const int e_n = n0 + lane % RW;
+    const int e_nc = e_n < N ? e_n : N - 1;
+    const float e_as = as[e_m < M ? e_m : M - 1];
+    const float e_ws = ws[e_nc];
+    const uint16_t e_b = (has_bias ? bias : reinterpret_cast<const uint16_t*>(ws))[e_nc];
+
+    int acc[MR][RW];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int q = 0; q < RW; ++q) acc[m][q] = 0;
+
+    v4i fa[ONE ? 1 : 2][IU][MR], fw[ONE ? 1 : 2][IU][RW];
+    auto load = [&](int set, int step) {
+#pragma unroll
+        for (int u = 0; u < IU; ++u) {
+            const int c = (step * IU + u) * 64 + lane;
+            const uint32_t col = c < KC ? static_cast<uint32_t>(c) * 16 : kOob;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const uint32_t o = (arow[m] + col) | ((arow[m] | col) & kOob);
+                fa[set][u][m] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, o, 0, 0));
+            }
+#pragma unroll
+            for (int q = 0; q < RW; ++q) {
+                const uint32_t o = (wrow[q] + col) | ((wrow[q] | col) & kOob);
+                fw[set][u][q] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
+            }
+        }
+    };
+    auto compute = [&](int set) {
+#pragma unroll
+        for (int u = 0; u < IU; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int q = 0; q < RW; ++q) {
+                    const v4i a = fa[set][u][m];
+                    const v4i w = fw[set][u][q];
+                    int t = acc[m][q];
+                    t = __builtin_amdgcn_sdot4(a.x, w.x, t, false);
+                    t = __builtin_amdgcn_sdot4(a.y, w.y, t, false);
+                    t = __builtin_amdgcn_sdot4(a.z, w.z, t, false);
+                    t = __builtin_amdgcn_sdot4(a.w, w.w, t, false);
+                    acc[m][q] = t;
+                }
+    };
+    load(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ONE) {
+        compute(0);
+    } else {
+    for (int st = 0; st < S; st += 2) {
+        load(1, st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0);
+        load(0, st + 2);  // past the end: zero-returning loads
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1);
+    }
+    }
+
+    // wave reductions; lane m*RW + q keeps the (m, q) total
+    int mine = 0;
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int q = 0; q < RW; ++q) {
+            const int tot = wave_sum(acc[m][q]);
+            mine = lane == m * RW + q ? tot : mine;
+        }
+    if (lane < MR * RW && e_m < M && e_n < N) {
+        const float v = dequant_elem<GELU>(static_cast<float>(mine), e_as, e_ws, has_bias, bf16_to_f32(e_b));
+        if (OUT_DT == QIMG_FP32)
+            reinterpret_cast<float*>(out)[static_cast<int64_t>(e_m) * N + e_n] = v;
+        else
+            reinterpret_cast<uint16_t*>(out)[static_cast<int64_t>(e_m) * N + e_n] = f32_to_bf16(v);
+    }
+}
+
+template <int MR, int RW, int IU, bool ONE>
+hipError_t launch_gemv(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
+                       const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
+    const int waves = (N + RW - 1) / RW;
+    const int blocks = (waves + SM_THR / 64 - 1) / (SM_THR / 64);
+    const uint8_t* A = static_cast<const uint8_t*>(a);
+    const uint8_t* Wq = static_cast<const uint8_t*>(w);
+#define QIMG_GEMV_LAUNCH(ODT, GL)                                                                        \
+    hipLaunchKernelGGL((gemv_i8_kernel<MR, RW, IU, ONE, ODT, GL>), dim3(blocks), dim3(SM_THR), 0, stream, A, Wq, \
+                       as, ws, bias, out, M, N, K)
+    if (out_dt == QIMG_FP32) {
+        if (gelu)
+            QIMG_GEMV_LAUNCH(QIMG_FP32, true);
+        else
+            QIMG_GEMV_LAUNCH(QIMG_FP32, false);
+    } else {
+        if (gelu)
+            QIMG_GEMV_LAUNCH(QIMG_BF16, true);
+        else
+            QIMG_GEMV_LAUNCH(QIMG_BF16, false);
+    }
+#undef QIMG_GEMV_LAUNCH
+    return hipGetLastError();
+}
+
+hipError_t dispatch_gemv(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
+                         const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
+    const int chunks = ((K >> 4) + 63) >> 6;  // 16-byte chunks per lane
+#define QIMG_GEMV(MR_, RW_, IU_, ONE_) \
+    return launch_gemv<MR_, RW_, IU_, ONE_>(a, as, M, K, w, ws, N, bias, out, out_dt, gelu, stream)
+    if (M <= 2 && chunks <= 4) {
+        if (M == 1) {
+            if (chunks == 1) QIMG_GEMV(1, 8, 1, true);
+            if (chunks == 2) QIMG_GEMV(1, 8, 2, true);
+            if (chunks == 3) QIMG_GEMV(1, 8, 3, true);
+            QIMG_GEMV(1, 8, 4, true);
+        }
+        if (chunks == 1) QIMG_GEMV(2, 8, 1, true);
+        if (chunks == 2) QIMG_GEMV(2, 8, 2, true);
+        if (chunks == 3) QIMG_GEMV(2, 8, 3, true);
+        QIMG_GEMV(2, 8, 4, true);
+    }
+    if (M == 1) QIMG_GEMV(1, 8, 2, false);
+    if (M == 2) QIMG_GEMV(2, 8, 2, false);
+    QIMG_GEMV(4, 4, 2, false);
+#undef QIMG_GEMV
+}
 }  // namespace
 
 int small_m_variant(int M, int N, int K) {
     if (M <= 0 || N <= 0 || (K % SM_KB) != 0) return 0;
+    if (static_cast<int64_t>(M) * K >= (int64_t{1} << 31) || static_cast<int64_t>(N) * K >= (int64_t{1} << 31))
+        return 0;
+    if (M <= GV_MAXM) return 3;
     if (M <= 32) return 1;
     const int64_t big_tiles = static_cast<int64_t>((M + 255) / 256) * ((N + 255) / 256);
     return big_tiles < 128 ? 2 : 0;
@@ -262,7 +479,12 @@ hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int
                                  const float* w_scales, int N, int mode, const uint16_t* bias, void* out,
                                  int out_dtype, int gelu, int variant, hipStream_t stream) {
     const bool fp8 = (mode == QIMG_QM_FP8_HADAMARD);
-    if ((K % SM_KB) != 0 || M <= 0 || N <= 0) return hipErrorInvalidValue;
+    if ((K % SM_KB) != 0 || M <= 0 || N <= 0 || static_cast<int64_t>(M) * K >= (int64_t{1} << 31) ||
+        static_cast<int64_t>(N) * K >= (int64_t{1} << 31))
+        return hipErrorInvalidValue;
+    if (variant == 3 && !fp8 && M <= GV_MAXM)
+        return dispatch_gemv(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype, gelu, stream);
+    if (variant == 3) variant = 1;  // e4m3, or more rows than the GEMV takes
     if (variant == 1)
         return fp8 ? launch_small<true, 1, 1, 8>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype,
                                                  gelu, stream)

@@ -560,7 +560,10 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
     const int choice = g_linear_kernel.load(std::memory_order_relaxed);
     int small = small_m_variant(M, N, K);
     if ((K % BK) == 0 && choice != QIMG_LINEAR_AUTO)
-        small = choice == QIMG_LINEAR_SMALL_32 ? 1 : choice == QIMG_LINEAR_SMALL_64 ? 2 : 0;
+        small = choice == QIMG_LINEAR_SMALL_32 ? 1
+                : choice == QIMG_LINEAR_SMALL_64 ? 2
+                : choice == QIMG_LINEAR_GEMV     ? 3
+                                                 : 0;
     if (small != 0)
         return launch_linear_small_m(act_q, act_scales, M, K, w_q, w_scales, N, mode, bias, out, out_dtype, gelu,
                                      small, stream);

@@ -30,7 +30,8 @@ int set_linear_kernel(int which);
 int get_linear_kernel();
 
 // gemm_small_m.hip: 0 = use the large-tile kernel, 1 = 32x32 tiles
-// (M <= 32), 2 = 64x64 tiles (few large tiles)
+// (M <= 32), 2 = 64x64 tiles (few large tiles), 3 = vector-ALU GEMV (int8,
+// M <= 4; e4m3 falls back to 1)
 int small_m_variant(int M, int N, int K);
 hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int M, int K, const void* w_q,
                                  const float* w_scales, int N, int mode, const uint16_t* bias, void* out,

@@ -37,7 +37,7 @@ def _qw(qimg, q, s, hbs, mode=0):
     return qimg.QuantizedWeight(_dev(q), _dev(s), hbs, mode)
 
 
-KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3}
+KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
@@ -49,7 +49,7 @@ KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3}
 def test_int8_gemm_exact(qimg, oracle, M, N, K, kernel):
     """Every kernel choice gives the exact int32 product (fp32 out with unit
     scales is fl(acc))."""
-    if kernel == "small32" and M * N > 2 ** 22:
+    if kernel in ("small32", "gemv") and M * N > 2 ** 22:
         pytest.skip("32x32 tiles at this size only repeat the small-shape cases")
     rng = np.random.default_rng(M + 3 * N + 7 * K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
@@ -219,8 +219,9 @@ def test_int8_gemm_partial_round_shapes_exact(qimg, oracle, M, N, K):
     np.testing.assert_array_equal(out1.cpu().numpy()[idx], ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 18432, 3072), (1, 3072, 256), (2, 18432, 3072), (17, 3072, 3072),
-                                   (256, 3072, 3072), (256, 12288, 3072), (256, 3072, 12288)])
+@pytest.mark.parametrize("M,N,K", [(1, 18432, 3072), (1, 3072, 256), (2, 18432, 3072), (3, 1000, 1088),
+                                   (4, 3072, 12288), (17, 3072, 3072), (256, 3072, 3072), (256, 12288, 3072),
+                                   (256, 3072, 12288)])
 def test_small_m_shapes_exact(qimg, oracle, M, N, K):
     """The step-level and text-stream shapes: modulation (M = 1 or 2 CFG rows,
     N = 18432), the timestep MLP (K = 256), text linears (M = 256). The int32
@@ -235,12 +236,16 @@ def test_small_m_shapes_exact(qimg, oracle, M, N, K):
     got_auto = qimg.linear_forward_prequantized(ad, sd, wd)
     with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
         got_large = qimg.linear_forward_prequantized(ad, sd, wd)
+    with qimg.linear_kernel(qimg.LINEAR_SMALL_32):
+        got_s32 = qimg.linear_forward_prequantized(ad, sd, wd)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(got_auto.cpu().numpy(), ref)
     np.testing.assert_array_equal(got_large.cpu().numpy(), ref)
+    np.testing.assert_array_equal(got_s32.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("M,N,K,gelu", [(1, 18432, 3072, False), (1, 3072, 256, True), (256, 3072, 3072, False),
+@pytest.mark.parametrize("M,N,K,gelu", [(1, 18432, 3072, False), (1, 3072, 256, True), (2, 3000, 3072, True),
+                                        (256, 3072, 3072, False),
                                         (256, 12288, 3072, True), (40, 200, 12288, False)])
 def test_small_m_linear_matches_oracle(qimg, oracle, M, N, K, gelu):
     """Full linear (activation FWHT + quant, GEMM, dequant epilogue) at the
