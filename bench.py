@@ -62,8 +62,10 @@ def _traffic_from_profiles(kernel):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--ramp-s", type=float, default=1.0,
+                    help="seconds of untimed steps before the warmup, so clocks are up when timing starts")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
@@ -126,6 +128,15 @@ def main():
         lambda: gemm(a2, s2, qw2, b2d, y, q.BF16, 0),
     ]
 
+    # Clock ramp: the GPU raises its clocks only under sustained load (the
+    # first few milliseconds of a burst run ~15% slower), so the step runs
+    # untimed for --ramp-s seconds before the W warmup steps.
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < args.ramp_s:
+        for _ in range(20):
+            for f in launches:
+                f()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         for f in launches:
             f()
@@ -213,7 +224,7 @@ def _calib_copy(torch):
     print(json.dumps({"calib_copy_bytes": n, "copies": 5}))
 
 
-def _time_cycle(torch, fns, iters=10, min_calls=20):
+def _time_cycle(torch, fns, iters=10, min_calls=20, ramp_s=0.2):
     """Median GPU time per call of `fns` (run in turn): the calls are captured
     into one HIP graph (at least `min_calls` calls) and the graph is replayed
     between two events, so host launch overhead is not part of the figure."""
@@ -230,8 +241,11 @@ def _time_cycle(torch, fns, iters=10, min_calls=20):
         for _ in range(reps):
             for f in fns:
                 f()
-    graph.replay()
-    torch.cuda.synchronize()
+    # replay untimed for a while first: clocks ramp up under sustained load
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < ramp_s:
+        graph.replay()
+        torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     ts = []

@@ -30,6 +30,8 @@
 //
 // Rows past M and columns past N read as zero and are never stored. The
 // byte sizes M*K and N*K must be below 2^31 (buffer offsets are 32-bit).
+#include <utility>
+
 #include "qimg_device.h"
 #include "qimg_internal.h"
 
@@ -42,6 +44,16 @@ constexpr int SM_KB = 64;    // bytes of K per block
 // Buffer resource word 3 for gfx9-family raw (unswizzled, unformatted) buffers.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>)
+template <typename F, int... Is>
+__device__ __forceinline__ void sm_static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void sm_static_for(F&& f) {
+    sm_static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <bool FP8>
 struct SmAcc;
 template <>
@@ -53,8 +65,143 @@ struct SmAcc<true> {
     typedef v16f type;
 };
 
-template <bool FP8, int TMW, int TNW, int DEPTH, int OUT_DT, bool GELU>
-__global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
+// Epilogue operands of the (row, 4-column run) groups a thread of the first
+// four waves stores (the mapping of sm_finish), loaded at kernel start so
+// their latency hides behind the operand stream: clamped indices, and a
+// branch-free bias load (from ws when there is no bias) so the loads issue
+// together.
+template <int NBLK>
+struct SmEpi {
+    float as[NBLK];
+    float ws[NBLK][4];
+    uint16_t b[NBLK][4];
+};
+
+template <int TMW, int TNW>
+__device__ __forceinline__ void sm_prefetch(SmEpi<TMW * TNW>& e, const float* as, const float* ws,
+                                            const uint16_t* bias, int m0, int n0, int M, int N) {
+    const uint16_t* bsrc = bias != nullptr ? bias : reinterpret_cast<const uint16_t*>(ws);
+#pragma unroll
+    for (int q = 0; q < TMW * TNW; ++q) {
+        const int idx = (threadIdx.x & (SM_THR - 1)) + SM_THR * q;
+        const int blk = idx >> 8;
+        const int m = m0 + 32 * (blk / TNW) + (idx & 31);
+        const int nb = n0 + 32 * (blk % TNW) + 8 * ((idx >> 6) & 3) + 4 * ((idx >> 5) & 1);
+        e.as[q] = as[m < M ? m : M - 1];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int n = nb + c < N ? nb + c : N - 1;
+            e.ws[q][c] = ws[n];
+            e.b[q][c] = bsrc[n];
+        }
+    }
+}
+
+// Sum the waves' partial tiles through LDS and store the dequantized tile.
+// Partial tiles go to LDS as [wave][block][run g][lane] of 16 bytes: lane
+// holds 4 consecutive n per run (MFMA 32x32 layout, D = W x A, so lane has
+// m = lane%32 and n = 8g + 4h + c for accumulator element 4g + c). With
+// eight waves, waves 4-7 store first and waves 0-3 add them in. The first
+// four waves then each own a quarter of the runs. `red` needs
+// 4 * TMW * TNW * 4 KB; callers synchronise before reusing other LDS for it.
+template <bool FP8, int TMW, int TNW, int NW, int OUT_DT, bool GELU, typename AccT>
+__device__ __forceinline__ void sm_finish(AccT (&acc)[TMW][TNW], v4i* red, int wave, int lane,
+                                          const SmEpi<TMW * TNW>& e, bool has_bias, void* out, int m0, int n0,
+                                          int M, int N) {
+    constexpr int NBLK = TMW * TNW;
+    auto store_partial = [&](int slot, bool add) {
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+#pragma unroll
+            for (int j = 0; j < TNW; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    v4i* dst = &red[((slot * NBLK + i * TNW + j) * 4 + g) * 64 + lane];
+                    // (each element is copied to a scalar first: a bit cast of a
+                    // vector-element lvalue reads element 0)
+                    int b[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const auto x = acc[i][j][4 * g + c];
+                        b[c] = __builtin_bit_cast(int, x);
+                    }
+                    v4i v = (v4i){b[0], b[1], b[2], b[3]};
+                    if (add) {
+                        const v4i o = *dst;
+                        if constexpr (FP8)
+                            v = __builtin_bit_cast(v4i, __builtin_bit_cast(v4f, v) + __builtin_bit_cast(v4f, o));
+                        else
+                            v += o;
+                    }
+                    *dst = v;
+                }
+    };
+    if constexpr (NW == 8) {
+        if (wave >= 4) store_partial(wave - 4, false);
+        __syncthreads();
+        if (wave < 4) store_partial(wave, true);
+    } else {
+        store_partial(wave, false);
+    }
+    __syncthreads();
+    if (wave >= 4) return;
+
+    const bool vec_ok = (N & 3) == 0;
+#pragma unroll
+    for (int q = 0; q < NBLK; ++q) {
+        const int idx = threadIdx.x + SM_THR * q;
+        const int blk = idx >> 8;
+        const int g = (idx >> 6) & 3;
+        const int ln = idx & 63;
+        const int i = blk / TNW;
+        const int j = blk % TNW;
+        const int m = m0 + 32 * i + (ln & 31);
+        const int nb = n0 + 32 * j + 8 * g + 4 * (ln >> 5);
+        if (m >= M || nb >= N) continue;
+        float v[4];
+        if constexpr (!FP8) {
+            v4i sum = red[(blk * 4 + g) * 64 + ln];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) sum += red[((w * NBLK + blk) * 4 + g) * 64 + ln];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = static_cast<float>(sum[c]);
+        } else {
+            v4f sum = __builtin_bit_cast(v4f, red[(blk * 4 + g) * 64 + ln]);
+#pragma unroll
+            for (int w = 1; w < 4; ++w)
+                sum += __builtin_bit_cast(v4f, red[((w * NBLK + blk) * 4 + g) * 64 + ln]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = sum[c];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            v[c] = dequant_elem<GELU>(v[c], e.as[q], e.ws[q][c], has_bias, bf16_to_f32(e.b[q][c]));
+        if (OUT_DT == QIMG_FP32) {
+            float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(m) * N + nb;
+            if (vec_ok) {
+                *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (nb + c < N) o[c] = v[c];
+            }
+        } else {
+            uint16_t* o = reinterpret_cast<uint16_t*>(out) + static_cast<int64_t>(m) * N + nb;
+            if (vec_ok) {
+                *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (nb + c < N) o[c] = f32_to_bf16(v[c]);
+            }
+        }
+    }
+}
+
+// NW waves per workgroup (4 or 8) split K; the epilogue runs on the first
+// four waves.
+template <bool FP8, int TMW, int TNW, int DEPTH, int NW, int OUT_DT, bool GELU>
+__global__ __launch_bounds__(64 * NW) void gemm_small_m_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
     int N, int K) {
@@ -76,28 +223,9 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
     const int r = lane & 31;
     const int h = lane >> 5;
 
-    // Epilogue operands of the (row, 4-column run) groups this thread stores
-    // (same mapping as the epilogue below), loaded now so their latency hides
-    // behind the operand stream: clamped indices, and a branch-free bias load
-    // (from ws when there is no bias) so the loads issue together.
     const bool has_bias = bias != nullptr;
-    const uint16_t* bsrc = has_bias ? bias : reinterpret_cast<const uint16_t*>(ws);
-    float e_as[NBLK], e_ws[NBLK][4];
-    uint16_t e_b[NBLK][4];
-#pragma unroll
-    for (int q = 0; q < NBLK; ++q) {
-        const int idx = threadIdx.x + SM_THR * q;
-        const int blk = idx >> 8;
-        const int m = m0 + 32 * (blk / TNW) + (idx & 31);
-        const int nb = n0 + 32 * (blk % TNW) + 8 * ((idx >> 6) & 3) + 4 * ((idx >> 5) & 1);
-        e_as[q] = as[m < M ? m : M - 1];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int n = nb + c < N ? nb + c : N - 1;
-            e_ws[q][c] = ws[n];
-            e_b[q][c] = bsrc[n];
-        }
-    }
+    SmEpi<NBLK> epi;
+    sm_prefetch<TMW, TNW>(epi, as, ws, bias, m0, n0, M, N);
 
     // K blocks are dealt round-robin to the waves (block 4t + wave), so the
     // four waves read adjacent 64-byte pieces of the same rows at the same
@@ -107,7 +235,7 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
     // branches, every wave runs the same number of blocks, and the loads of
     // DEPTH blocks stay in flight while older blocks are consumed.
     const int nkb = K / SM_KB;
-    const int T = (nkb + 3) >> 2;
+    const int T = (nkb + NW - 1) / NW;
     const int Tp = ((T + DEPTH - 1) / DEPTH) * DEPTH;
     constexpr uint32_t kOob = 0x80000000u;  // >= num_records: reads as zero
     const __amdgpu_buffer_rsrc_t ra =
@@ -140,7 +268,7 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
     v4i ba[DEPTH][TMW][2];
     v4i bw[DEPTH][TNW][2];
     auto load = [&](int d, int t) {
-        const int kb = 4 * t + wave;
+        const int kb = NW * t + wave;
         // block past K: the out-of-range bit (branch-free, wave-uniform)
         const uint32_t koff = (static_cast<uint32_t>(kb) * SM_KB) | (kb < nkb ? 0u : kOob);
 #pragma unroll
@@ -198,87 +326,18 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_m_kernel(
         }
     }
 
-    // Partial tiles -> LDS as [wave][block][run g][lane] of 16 bytes: lane
-    // holds 4 consecutive n per run (MFMA 32x32 layout, D = W x A, so lane
-    // has m = lane%32 and n = 8g + 4h + c for accumulator element 4g + c).
-#pragma unroll
-    for (int i = 0; i < TMW; ++i)
-#pragma unroll
-        for (int j = 0; j < TNW; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                // (each element is copied to a scalar first: a bit cast of a
-                // vector-element lvalue reads element 0)
-                int b[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const auto e = acc[i][j][4 * g + c];
-                    b[c] = __builtin_bit_cast(int, e);
-                }
-                red[((wave * NBLK + i * TNW + j) * 4 + g) * 64 + lane] = (v4i){b[0], b[1], b[2], b[3]};
-            }
-    __syncthreads();
-
-    const bool vec_ok = (N & 3) == 0;
-#pragma unroll
-    for (int q = 0; q < NBLK; ++q) {
-        const int idx = threadIdx.x + SM_THR * q;
-        const int blk = idx >> 8;
-        const int g = (idx >> 6) & 3;
-        const int ln = idx & 63;
-        const int i = blk / TNW;
-        const int j = blk % TNW;
-        const int m = m0 + 32 * i + (ln & 31);
-        const int nb = n0 + 32 * j + 8 * g + 4 * (ln >> 5);
-        if (m >= M || nb >= N) continue;
-        float v[4];
-        if constexpr (!FP8) {
-            v4i s = red[(blk * 4 + g) * 64 + ln];
-#pragma unroll
-            for (int w = 1; w < 4; ++w) s += red[((w * NBLK + blk) * 4 + g) * 64 + ln];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = static_cast<float>(s[c]);
-        } else {
-            v4f s = __builtin_bit_cast(v4f, red[(blk * 4 + g) * 64 + ln]);
-#pragma unroll
-            for (int w = 1; w < 4; ++w) s += __builtin_bit_cast(v4f, red[((w * NBLK + blk) * 4 + g) * 64 + ln]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = s[c];
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            v[c] = dequant_elem<GELU>(v[c], e_as[q], e_ws[q][c], has_bias, bf16_to_f32(e_b[q][c]));
-        if (OUT_DT == QIMG_FP32) {
-            float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(m) * N + nb;
-            if (vec_ok) {
-                *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (nb + c < N) o[c] = v[c];
-            }
-        } else {
-            uint16_t* o = reinterpret_cast<uint16_t*>(out) + static_cast<int64_t>(m) * N + nb;
-            if (vec_ok) {
-                *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (nb + c < N) o[c] = f32_to_bf16(v[c]);
-            }
-        }
-    }
+    sm_finish<FP8, TMW, TNW, NW, OUT_DT, GELU>(acc, red, wave, lane, epi, has_bias, out, m0, n0, M, N);
 }
 
-template <bool FP8, int TMW, int TNW, int DEPTH>
+template <bool FP8, int TMW, int TNW, int DEPTH, int NW>
 hipError_t launch_small(const void* a, const float* as, int M, int K, const void* w, const float* ws,
                         int N, const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
     const int tiles = ((M + 32 * TMW - 1) / (32 * TMW)) * ((N + 32 * TNW - 1) / (32 * TNW));
     const uint8_t* A = static_cast<const uint8_t*>(a);
     const uint8_t* Wq = static_cast<const uint8_t*>(w);
 #define QIMG_SMALL_LAUNCH(ODT, GL)                                                                      \
-    hipLaunchKernelGGL((gemm_small_m_kernel<FP8, TMW, TNW, DEPTH, ODT, GL>), dim3(tiles), dim3(SM_THR), 0, \
-                       stream, A, Wq, as, ws, bias, out, M, N, K)
+    hipLaunchKernelGGL((gemm_small_m_kernel<FP8, TMW, TNW, DEPTH, NW, ODT, GL>), dim3(tiles), dim3(64 * NW), \
+                       0, stream, A, Wq, as, ws, bias, out, M, N, K)
     if (out_dt == QIMG_FP32) {
         if (gelu)
             QIMG_SMALL_LAUNCH(QIMG_FP32, true);
@@ -294,6 +353,181 @@ hipError_t launch_small(const void* a, const float* as, int M, int K, const void
     return hipGetLastError();
 }
 
+
+// LDS-staged variant for K a multiple of 256. A load instruction whose 64
+// lanes touch 32 different rows (the direct fragment loads above) costs the
+// address unit several times more than one whose lane quads read 64
+// contiguous bytes, so here each wave copies its K blocks into its own LDS
+// ring with global -> LDS DMA (16 rows x 64 bytes per instruction, the same
+// XOR swizzle as the large-tile kernel) and reads MFMA fragments from LDS.
+// The rings are private to their waves, so the main loop needs no barrier:
+// a wave waits only for its own DMA (vmcnt) and its own reads (lgkmcnt).
+// Rows past M or N are clamped (computed, never stored); K is split exactly.
+template <bool FP8, int TMW, int TNW, int D, int OUT_DT, bool GELU>
+__global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
+    int N, int K) {
+    constexpr int NW = SM_THR / 64;
+    constexpr int MB = 32 * TMW;
+    constexpr int NB = 32 * TNW;
+    constexpr int NBLK = TMW * TNW;
+    constexpr int ROWS = MB + NB;
+    constexpr int SLOT = ROWS * SM_KB;  // one K block of the tile's rows
+    constexpr int NDMA = ROWS / 16;     // DMA instructions per block
+    constexpr int RING = D * SLOT;      // per wave
+    constexpr int LDS_RING = NW * RING;
+    constexpr int LDS_RED = 4 * NBLK * 4 * 64 * 16;
+    constexpr int LDS_BYTES = LDS_RING > LDS_RED ? LDS_RING : LDS_RED;
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+
+    const int tiles_m = (M + MB - 1) / MB;
+    const int tiles_n = (N + NB - 1) / NB;
+    const int logical = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+    const int m0 = (logical % tiles_m) * MB;
+    const int n0 = (logical / tiles_m) * NB;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 31;
+    const int h = lane >> 5;
+
+    const bool has_bias = bias != nullptr;
+    SmEpi<NBLK> epi;
+    sm_prefetch<TMW, TNW>(epi, as, ws, bias, m0, n0, M, N);
+
+    // Block t of this wave is K block NW*t + wave. DMA instruction i fills
+    // slot rows 16i .. 16i+15 (A rows first, then W rows); lane -> row
+    // 16i + lane/4 at physical chunk lane%4.
+    const int T = K / (SM_KB * NW);
+    const uint8_t* src[NDMA];
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+        const int row = 16 * i + (lane >> 2);
+        const int c = (lane & 3) ^ swz_row(row);
+        const uint8_t* base;
+        if (16 * i < MB) {
+            const int gm = m0 + row < M ? m0 + row : M - 1;
+            base = A + static_cast<int64_t>(gm) * K;
+        } else {
+            const int gn = n0 + row - MB < N ? n0 + row - MB : N - 1;
+            base = W + static_cast<int64_t>(gn) * K;
+        }
+        src[i] = base + wave * SM_KB + c * 16;
+    }
+    uint8_t* ring = lds + wave * RING;
+    auto issue = [&](int t, int slot) {
+        const int64_t koff = static_cast<int64_t>(t) * (NW * SM_KB);
+        uint8_t* dst = ring + slot * SLOT;
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i)
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(src[i] + koff), (lds_ptr_t)(dst + i * 1024), 16, 0, 1);
+    };
+
+    typedef typename SmAcc<FP8>::type acc_t;
+    acc_t acc[TMW][TNW];
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+#pragma unroll
+        for (int j = 0; j < TNW; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    auto frag = [&](const uint8_t* base, int row, int chunk) {
+        return *reinterpret_cast<const v4i*>(base + row * SM_KB + ((chunk ^ swz_row(row)) << 4));
+    };
+    auto compute = [&](int slot) {
+        const uint8_t* base = ring + slot * SLOT;
+        if constexpr (!FP8) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                v4i fa[TMW], fw[TNW];
+#pragma unroll
+                for (int i = 0; i < TMW; ++i) fa[i] = frag(base, 32 * i + r, 2 * h + s);
+#pragma unroll
+                for (int j = 0; j < TNW; ++j) fw[j] = frag(base, MB + 32 * j + r, 2 * h + s);
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TNW; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
+            }
+        } else {
+            v8i fa[TMW], fw[TNW];
+#pragma unroll
+            for (int i = 0; i < TMW; ++i) {
+                const v4i lo = frag(base, 32 * i + r, 2 * h), hi = frag(base, 32 * i + r, 2 * h + 1);
+                fa[i] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+#pragma unroll
+            for (int j = 0; j < TNW; ++j) {
+                const v4i lo = frag(base, MB + 32 * j + r, 2 * h), hi = frag(base, MB + 32 * j + r, 2 * h + 1);
+                fw[j] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            }
+#pragma unroll
+            for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                for (int j = 0; j < TNW; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], 0, 0, 0,
+                                                                                127, 0, 127);
+        }
+    };
+
+    // Prologue: the first min(T, D) blocks. Steady state: block t lands
+    // (all but the D-1 younger blocks' DMA done), is consumed, and its slot
+    // is refilled with block t + D once this wave's reads of it returned.
+    // Tail: the last D blocks, with the wait shrinking as no younger blocks
+    // are issued.
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (d < T) issue(d, d);
+    int t = 0;
+    for (; t + D < T; ++t) {
+        const int slot = t % D;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<(D - 1) * NDMA>();
+        compute(slot);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        issue(t + D, slot);
+    }
+    sm_static_for<D>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int tt = T - D + j;
+        if (tt >= 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<(D - 1 - j) * NDMA>();
+            compute(tt % D);
+        }
+    });
+    __syncthreads();  // every wave is done with its ring: reuse LDS for the reduction
+    sm_finish<FP8, TMW, TNW, NW, OUT_DT, GELU>(acc, reinterpret_cast<v4i*>(lds), wave, lane, epi, has_bias, out,
+                                               m0, n0, M, N);
+}
+
+template <bool FP8, int TMW, int TNW, int D>
+hipError_t launch_small_dma(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
+                            const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
+    const int tiles = ((M + 32 * TMW - 1) / (32 * TMW)) * ((N + 32 * TNW - 1) / (32 * TNW));
+    const uint8_t* A = static_cast<const uint8_t*>(a);
+    const uint8_t* Wq = static_cast<const uint8_t*>(w);
+#define QIMG_SMALL_DMA_LAUNCH(ODT, GL)                                                                            \
+    hipLaunchKernelGGL((gemm_small_dma_kernel<FP8, TMW, TNW, D, ODT, GL>), dim3(tiles), dim3(SM_THR), 0, stream, A, \
+                       Wq, as, ws, bias, out, M, N, K)
+    if (out_dt == QIMG_FP32) {
+        if (gelu)
+            QIMG_SMALL_DMA_LAUNCH(QIMG_FP32, true);
+        else
+            QIMG_SMALL_DMA_LAUNCH(QIMG_FP32, false);
+    } else {
+        if (gelu)
+            QIMG_SMALL_DMA_LAUNCH(QIMG_BF16, true);
+        else
+            QIMG_SMALL_DMA_LAUNCH(QIMG_BF16, false);
+    }
+#undef QIMG_SMALL_DMA_LAUNCH
+    return hipGetLastError();
+}
 
 // int8 rows of A at most GV_MAXM: a weight-streaming GEMV on the vector ALU.
 // Each wave owns RW consecutive weight rows and reads them front to back,
@@ -465,10 +699,13 @@ hipError_t dispatch_gemv(const void* a, const float* as, int M, int K, const voi
 }
 }  // namespace
 
+bool small_m_fits(int M, int N, int K) {
+    return M > 0 && N > 0 && (K % SM_KB) == 0 && static_cast<int64_t>(M) * K < (int64_t{1} << 31) &&
+           static_cast<int64_t>(N) * K < (int64_t{1} << 31);
+}
+
 int small_m_variant(int M, int N, int K) {
-    if (M <= 0 || N <= 0 || (K % SM_KB) != 0) return 0;
-    if (static_cast<int64_t>(M) * K >= (int64_t{1} << 31) || static_cast<int64_t>(N) * K >= (int64_t{1} << 31))
-        return 0;
+    if (!small_m_fits(M, N, K)) return 0;
     if (M <= GV_MAXM) return 3;
     if (M <= 32) return 1;
     const int64_t big_tiles = static_cast<int64_t>((M + 255) / 256) * ((N + 255) / 256);
@@ -479,21 +716,40 @@ hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int
                                  const float* w_scales, int N, int mode, const uint16_t* bias, void* out,
                                  int out_dtype, int gelu, int variant, hipStream_t stream) {
     const bool fp8 = (mode == QIMG_QM_FP8_HADAMARD);
-    if ((K % SM_KB) != 0 || M <= 0 || N <= 0 || static_cast<int64_t>(M) * K >= (int64_t{1} << 31) ||
-        static_cast<int64_t>(N) * K >= (int64_t{1} << 31))
-        return hipErrorInvalidValue;
+    if (!small_m_fits(M, N, K)) return hipErrorInvalidValue;
+    // The LDS-staged kernels split K exactly over four waves.
+    const bool lds_staged = (K % (SM_KB * (SM_THR / 64))) == 0;
     if (variant == 3 && !fp8 && M <= GV_MAXM)
         return dispatch_gemv(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype, gelu, stream);
     if (variant == 3) variant = 1;  // e4m3, or more rows than the GEMV takes
+    if (variant == 1 && lds_staged)
+        return fp8 ? launch_small_dma<true, 1, 1, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                     out_dtype, gelu, stream)
+                   : launch_small_dma<false, 1, 1, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                      out_dtype, gelu, stream);
+    if (variant == 2 && lds_staged) {
+        // two slots per wave (64 KB) leave room for two workgroups per CU
+        // when there are enough tiles to use them
+        const int64_t tiles = static_cast<int64_t>((M + 63) / 64) * ((N + 63) / 64);
+        if (tiles > 256)
+            return fp8 ? launch_small_dma<true, 2, 2, 2>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                         out_dtype, gelu, stream)
+                       : launch_small_dma<false, 2, 2, 2>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                          out_dtype, gelu, stream);
+        return fp8 ? launch_small_dma<true, 2, 2, 3>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                     out_dtype, gelu, stream)
+                   : launch_small_dma<false, 2, 2, 3>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                      out_dtype, gelu, stream);
+    }
     if (variant == 1)
-        return fp8 ? launch_small<true, 1, 1, 8>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype,
+        return fp8 ? launch_small<true, 1, 1, 8, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype,
                                                  gelu, stream)
-                   : launch_small<false, 1, 1, 8>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                   : launch_small<false, 1, 1, 8, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
                                                   out_dtype, gelu, stream);
     if (variant == 2)
-        return fp8 ? launch_small<true, 2, 2, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype,
+        return fp8 ? launch_small<true, 2, 2, 4, 8>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype,
                                                  gelu, stream)
-                   : launch_small<false, 2, 2, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                   : launch_small<false, 2, 2, 4, 8>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
                                                   out_dtype, gelu, stream);
     return hipErrorInvalidValue;
 }

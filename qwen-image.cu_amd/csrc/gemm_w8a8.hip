@@ -14,27 +14,33 @@
 // unit scales for e4m3); the 256 accumulator registers live in AGPRs. Both
 // operands are K-major [rows, K] as the reference stores them (TN GEMM).
 //
-// K advances 64 bytes per stage through a four-slot LDS ring (4 x 32 KB),
-// so three stages are in flight while one is consumed. Stages are filled by
+// K advances 128 bytes per stage through a two-slot LDS ring (2 x 64 KB):
+// while one stage is consumed the next is in flight. Stages are filled by
 // direct global->LDS DMA (global_load_lds_dwordx4): no VGPR staging and no
-// ds_write instructions. Each DMA instruction writes 1 KB = 16 LDS rows of
-// 64 bytes; lane i fetches the global chunk that the row's XOR swizzle
-// places at physical chunk i%4, with swizzle(row) = ((row>>1) ^ (row>>3)) & 3,
-// so MFMA fragment reads of 8 or 16 consecutive rows at one logical chunk hit
-// distinct LDS banks. Stage hand-off uses s_waitcnt vmcnt(<stages still in
-// flight>) + s_barrier rather than __syncthreads(), whose workgroup fence
-// would drain every outstanding DMA. The hand-off sits in the middle of a
-// stage's MFMA work, and the LDS fragment reads for the next k-step are
-// interleaved with the current k-step's MFMAs (sched_group_barrier), so with
-// one wave per SIMD the matrix core is fed without waiting on LDS latency.
+// ds_write instructions. Each DMA instruction writes 1 KB = 8 LDS rows of
+// 128 bytes, so every lane octet reads one whole 128-byte cache line: on
+// gfx950 a DMA instruction that touches 16 half lines (64-byte rows) moves
+// half the bytes per unit time of one that touches 8 full lines (measured
+// 62 vs 122 GB/s per CU from L2), which outweighs the shallower ring. Lane i
+// fetches the global chunk that the row's XOR swizzle places at physical
+// chunk i%8, swizzle(row) = row & 7, so MFMA fragment reads of 8
+// consecutive rows at one logical chunk hit distinct LDS banks. Stage
+// hand-off uses s_waitcnt + s_barrier rather than __syncthreads(), whose
+// workgroup fence would drain every outstanding DMA; it sits before the last
+// k-step of a stage, right after the reads of that k-step's fragments, and
+// the refill of the freed slot is issued as soon as the barrier passes. The
+// LDS fragment reads for the next k-step are interleaved with the current
+// k-step's MFMAs (sched_group_barrier), so with one wave per SIMD the matrix
+// core is fed without waiting on LDS latency.
 //
 // The tile's activation scales, weight scales and bias are loaded into
 // registers at kernel start and written to LDS (in ring space) after the main
 // loop, so the epilogue reads them without global latency.
 //
-// K ordering: within a stage, lane half h of a fragment holds logical
-// chunks 2h, 2h+1; int8 k-step s uses chunk 2h+s (16 bytes), e4m3 uses both
-// (32 bytes, one k-step). Both operands use the same assignment, so each dot
+// K ordering: a stage row holds eight 16-byte chunks. Lane half h of an int8
+// fragment takes chunk 4h + s in k-step s (four 32-byte k-steps per stage);
+// an e4m3 fragment takes chunks 4h + 2s and 4h + 2s + 1 in k-step s (two
+// 64-byte k-steps). Both operands use the same assignment, so each dot
 // product covers every k exactly once and the int8 result is exact.
 #include <atomic>
 
@@ -47,14 +53,14 @@ namespace {
 
 constexpr int BM = 256;
 constexpr int BN = 256;
-constexpr int BK = 64;     // bytes of K per stage
-constexpr int NSLOT = 4;   // LDS ring depth (4 x 32 KB; 3 and 5 measured no better)
+constexpr int BK = 128;    // bytes of K per stage
+constexpr int NSLOT = 2;   // LDS ring depth (2 x 64 KB)
 constexpr int NTHR = 256;
 constexpr int WTM = 128;  // wave tile
 constexpr int WTN = 128;
 constexpr int TM = WTM / 32;  // 32x32 blocks per wave
 constexpr int TN = WTN / 32;
-constexpr int STAGE_BYTES = (BM + BN) * BK;   // 32 KB
+constexpr int STAGE_BYTES = (BM + BN) * BK;   // 64 KB
 constexpr int DMA_ROWS = 1024 / BK;           // rows per DMA instruction
 constexpr int NDMA = BM / (4 * DMA_ROWS);     // DMA instructions per operand per wave per stage
 constexpr int LDS_BYTES = NSLOT * STAGE_BYTES;
@@ -66,17 +72,13 @@ constexpr int GROUP_M = 4;  // tile rows per group in the tile order
 // default policy at the MMDiT shapes; the non-temporal policy is slower).
 constexpr int kDmaPolicy = 1;
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
 
-__device__ __forceinline__ int swz_row(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ __forceinline__ int swz8(int row) { return row & 7; }
 
 __device__ __forceinline__ int lds_addr(int row, int chunk) {
-    return row * BK + ((chunk ^ swz_row(row)) << 4);
+    return row * BK + ((chunk ^ swz8(row)) << 4);
 }
 
-// s_waitcnt lgkmcnt(0), the other counters left alone.
-__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 // sched_group_barrier instruction classes
 constexpr int SG_MFMA = 0x008;
@@ -84,12 +86,6 @@ constexpr int SG_VMEM = 0x010;
 constexpr int SG_DS_READ = 0x100;
 #define SGB(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
 
-// s_waitcnt with vmcnt = n (0..63) and the other counters left alone.
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((0x0f70 & ~0xc00f) | (n & 15) | ((n >> 4) << 14));
-}
 
 template <bool FP8>
 struct Acc;
@@ -145,13 +141,13 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
 
     // DMA assignment: wave w, instruction i fills LDS rows
     // DMA_ROWS*(4*i + w) .. +DMA_ROWS of the A tile (and the same rows of
-    // the W tile); lane -> row +lane/4, physical chunk lane%4.
+    // the W tile); lane -> row +lane/8, physical chunk lane%8.
     const uint8_t* a_src[NDMA];
     const uint8_t* w_src[NDMA];
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-        const int r = DMA_ROWS * (4 * i + wave) + (lane >> 2);
-        const int c = (lane & 3) ^ swz_row(r);
+        const int r = DMA_ROWS * (4 * i + wave) + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(r);
         int gm = m0 + r;
         gm = gm < M ? gm : M - 1;  // clamp: rows past M are computed, never stored
         int gn = n0 + r;
@@ -193,36 +189,39 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) wrow[j] = wn * WTN + j * 32 + frag_row;
 
-    // prologue: stages 0 .. NSLOT-2 in flight.
-#pragma unroll
-    for (int p = 0; p < NSLOT - 1; ++p) issue_stage(p, p);
-    constexpr int KEEP = (NSLOT - 2) * 2 * NDMA;  // DMA instructions allowed in flight at a hand-off
-    wait_vmcnt<KEEP>();
+    // prologue: stages 0 and 1 in flight; wait for stage 0.
+    issue_stage(0, 0);
+    issue_stage(1, 1);
+    wait_vmcnt<2 * NDMA>();
     __builtin_amdgcn_s_barrier();
 
-    // Stage hand-off at the middle of each stage's MFMA work: this wave's
-    // reads of the current slot are complete (so no wave's next DMA can
-    // overwrite data still being read), this wave's share of stage kt+1 has
-    // landed, then the workgroup barrier makes every wave's share visible.
+    // Hand-off before a stage's last k-step, right after that k-step's
+    // fragment reads were issued: this wave's reads of the current slot are
+    // complete (so the refill DMA issued next cannot overwrite data still
+    // being read), the next stage has landed (vmcnt 0: it is the only DMA in
+    // flight), then the workgroup barrier makes every wave's share visible
+    // and tells every wave the current slot is free.
     auto handoff = [&]() {
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0();
-        wait_vmcnt<KEEP>();
+        wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
     };
 
     if constexpr (!FP8) {
-        // Two 32-byte k-steps per stage. Fragments of k-step 1 are read while
-        // k-step 0's 16 MFMAs run; fragments of the next stage's k-step 0 are
-        // read while k-step 1's MFMAs run. The sched_group_barrier sequences
-        // pin that interleave (the default schedule sinks every LDS read to
-        // just before its first use, which serialises them with the MFMAs).
+        // Four 32-byte k-steps per stage; the fragments of k-step s+1 are read
+        // while k-step s's 16 MFMAs run, and the next stage's k-step 0 is
+        // read during k-step 3. The sched_group_barrier sequences pin that
+        // interleave (the default schedule sinks every LDS read to just before
+        // its first use, which serialises them with the MFMAs). An MFMA leads
+        // each pair so its wait on the previous reads does not also wait on
+        // the read just issued.
         v4i fa0[TM], fw0[TN], fa1[TM], fw1[TN];
         auto read_frags = [&](v4i* fa, v4i* fw, int slot, int ks) {
             const uint8_t* la = lds + slot * STAGE_BYTES;
             const uint8_t* lw = la + BM * BK;
-            const int chunk = 2 * half + ks;
+            const int chunk = 4 * half + ks;
 #pragma unroll
             for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + lds_addr(arow[i], chunk));
 #pragma unroll
@@ -235,45 +234,42 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
         };
-        read_frags(fa0, fw0, 0, 0);
-        for (int kt = 0; kt < KT; ++kt) {
-            const int slot = kt % NSLOT;
-            issue_stage(kt + NSLOT - 1, (kt + NSLOT - 1) % NSLOT);
-            read_frags(fa1, fw1, slot, 1);
-            mfma_all(fa0, fw0);
-            // The DMA writes LDS, so the compiler keeps the reads after it:
-            // the 8 DMA instructions issue first, then reads and MFMAs alternate.
-            // An MFMA leads each pair so its wait on the previous half's reads
-            // does not also wait on the read just issued.
-            SGB(SG_VMEM, 2 * NDMA);
+        auto interleave = [&]() {
 #pragma unroll
             for (int i = 0; i < TM + TN; ++i) {
                 SGB(SG_MFMA, 1);
                 SGB(SG_DS_READ, 1);
-            }
-            SGB(SG_MFMA, TM * TN - (TM + TN));
-            handoff();
-            read_frags(fa0, fw0, (kt + 1) % NSLOT, 0);
-            mfma_all(fa1, fw1);
-#pragma unroll
-            for (int i = 0; i < TM + TN; ++i) {
-                SGB(SG_DS_READ, 1);
-                SGB(SG_MFMA, 1);
             }
             SGB(SG_MFMA, TM * TN - (TM + TN));
             __builtin_amdgcn_sched_barrier(0);
+        };
+        read_frags(fa0, fw0, 0, 0);
+        for (int kt = 0; kt < KT; ++kt) {
+            const int slot = kt & 1;
+            read_frags(fa1, fw1, slot, 1);
+            mfma_all(fa0, fw0);
+            interleave();
+            read_frags(fa0, fw0, slot, 2);
+            mfma_all(fa1, fw1);
+            interleave();
+            read_frags(fa1, fw1, slot, 3);
+            mfma_all(fa0, fw0);
+            interleave();
+            handoff();
+            issue_stage(kt + 2, slot);
+            read_frags(fa0, fw0, slot ^ 1, 0);
+            mfma_all(fa1, fw1);
+            SGB(SG_VMEM, 2 * NDMA);
+            interleave();
         }
     } else {
-        // One 64-byte k-step per stage (v_mfma_scale_f32_32x32x64_f8f6f4,
-        // unit scales). The first half of the 16 MFMAs overlaps the DMA
-        // issue; after the hand-off the second half overlaps the reads of
-        // the next stage's fragments into the other register set. The loop
-        // is unrolled by two so the register sets alternate without copies.
+        // Two 64-byte k-steps per stage (v_mfma_scale_f32_32x32x64_f8f6f4,
+        // unit scales), with the same read-ahead and hand-off.
         v8i fa0[TM], fw0[TN], fa1[TM], fw1[TN];
-        auto read_frags = [&](v8i* fa, v8i* fw, int slot) {
+        auto read_frags = [&](v8i* fa, v8i* fw, int slot, int ks) {
             const uint8_t* la = lds + slot * STAGE_BYTES;
             const uint8_t* lw = la + BM * BK;
-            const int c0 = 2 * half;
+            const int c0 = 4 * half + 2 * ks;
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const v4i lo4 = *reinterpret_cast<const v4i*>(la + lds_addr(arow[i], c0));
@@ -287,37 +283,36 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
                 fw[j] = (v8i){lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
             }
         };
-        auto mfma_rows = [&](const v8i* fa, const v8i* fw, int i0) {
+        auto mfma_all = [&](const v8i* fa, const v8i* fw) {
 #pragma unroll
-            for (int i = i0; i < i0 + TM / 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        fw[j], fa[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], 0, 0, 0,
+                                                                                127, 0, 127);
         };
-        auto stage = [&](int kt, const v8i* fa, const v8i* fw, v8i* na, v8i* nw) {
-            issue_stage(kt + NSLOT - 1, (kt + NSLOT - 1) % NSLOT);
-            mfma_rows(fa, fw, 0);
-            SGB(SG_VMEM, 2 * NDMA);
-            SGB(SG_MFMA, TM * TN / 2);
-            handoff();
-            read_frags(na, nw, (kt + 1) % NSLOT);
-            mfma_rows(fa, fw, TM / 2);
+        auto interleave = [&]() {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                SGB(SG_DS_READ, 4);
+            for (int i = 0; i < TM + TN; ++i) {
                 SGB(SG_MFMA, 1);
+                SGB(SG_DS_READ, 2);
             }
-            SGB(SG_MFMA, TM * TN / 2 - TM);
+            SGB(SG_MFMA, TM * TN - (TM + TN));
             __builtin_amdgcn_sched_barrier(0);
         };
-        read_frags(fa0, fw0, 0);
-        int kt = 0;
-        for (; kt + 1 < KT; kt += 2) {
-            stage(kt, fa0, fw0, fa1, fw1);
-            stage(kt + 1, fa1, fw1, fa0, fw0);
+        read_frags(fa0, fw0, 0, 0);
+        for (int kt = 0; kt < KT; ++kt) {
+            const int slot = kt & 1;
+            read_frags(fa1, fw1, slot, 1);
+            mfma_all(fa0, fw0);
+            interleave();
+            handoff();
+            issue_stage(kt + 2, slot);
+            read_frags(fa0, fw0, slot ^ 1, 0);
+            mfma_all(fa1, fw1);
+            SGB(SG_VMEM, 2 * NDMA);
+            interleave();
         }
-        if (kt < KT) stage(kt, fa0, fw0, fa1, fw1);
     }
 
     // The last iterations re-fetched a valid stage into idle slots; drain
@@ -559,11 +554,13 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
     const bool fp8 = (mode == QIMG_QM_FP8_HADAMARD);
     const int choice = g_linear_kernel.load(std::memory_order_relaxed);
     int small = small_m_variant(M, N, K);
-    if ((K % BK) == 0 && choice != QIMG_LINEAR_AUTO)
+    if ((K % 64) == 0 && choice != QIMG_LINEAR_AUTO)
         small = choice == QIMG_LINEAR_SMALL_32 ? 1
                 : choice == QIMG_LINEAR_SMALL_64 ? 2
                 : choice == QIMG_LINEAR_GEMV     ? 3
                                                  : 0;
+    // the large tiles need K % 128 == 0; other multiples of 64 take 64x64 tiles
+    if (small == 0 && (K % BK) != 0 && small_m_fits(M, N, K)) small = 2;
     if (small != 0)
         return launch_linear_small_m(act_q, act_scales, M, K, w_q, w_scales, N, mode, bias, out, out_dtype, gelu,
                                      small, stream);
@@ -575,7 +572,7 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
     }
     const int64_t total = static_cast<int64_t>(M) * N;
     const int blocks = static_cast<int>((total + 255) / 256);
-    if (fp8) return hipErrorInvalidValue;  // e4m3 needs K % 64 == 0 (checked by the caller)
+    if (fp8) return hipErrorInvalidValue;  // e4m3 needs K % 64 == 0 (checked by the caller) and fitting sizes
     hipLaunchKernelGGL(gemm_i8_simple_kernel, dim3(blocks), dim3(256), 0, stream,
                        static_cast<const int8_t*>(act_q), static_cast<const int8_t*>(w_q),
                        act_scales, w_scales, bias, out, M, N, K, out_dtype, gelu);

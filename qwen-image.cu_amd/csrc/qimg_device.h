@@ -76,6 +76,27 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
     return s | out;
 }
 
+// Address-space pointer types of the global -> LDS DMA builtin
+// (global_load_lds_dwordx4: each lane's 16 bytes land at the LDS base
+// + 16 * lane).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+
+// XOR swizzle of the four 16-byte chunks of a 64-byte LDS row: chunk c of
+// row r is stored at physical chunk c ^ swz_row(r), so 16-byte fragment reads
+// of 8 consecutive rows at one logical chunk hit distinct banks.
+__device__ __forceinline__ int swz_row(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+// s_waitcnt lgkmcnt(0), the other counters left alone.
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// s_waitcnt with vmcnt = n (0..63) and the other counters left alone.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((0x0f70 & ~0xc00f) | (n & 15) | ((n >> 4) << 14));
+}
+
 // Map the hardware workgroup id so that each XCD (workgroups are dispatched
 // round-robin over 8 XCDs) receives a contiguous range of logical tiles,
 // which keeps the tiles that share operand rows in one L2.

@@ -33,6 +33,7 @@ int get_linear_kernel();
 // (M <= 32), 2 = 64x64 tiles (few large tiles), 3 = vector-ALU GEMV (int8,
 // M <= 4; e4m3 falls back to 1)
 int small_m_variant(int M, int N, int K);
+bool small_m_fits(int M, int N, int K);  // sizes the small-tile kernels can address
 hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int M, int K, const void* w_q,
                                  const float* w_scales, int N, int mode, const uint16_t* bias, void* out,
                                  int out_dtype, int gelu, int variant, hipStream_t stream);

@@ -367,8 +367,6 @@ __device__ __forceinline__ void attn_wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt(0x0070 | (n & 15) | ((n >> 4) << 14));
 }
 
-typedef __attribute__((address_space(3))) void* attn_lds_ptr_t;
-typedef const __attribute__((address_space(1))) void* attn_gbl_ptr_t;
 
 template <int D, bool CAUSAL, int OUT_DT>
 __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
@@ -443,15 +441,15 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
                 int tok = kt * KTILE + row;
                 tok = tok < S ? tok : S - 1;  // rows past S are loaded but masked
                 __builtin_amdgcn_global_load_lds(
-                    (attn_gbl_ptr_t)(Kh + static_cast<int64_t>(tok) * D + chunk * 16),
-                    (attn_lds_ptr_t)(base + j * 1024), 16, 0, 0);
+                    (gbl_ptr_t)(Kh + static_cast<int64_t>(tok) * D + chunk * 16),
+                    (lds_ptr_t)(base + j * 1024), 16, 0, 0);
             } else {
                 const int jj = j - C::K_INSTR;
                 const int row = jj * 8 + (lane >> 3);  // d row of V^T
                 const int chunk = swz_chunk<8>(row, lane & 7);
                 __builtin_amdgcn_global_load_lds(
-                    (attn_gbl_ptr_t)(Vh + (static_cast<int64_t>(kt) * D + row) * KTILE + chunk * 8),
-                    (attn_lds_ptr_t)(base + C::K_BYTES + jj * 1024), 16, 0, 0);
+                    (gbl_ptr_t)(Vh + (static_cast<int64_t>(kt) * D + row) * KTILE + chunk * 8),
+                    (lds_ptr_t)(base + C::K_BYTES + jj * 1024), 16, 0, 0);
             }
         }
     };
