@@ -552,6 +552,20 @@ hipError_t dispatch_tiled(const void* a, const float* as, int M, int K, const vo
 
 static std::atomic<int> g_linear_kernel{QIMG_LINEAR_AUTO};
 
+// Compute units of the current device (queried once per device).
+static int device_cu_count() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cache[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 int set_linear_kernel(int which) { return g_linear_kernel.exchange(which); }
 int get_linear_kernel() { return g_linear_kernel.load(); }
 
@@ -585,10 +599,39 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
         return launch_linear_small_m(act_q, act_scales, M, K, w_q, w_scales, N, mode, bias, out, out_dtype, gelu,
                                      small, stream);
     if ((K % BK) == 0) {
-        return fp8 ? dispatch_tiled<true>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
-                                          out_dtype, gelu, stream)
-                   : dispatch_tiled<false>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
-                                           out_dtype, gelu, stream);
+        // Tile rounds: one 256x256 tile per CU at a time. When the last
+        // round would be mostly idle, the trailing tile rows (at most two)
+        // go to the 64x64 kernel instead, which spreads them over every CU
+        // (e.g. M = 4352 = 4096 + 256 rows, N = 12288: 816 tiles = 3 rounds
+        // + 48 tiles; the 48 become 192 small tiles).
+        int m_big = M;
+        if (choice == QIMG_LINEAR_AUTO) {
+            const int cus = device_cu_count();
+            const int tiles_n = (N + BN - 1) / BN;
+            const int tiles_m = (M + BM - 1) / BM;
+            const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
+            const int64_t rounds = (total + cus - 1) / cus;
+            const int64_t tail = total - (rounds - 1) * cus;
+            if (cus > 0 && rounds > 1 && tail * 2 < cus) {
+                for (int r = 1; r <= 2 && r < tiles_m; ++r) {
+                    if (static_cast<int64_t>(tiles_m - r) * tiles_n <= (rounds - 1) * cus) {
+                        m_big = (tiles_m - r) * BM;
+                        break;
+                    }
+                }
+            }
+            if (m_big < M && !small_m_fits(M - m_big, N, K)) m_big = M;
+        }
+        hipError_t e = fp8 ? dispatch_tiled<true>(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out,
+                                                  out_dtype, gelu, stream)
+                           : dispatch_tiled<false>(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out,
+                                                   out_dtype, gelu, stream);
+        if (e != hipSuccess || m_big == M) return e;
+        const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
+        return launch_linear_small_m(static_cast<const uint8_t*>(act_q) + static_cast<int64_t>(m_big) * K,
+                                     act_scales + m_big, M - m_big, K, w_q, w_scales, N, mode, bias,
+                                     static_cast<uint8_t*>(out) + static_cast<int64_t>(m_big) * N * esz,
+                                     out_dtype, gelu, 2, stream);
     }
     const int64_t total = static_cast<int64_t>(M) * N;
     const int blocks = static_cast<int>((total + 255) / 256);

@@ -290,3 +290,27 @@ def test_small_m_fp8(qimg, oracle, M, N, K):
     bound = 1e-5 * np.abs(ref).max() * np.sqrt(K / 64)
     assert np.max(np.abs(got.cpu().numpy() - ref)) <= bound
     assert np.max(np.abs(got_l.cpu().numpy() - ref)) <= bound
+
+
+@pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4400, 12288, 1024), (4352, 12288, 256)])
+def test_tail_round_split_exact(qimg, oracle, M, N, K):
+    """When the last round of 256x256 tiles would be mostly idle, the automatic
+    choice runs the trailing tile rows on the 64x64 kernel (here rows 4096..M).
+    The result is identical to the all-large-tile run and exact on sampled
+    rows from both parts (including the ragged end of M)."""
+    rng = np.random.default_rng(M + N + K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa = (rng.random(M) * 0.01 + 1e-3).astype(np.float32)
+    sw = (rng.random(N) * 0.01 + 1e-3).astype(np.float32)
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    ad, qw, bd, sd = _dev(a), _qw(qimg, w, sw, 1), _bf16_dev(b_bits), _dev(sa)
+    got = qimg.linear_forward_prequantized(ad, sd, qw, bd, apply_gelu=True)
+    with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
+        big = qimg.linear_forward_prequantized(ad, sd, qw, bd, apply_gelu=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), big.cpu().numpy())
+    idx = np.unique(np.concatenate([[0, 4095, 4096, M - 1], rng.integers(0, M, 12)]))
+    c = (a[idx].astype(np.float64) @ w.astype(np.float64).T).astype(np.int32)
+    ref = oracle.dequant_epilogue(c, sa[idx], sw, b_bits, gelu=True)
+    np.testing.assert_allclose(got.cpu().numpy()[idx], ref, rtol=2e-6, atol=2e-6)
