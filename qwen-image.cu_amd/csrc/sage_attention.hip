@@ -348,11 +348,15 @@ struct AttnCfg {
     static constexpr int KEEP = (ANSLOT - 2) * PER_WAVE;  // DMA instructions in flight at a hand-off
 };
 
-// physical 16-byte chunk of logical chunk c in row `row` (involution)
+// physical 16-byte chunk of logical chunk c in row `row` (involution).
+// ds_read_b128 serves 16 lanes per cycle from 64 banks (256 bytes); a
+// fragment read has 16 consecutive rows at one logical chunk, so the 16
+// physical (row, chunk) bank groups must differ: for 128-byte rows the rows
+// of each parity need distinct chunks, for 64-byte rows each residue mod 4.
 template <int CPR>
 __device__ __forceinline__ int swz_chunk(int row, int c) {
-    if constexpr (CPR == 8) return c ^ (row & 7);
-    else return c ^ ((row >> 1) & 3);
+    if constexpr (CPR == 8) return c ^ ((row >> 1) & 7);
+    else return c ^ swz_row(row);
 }
 
 // s_waitcnt vmcnt(n) (other counters untouched), and vmcnt(n) + lgkmcnt(0)
