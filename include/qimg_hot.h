@@ -184,6 +184,101 @@ int qimg_sage_attention(const uint16_t* q_f16, const uint16_t* k_f16, const uint
                         void* out, int out_dtype, float sm_scale, int BH, int S, int D,
                         int causal, void* scratch, int64_t scratch_bytes, void* stream);
 
+/* ---- MMDiT joint block: the operations around the hot path ------------ */
+
+/* silu_fp32 (cuda_kernels.cu:1881-1893): out[i] = x[i] / (1 + exp(-x[i])). */
+int qimg_silu(const float* x, float* out, int64_t n, void* stream);
+
+/* layer_norm_modulate_fp32 (cuda_kernels.cu:1799-1859), per row of `dim`:
+ * (x - mean) * rsqrt(var + eps) * (1 + scale) + shift, fp32 [rows, dim];
+ * dim a multiple of 4, at most 4096. */
+int qimg_layernorm_modulate(const float* x, const float* shift, const float* scale, float* out,
+                            int rows, int dim, float eps, void* stream);
+
+/* rms_norm_fp32 on the per-head Q or K rows (cuda_kernels.cu:1656-1692)
+ * + concat_transpose_fused_fp32 (transformer.cu:106-130, text tokens
+ * first) + rope_apply_fp32_to_fp16 (cuda_kernels.cu:1935-1971), fused:
+ * txt [n_txt, H*128] and img [n_img, H*128] fp32 -> out fp16
+ * [H, n_txt + n_img, 128]. norm_txt / norm_img are the bf16 [128] RMSNorm
+ * weights (norm_added_q / norm_q), pe is [n_txt + n_img, 64, 4] fp32
+ * (cos, -sin, sin, cos) as RoPE::gen_qwen_image_pe (rope.h:154-160) lays it
+ * out. With norm_txt == NULL only the concat/transpose/fp16 is applied (the
+ * V path, transformer.cu:649-650). */
+int qimg_joint_heads_f16(const float* txt, const float* img, const uint16_t* norm_txt,
+                         const uint16_t* norm_img, const float* pe, uint16_t* out, int n_txt, int n_img,
+                         int H, float eps, void* stream);
+
+/* transpose_split_fused_fp32 (transformer.cu:84-104) on an fp16 attention
+ * output [H, n_txt + n_img, 128]: -> txt [n_txt, H*128], img [n_img, H*128]
+ * fp32. */
+int qimg_split_heads(const uint16_t* attn_f16, float* txt, float* img, int n_txt, int n_img, int H,
+                     void* stream);
+
+/* gate_add_fp32f (cuda_kernels.cu:2181-2197): out[r,c] = x[r,c] +
+ * gate[c] * y[r,c], fp32 [rows, dim], dim a multiple of 4; out may be x. */
+int qimg_gate_add(const float* x, const float* gate, const float* y, float* out, int rows, int dim,
+                  void* stream);
+
+/* One quantized linear of a block: weight [N, K] (int8 or e4m3 bytes),
+ * fp32 scales [N], Hadamard block size, mode, bf16 bias [N] or NULL. */
+typedef struct {
+    const void* w;
+    const float* scales;
+    int N, K, hbs, mode;
+    const uint16_t* bias;
+} qimg_qlinear;
+
+/* The weights of one MMDiT joint block, field for field as
+ * TransformerWeights::Block (transformer.h:89-140): hidden 3072 (24 heads
+ * of 128), MLP 12288, modulation 6 x 3072 per stream. */
+typedef struct {
+    qimg_qlinear img_mod, txt_mod;
+    qimg_qlinear to_q, to_k, to_v, add_q_proj, add_k_proj, add_v_proj;
+    qimg_qlinear to_out, to_add_out;
+    qimg_qlinear img_mlp_fc1, img_mlp_fc2, txt_mlp_fc1, txt_mlp_fc2;
+    const uint16_t* norm_q;        /* bf16 [128] */
+    const uint16_t* norm_k;
+    const uint16_t* norm_added_q;
+    const uint16_t* norm_added_k;
+} qimg_mmdit_block;
+
+/* Profile categories of qimg_mmdit_block_forward, in the order of the
+ * reference's PROFILE_BLOCK report (transformer.cu:843-857). RMSNorm,
+ * concat/transpose and RoPE of Q/K run as one fused kernel here: its time
+ * is reported under QK_NORM, the V concat/transpose under
+ * CONCAT_TRANSPOSE, and ROPE stays 0. */
+enum {
+    QIMG_PROF_MODULATION = 0,
+    QIMG_PROF_ATTN_NORM,
+    QIMG_PROF_QKV_GEMM,
+    QIMG_PROF_QK_NORM,
+    QIMG_PROF_CONCAT_TRANSPOSE,
+    QIMG_PROF_ROPE,
+    QIMG_PROF_ATTENTION,
+    QIMG_PROF_TRANSPOSE_SPLIT,
+    QIMG_PROF_OUT_GEMM,
+    QIMG_PROF_GATE_ATTN,
+    QIMG_PROF_MLP_NORM,
+    QIMG_PROF_MLP_GEMM,
+    QIMG_PROF_GATE_MLP,
+    QIMG_PROF_COUNT
+};
+
+/* Scratch bytes for qimg_mmdit_block_forward at n_img + n_txt tokens. */
+int64_t qimg_mmdit_block_scratch_bytes(int n_img, int n_txt);
+
+/* One iteration of the MMDiT joint-block loop (transformer.cu:506-817):
+ * modulation from silu(t_emb), LayerNorm + modulate, shared-quant QKV
+ * linears, per-head RMSNorm + RoPE, joint SageAttention (text tokens
+ * first), out-projections, gated residual, LayerNorm + modulate, GELU MLP,
+ * gated residual. img [n_img, 3072] and txt [n_txt, 3072] fp32 are updated
+ * in place; t_emb is fp32 [3072]; pe is [n_txt + n_img, 64, 4] fp32. With
+ * prof_ms != NULL the stream is synchronised once at the end and the
+ * QIMG_PROF_COUNT category times (ms) are written there. */
+int qimg_mmdit_block_forward(const qimg_mmdit_block* block, float* img, float* txt, const float* t_emb,
+                             const float* pe, int n_img, int n_txt, void* scratch, int64_t scratch_bytes,
+                             float* prof_ms, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,7 +42,8 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function",
 ]
 
-SOURCES = ["hadamard_quant.hip", "gemm_w8a8.hip", "gemm_small_m.hip", "sage_attention.hip", "capi.hip"]
+SOURCES = ["hadamard_quant.hip", "gemm_w8a8.hip", "gemm_small_m.hip", "sage_attention.hip", "block_ops.hip",
+           "mmdit_block.hip", "capi.hip"]
 HOST_SOURCES = ["kernels.cpp"]
 
 

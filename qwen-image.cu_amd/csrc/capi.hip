@@ -302,4 +302,127 @@ int qimg_sage_attention(const uint16_t* q_f16, const uint16_t* k_f16, const uint
                       fn);
 }
 
+
+/* ---- MMDiT joint block ------------------------------------------------ */
+
+int qimg_silu(const float* x, float* out, int64_t n, void* stream) {
+    const char* fn = "qimg_silu";
+    QIMG_REQUIRE(n >= 0, "%s: bad n=%lld", fn, static_cast<long long>(n));
+    if (n == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && out, "%s: null pointer", fn);
+    return hip_status(qimg::launch_silu(x, out, n, static_cast<hipStream_t>(stream)), fn);
+}
+
+int qimg_layernorm_modulate(const float* x, const float* shift, const float* scale, float* out, int rows, int dim,
+                            float eps, void* stream) {
+    const char* fn = "qimg_layernorm_modulate";
+    QIMG_REQUIRE(rows >= 0 && dim > 0 && dim % 4 == 0 && dim <= 4096,
+                 "%s: need rows >= 0 and dim a multiple of 4 in (0, 4096] (rows=%d dim=%d)", fn, rows, dim);
+    if (rows == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && shift && scale && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(x) && aligned16(shift) && aligned16(scale) && aligned16(out),
+                 "%s: buffers must be 16-byte aligned", fn);
+    return hip_status(qimg::launch_layernorm_modulate(x, shift, scale, out, rows, dim, eps,
+                                                      static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+static int check_heads(const char* fn, int n_txt, int n_img, int H) {
+    QIMG_REQUIRE(n_txt >= 0 && n_img >= 0 && H > 0, "%s: bad sizes n_txt=%d n_img=%d H=%d", fn, n_txt, n_img, H);
+    QIMG_REQUIRE(static_cast<int64_t>(n_txt + n_img) * H * 128 < (int64_t{1} << 31), "%s: too many elements", fn);
+    return QIMG_OK;
+}
+
+int qimg_joint_heads_f16(const float* txt, const float* img, const uint16_t* norm_txt, const uint16_t* norm_img,
+                         const float* pe, uint16_t* out, int n_txt, int n_img, int H, float eps, void* stream) {
+    const char* fn = "qimg_joint_heads_f16";
+    int st = check_heads(fn, n_txt, n_img, H);
+    if (st) return st;
+    if (n_txt + n_img == 0) return QIMG_OK;
+    QIMG_REQUIRE(out && (txt || n_txt == 0) && (img || n_img == 0), "%s: null pointer", fn);
+    QIMG_REQUIRE((norm_txt == nullptr) == (norm_img == nullptr), "%s: give both RMSNorm weights or neither", fn);
+    QIMG_REQUIRE(norm_txt == nullptr || pe != nullptr, "%s: RMSNorm + RoPE needs pe", fn);
+    return hip_status(qimg::launch_joint_heads_f16(txt, img, norm_txt, norm_img, pe, out, n_txt, n_img, H, eps,
+                                                   static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
+int qimg_split_heads(const uint16_t* attn_f16, float* txt, float* img, int n_txt, int n_img, int H, void* stream) {
+    const char* fn = "qimg_split_heads";
+    int st = check_heads(fn, n_txt, n_img, H);
+    if (st) return st;
+    if (n_txt + n_img == 0) return QIMG_OK;
+    QIMG_REQUIRE(attn_f16 && (txt || n_txt == 0) && (img || n_img == 0), "%s: null pointer", fn);
+    return hip_status(
+        qimg::launch_split_heads(attn_f16, txt, img, n_txt, n_img, H, static_cast<hipStream_t>(stream)), fn);
+}
+
+int qimg_gate_add(const float* x, const float* gate, const float* y, float* out, int rows, int dim, void* stream) {
+    const char* fn = "qimg_gate_add";
+    QIMG_REQUIRE(rows >= 0 && dim > 0 && dim % 4 == 0, "%s: need dim a multiple of 4 (rows=%d dim=%d)", fn, rows,
+                 dim);
+    if (rows == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && gate && y && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(x) && aligned16(gate) && aligned16(y) && aligned16(out),
+                 "%s: buffers must be 16-byte aligned", fn);
+    return hip_status(qimg::launch_gate_add(x, gate, y, out, rows, dim, static_cast<hipStream_t>(stream)), fn);
+}
+
+int64_t qimg_mmdit_block_scratch_bytes(int n_img, int n_txt) {
+    if (n_img < 0 || n_txt < 0 || n_img + n_txt == 0) return 0;
+    return qimg::mmdit_block_scratch_layout(n_img, n_txt, nullptr, nullptr);
+}
+
+static int check_qlinear(const char* fn, const char* name, const qimg_qlinear& l, int N, int K) {
+    QIMG_REQUIRE(l.w && l.scales, "%s: %s: null weight", fn, name);
+    QIMG_REQUIRE(l.N == N && l.K == K, "%s: %s is [%d, %d], expected [%d, %d]", fn, name, l.N, l.K, N, K);
+    QIMG_REQUIRE(l.mode == QIMG_QM_INT8_HADAMARD || l.mode == QIMG_QM_FP8_HADAMARD, "%s: %s: bad mode %d", fn, name,
+                 l.mode);
+    QIMG_REQUIRE(l.hbs == (K & -K), "%s: %s: hbs %d must be K & -K = %d", fn, name, l.hbs, K & -K);
+    QIMG_REQUIRE(aligned16(l.w) && aligned16(l.scales), "%s: %s: weights must be 16-byte aligned", fn, name);
+    return QIMG_OK;
+}
+
+int qimg_mmdit_block_forward(const qimg_mmdit_block* b, float* img, float* txt, const float* t_emb, const float* pe,
+                             int n_img, int n_txt, void* scratch, int64_t scratch_bytes, float* prof_ms,
+                             void* stream) {
+    const char* fn = "qimg_mmdit_block_forward";
+    QIMG_REQUIRE(b != nullptr, "%s: null block", fn);
+    QIMG_REQUIRE(n_img >= 0 && n_txt >= 0 && n_img + n_txt > 0, "%s: bad token counts n_img=%d n_txt=%d", fn,
+                 n_img, n_txt);
+    QIMG_REQUIRE(static_cast<int64_t>(n_img + n_txt) * 3072 < (int64_t{1} << 31) &&
+                     static_cast<int64_t>(n_img > n_txt ? n_img : n_txt) * 12288 < (int64_t{1} << 31),
+                 "%s: too many tokens", fn);
+    QIMG_REQUIRE((img || n_img == 0) && (txt || n_txt == 0) && t_emb && pe, "%s: null pointer", fn);
+    QIMG_REQUIRE((n_img == 0 || aligned16(img)) && (n_txt == 0 || aligned16(txt)),
+                 "%s: img/txt must be 16-byte aligned", fn);
+    QIMG_REQUIRE(b->norm_q && b->norm_k && b->norm_added_q && b->norm_added_k, "%s: null RMSNorm weight", fn);
+    const int D = 3072, F = 12288;
+    struct {
+        const char* name;
+        const qimg_qlinear* l;
+        int N, K;
+    } lin[] = {{"img_mod", &b->img_mod, 6 * D, D},      {"txt_mod", &b->txt_mod, 6 * D, D},
+               {"to_q", &b->to_q, D, D},                {"to_k", &b->to_k, D, D},
+               {"to_v", &b->to_v, D, D},                {"add_q_proj", &b->add_q_proj, D, D},
+               {"add_k_proj", &b->add_k_proj, D, D},    {"add_v_proj", &b->add_v_proj, D, D},
+               {"to_out", &b->to_out, D, D},            {"to_add_out", &b->to_add_out, D, D},
+               {"img_mlp_fc1", &b->img_mlp_fc1, F, D},  {"img_mlp_fc2", &b->img_mlp_fc2, D, F},
+               {"txt_mlp_fc1", &b->txt_mlp_fc1, F, D},  {"txt_mlp_fc2", &b->txt_mlp_fc2, D, F}};
+    for (const auto& e : lin) {
+        int st = check_qlinear(fn, e.name, *e.l, e.N, e.K);
+        if (st) return st;
+    }
+    const int64_t need = qimg::mmdit_block_scratch_layout(n_img, n_txt, nullptr, nullptr);
+    if (!scratch || scratch_bytes < need)
+        return fail(QIMG_ERR_SCRATCH, "%s: scratch %lld bytes < required %lld", fn,
+                    static_cast<long long>(scratch_bytes), static_cast<long long>(need));
+    QIMG_REQUIRE(aligned16(scratch), "%s: scratch must be 16-byte aligned", fn);
+    qimg::BlockScratch ws;
+    qimg::mmdit_block_scratch_layout(n_img, n_txt, scratch, &ws);
+    return hip_status(
+        qimg::run_mmdit_block(*b, img, txt, t_emb, pe, n_img, n_txt, ws, prof_ms, static_cast<hipStream_t>(stream)),
+        fn);
+}
+
 }  // extern "C"

@@ -60,4 +60,39 @@ hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
                             int BH, int S, int D, float sm_scale, int causal, uint16_t* v_t,
                             hipStream_t stream);
 
+
+// block_ops.hip
+hipError_t launch_silu(const float* x, float* out, int64_t n, hipStream_t stream);
+hipError_t launch_layernorm_modulate(const float* x, const float* shift, const float* scale, float* out, int rows,
+                                     int dim, float eps, hipStream_t stream);
+hipError_t launch_joint_heads_f16(const float* txt, const float* img, const uint16_t* w_txt, const uint16_t* w_img,
+                                  const float* pe, uint16_t* out, int n_txt, int n_img, int H, float eps,
+                                  hipStream_t stream);
+hipError_t launch_split_heads(const uint16_t* in, float* txt, float* img, int n_txt, int n_img, int H,
+                              hipStream_t stream);
+hipError_t launch_gate_add(const float* x, const float* gate, const float* y, float* out, int rows, int dim,
+                           hipStream_t stream);
+
+// mmdit_block.hip
+struct BlockScratch {
+    float* t_silu;
+    float* img_mods;
+    float* txt_mods;
+    float* img_norm;
+    float* txt_norm;
+    uint8_t* act_q;
+    float* act_scales;
+    float* img_qkv[3];
+    float* txt_qkv[3];
+    uint16_t* qkv16[3];
+    uint16_t* attn16;
+    float* img_mlp;
+    float* txt_mlp;
+    uint8_t* sage;
+    int64_t sage_bytes;
+};
+int64_t mmdit_block_scratch_layout(int n_img, int n_txt, void* base, BlockScratch* out);
+hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
+                           int n_img, int n_txt, const BlockScratch& w, float* prof_ms, hipStream_t s);
+
 }  // namespace qimg

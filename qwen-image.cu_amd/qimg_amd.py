@@ -49,6 +49,13 @@ _SIGS = {
     "qimg_sage_quant_k": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "qimg_sage_attn_quantized": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P, _I64, _P]),
     "qimg_sage_attention": (_I, [_P, _P, _P, _P, _I, _F, _I, _I, _I, _I, _P, _I64, _P]),
+    "qimg_silu": (_I, [_P, _P, _I64, _P]),
+    "qimg_layernorm_modulate": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "qimg_joint_heads_f16": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
+    "qimg_split_heads": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "qimg_gate_add": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "qimg_mmdit_block_scratch_bytes": (_I64, [_I, _I]),
+    "qimg_mmdit_block_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _I64, _P, _P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -311,3 +318,142 @@ def attention_forward_sage_fp16io(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     _check(_lib.qimg_sage_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _DT[out.dtype], float(scale),
                                     BH, S, D, int(bool(causal)), _ptr(scratch), scratch.numel(), _stream()))
     return out
+
+
+# ------------------------------------------------------- MMDiT joint block
+HIDDEN, HEADS, HEAD_DIM, MLP_DIM = 3072, 24, 128, 12288
+PROF_CATEGORIES = ("modulation", "attn_norm", "qkv_gemm", "qk_norm", "concat_transpose", "rope", "attention",
+                   "transpose_split", "out_gemm", "gate_attn", "mlp_norm", "mlp_gemm", "gate_mlp")
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """silu_fp32 (cuda_kernels.cu:1881-1893)."""
+    _dev(x, "x")
+    out = torch.empty_like(x)
+    _check(_lib.qimg_silu(_ptr(x), _ptr(out), x.numel(), _stream()))
+    return out
+
+
+def layer_norm_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """layer_norm_modulate_fp32 (cuda_kernels.cu:1799-1859): fp32 [rows, dim]."""
+    _dev(x, "x")
+    rows, dim = x.shape
+    out = torch.empty_like(x)
+    _check(_lib.qimg_layernorm_modulate(_ptr(x), _ptr(shift), _ptr(scale), _ptr(out), rows, dim, float(eps),
+                                        _stream()))
+    return out
+
+
+def joint_heads_f16(txt: torch.Tensor, img: torch.Tensor, norm_txt=None, norm_img=None, pe=None,
+                    eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm per head + txt-first concat + [S,H,D] -> [H,S,D] + RoPE -> fp16
+    (cuda_kernels.cu:1656-1692, transformer.cu:106-130, cuda_kernels.cu:1935-1971).
+    Without norm weights only the concat/transpose/fp16 (the V path)."""
+    n_txt, n_img = txt.shape[0], img.shape[0]
+    H = txt.shape[1] // HEAD_DIM
+    out = torch.empty((H, n_txt + n_img, HEAD_DIM), dtype=torch.float16, device=txt.device)
+    _check(_lib.qimg_joint_heads_f16(_ptr(txt), _ptr(img), _ptr(norm_txt), _ptr(norm_img), _ptr(pe), _ptr(out),
+                                     n_txt, n_img, H, float(eps), _stream()))
+    return out
+
+
+def split_heads(attn: torch.Tensor, n_txt: int):
+    """transpose_split_fused_fp32 (transformer.cu:84-104) from fp16 [H,S,128]."""
+    H, S, _ = attn.shape
+    txt = torch.empty((n_txt, H * HEAD_DIM), dtype=torch.float32, device=attn.device)
+    img = torch.empty((S - n_txt, H * HEAD_DIM), dtype=torch.float32, device=attn.device)
+    _check(_lib.qimg_split_heads(_ptr(attn), _ptr(txt), _ptr(img), n_txt, S - n_txt, H, _stream()))
+    return txt, img
+
+
+def gate_add(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """gate_add_fp32f (cuda_kernels.cu:2181-2197): x + gate[c] * y."""
+    rows, dim = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    _check(_lib.qimg_gate_add(_ptr(x), _ptr(gate), _ptr(y), _ptr(out), rows, dim, _stream()))
+    return out
+
+
+def qwen_image_pe(h: int, w: int, patch_size: int = 2, context_len: int = 256, theta: float = 10000.0,
+                  axes_dim=(16, 56, 56)):
+    """RoPE::gen_qwen_image_pe (rope.h:154-160) for batch 1: [context_len +
+    (h/p)*(w/p), 64, 4] float32 rows of (cos, -sin, sin, cos), text tokens
+    first. Host-side, in float32 like the reference's std::vector<float>."""
+    import numpy as np
+
+    h_len = (h + patch_size // 2) // patch_size
+    w_len = (w + patch_size // 2) // patch_size
+    t0 = max(h_len, w_len)
+    f32 = np.float32
+
+    def linspace(a, b, n):
+        if n == 1:
+            return np.array([a], f32)
+        step = f32((f32(b) - f32(a)) / f32(n - 1))
+        return np.array([f32(a) + f32(i) * step for i in range(n)], f32)
+
+    txt = linspace(t0, context_len + t0, context_len)
+    ids = [np.stack([txt, txt, txt], 1)]
+    rows = linspace(-(h_len // 2), -(h_len // 2) + h_len - 1, h_len)
+    cols = linspace(-(w_len // 2), -(w_len // 2) + w_len - 1, w_len)
+    img = np.zeros((h_len * w_len, 3), f32)
+    img[:, 1] = np.repeat(rows, w_len)
+    img[:, 2] = np.tile(cols, h_len)
+    ids = np.concatenate(ids + [img], 0)
+    parts = []
+    for axis, dim in enumerate(axes_dim):
+        half = dim // 2
+        scale = linspace(0.0, (dim * 1.0 - 2.0) / dim, half)
+        omega = np.array([f32(1.0) / f32(np.power(np.float32(theta), s, dtype=np.float32)) for s in scale], f32)
+        ang = (ids[:, axis:axis + 1] * omega[None, :]).astype(f32)
+        c, s = np.cos(ang).astype(f32), np.sin(ang).astype(f32)
+        parts.append(np.stack([c, -s, s, c], -1))
+    return np.ascontiguousarray(np.concatenate(parts, 1), dtype=np.float32)
+
+
+class _QLinear(ctypes.Structure):
+    _fields_ = [("w", _P), ("scales", _P), ("N", _I), ("K", _I), ("hbs", _I), ("mode", _I), ("bias", _P)]
+
+
+_BLOCK_LINEARS = ("img_mod", "txt_mod", "to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj",
+                  "to_out", "to_add_out", "img_mlp_fc1", "img_mlp_fc2", "txt_mlp_fc1", "txt_mlp_fc2")
+_BLOCK_NORMS = ("norm_q", "norm_k", "norm_added_q", "norm_added_k")
+
+
+class _Block(ctypes.Structure):
+    _fields_ = [(n, _QLinear) for n in _BLOCK_LINEARS] + [(n, _P) for n in _BLOCK_NORMS]
+
+
+def mmdit_block_scratch_bytes(n_img: int, n_txt: int) -> int:
+    return int(_lib.qimg_mmdit_block_scratch_bytes(int(n_img), int(n_txt)))
+
+
+def mmdit_block_forward(weights: dict, biases: dict, norms: dict, img: torch.Tensor, txt: torch.Tensor,
+                        t_emb: torch.Tensor, pe: torch.Tensor, scratch: torch.Tensor | None = None,
+                        profile: bool = False):
+    """One MMDiT joint block (transformer.cu:506-817), img [n_img, 3072] and
+    txt [n_txt, 3072] fp32 updated in place. `weights` maps the names of
+    TransformerWeights::Block (img_mod, to_q, ..., txt_mlp_fc2) to
+    QuantizedWeight, `biases` the same names to bf16 [N] tensors, `norms`
+    norm_q / norm_k / norm_added_q / norm_added_k to bf16 [128]. With
+    profile=True returns {category: ms} (the stream is synchronised)."""
+    b = _Block()
+    for n in _BLOCK_LINEARS:
+        qw = weights[n]
+        N, K = qw.data.shape
+        bias = biases.get(n)
+        setattr(b, n, _QLinear(qw.data.data_ptr(), qw.scales.data_ptr(), N, K, int(qw.had_block_size),
+                               int(qw.mode), bias.data_ptr() if bias is not None else None))
+    for n in _BLOCK_NORMS:
+        setattr(b, n, norms[n].data_ptr())
+    n_img, n_txt = img.shape[0], txt.shape[0]
+    if scratch is None:
+        scratch = torch.empty((mmdit_block_scratch_bytes(n_img, n_txt),), dtype=torch.uint8, device=img.device)
+    prof = (ctypes.c_float * len(PROF_CATEGORIES))() if profile else None
+    _check(_lib.qimg_mmdit_block_forward(ctypes.addressof(b), _ptr(img), _ptr(txt), _ptr(t_emb), _ptr(pe), n_img,
+                                         n_txt, _ptr(scratch), scratch.numel(),
+                                         ctypes.addressof(prof) if profile else None, _stream()))
+    if profile:
+        return {n: float(prof[i]) for i, n in enumerate(PROF_CATEGORIES)}
+    return None

@@ -1,0 +1,280 @@
+"""GPU parity of the MMDiT joint block (transformer.cu:506-817) and its
+element-wise / per-row operations, against the CPU restatement in
+oracle/block.py on the same seeded inputs.
+
+Tolerances: the glue operations reduce in fp32 trees on the GPU and in
+float64 in the oracle, so they agree to a few fp32 ulp (fp16 outputs to about
+one fp16 ulp). The block is checked stage by stage on identical inputs (each
+operation at its own bar, and the fused entry point bit-identical to the
+composition), and end to end against the oracle's own sensitivity to
+rounding-level perturbations (see the test's docstring).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _bf16_dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(DEV).view(torch.bfloat16)
+
+
+def _metrics(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    rel = np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30)
+    cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+    return rel, cos
+
+
+@pytest.fixture(scope="module")
+def blk():
+    from oracle import block
+    return block
+
+
+def test_silu(qimg, blk):
+    x = np.random.default_rng(1).standard_normal(3072 * 7 + 5).astype(np.float32) * 4
+    got = qimg.silu(_dev(x)).cpu().numpy()
+    np.testing.assert_allclose(got, blk.silu(x), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 3072), (300, 3072), (7, 4096), (5, 1024)])
+def test_layer_norm_modulate(qimg, blk, rows, dim):
+    rng = np.random.default_rng(rows + dim)
+    x = (rng.standard_normal((rows, dim)) * 3 + 0.5).astype(np.float32)
+    shift = rng.standard_normal(dim).astype(np.float32)
+    scale = (rng.standard_normal(dim) * 0.3).astype(np.float32)
+    got = qimg.layer_norm_modulate(_dev(x), _dev(shift), _dev(scale)).cpu().numpy()
+    ref = blk.layer_norm_modulate(x, shift, scale)
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize("n_txt,n_img", [(64, 256), (0, 96), (7, 0), (256, 4096)])
+def test_joint_heads_norm_rope_and_split(qimg, blk, n_txt, n_img):
+    rng = np.random.default_rng(n_txt * 7 + n_img)
+    txt = rng.standard_normal((n_txt, 3072)).astype(np.float32)
+    img = rng.standard_normal((n_img, 3072)).astype(np.float32) * 2
+    from oracle import oracle as o
+    w_txt = o.bf16_bits_from_f32((1 + rng.standard_normal(128) * 0.1).astype(np.float32))
+    w_img = o.bf16_bits_from_f32((1 + rng.standard_normal(128) * 0.1).astype(np.float32))
+    S = n_txt + n_img
+    pe = qimg.qwen_image_pe(32, 32, 2, 64)
+    pe = np.resize(pe, (S, 64, 4)).astype(np.float32) if S else pe[:0]
+    got = qimg.joint_heads_f16(_dev(txt), _dev(img), _bf16_dev(w_txt), _bf16_dev(w_img), _dev(pe))
+    v16 = qimg.joint_heads_f16(_dev(txt), _dev(img))
+    torch.cuda.synchronize()
+    if S == 0:
+        return
+    ref = blk.rope_f16(blk.concat_transpose(blk.rms_norm_heads(txt, w_txt), blk.rms_norm_heads(img, w_img)), pe)
+    # one fp16 rounding of the value, plus a small absolute term for RoPE
+    # pairs that nearly cancel (fp32 reduction and FMA order differ)
+    g = got.cpu().numpy().astype(np.float64)
+    r = ref.astype(np.float64)
+    assert np.all(np.abs(g - r) <= 2.0 ** -10 * np.abs(r) + 2.0 ** -14 * np.abs(r).max())
+    np.testing.assert_array_equal(v16.cpu().numpy(), blk.concat_transpose(txt, img).astype(np.float16))
+    # split is the exact inverse of the V concat/transpose (fp16 -> fp32)
+    st, si = qimg.split_heads(v16, n_txt)
+    rt, ri = blk.split(v16.cpu().numpy(), n_txt)
+    np.testing.assert_array_equal(st.cpu().numpy(), rt)
+    np.testing.assert_array_equal(si.cpu().numpy(), ri)
+
+
+def test_gate_add_in_place(qimg, blk):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((300, 3072)).astype(np.float32)
+    y = rng.standard_normal((300, 3072)).astype(np.float32)
+    g = rng.standard_normal(3072).astype(np.float32)
+    xd = _dev(x)
+    qimg.gate_add(xd, _dev(g), _dev(y), out=xd)
+    np.testing.assert_allclose(xd.cpu().numpy(), blk.gate_add(x, g, y), rtol=1e-6, atol=1e-6)
+
+
+def _random_block(qimg, oracle, rng, mode=0):
+    """Random N(0,0.02) block weights (bf16 -> library quantization) and
+    N(0,0.01) biases; returns (device dicts, oracle dict)."""
+    shapes = {"img_mod": (18432, 3072), "txt_mod": (18432, 3072)}
+    for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
+        shapes[n] = (3072, 3072)
+    for s in ("img", "txt"):
+        shapes[f"{s}_mlp_fc1"] = (12288, 3072)
+        shapes[f"{s}_mlp_fc2"] = (3072, 12288)
+    weights, biases, norms, ref = {}, {}, {}, {}
+    for n, (N, K) in shapes.items():
+        w = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        b = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+        qw = qimg.quantize_weight_tensor(_bf16_dev(w), mode=mode)
+        weights[n], biases[n] = qw, _bf16_dev(b)
+        if mode == 0:
+            wq, ws, hbs = oracle.quantize_weight_bf16(w)
+            np.testing.assert_array_equal(qw.data.cpu().numpy(), wq)
+            ref[n] = (wq, ws, hbs, b)
+    for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+        bits = oracle.bf16_bits_from_f32((1 + rng.standard_normal(128) * 0.1).astype(np.float32))
+        norms[n], ref[n] = _bf16_dev(bits), bits
+    return weights, biases, norms, ref
+
+
+@pytest.fixture(scope="module")
+def int8_block(qimg, oracle):
+    return _random_block(qimg, oracle, np.random.default_rng(2024))
+
+
+def _block_inputs(qimg, rng, n_img, n_txt):
+    img = rng.standard_normal((n_img, 3072)).astype(np.float32)
+    txt = rng.standard_normal((n_txt, 3072)).astype(np.float32)
+    t_emb = rng.standard_normal(3072).astype(np.float32)
+    h = w = int(np.sqrt(n_img)) * 2
+    pe = qimg.qwen_image_pe(h, w, 2, n_txt)
+    assert pe.shape == (n_img + n_txt, 64, 4)
+    return img, txt, t_emb, pe
+
+
+def _close(got, want, rel_max, cos_min, what):
+    rel, cos = _metrics(got, want)
+    assert rel <= rel_max and cos >= cos_min, (what, rel, cos)
+
+
+BLOCK_SIZES = [(256, 64), (64, 0)]
+
+
+@pytest.mark.parametrize("n_img,n_txt", BLOCK_SIZES)
+def test_mmdit_block_stagewise(qimg, oracle, blk, int8_block, n_img, n_txt):
+    """Every stage of the block (transformer.cu:506-817) run through the
+    C-ABI operations and checked against the oracle on the GPU's own inputs
+    of that stage, at that operation's bar; then the fused block entry point
+    must reproduce the composition bit for bit.
+
+    On identical inputs the activation int8 values and scales are bit-exact,
+    so a quantized linear differs only by the fp32 epilogue rounding
+    (rel <= 1e-5); the attention is held to max-rel 2e-2 / cos 0.999."""
+    W, B, N, ref = int8_block
+    img, txt, t_emb, pe = _block_inputs(qimg, np.random.default_rng(n_img + 31 * n_txt), n_img, n_txt)
+    D = 3072
+    h = lambda t: t.cpu().numpy()
+
+    def lin(x, name, gelu=False):
+        got = qimg.linear_forward_quantized(x, W[name], B[name], apply_gelu=gelu)
+        wq, ws, hbs, b = ref[name]
+        _close(h(got), oracle.linear_w8a8(h(x), wq, ws, hbs, b, gelu=gelu), 1e-5, 0.9999999, name)
+        return got
+
+    def ln(x, shift, scale):
+        got = qimg.layer_norm_modulate(x, shift.contiguous(), scale.contiguous())
+        np.testing.assert_allclose(h(got), blk.layer_norm_modulate(h(x), h(shift), h(scale)), rtol=2e-5, atol=2e-5)
+        return got
+
+    def gate(x, g, y):
+        got = qimg.gate_add(x, g.contiguous(), y)
+        np.testing.assert_allclose(h(got), blk.gate_add(h(x), h(g), h(y)), rtol=1e-6, atol=1e-6)
+        return got
+
+    streams = {"img": (_dev(img), "img_mod", ("to_q", "to_k", "to_v"), "to_out", "img_mlp"),
+               "txt": (_dev(txt), "txt_mod", ("add_q_proj", "add_k_proj", "add_v_proj"), "to_add_out", "txt_mlp")}
+    ts = qimg.silu(_dev(t_emb))
+    np.testing.assert_allclose(h(ts), blk.silu(t_emb), rtol=2e-6, atol=1e-7)
+    mods, qkv, normed = {}, {}, {}
+    for s, (x, mod, names, _, _) in streams.items():
+        mods[s] = lin(ts.view(1, D), mod).view(6, D)
+        if x.shape[0] == 0:
+            qkv[s] = [torch.empty((0, D), device=DEV)] * 3
+            continue
+        normed[s] = ln(x, mods[s][0], mods[s][1])
+        qkv[s] = [lin(normed[s], n) for n in names]
+    pe_d = _dev(pe)
+    heads = []
+    for i, (wt, wi) in enumerate((("norm_added_q", "norm_q"), ("norm_added_k", "norm_k"))):
+        got = qimg.joint_heads_f16(qkv["txt"][i], qkv["img"][i], N[wt], N[wi], pe_d)
+        want = blk.rope_f16(blk.concat_transpose(blk.rms_norm_heads(h(qkv["txt"][i]), ref[wt]),
+                                                 blk.rms_norm_heads(h(qkv["img"][i]), ref[wi])), pe)
+        g, r = h(got).astype(np.float64), want.astype(np.float64)
+        assert np.all(np.abs(g - r) <= 2.0 ** -10 * np.abs(r) + 2.0 ** -14 * np.abs(r).max())
+        heads.append(got)
+    v16 = qimg.joint_heads_f16(qkv["txt"][2], qkv["img"][2])
+    np.testing.assert_array_equal(h(v16), blk.concat_transpose(h(qkv["txt"][2]), h(qkv["img"][2])).astype(np.float16))
+    att = qimg.attention_forward_sage_fp16io(heads[0], heads[1], v16, 1 / np.sqrt(128.0), out_dtype=torch.float16)
+    want = oracle.sage_attention_fp16io(h(heads[0]), h(heads[1]), h(v16), 1 / np.sqrt(128.0), False)
+    _close(h(att).astype(np.float32), want.astype(np.float32), 2e-2, 0.999, "attention")
+    split = dict(zip(("txt", "img"), qimg.split_heads(att, n_txt)))
+    for s, want in zip(("txt", "img"), blk.split(h(att), n_txt)):
+        np.testing.assert_array_equal(h(split[s]), want)
+    final = {}
+    for s, (x, _, _, out_name, mlp) in streams.items():
+        if x.shape[0] == 0:
+            final[s] = x
+            continue
+        m = mods[s]
+        x1 = gate(x, m[2], lin(split[s], out_name))
+        y = lin(lin(ln(x1, m[3], m[4]), f"{mlp}_fc1", gelu=True), f"{mlp}_fc2")
+        final[s] = gate(x1, m[5], y)
+    img_d, txt_d = _dev(img), _dev(txt)
+    qimg.mmdit_block_forward(W, B, N, img_d, txt_d, _dev(t_emb), pe_d)
+    torch.cuda.synchronize()
+    assert torch.equal(img_d, final["img"])
+    assert torch.equal(txt_d, final["txt"])
+
+
+@pytest.mark.parametrize("n_img,n_txt", BLOCK_SIZES)
+def test_mmdit_block_within_oracle_noise_floor(qimg, oracle, blk, int8_block, n_img, n_txt):
+    """End to end against the oracle block on the same inputs.
+
+    The block amplifies rounding-level differences: a change far below the
+    kernels' tolerances (even one fp32 ulp) flips int8 roundings of the
+    activation quantization, and at the fc2 input the step is coarse (after
+    the FWHT the DC coefficient of the non-negative-mean GELU output sets the
+    row maximum), so flips move whole quantization steps. The oracle itself,
+    given the image stream perturbed by 1e-6 relative noise, moves by
+    max-rel ~0.03, cos ~0.9997 at these sizes. The GPU block is held to
+    cos >= 0.999 and to within 2.5x the oracle's own spread measured here."""
+    W, B, N, ref = int8_block
+    rng = np.random.default_rng(n_img + 31 * n_txt)
+    img, txt, t_emb, pe = _block_inputs(qimg, rng, n_img, n_txt)
+    img_d, txt_d = _dev(img), _dev(txt)
+    prof = qimg.mmdit_block_forward(W, B, N, img_d, txt_d, _dev(t_emb), _dev(pe), profile=True)
+    torch.cuda.synchronize()
+    assert set(prof) == set(qimg.PROF_CATEGORIES) and all(v >= 0 for v in prof.values())
+    ri, rt = blk.mmdit_block(ref, img, txt, t_emb, pe)
+    img_p = (img * (1 + 1e-6 * rng.standard_normal(img.shape))).astype(np.float32)
+    pi, pt = blk.mmdit_block(ref, img_p, txt, t_emb, pe)
+    for got, want, pert in ((img_d.cpu().numpy(), ri, pi), (txt_d.cpu().numpy(), rt, pt)):
+        if want.size == 0:
+            continue
+        assert np.all(np.isfinite(got))
+        rel, cos = _metrics(got, want)
+        rel_self, cos_self = _metrics(pert, want)
+        assert cos >= 0.999, (rel, cos)
+        assert rel <= max(2e-2, 2.5 * rel_self), (rel, rel_self)
+        assert 1 - cos <= max(1e-5, 2.5 * (1 - cos_self)), (cos, cos_self)
+
+
+def test_mmdit_block_fp8_runs_close_to_int8(qimg, oracle, int8_block):
+    """e4m3 weights through the same block: finite, deterministic, and close
+    to the int8 block (both approximate the same bf16 weights). The fp8 linear
+    itself is pinned against the oracle in the GEMM tests; here e4m3's 3-bit
+    mantissa rounds weights and activations with ~3.6% rms relative error
+    (per-row int8 over a Gaussian row: ~1%), compounded over the stacked
+    linears of the residual branches, so the two blocks agree to cos ~0.995."""
+    rng = np.random.default_rng(77)
+    n_img, n_txt = 64, 16
+    w8, b8, nr, _ = int8_block
+    wf, bf, nf, _ = _random_block(qimg, oracle, np.random.default_rng(2024), mode=qimg.FP8_HADAMARD)
+    img = rng.standard_normal((n_img, 3072)).astype(np.float32)
+    txt = rng.standard_normal((n_txt, 3072)).astype(np.float32)
+    t_emb = rng.standard_normal(3072).astype(np.float32)
+    pe = _dev(qimg.qwen_image_pe(16, 16, 2, n_txt))
+    outs = []
+    for W, B, N in ((w8, b8, nr), (wf, bf, nf), (wf, bf, nf)):
+        i, t = _dev(img), _dev(txt)
+        qimg.mmdit_block_forward(W, B, N, i, t, _dev(t_emb), pe)
+        outs.append(i.cpu().numpy())
+    torch.cuda.synchronize()
+    assert np.all(np.isfinite(outs[1]))
+    np.testing.assert_array_equal(outs[1], outs[2])
+    rel, cos = _metrics(outs[1], outs[0])
+    assert cos >= 0.99, (rel, cos)
