@@ -17,7 +17,9 @@ Also printed in the same JSON line:
                MLP pair on the host cores
   extra        single linear (M=4096, 3072x3072), SageAttention (24 heads,
                S=4352, D=128), activation-quant bandwidth, and the small-M
-               linears (modulation M=1/2 as HBM GB/s, text-stream M=256)
+               linears (modulation M=1/2 as HBM GB/s, text-stream M=256), and
+               one MMDiT joint block at 4096 + 256 tokens (ms/block and the
+               13-category split of transformer.cu:487-490)
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -344,7 +346,74 @@ def _extra(q, torch, dev):
         out[f"{tag}_linear_us"] = round(ms_l * 1e3, 2)
         out[f"{tag}_large_tile_gemm_us"] = round(ms_big * 1e3, 2)
         del qws, qw0
+    out.update(_block_c4(q, torch, dev, g))
     return out
+
+
+def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
+    """One MMDiT joint block at 4096 image + 256 text tokens
+    (transformer.cu:497-836): W8A8 + Hadamard linears with N(0, 0.02)
+    weights and N(0, 0.01) biases, RMSNorm weights 1, the Qwen-Image RoPE
+    table for a 64x64 latent grid, SageAttention. `copies` weight sets
+    (340 MB each) alternate so weights stream from HBM as in a 60-block
+    forward. ms/block from a HIP graph of `blocks` consecutive blocks; the
+    13-category split from events around each category (no synchronisation
+    between categories), averaged over `profiled` eager blocks."""
+    n_img, n_txt, D, MLPD = 4096, 256, 3072, 12288
+    shapes = {"img_mod": (6 * D, D), "txt_mod": (6 * D, D)}
+    for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
+        shapes[n] = (D, D)
+    for s in ("img", "txt"):
+        shapes[f"{s}_mlp_fc1"] = (MLPD, D)
+        shapes[f"{s}_mlp_fc2"] = (D, MLPD)
+    sets = []
+    for _ in range(copies):
+        W, B = {}, {}
+        for n, (N, K) in shapes.items():
+            w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+            W[n] = q.quantize_weight_tensor(w)
+            B[n] = (torch.randn(N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+            del w
+        sets.append((W, B))
+    ones = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    norms = {n: ones for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k")}
+    img = torch.randn(n_img, D, generator=g).to(dev)
+    txt = torch.randn(n_txt, D, generator=g).to(dev)
+    t_emb = torch.randn(D, generator=g).to(dev)
+    pe = torch.from_numpy(q.qwen_image_pe(128, 128, 2, n_txt)).to(dev)
+    scratch = torch.empty(q.mmdit_block_scratch_bytes(n_img, n_txt), dtype=torch.uint8, device=dev)
+    img0, txt0 = img.clone(), txt.clone()
+
+    def block(i):
+        W, B = sets[i % copies]
+        return lambda: q.mmdit_block_forward(W, B, norms, img, txt, t_emb, pe, scratch=scratch)
+
+    fns = [block(i) for i in range(blocks)]
+    ms_graph = _time_cycle(torch, fns, iters=5, min_calls=blocks, ramp_s=0.5)
+    img.copy_(img0)
+    txt.copy_(txt0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    ms_eager = (time.perf_counter() - t0) * 1e3 / blocks
+    cats = {}
+    for i in range(profiled):
+        W, B = sets[i % copies]
+        for k, v in q.mmdit_block_forward(W, B, norms, img, txt, t_emb, pe, scratch=scratch, profile=True).items():
+            cats[k] = cats.get(k, 0.0) + v / profiled
+    finite = bool(torch.isfinite(img).all().item() and torch.isfinite(txt).all().item())
+    S = n_img + n_txt
+    lin_ops = sum(2.0 * (n_img if not n.startswith(("txt", "add_")) and n != "to_add_out" else n_txt) * N * K
+                  for n, (N, K) in shapes.items() if not n.endswith("_mod"))
+    lin_ops += 2 * 2.0 * shapes["img_mod"][0] * D
+    att_ops = 4.0 * 24 * S * S * 128
+    return {"block_c4_ms": round(ms_graph, 4), "block_c4_eager_ms": round(ms_eager, 4),
+            "block_c4_gop": round((lin_ops + att_ops) / 1e9, 2),
+            "block_c4_tflops": round((lin_ops + att_ops) / ms_graph / 1e9, 1),
+            "block_c4_categories_ms": {k: round(v, 4) for k, v in cats.items()},
+            "block_c4_finite": finite}
 
 
 def _cpu_baseline(np, torch, x, w1, w2, b1, b2, y_gpu, M, D, H, min_seconds=10.0, max_runs=20):
