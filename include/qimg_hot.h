@@ -279,6 +279,23 @@ int qimg_mmdit_block_forward(const qimg_mmdit_block* block, float* img, float* t
                              const float* pe, int n_img, int n_txt, void* scratch, int64_t scratch_bytes,
                              float* prof_ms, void* stream);
 
+/* Scratch bytes for qimg_mmdit_blocks_forward over `batch` sequences of
+ * n_img + n_txt tokens. */
+int64_t qimg_mmdit_blocks_scratch_bytes(int n_img, int n_txt, int batch);
+
+/* The joint-block loop of TransformerWeights::forward
+ * (transformer.cu:497-836): blocks[0 .. n_blocks) in order, each as
+ * qimg_mmdit_block_forward, over `batch` sequences that share t_emb and pe
+ * and have the same n_img and n_txt (batch 2 runs the two classifier-free-
+ * guidance forwards of main.cu:761-773 together, each row and head
+ * computing exactly what it computes alone). img is [batch, n_img, 3072],
+ * txt [batch, n_txt, 3072], fp32, updated in place. With prof_ms != NULL
+ * the stream is synchronised after each block and prof_ms holds the
+ * category times summed over the blocks. */
+int qimg_mmdit_blocks_forward(const qimg_mmdit_block* blocks, int n_blocks, float* img, float* txt,
+                              const float* t_emb, const float* pe, int n_img, int n_txt, int batch, void* scratch,
+                              int64_t scratch_bytes, float* prof_ms, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,14 +75,25 @@ def gate_add(x, gate, y):
     return (np.asarray(x, F32) + np.asarray(gate, F32)[None] * np.asarray(y, F32)).astype(F32)
 
 
+def qlinear(entry, x, gelu=False):
+    """One quantized linear: entry = (w_q, w_scales, hbs, bias_bits) for
+    int8 + Hadamard (cuda_kernels.cu:2674-2827), or the same with a fifth
+    element 1 for e4m3 weights and activations behind the same FWHT."""
+    wq, ws, hbs, b = entry[:4]
+    x = np.asarray(x, F32)
+    if len(entry) > 4 and entry[4] == 1:
+        aq, asc = o.quantize_activation_fp8(x, hbs)
+        return o.gemm_fp8_epilogue(aq, wq, asc, ws, b, gelu=gelu)
+    return o.linear_w8a8(x, wq, ws, hbs, b, gelu=gelu)
+
+
 def mmdit_block(q, img, txt, t_emb, pe):
     """One block as transformer.cu:506-817. `q` maps the block's linear names
-    (img_mod, to_q, ..., txt_mlp_fc2) to (w_q, w_scales, hbs, bias_bits) and
-    norm_q / norm_k / norm_added_q / norm_added_k to bf16 bits [128].
-    Returns the updated (img, txt)."""
+    (img_mod, to_q, ..., txt_mlp_fc2) to qlinear entries and norm_q / norm_k /
+    norm_added_q / norm_added_k to bf16 bits [128]. Returns the updated
+    (img, txt)."""
     def lin(x, name, gelu=False):
-        wq, ws, hbs, b = q[name]
-        return o.linear_w8a8(np.asarray(x, F32), wq, ws, hbs, b, gelu=gelu)
+        return qlinear(q[name], x, gelu)
 
     n_txt = txt.shape[0]
     ts = silu(t_emb).reshape(1, DIM)

@@ -88,7 +88,8 @@ __global__ __launch_bounds__(LN_THR) void layernorm_modulate_kernel(const float*
     }
 }
 
-// One wave per (token s, head h) of the joint sequence (txt tokens first):
+// One wave per (sequence b, token s, head h) of the joint sequences (txt
+// tokens first; the pe table is shared by the sequences):
 // optional RMSNorm over the head's 128 values with a bf16 weight
 // (rms_norm_fp32_kernel, cuda_kernels.cu:1656-1687), optional RoPE on the
 // pair (2l, 2l+1) held by lane l with pe[s][l] = (cos, -sin, sin, cos)
@@ -101,16 +102,18 @@ __global__ __launch_bounds__(256) void joint_heads_f16_kernel(const float* __res
                                                               const uint16_t* __restrict__ w_img,
                                                               const float* __restrict__ pe,
                                                               uint16_t* __restrict__ out, int n_txt, int n_img,
-                                                              int H, float eps) {
+                                                              int batch, int H, float eps) {
     const int S = n_txt + n_img;
     const int64_t gw = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-    if (gw >= static_cast<int64_t>(S) * H) return;  // wave-uniform
+    if (gw >= static_cast<int64_t>(batch) * S * H) return;  // wave-uniform
     const int lane = threadIdx.x & 63;
-    const int s = static_cast<int>(gw / H);
-    const int h = static_cast<int>(gw % H);
+    const int b = static_cast<int>(gw / (static_cast<int64_t>(S) * H));
+    const int sh = static_cast<int>(gw - static_cast<int64_t>(b) * S * H);
+    const int s = sh / H;
+    const int h = sh - s * H;
     const bool is_txt = s < n_txt;
-    const float* src = is_txt ? txt + (static_cast<int64_t>(s) * H + h) * HD
-                              : img + (static_cast<int64_t>(s - n_txt) * H + h) * HD;
+    const float* src = is_txt ? txt + ((static_cast<int64_t>(b) * n_txt + s) * H + h) * HD
+                              : img + ((static_cast<int64_t>(b) * n_img + s - n_txt) * H + h) * HD;
     float2 x = reinterpret_cast<const float2*>(src)[lane];
     if constexpr (NORM_ROPE) {
         const float ss = wave_sum(x.x * x.x + x.y * x.y);
@@ -125,24 +128,28 @@ __global__ __launch_bounds__(256) void joint_heads_f16_kernel(const float* __res
         x = make_float2(o0, o1);
     }
     const uint32_t packed = static_cast<uint32_t>(f32_to_f16(x.x)) | (static_cast<uint32_t>(f32_to_f16(x.y)) << 16);
-    reinterpret_cast<uint32_t*>(out + (static_cast<int64_t>(h) * S + s) * HD)[lane] = packed;
+    reinterpret_cast<uint32_t*>(out + ((static_cast<int64_t>(b) * H + h) * S + s) * HD)[lane] = packed;
 }
 
 // transpose_split_fused_fp32 (transformer.cu:84-104) on the fp16
-// attention output [H][S][128]: token s < n_txt goes to txt[s][h*128..],
-// the rest to img[s - n_txt][h*128..], as fp32.
+// attention output [batch][H][S][128]: token s < n_txt of sequence b goes
+// to txt[b][s][h*128..], the rest to img[b][s - n_txt][h*128..], as fp32.
 __global__ __launch_bounds__(256) void split_heads_kernel(const uint16_t* __restrict__ in, float* __restrict__ txt,
-                                                          float* __restrict__ img, int n_txt, int n_img, int H) {
+                                                          float* __restrict__ img, int n_txt, int n_img, int batch,
+                                                          int H) {
     const int S = n_txt + n_img;
     const int64_t gw = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-    if (gw >= static_cast<int64_t>(S) * H) return;
+    if (gw >= static_cast<int64_t>(batch) * S * H) return;
     const int lane = threadIdx.x & 63;
-    const int s = static_cast<int>(gw / H);
-    const int h = static_cast<int>(gw % H);
-    const uint32_t v = reinterpret_cast<const uint32_t*>(in + (static_cast<int64_t>(h) * S + s) * HD)[lane];
+    const int b = static_cast<int>(gw / (static_cast<int64_t>(S) * H));
+    const int sh = static_cast<int>(gw - static_cast<int64_t>(b) * S * H);
+    const int s = sh / H;
+    const int h = sh - s * H;
+    const uint32_t v =
+        reinterpret_cast<const uint32_t*>(in + ((static_cast<int64_t>(b) * H + h) * S + s) * HD)[lane];
     const float2 f = make_float2(f16_to_f32(static_cast<uint16_t>(v & 0xffffu)), f16_to_f32(static_cast<uint16_t>(v >> 16)));
-    float* dst = s < n_txt ? txt + (static_cast<int64_t>(s) * H + h) * HD
-                           : img + (static_cast<int64_t>(s - n_txt) * H + h) * HD;
+    float* dst = s < n_txt ? txt + ((static_cast<int64_t>(b) * n_txt + s) * H + h) * HD
+                           : img + ((static_cast<int64_t>(b) * n_img + s - n_txt) * H + h) * HD;
     reinterpret_cast<float2*>(dst)[lane] = f;
 }
 
@@ -177,26 +184,26 @@ hipError_t launch_layernorm_modulate(const float* x, const float* shift, const f
 }
 
 hipError_t launch_joint_heads_f16(const float* txt, const float* img, const uint16_t* w_txt, const uint16_t* w_img,
-                                  const float* pe, uint16_t* out, int n_txt, int n_img, int H, float eps,
+                                  const float* pe, uint16_t* out, int n_txt, int n_img, int batch, int H, float eps,
                                   hipStream_t stream) {
-    const int64_t waves = static_cast<int64_t>(n_txt + n_img) * H;
+    const int64_t waves = static_cast<int64_t>(n_txt + n_img) * H * batch;
     if (waves == 0) return hipSuccess;
     const int blocks = div_up_i(waves, 4);
     if (w_txt != nullptr)
         hipLaunchKernelGGL(joint_heads_f16_kernel<true>, dim3(blocks), dim3(256), 0, stream, txt, img, w_txt, w_img,
-                           pe, out, n_txt, n_img, H, eps);
+                           pe, out, n_txt, n_img, batch, H, eps);
     else
         hipLaunchKernelGGL(joint_heads_f16_kernel<false>, dim3(blocks), dim3(256), 0, stream, txt, img, w_txt, w_img,
-                           pe, out, n_txt, n_img, H, eps);
+                           pe, out, n_txt, n_img, batch, H, eps);
     return hipGetLastError();
 }
 
-hipError_t launch_split_heads(const uint16_t* in, float* txt, float* img, int n_txt, int n_img, int H,
+hipError_t launch_split_heads(const uint16_t* in, float* txt, float* img, int n_txt, int n_img, int batch, int H,
                               hipStream_t stream) {
-    const int64_t waves = static_cast<int64_t>(n_txt + n_img) * H;
+    const int64_t waves = static_cast<int64_t>(n_txt + n_img) * H * batch;
     if (waves == 0) return hipSuccess;
     hipLaunchKernelGGL(split_heads_kernel, dim3(div_up_i(waves, 4)), dim3(256), 0, stream, in, txt, img, n_txt, n_img,
-                       H);
+                       batch, H);
     return hipGetLastError();
 }
 

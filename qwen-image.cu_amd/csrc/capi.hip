@@ -342,7 +342,7 @@ int qimg_joint_heads_f16(const float* txt, const float* img, const uint16_t* nor
     QIMG_REQUIRE(out && (txt || n_txt == 0) && (img || n_img == 0), "%s: null pointer", fn);
     QIMG_REQUIRE((norm_txt == nullptr) == (norm_img == nullptr), "%s: give both RMSNorm weights or neither", fn);
     QIMG_REQUIRE(norm_txt == nullptr || pe != nullptr, "%s: RMSNorm + RoPE needs pe", fn);
-    return hip_status(qimg::launch_joint_heads_f16(txt, img, norm_txt, norm_img, pe, out, n_txt, n_img, H, eps,
+    return hip_status(qimg::launch_joint_heads_f16(txt, img, norm_txt, norm_img, pe, out, n_txt, n_img, 1, H, eps,
                                                    static_cast<hipStream_t>(stream)),
                       fn);
 }
@@ -354,7 +354,7 @@ int qimg_split_heads(const uint16_t* attn_f16, float* txt, float* img, int n_txt
     if (n_txt + n_img == 0) return QIMG_OK;
     QIMG_REQUIRE(attn_f16 && (txt || n_txt == 0) && (img || n_img == 0), "%s: null pointer", fn);
     return hip_status(
-        qimg::launch_split_heads(attn_f16, txt, img, n_txt, n_img, H, static_cast<hipStream_t>(stream)), fn);
+        qimg::launch_split_heads(attn_f16, txt, img, n_txt, n_img, 1, H, static_cast<hipStream_t>(stream)), fn);
 }
 
 int qimg_gate_add(const float* x, const float* gate, const float* y, float* out, int rows, int dim, void* stream) {
@@ -368,10 +368,12 @@ int qimg_gate_add(const float* x, const float* gate, const float* y, float* out,
     return hip_status(qimg::launch_gate_add(x, gate, y, out, rows, dim, static_cast<hipStream_t>(stream)), fn);
 }
 
-int64_t qimg_mmdit_block_scratch_bytes(int n_img, int n_txt) {
-    if (n_img < 0 || n_txt < 0 || n_img + n_txt == 0) return 0;
-    return qimg::mmdit_block_scratch_layout(n_img, n_txt, nullptr, nullptr);
+int64_t qimg_mmdit_blocks_scratch_bytes(int n_img, int n_txt, int batch) {
+    if (n_img < 0 || n_txt < 0 || n_img + n_txt == 0 || batch < 1) return 0;
+    return qimg::mmdit_block_scratch_layout(n_img, n_txt, batch, nullptr, nullptr);
 }
+
+int64_t qimg_mmdit_block_scratch_bytes(int n_img, int n_txt) { return qimg_mmdit_blocks_scratch_bytes(n_img, n_txt, 1); }
 
 static int check_qlinear(const char* fn, const char* name, const qimg_qlinear& l, int N, int K) {
     QIMG_REQUIRE(l.w && l.scales, "%s: %s: null weight", fn, name);
@@ -383,20 +385,9 @@ static int check_qlinear(const char* fn, const char* name, const qimg_qlinear& l
     return QIMG_OK;
 }
 
-int qimg_mmdit_block_forward(const qimg_mmdit_block* b, float* img, float* txt, const float* t_emb, const float* pe,
-                             int n_img, int n_txt, void* scratch, int64_t scratch_bytes, float* prof_ms,
-                             void* stream) {
-    const char* fn = "qimg_mmdit_block_forward";
-    QIMG_REQUIRE(b != nullptr, "%s: null block", fn);
-    QIMG_REQUIRE(n_img >= 0 && n_txt >= 0 && n_img + n_txt > 0, "%s: bad token counts n_img=%d n_txt=%d", fn,
-                 n_img, n_txt);
-    QIMG_REQUIRE(static_cast<int64_t>(n_img + n_txt) * 3072 < (int64_t{1} << 31) &&
-                     static_cast<int64_t>(n_img > n_txt ? n_img : n_txt) * 12288 < (int64_t{1} << 31),
-                 "%s: too many tokens", fn);
-    QIMG_REQUIRE((img || n_img == 0) && (txt || n_txt == 0) && t_emb && pe, "%s: null pointer", fn);
-    QIMG_REQUIRE((n_img == 0 || aligned16(img)) && (n_txt == 0 || aligned16(txt)),
-                 "%s: img/txt must be 16-byte aligned", fn);
-    QIMG_REQUIRE(b->norm_q && b->norm_k && b->norm_added_q && b->norm_added_k, "%s: null RMSNorm weight", fn);
+static int check_block(const char* fn, int index, const qimg_mmdit_block* b) {
+    QIMG_REQUIRE(b->norm_q && b->norm_k && b->norm_added_q && b->norm_added_k, "%s: block %d: null RMSNorm weight",
+                 fn, index);
     const int D = 3072, F = 12288;
     struct {
         const char* name;
@@ -413,16 +404,51 @@ int qimg_mmdit_block_forward(const qimg_mmdit_block* b, float* img, float* txt, 
         int st = check_qlinear(fn, e.name, *e.l, e.N, e.K);
         if (st) return st;
     }
-    const int64_t need = qimg::mmdit_block_scratch_layout(n_img, n_txt, nullptr, nullptr);
+    return QIMG_OK;
+}
+
+int qimg_mmdit_blocks_forward(const qimg_mmdit_block* blocks, int n_blocks, float* img, float* txt,
+                              const float* t_emb, const float* pe, int n_img, int n_txt, int batch, void* scratch,
+                              int64_t scratch_bytes, float* prof_ms, void* stream) {
+    const char* fn = "qimg_mmdit_blocks_forward";
+    QIMG_REQUIRE(blocks != nullptr && n_blocks >= 1, "%s: need at least one block (n_blocks=%d)", fn, n_blocks);
+    QIMG_REQUIRE(batch >= 1, "%s: batch must be >= 1 (got %d)", fn, batch);
+    QIMG_REQUIRE(n_img >= 0 && n_txt >= 0 && n_img + n_txt > 0, "%s: bad token counts n_img=%d n_txt=%d", fn,
+                 n_img, n_txt);
+    const int64_t rows = static_cast<int64_t>(batch) * (n_img > n_txt ? n_img : n_txt);
+    QIMG_REQUIRE(static_cast<int64_t>(batch) * (n_img + n_txt) * 3072 < (int64_t{1} << 31) &&
+                     rows * 12288 < (int64_t{1} << 31),
+                 "%s: too many tokens", fn);
+    QIMG_REQUIRE((img || n_img == 0) && (txt || n_txt == 0) && t_emb && pe, "%s: null pointer", fn);
+    QIMG_REQUIRE((n_img == 0 || aligned16(img)) && (n_txt == 0 || aligned16(txt)),
+                 "%s: img/txt must be 16-byte aligned", fn);
+    for (int i = 0; i < n_blocks; ++i) {
+        int st = check_block(fn, i, blocks + i);
+        if (st) return st;
+    }
+    const int64_t need = qimg::mmdit_block_scratch_layout(n_img, n_txt, batch, nullptr, nullptr);
     if (!scratch || scratch_bytes < need)
         return fail(QIMG_ERR_SCRATCH, "%s: scratch %lld bytes < required %lld", fn,
                     static_cast<long long>(scratch_bytes), static_cast<long long>(need));
     QIMG_REQUIRE(aligned16(scratch), "%s: scratch must be 16-byte aligned", fn);
     qimg::BlockScratch ws;
-    qimg::mmdit_block_scratch_layout(n_img, n_txt, scratch, &ws);
-    return hip_status(
-        qimg::run_mmdit_block(*b, img, txt, t_emb, pe, n_img, n_txt, ws, prof_ms, static_cast<hipStream_t>(stream)),
-        fn);
+    qimg::mmdit_block_scratch_layout(n_img, n_txt, batch, scratch, &ws);
+    if (prof_ms)
+        for (int c = 0; c < QIMG_PROF_COUNT; ++c) prof_ms[c] = 0.0f;
+    for (int i = 0; i < n_blocks; ++i) {
+        const int st = hip_status(qimg::run_mmdit_block(blocks[i], img, txt, t_emb, pe, n_img, n_txt, batch, ws,
+                                                        prof_ms, static_cast<hipStream_t>(stream)),
+                                  fn);
+        if (st) return st;
+    }
+    return QIMG_OK;
+}
+
+int qimg_mmdit_block_forward(const qimg_mmdit_block* b, float* img, float* txt, const float* t_emb, const float* pe,
+                             int n_img, int n_txt, void* scratch, int64_t scratch_bytes, float* prof_ms,
+                             void* stream) {
+    return qimg_mmdit_blocks_forward(b, 1, img, txt, t_emb, pe, n_img, n_txt, 1, scratch, scratch_bytes, prof_ms,
+                                     stream);
 }
 
 }  // extern "C"

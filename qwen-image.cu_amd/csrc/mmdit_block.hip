@@ -12,7 +12,11 @@
 //  - the attention writes fp16 and the split reads it (the reference
 //    widens to fp32 first; fp16 -> fp32 is exact);
 //  - buffers whose producer has been consumed are reused (q/k/v of each
-//    stream hold the attention output, the projection and the MLP output).
+//    stream hold the attention output, the projection and the MLP output);
+//  - `batch` sequences of equal lengths that share t_emb and pe (the two
+//    classifier-free-guidance forwards of main.cu:761-773) can run as one:
+//    the linears see batch * n rows, the attention batch * 24 heads; each
+//    row and head computes exactly what it computes alone.
 #include "qimg_device.h"
 #include "qimg_internal.h"
 
@@ -30,9 +34,11 @@ inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t{255}; }
 
 }  // namespace
 
-int64_t mmdit_block_scratch_layout(int n_img, int n_txt, void* base, BlockScratch* out) {
+int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, BlockScratch* out) {
     const int S = n_img + n_txt;
-    const int mmax = n_img > n_txt ? n_img : (n_txt > 1 ? n_txt : 1);
+    const int64_t ri = int64_t{batch} * n_img;  // image rows of all sequences
+    const int64_t rt = int64_t{batch} * n_txt;
+    const int64_t mmax = ri > rt ? ri : (rt > 1 ? rt : 1);
     uint8_t* p = static_cast<uint8_t*>(base);
     int64_t off = 0;
     auto take = [&](int64_t bytes) {
@@ -44,19 +50,19 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, void* base, BlockScratc
     w.t_silu = reinterpret_cast<float*>(take(4 * DIM));
     w.img_mods = reinterpret_cast<float*>(take(4 * 6 * DIM));
     w.txt_mods = reinterpret_cast<float*>(take(4 * 6 * DIM));
-    w.img_norm = reinterpret_cast<float*>(take(int64_t{4} * n_img * DIM));
-    w.txt_norm = reinterpret_cast<float*>(take(int64_t{4} * n_txt * DIM));
-    w.act_q = take(static_cast<int64_t>(mmax) * MLP);
-    w.act_scales = reinterpret_cast<float*>(take(4 * int64_t{mmax}));
+    w.img_norm = reinterpret_cast<float*>(take(4 * ri * DIM));
+    w.txt_norm = reinterpret_cast<float*>(take(4 * rt * DIM));
+    w.act_q = take(mmax * MLP);
+    w.act_scales = reinterpret_cast<float*>(take(4 * mmax));
     for (int i = 0; i < 3; ++i) {
-        w.img_qkv[i] = reinterpret_cast<float*>(take(int64_t{4} * n_img * DIM));
-        w.txt_qkv[i] = reinterpret_cast<float*>(take(int64_t{4} * n_txt * DIM));
-        w.qkv16[i] = reinterpret_cast<uint16_t*>(take(int64_t{2} * S * DIM));
+        w.img_qkv[i] = reinterpret_cast<float*>(take(4 * ri * DIM));
+        w.txt_qkv[i] = reinterpret_cast<float*>(take(4 * rt * DIM));
+        w.qkv16[i] = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
     }
-    w.attn16 = reinterpret_cast<uint16_t*>(take(int64_t{2} * S * DIM));
-    w.img_mlp = reinterpret_cast<float*>(take(int64_t{4} * n_img * MLP));
-    w.txt_mlp = reinterpret_cast<float*>(take(int64_t{4} * n_txt * MLP));
-    const int64_t sage = sage_scratch_layout(HEADS, S > 0 ? S : 1, HEAD_DIM, nullptr, nullptr);
+    w.attn16 = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
+    w.img_mlp = reinterpret_cast<float*>(take(4 * ri * MLP));
+    w.txt_mlp = reinterpret_cast<float*>(take(4 * rt * MLP));
+    const int64_t sage = sage_scratch_layout(HEADS * batch, S > 0 ? S : 1, HEAD_DIM, nullptr, nullptr);
     w.sage = take(sage);
     w.sage_bytes = sage;
     if (out) *out = w;
@@ -64,8 +70,11 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, void* base, BlockScratc
 }
 
 hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
-                           int n_img, int n_txt, const BlockScratch& w, float* prof_ms, hipStream_t s) {
+                           int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s) {
     const int S = n_img + n_txt;
+    // row counts of the img / txt streams over all sequences
+    const int Mi = batch * n_img;
+    const int Mt = batch * n_txt;
     hipEvent_t ev[QIMG_PROF_COUNT + 1] = {};
     const bool prof = prof_ms != nullptr;
     hipError_t e = hipSuccess;
@@ -111,8 +120,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
 
         // LayerNorm + modulate (transformer.cu:526-540)
         QIMG_TRY(mark(QIMG_PROF_ATTN_NORM));
-        QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, n_img, DIM, EPS, s));
-        QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, n_txt, DIM, EPS, s));
+        QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, Mi, DIM, EPS, s));
+        QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
 
         // QKV with one activation quant per stream (transformer.cu:557-606)
         QIMG_TRY(mark(QIMG_PROF_QKV_GEMM));
@@ -123,7 +132,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                 const qimg_qlinear* const* L = pass == 0 ? il : tl;
                 const float* x = pass == 0 ? w.img_norm : w.txt_norm;
                 float* const* outs = pass == 0 ? w.img_qkv : w.txt_qkv;
-                const int M = pass == 0 ? n_img : n_txt;
+                const int M = pass == 0 ? Mi : Mt;
                 if (M == 0) continue;
                 const bool share = same_quant(*L[0], *L[1]) && same_quant(*L[0], *L[2]);
                 if (share) QIMG_TRY(quant(x, M, *L[0]));
@@ -139,24 +148,24 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // RMSNorm + concat + transpose + RoPE -> fp16 (transformer.cu:617-666)
         QIMG_TRY(mark(QIMG_PROF_QK_NORM));
         QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, w.qkv16[0], n_txt,
-                                        n_img, HEADS, EPS, s));
+                                        n_img, batch, HEADS, EPS, s));
         QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.qkv16[1], n_txt,
-                                        n_img, HEADS, EPS, s));
+                                        n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_CONCAT_TRANSPOSE));
         QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[2], w.img_qkv[2], nullptr, nullptr, nullptr, w.qkv16[2], n_txt,
-                                        n_img, HEADS, EPS, s));
+                                        n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_ROPE));
 
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)
         QIMG_TRY(mark(QIMG_PROF_ATTENTION));
         {
             SageScratch ss;
-            sage_scratch_layout(HEADS, S, HEAD_DIM, w.sage, &ss);
-            QIMG_TRY(launch_sage_k_mean(w.qkv16[1], ss.k_mean, HEADS, S, HEAD_DIM, s));
-            QIMG_TRY(launch_sage_quant_q(w.qkv16[0], ss.q_i8, ss.q_scale, HEADS, S, HEAD_DIM, s));
-            QIMG_TRY(launch_sage_quant_k(w.qkv16[1], ss.k_mean, ss.k_i8, ss.k_scale, HEADS, S, HEAD_DIM, s));
+            sage_scratch_layout(HEADS * batch, S, HEAD_DIM, w.sage, &ss);
+            QIMG_TRY(launch_sage_k_mean(w.qkv16[1], ss.k_mean, HEADS * batch, S, HEAD_DIM, s));
+            QIMG_TRY(launch_sage_quant_q(w.qkv16[0], ss.q_i8, ss.q_scale, HEADS * batch, S, HEAD_DIM, s));
+            QIMG_TRY(launch_sage_quant_k(w.qkv16[1], ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
             QIMG_TRY(launch_sage_attn(ss.q_i8, ss.k_i8, w.qkv16[2], ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
-                                      HEADS, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, ss.v_t, s));
+                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, ss.v_t, s));
         }
 
         // transpose + split back to the streams (transformer.cu:693-703);
@@ -164,38 +173,38 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(mark(QIMG_PROF_TRANSPOSE_SPLIT));
         float* img_attn = w.img_qkv[0];
         float* txt_attn = w.txt_qkv[0];
-        QIMG_TRY(launch_split_heads(w.attn16, txt_attn, img_attn, n_txt, n_img, HEADS, s));
+        QIMG_TRY(launch_split_heads(w.attn16, txt_attn, img_attn, n_txt, n_img, batch, HEADS, s));
 
         // out projections (transformer.cu:723-732), into the k buffers
         QIMG_TRY(mark(QIMG_PROF_OUT_GEMM));
         float* img_proj = w.img_qkv[1];
         float* txt_proj = w.txt_qkv[1];
-        QIMG_TRY(linear(img_attn, n_img, b.to_out, img_proj, 0));
-        QIMG_TRY(linear(txt_attn, n_txt, b.to_add_out, txt_proj, 0));
+        QIMG_TRY(linear(img_attn, Mi, b.to_out, img_proj, 0));
+        QIMG_TRY(linear(txt_attn, Mt, b.to_add_out, txt_proj, 0));
 
         // residual with gate1 (transformer.cu:740-746)
         QIMG_TRY(mark(QIMG_PROF_GATE_ATTN));
-        QIMG_TRY(launch_gate_add(img, im + 2 * DIM, img_proj, img, n_img, DIM, s));
-        QIMG_TRY(launch_gate_add(txt, tm + 2 * DIM, txt_proj, txt, n_txt, DIM, s));
+        QIMG_TRY(launch_gate_add(img, im + 2 * DIM, img_proj, img, Mi, DIM, s));
+        QIMG_TRY(launch_gate_add(txt, tm + 2 * DIM, txt_proj, txt, Mt, DIM, s));
 
         // LayerNorm + modulate (transformer.cu:754-764)
         QIMG_TRY(mark(QIMG_PROF_MLP_NORM));
-        QIMG_TRY(launch_layernorm_modulate(img, im + 3 * DIM, im + 4 * DIM, w.img_norm, n_img, DIM, EPS, s));
-        QIMG_TRY(launch_layernorm_modulate(txt, tm + 3 * DIM, tm + 4 * DIM, w.txt_norm, n_txt, DIM, EPS, s));
+        QIMG_TRY(launch_layernorm_modulate(img, im + 3 * DIM, im + 4 * DIM, w.img_norm, Mi, DIM, EPS, s));
+        QIMG_TRY(launch_layernorm_modulate(txt, tm + 3 * DIM, tm + 4 * DIM, w.txt_norm, Mt, DIM, EPS, s));
 
         // GELU MLP (transformer.cu:780-808), output into the v buffers
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));
         float* img_out = w.img_qkv[2];
         float* txt_out = w.txt_qkv[2];
-        QIMG_TRY(linear(w.img_norm, n_img, b.img_mlp_fc1, w.img_mlp, 1));
-        QIMG_TRY(linear(w.img_mlp, n_img, b.img_mlp_fc2, img_out, 0));
-        QIMG_TRY(linear(w.txt_norm, n_txt, b.txt_mlp_fc1, w.txt_mlp, 1));
-        QIMG_TRY(linear(w.txt_mlp, n_txt, b.txt_mlp_fc2, txt_out, 0));
+        QIMG_TRY(linear(w.img_norm, Mi, b.img_mlp_fc1, w.img_mlp, 1));
+        QIMG_TRY(linear(w.img_mlp, Mi, b.img_mlp_fc2, img_out, 0));
+        QIMG_TRY(linear(w.txt_norm, Mt, b.txt_mlp_fc1, w.txt_mlp, 1));
+        QIMG_TRY(linear(w.txt_mlp, Mt, b.txt_mlp_fc2, txt_out, 0));
 
         // residual with gate2 (transformer.cu:812-818)
         QIMG_TRY(mark(QIMG_PROF_GATE_MLP));
-        QIMG_TRY(launch_gate_add(img, im + 5 * DIM, img_out, img, n_img, DIM, s));
-        QIMG_TRY(launch_gate_add(txt, tm + 5 * DIM, txt_out, txt, n_txt, DIM, s));
+        QIMG_TRY(launch_gate_add(img, im + 5 * DIM, img_out, img, Mi, DIM, s));
+        QIMG_TRY(launch_gate_add(txt, tm + 5 * DIM, txt_out, txt, Mt, DIM, s));
         QIMG_TRY(mark(QIMG_PROF_COUNT));
 
         if (prof) {
@@ -203,7 +212,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             for (int c = 0; c < QIMG_PROF_COUNT; ++c) {
                 float ms = 0.0f;
                 QIMG_TRY(hipEventElapsedTime(&ms, ev[c], ev[c + 1]));
-                prof_ms[c] = ms;
+                prof_ms[c] += ms;
             }
         }
     }

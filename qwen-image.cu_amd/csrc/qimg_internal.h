@@ -66,9 +66,9 @@ hipError_t launch_silu(const float* x, float* out, int64_t n, hipStream_t stream
 hipError_t launch_layernorm_modulate(const float* x, const float* shift, const float* scale, float* out, int rows,
                                      int dim, float eps, hipStream_t stream);
 hipError_t launch_joint_heads_f16(const float* txt, const float* img, const uint16_t* w_txt, const uint16_t* w_img,
-                                  const float* pe, uint16_t* out, int n_txt, int n_img, int H, float eps,
+                                  const float* pe, uint16_t* out, int n_txt, int n_img, int batch, int H, float eps,
                                   hipStream_t stream);
-hipError_t launch_split_heads(const uint16_t* in, float* txt, float* img, int n_txt, int n_img, int H,
+hipError_t launch_split_heads(const uint16_t* in, float* txt, float* img, int n_txt, int n_img, int batch, int H,
                               hipStream_t stream);
 hipError_t launch_gate_add(const float* x, const float* gate, const float* y, float* out, int rows, int dim,
                            hipStream_t stream);
@@ -91,8 +91,12 @@ struct BlockScratch {
     uint8_t* sage;
     int64_t sage_bytes;
 };
-int64_t mmdit_block_scratch_layout(int n_img, int n_txt, void* base, BlockScratch* out);
+// `batch` sequences of n_img + n_txt tokens (same lengths, shared t_emb
+// and pe): img [batch, n_img, 3072], txt [batch, n_txt, 3072].
+int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, BlockScratch* out);
+// prof_ms != nullptr: the stream is synchronised at the end and each
+// category's time is ADDED to prof_ms[c].
 hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
-                           int n_img, int n_txt, const BlockScratch& w, float* prof_ms, hipStream_t s);
+                           int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s);
 
 }  // namespace qimg

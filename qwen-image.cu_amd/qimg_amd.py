@@ -56,6 +56,8 @@ _SIGS = {
     "qimg_gate_add": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "qimg_mmdit_block_scratch_bytes": (_I64, [_I, _I]),
     "qimg_mmdit_block_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _I64, _P, _P]),
+    "qimg_mmdit_blocks_scratch_bytes": (_I64, [_I, _I, _I]),
+    "qimg_mmdit_blocks_forward": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _P, _I64, _P, _P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -425,8 +427,55 @@ class _Block(ctypes.Structure):
     _fields_ = [(n, _QLinear) for n in _BLOCK_LINEARS] + [(n, _P) for n in _BLOCK_NORMS]
 
 
-def mmdit_block_scratch_bytes(n_img: int, n_txt: int) -> int:
-    return int(_lib.qimg_mmdit_block_scratch_bytes(int(n_img), int(n_txt)))
+def mmdit_block_scratch_bytes(n_img: int, n_txt: int, batch: int = 1) -> int:
+    return int(_lib.qimg_mmdit_blocks_scratch_bytes(int(n_img), int(n_txt), int(batch)))
+
+
+def _block_struct(weights: dict, biases: dict, norms: dict, b=None):
+    b = _Block() if b is None else b
+    for n in _BLOCK_LINEARS:
+        qw = weights[n]
+        N, K = qw.data.shape
+        bias = biases.get(n)
+        setattr(b, n, _QLinear(qw.data.data_ptr(), qw.scales.data_ptr(), N, K, int(qw.had_block_size),
+                               int(qw.mode), bias.data_ptr() if bias is not None else None))
+    for n in _BLOCK_NORMS:
+        setattr(b, n, norms[n].data_ptr())
+    return b
+
+
+class BlockTable:
+    """A C array of qimg_mmdit_block for a list of (weights, biases, norms)
+    dicts, built once: the tensors must outlive the table."""
+
+    def __init__(self, blocks):
+        self.n = len(blocks)
+        self.array = (_Block * self.n)()
+        for i, (w, b, nr) in enumerate(blocks):
+            _block_struct(w, b, nr, self.array[i])
+
+
+def mmdit_blocks_forward(table: "BlockTable", img: torch.Tensor, txt: torch.Tensor, t_emb: torch.Tensor,
+                         pe: torch.Tensor, scratch: torch.Tensor | None = None, profile: bool = False):
+    """The block loop (transformer.cu:497-836) over every block of `table`.
+    img [batch, n_img, 3072] / txt [batch, n_txt, 3072] fp32 (or 2-D for
+    batch 1) are updated in place; the sequences share t_emb and pe. With
+    profile=True returns {category: ms} summed over the blocks."""
+    batch = img.shape[0] if img.dim() == 3 else 1
+    n_img = img.shape[-2]
+    n_txt = txt.shape[-2]
+    if txt.dim() == 3 and txt.shape[0] != batch:
+        raise ValueError("img and txt batch differ")
+    if scratch is None:
+        scratch = torch.empty((mmdit_block_scratch_bytes(n_img, n_txt, batch),), dtype=torch.uint8,
+                              device=img.device)
+    prof = (ctypes.c_float * len(PROF_CATEGORIES))() if profile else None
+    _check(_lib.qimg_mmdit_blocks_forward(ctypes.addressof(table.array), table.n, _ptr(img), _ptr(txt), _ptr(t_emb),
+                                          _ptr(pe), n_img, n_txt, batch, _ptr(scratch), scratch.numel(),
+                                          ctypes.addressof(prof) if profile else None, _stream()))
+    if profile:
+        return {n: float(prof[i]) for i, n in enumerate(PROF_CATEGORIES)}
+    return None
 
 
 def mmdit_block_forward(weights: dict, biases: dict, norms: dict, img: torch.Tensor, txt: torch.Tensor,
@@ -438,15 +487,7 @@ def mmdit_block_forward(weights: dict, biases: dict, norms: dict, img: torch.Ten
     QuantizedWeight, `biases` the same names to bf16 [N] tensors, `norms`
     norm_q / norm_k / norm_added_q / norm_added_k to bf16 [128]. With
     profile=True returns {category: ms} (the stream is synchronised)."""
-    b = _Block()
-    for n in _BLOCK_LINEARS:
-        qw = weights[n]
-        N, K = qw.data.shape
-        bias = biases.get(n)
-        setattr(b, n, _QLinear(qw.data.data_ptr(), qw.scales.data_ptr(), N, K, int(qw.had_block_size),
-                               int(qw.mode), bias.data_ptr() if bias is not None else None))
-    for n in _BLOCK_NORMS:
-        setattr(b, n, norms[n].data_ptr())
+    b = _block_struct(weights, biases, norms)
     n_img, n_txt = img.shape[0], txt.shape[0]
     if scratch is None:
         scratch = torch.empty((mmdit_block_scratch_bytes(n_img, n_txt),), dtype=torch.uint8, device=img.device)
