@@ -19,7 +19,9 @@ Also printed in the same JSON line:
                S=4352, D=128), activation-quant bandwidth, and the small-M
                linears (modulation M=1/2 as HBM GB/s, text-stream M=256), and
                one MMDiT joint block at 4096 + 256 tokens (ms/block and the
-               13-category split of transformer.cu:487-490)
+               13-category split of transformer.cu:487-490), and the 60-block
+               e4m3 step at 1328x1328 (6889 + 512 tokens, two CFG branches,
+               sequential and batched)
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -347,7 +349,85 @@ def _extra(q, torch, dev):
         out[f"{tag}_large_tile_gemm_us"] = round(ms_big * 1e3, 2)
         del qws, qw0
     out.update(_block_c4(q, torch, dev, g))
+    out.update(_step_c5(q, torch, dev))
     return out
+
+
+def _step_c5(q, torch, dev, n_blocks=60, steps=3):
+    """One denoising step's transformer blocks at 1328x1328: 60 MMDiT joint
+    blocks over 6889 image + 512 text tokens with e4m3 weights (FWHT front
+    end, N(0, 0.02) weights, N(0, 0.01) biases, RMSNorm weights 1), for the
+    two classifier-free-guidance branches (main.cu:761-773), run as two
+    sequential forwards and as one forward of batch 2. The weights (20.4 GB)
+    are drawn on the GPU; every block has its own."""
+    n_img, n_txt, D, F = 83 * 83, 512, 3072, 12288
+    gen = torch.Generator(device=dev).manual_seed(5)
+    shapes = {"img_mod": (6 * D, D), "txt_mod": (6 * D, D)}
+    for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
+        shapes[n] = (D, D)
+    for s in ("img", "txt"):
+        shapes[f"{s}_mlp_fc1"] = (F, D)
+        shapes[f"{s}_mlp_fc2"] = (D, F)
+    ones = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    norms = {n: ones for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k")}
+    t_build = time.perf_counter()
+    blocks = []
+    for _ in range(n_blocks):
+        W, B = {}, {}
+        for n, (N, K) in shapes.items():
+            w = (torch.randn(N, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+            W[n] = q.quantize_weight_tensor(w, mode=q.FP8_HADAMARD)
+            B[n] = (torch.randn(N, generator=gen, device=dev) * 0.01).to(torch.bfloat16)
+            del w
+        blocks.append((W, B, norms))
+    table = q.BlockTable(blocks)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t_build
+    img0 = torch.randn(n_img, D, generator=gen, device=dev)
+    txts = [torch.randn(n_txt, D, generator=gen, device=dev) for _ in range(2)]
+    t_emb = torch.randn(D, generator=gen, device=dev)
+    pe = torch.from_numpy(q.qwen_image_pe(166, 166, 2, n_txt)).to(dev)
+    assert pe.shape[0] == n_img + n_txt
+    sc1 = torch.empty(q.mmdit_block_scratch_bytes(n_img, n_txt, 1), dtype=torch.uint8, device=dev)
+    sc2 = torch.empty(q.mmdit_block_scratch_bytes(n_img, n_txt, 2), dtype=torch.uint8, device=dev)
+    seq = [(img0.clone(), t.clone()) for t in txts]
+    bat_img = torch.stack([img0, img0]).contiguous()
+    bat_txt = torch.stack(txts).contiguous()
+
+    def run_seq():
+        for i, t in seq:
+            q.mmdit_blocks_forward(table, i, t, t_emb, pe, scratch=sc1)
+
+    def run_bat():
+        q.mmdit_blocks_forward(table, bat_img, bat_txt, t_emb, pe, scratch=sc2)
+
+    res = {}
+    for tag, fn in (("seq", run_seq), ("batched", run_bat)):
+        fn()  # warm-up step
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        res[tag] = e0.elapsed_time(e1) / steps
+    prof = q.mmdit_blocks_forward(table, bat_img, bat_txt, t_emb, pe, scratch=sc2, profile=True)
+    finite = all(bool(torch.isfinite(x).all().item()) for x in (bat_img, bat_txt, seq[0][0], seq[1][1]))
+    S = n_img + n_txt
+    lin = 0.0
+    for n, (N, K) in shapes.items():
+        rows = 1 if n.endswith("_mod") else (n_txt if n.startswith(("txt", "add_")) or n == "to_add_out" else n_img)
+        lin += 2.0 * rows * N * K
+    att = 4.0 * 24 * S * S * 128
+    step_ops = 2 * n_blocks * (lin + att)
+    del table, blocks
+    return {"step_c5_seq_ms": round(res["seq"], 2), "step_c5_batched_ms": round(res["batched"], 2),
+            "step_c5_top": round(step_ops / 1e12, 2),
+            "step_c5_seq_tflops": round(step_ops / res["seq"] / 1e9, 1),
+            "step_c5_batched_tflops": round(step_ops / res["batched"] / 1e9, 1),
+            "step_c5_batched_categories_ms": {k: round(v, 3) for k, v in prof.items()},
+            "step_c5_weights_build_s": round(build_s, 1), "step_c5_finite": finite}
 
 
 def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
