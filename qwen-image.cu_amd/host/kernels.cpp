@@ -118,6 +118,30 @@ SageWorkspace& sage_ws() {
     return ws;
 }
 
+// The same for the block loop's workspace.
+SageWorkspace& block_ws() {
+    static SageWorkspace ws;
+    return ws;
+}
+
+void* grown(SageWorkspace& w, int64_t need) {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(w.mu);
+    if (static_cast<int>(w.buf.size()) <= dev) {
+        w.buf.resize(dev + 1, nullptr);
+        w.bytes.resize(dev + 1, 0);
+    }
+    if (w.bytes[dev] < need) {
+        // the previous buffer may still be read by work queued earlier
+        HIP_CHECK(hipDeviceSynchronize());
+        if (w.buf[dev]) HIP_CHECK(hipFree(w.buf[dev]));
+        HIP_CHECK(hipMalloc(&w.buf[dev], need));
+        w.bytes[dev] = need;
+    }
+    return w.buf[dev];
+}
+
 }  // namespace
 
 void fwht_inplace(float* data, int M, int K, int had_block_size, hipStream_t stream) {
@@ -239,27 +263,42 @@ void attention_forward_sage_sm80_fp16io(const __half* q, const __half* k, const 
     REQUIRE(D == 64 || D == 128, fn, "head_dim %d not supported (64 or 128)", D);
     REQUIRE(BH > 0 && S > 0, fn, "need BH > 0 and S > 0 (BH=%d S=%d)", BH, S);
     const int64_t need = qimg_sage_scratch_bytes(BH, S, D);
-    void* ws = nullptr;
-    if (need > 0) {
-        int dev = 0;
-        HIP_CHECK(hipGetDevice(&dev));
-        SageWorkspace& w = sage_ws();
-        std::lock_guard<std::mutex> lock(w.mu);
-        if (static_cast<int>(w.buf.size()) <= dev) {
-            w.buf.resize(dev + 1, nullptr);
-            w.bytes.resize(dev + 1, 0);
-        }
-        if (w.bytes[dev] < need) {
-            // the previous buffer may still be read by work queued earlier
-            HIP_CHECK(hipDeviceSynchronize());
-            if (w.buf[dev]) HIP_CHECK(hipFree(w.buf[dev]));
-            HIP_CHECK(hipMalloc(&w.buf[dev], need));
-            w.bytes[dev] = need;
-        }
-        ws = w.buf[dev];
-    }
+    void* ws = need > 0 ? grown(sage_ws(), need) : nullptr;
     check(qimg_sage_attention(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
                               reinterpret_cast<const uint16_t*>(v), out, QIMG_FP32, scale, BH, S, D, causal ? 1 : 0,
                               ws, need, stream),
+          fn);
+}
+
+qimg_qlinear qlinear_view(const QuantizedWeight& w, const Tensor* bias) {
+    const char* fn = "qlinear_view";
+    REQUIRE(w.data.ndim == 2 && w.scales.data, fn, "weight must be a quantized [N, K] tensor");
+    REQUIRE(!bias || !bias->data || bias->dtype == DType::BF16, fn, "bias must be BF16");
+    return {w.data.data, static_cast<const float*>(w.scales.data), static_cast<int>(w.data.shape[0]),
+            static_cast<int>(w.data.shape[1]), w.had_block_size, qmode(w.mode, fn),
+            bias && bias->data ? static_cast<const uint16_t*>(bias->data) : nullptr};
+}
+
+void mmdit_blocks_forward(const std::vector<qimg_mmdit_block>& table, Tensor& img, Tensor& txt, const Tensor& temb,
+                          const Tensor& pe, int batch, float* prof_ms, hipStream_t stream) {
+    const char* fn = "mmdit_blocks_forward";
+    REQUIRE(!table.empty(), fn, "no blocks");
+    REQUIRE(batch >= 1, fn, "batch must be >= 1 (got %d)", batch);
+    REQUIRE(img.dtype == DType::FP32 && txt.dtype == DType::FP32 && temb.dtype == DType::FP32 &&
+                pe.dtype == DType::FP32,
+            fn, "img, txt, temb and pe must be FP32");
+    REQUIRE(img.numel() % (int64_t{batch} * 3072) == 0 && txt.numel() % (int64_t{batch} * 3072) == 0, fn,
+            "img/txt must hold batch x n x 3072 values");
+    const int n_img = static_cast<int>(img.numel() / (int64_t{batch} * 3072));
+    const int n_txt = static_cast<int>(txt.numel() / (int64_t{batch} * 3072));
+    REQUIRE(temb.numel() == 3072, fn, "temb must be [3072]");
+    REQUIRE(pe.numel() == static_cast<int64_t>(n_img + n_txt) * 256, fn, "pe must be [%d, 64, 4]", n_img + n_txt);
+    const int64_t need = qimg_mmdit_blocks_scratch_bytes(n_img, n_txt, batch);
+    REQUIRE(need > 0, fn, "bad token counts n_img=%d n_txt=%d", n_img, n_txt);
+    void* ws = grown(block_ws(), need);
+    check(qimg_mmdit_blocks_forward(table.data(), static_cast<int>(table.size()), static_cast<float*>(img.data),
+                                    static_cast<float*>(txt.data), static_cast<const float*>(temb.data),
+                                    static_cast<const float*>(pe.data), n_img, n_txt, batch, ws, need, prof_ms,
+                                    stream),
           fn);
 }

@@ -22,7 +22,9 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <vector>
 
+#include "qimg_hot.h"
 #include "tensor.h"
 
 enum class QuantMode { INT8_HADAMARD, INT4_SVD, BF16, INT4_AWQ, FP8_HADAMARD };
@@ -105,3 +107,46 @@ void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& wei
 void attention_forward_sage_sm80_fp16io(const __half* q, const __half* k, const __half* v, float* out,
                                         float scale, int BH, int S, int D, bool causal = false,
                                         hipStream_t stream = 0);
+
+// ---- the joint-block loop (transformer.cu:497-836) ---------------------
+// View of one quantized linear and its BF16 bias (or nullptr) for the
+// library's block loop. The tensors must outlive the view.
+qimg_qlinear qlinear_view(const QuantizedWeight& w, const Tensor* bias);
+
+// View of one TransformerWeights::Block (transformer.h:94-140). `Block` is
+// any struct with the reference's field names (img_mod_weight,
+// img_mod_bias, ..., norm_added_k_weight), so the reference's own type can
+// be passed as is.
+template <class Block>
+qimg_mmdit_block mmdit_block_view(const Block& b) {
+    qimg_mmdit_block v{};
+    v.img_mod = qlinear_view(b.img_mod_weight, &b.img_mod_bias);
+    v.txt_mod = qlinear_view(b.txt_mod_weight, &b.txt_mod_bias);
+    v.to_q = qlinear_view(b.to_q_weight, &b.to_q_bias);
+    v.to_k = qlinear_view(b.to_k_weight, &b.to_k_bias);
+    v.to_v = qlinear_view(b.to_v_weight, &b.to_v_bias);
+    v.add_q_proj = qlinear_view(b.add_q_proj_weight, &b.add_q_proj_bias);
+    v.add_k_proj = qlinear_view(b.add_k_proj_weight, &b.add_k_proj_bias);
+    v.add_v_proj = qlinear_view(b.add_v_proj_weight, &b.add_v_proj_bias);
+    v.to_out = qlinear_view(b.to_out_weight, &b.to_out_bias);
+    v.to_add_out = qlinear_view(b.to_add_out_weight, &b.to_add_out_bias);
+    v.img_mlp_fc1 = qlinear_view(b.img_mlp_fc1_weight, &b.img_mlp_fc1_bias);
+    v.img_mlp_fc2 = qlinear_view(b.img_mlp_fc2_weight, &b.img_mlp_fc2_bias);
+    v.txt_mlp_fc1 = qlinear_view(b.txt_mlp_fc1_weight, &b.txt_mlp_fc1_bias);
+    v.txt_mlp_fc2 = qlinear_view(b.txt_mlp_fc2_weight, &b.txt_mlp_fc2_bias);
+    v.norm_q = static_cast<const uint16_t*>(b.norm_q_weight.data);
+    v.norm_k = static_cast<const uint16_t*>(b.norm_k_weight.data);
+    v.norm_added_q = static_cast<const uint16_t*>(b.norm_added_q_weight.data);
+    v.norm_added_k = static_cast<const uint16_t*>(b.norm_added_k_weight.data);
+    return v;
+}
+
+// The blocks of `table` in order over `batch` sequences that share temb
+// and pe (batch 2 runs the two CFG forwards of main.cu:761-773 as one):
+// img FP32 [batch * n_img, 3072], txt FP32 [batch * n_txt, 3072], both
+// updated in place; temb FP32 [3072]; pe FP32 [n_txt + n_img, 64, 4], text
+// first (rope.h:154-160). The library grows a per-device workspace.
+// prof_ms, if given, receives the QIMG_PROF_COUNT PROFILE_BLOCK categories
+// (transformer.cu:486-495) summed over the blocks.
+void mmdit_blocks_forward(const std::vector<qimg_mmdit_block>& table, Tensor& img, Tensor& txt, const Tensor& temb,
+                          const Tensor& pe, int batch = 1, float* prof_ms = nullptr, hipStream_t stream = 0);

@@ -280,6 +280,88 @@ void case_sage(int BH, int S, int D, bool causal) {
 }
 
 // Host-side rejections: fake device pointers that must never be touched.
+// The reference's TransformerWeights::Block field names (transformer.h:94-140),
+// which mmdit_block_view reads.
+struct RefBlock {
+    QuantizedWeight img_mod_weight, txt_mod_weight, to_q_weight, to_k_weight, to_v_weight, add_q_proj_weight,
+        add_k_proj_weight, add_v_proj_weight, to_out_weight, to_add_out_weight, img_mlp_fc1_weight,
+        img_mlp_fc2_weight, txt_mlp_fc1_weight, txt_mlp_fc2_weight;
+    Tensor img_mod_bias, txt_mod_bias, to_q_bias, to_k_bias, to_v_bias, add_q_proj_bias, add_k_proj_bias,
+        add_v_proj_bias, to_out_bias, to_add_out_bias, img_mlp_fc1_bias, img_mlp_fc2_bias, txt_mlp_fc1_bias,
+        txt_mlp_fc2_bias;
+    Tensor norm_q_weight, norm_k_weight, norm_added_q_weight, norm_added_k_weight;
+};
+
+// The block loop through the C++ layer (batch 2, one TransformerWeights::
+// Block-shaped struct) against the C ABI's one-block entry point run on each
+// sequence alone: bit-identical.
+void case_block_loop() {
+    Rng r(99);
+    RefBlock b;
+    const int D = 3072, F = 12288;
+    auto lin = [&](QuantizedWeight& w, Tensor& bias, int N, int K) {
+        std::vector<uint16_t> h(static_cast<size_t>(N) * K);
+        for (auto& x : h) x = or_f32_to_bf16((r.uniform() - 0.5f) * 0.07f);
+        Tensor wt = upload(h, {N, K}, DType::BF16);
+        w = quantize_weight_tensor(wt);
+        bias = upload(bf16_normal(r, N, 0.01f), {N}, DType::BF16);
+    };
+    lin(b.img_mod_weight, b.img_mod_bias, 6 * D, D);
+    lin(b.txt_mod_weight, b.txt_mod_bias, 6 * D, D);
+    lin(b.to_q_weight, b.to_q_bias, D, D);
+    lin(b.to_k_weight, b.to_k_bias, D, D);
+    lin(b.to_v_weight, b.to_v_bias, D, D);
+    lin(b.add_q_proj_weight, b.add_q_proj_bias, D, D);
+    lin(b.add_k_proj_weight, b.add_k_proj_bias, D, D);
+    lin(b.add_v_proj_weight, b.add_v_proj_bias, D, D);
+    lin(b.to_out_weight, b.to_out_bias, D, D);
+    lin(b.to_add_out_weight, b.to_add_out_bias, D, D);
+    lin(b.img_mlp_fc1_weight, b.img_mlp_fc1_bias, F, D);
+    lin(b.img_mlp_fc2_weight, b.img_mlp_fc2_bias, D, F);
+    lin(b.txt_mlp_fc1_weight, b.txt_mlp_fc1_bias, F, D);
+    lin(b.txt_mlp_fc2_weight, b.txt_mlp_fc2_bias, D, F);
+    for (Tensor* t : {&b.norm_q_weight, &b.norm_k_weight, &b.norm_added_q_weight, &b.norm_added_k_weight}) {
+        std::vector<uint16_t> h(128);
+        for (auto& x : h) x = or_f32_to_bf16(1.0f + 0.1f * r.normal());
+        *t = upload(h, {128}, DType::BF16);
+    }
+    const int n_img = 64, n_txt = 16, S = n_img + n_txt;
+    std::vector<float> hi = f32_normal(r, 2 * n_img * D, 1.0f), ht = f32_normal(r, 2 * n_txt * D, 1.0f);
+    std::vector<float> hte = f32_normal(r, D, 1.0f), hpe(static_cast<size_t>(S) * 256);
+    for (int s = 0; s < S; ++s)
+        for (int j = 0; j < 64; ++j) {
+            const float a = 0.01f * s * (j + 1), c = std::cos(a), sn = std::sin(a);
+            float* p = &hpe[(static_cast<size_t>(s) * 64 + j) * 4];
+            p[0] = c, p[1] = -sn, p[2] = sn, p[3] = c;
+        }
+    Tensor img = upload(hi, {2 * n_img, D}, DType::FP32), txt = upload(ht, {2 * n_txt, D}, DType::FP32);
+    Tensor temb = upload(hte, {D}, DType::FP32), pe = upload(hpe, {S, 64, 4}, DType::FP32);
+    std::vector<qimg_mmdit_block> table{mmdit_block_view(b)};
+    float prof[QIMG_PROF_COUNT];
+    mmdit_blocks_forward(table, img, txt, temb, pe, 2, prof);
+    std::vector<float> gi = download<float>(img), gt = download<float>(txt);
+    bool ok = true;
+    const int64_t bytes = qimg_mmdit_block_scratch_bytes(n_img, n_txt);
+    Tensor scratch = Tensor::alloc({bytes}, DType::UINT8);
+    for (int q = 0; q < 2; ++q) {
+        std::vector<float> si(hi.begin() + q * n_img * D, hi.begin() + (q + 1) * n_img * D);
+        std::vector<float> st(ht.begin() + q * n_txt * D, ht.begin() + (q + 1) * n_txt * D);
+        Tensor i1 = upload(si, {n_img, D}, DType::FP32), t1 = upload(st, {n_txt, D}, DType::FP32);
+        const int rc = qimg_mmdit_block_forward(&table[0], static_cast<float*>(i1.data), static_cast<float*>(t1.data),
+                                                static_cast<const float*>(temb.data),
+                                                static_cast<const float*>(pe.data), n_img, n_txt, scratch.data,
+                                                bytes, nullptr, nullptr);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> ri = download<float>(i1), rt = download<float>(t1);
+        ok = ok && rc == QIMG_OK && std::memcmp(ri.data(), gi.data() + q * n_img * D, ri.size() * 4) == 0 &&
+             std::memcmp(rt.data(), gt.data() + q * n_txt * D, rt.size() * 4) == 0;
+    }
+    double total = 0;
+    for (float v : prof) total += v;
+    for (float v : gi) ok = ok && std::isfinite(v);
+    report("mmdit_blocks_forward", ok && total > 0, "batch 2 vs two single-sequence blocks");
+}
+
 int expect_error(const std::string& c) {
     void* fake = reinterpret_cast<void*>(0x10000);
     Tensor x = Tensor::wrap(fake, {4, 64}, DType::FP32);
@@ -311,6 +393,13 @@ int expect_error(const std::string& c) {
         attention_forward_sage_sm80_fp16io(static_cast<const __half*>(fake), static_cast<const __half*>(fake),
                                            static_cast<const __half*>(fake), static_cast<float*>(fake), 0.1f, 2, 64,
                                            96);
+    } else if (c == "block_pe") {
+        Tensor img = Tensor::wrap(fake, {64, 3072}, DType::FP32);
+        Tensor txt = Tensor::wrap(fake, {16, 3072}, DType::FP32);
+        Tensor temb = Tensor::wrap(fake, {3072}, DType::FP32);
+        Tensor pe = Tensor::wrap(fake, {64, 64, 4}, DType::FP32);
+        std::vector<qimg_mmdit_block> table(1);
+        mmdit_blocks_forward(table, img, txt, temb, pe);
     } else {
         fprintf(stderr, "unknown case %s\n", c.c_str());
         return 2;
@@ -336,6 +425,7 @@ int main(int argc, char** argv) {
     case_fp8_linear();
     case_sage(2, 300, 128, false);
     case_sage(3, 129, 64, true);
+    case_block_loop();
     printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "PASSED", g_fail);
     return g_fail ? 1 : 0;
 }

@@ -23,6 +23,7 @@ REJECTIONS = {
     "scratch": "scratch 16 bytes < required",
     "hbs": "hbs=48 is not a power of two",
     "sage_head_dim": "head_dim 96 not supported",
+    "block_pe": "mmdit_blocks_forward: pe must be [80, 64, 4]",
 }
 
 
