@@ -110,22 +110,46 @@ struct Acc<true> {
     typedef v16f type;
 };
 
+// One GEMM of a launch: out[M,N] = epilogue(A[M,K] . W[N,K]^T), `tiles` =
+// its number of BM x BN tiles.
+struct TileProblem {
+    const uint8_t* A;
+    const uint8_t* W;
+    const float* as;
+    const float* ws;
+    const uint16_t* bias;
+    void* out;
+    int M, N, K, tiles;
+};
+
 template <bool FP8, int OUT_DT, bool GELU>
-__global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(
-    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
-    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
-    int N, int K) {
+__global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, TileProblem p1) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
     float* s_ws = s_as + 256;
     float* s_bias = s_ws + 256;
 
-    const int tiles_m = (M + BM - 1) / BM;
+    // Two problems share the grid: tiles [0, p0.tiles) are problem 0, the
+    // rest problem 1 (e.g. the text-stream linear in the CUs the image-stream
+    // linear leaves idle in its last round).
+    int logical = xcd_remap(blockIdx.x, p0.tiles + p1.tiles);
+    const bool second = logical >= p0.tiles;
+    if (second) logical -= p0.tiles;
+    const uint8_t* __restrict__ A = second ? p1.A : p0.A;
+    const uint8_t* __restrict__ W = second ? p1.W : p0.W;
+    const float* __restrict__ as = second ? p1.as : p0.as;
+    const float* __restrict__ ws = second ? p1.ws : p0.ws;
+    const uint16_t* __restrict__ bias = second ? p1.bias : p0.bias;
+    void* __restrict__ out = second ? p1.out : p0.out;
+    const int M = second ? p1.M : p0.M;
+    const int N = second ? p1.N : p0.N;
+    const int K = second ? p1.K : p0.K;
+
     const int tiles_n = (N + BN - 1) / BN;
+    const int tiles_m = (M + BM - 1) / BM;
     // Grouped tile order: groups of GROUP_M tile rows, column-major inside a
     // group, so the 32 tiles an XCD runs at once form a 4 x 8 block that
     // shares 4 activation slices and 8 weight slices in that XCD's L2.
-    const int logical = xcd_remap(blockIdx.x, tiles_m * tiles_n);
     const int gsz = GROUP_M * tiles_n;
     const int first_m = (logical / gsz) * GROUP_M;
     const int gm = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
@@ -527,25 +551,24 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
 }
 
 template <bool FP8, int OUT_DT, bool GELU>
-hipError_t launch_tiled(const void* a, const float* as, int M, int K, const void* w,
-                        const float* ws, int N, const uint16_t* bias, void* out,
-                        hipStream_t stream) {
-    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_w8a8_kernel<FP8, OUT_DT, GELU>), dim3(tiles), dim3(NTHR), 0, stream,
-                       static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias,
-                       out, M, N, K);
+hipError_t launch_tiled(const TileProblem& p0, const TileProblem& p1, hipStream_t stream) {
+    hipLaunchKernelGGL((gemm_w8a8_kernel<FP8, OUT_DT, GELU>), dim3(p0.tiles + p1.tiles), dim3(NTHR), 0, stream, p0,
+                       p1);
     return hipGetLastError();
 }
 
+TileProblem tile_problem(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
+                         const uint16_t* bias, void* out) {
+    return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, M, N, K,
+            ((M + BM - 1) / BM) * ((N + BN - 1) / BN)};
+}
+
 template <bool FP8>
-hipError_t dispatch_tiled(const void* a, const float* as, int M, int K, const void* w,
-                          const float* ws, int N, const uint16_t* bias, void* out, int out_dt,
-                          int gelu, hipStream_t stream) {
+hipError_t dispatch_tiled(const TileProblem& p0, const TileProblem& p1, int out_dt, int gelu, hipStream_t stream) {
     if (out_dt == QIMG_FP32)
-        return gelu ? launch_tiled<FP8, QIMG_FP32, true>(a, as, M, K, w, ws, N, bias, out, stream)
-                    : launch_tiled<FP8, QIMG_FP32, false>(a, as, M, K, w, ws, N, bias, out, stream);
-    return gelu ? launch_tiled<FP8, QIMG_BF16, true>(a, as, M, K, w, ws, N, bias, out, stream)
-                : launch_tiled<FP8, QIMG_BF16, false>(a, as, M, K, w, ws, N, bias, out, stream);
+        return gelu ? launch_tiled<FP8, QIMG_FP32, true>(p0, p1, stream)
+                    : launch_tiled<FP8, QIMG_FP32, false>(p0, p1, stream);
+    return gelu ? launch_tiled<FP8, QIMG_BF16, true>(p0, p1, stream) : launch_tiled<FP8, QIMG_BF16, false>(p0, p1, stream);
 }
 
 }  // namespace
@@ -622,10 +645,10 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
             }
             if (m_big < M && !small_m_fits(M - m_big, N, K)) m_big = M;
         }
-        hipError_t e = fp8 ? dispatch_tiled<true>(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out,
-                                                  out_dtype, gelu, stream)
-                           : dispatch_tiled<false>(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out,
-                                                   out_dtype, gelu, stream);
+        const TileProblem p0 = tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out);
+        const TileProblem none{};
+        hipError_t e = fp8 ? dispatch_tiled<true>(p0, none, out_dtype, gelu, stream)
+                           : dispatch_tiled<false>(p0, none, out_dtype, gelu, stream);
         if (e != hipSuccess || m_big == M) return e;
         const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
         return launch_linear_small_m(static_cast<const uint8_t*>(act_q) + static_cast<int64_t>(m_big) * K,
@@ -640,6 +663,41 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
                        static_cast<const int8_t*>(act_q), static_cast<const int8_t*>(w_q),
                        act_scales, w_scales, bias, out, M, N, K, out_dtype, gelu);
     return hipGetLastError();
+}
+
+// Two linears of the same mode, output type and epilogue in one launch
+// when the second one's tiles fit into the first one's last round
+// (transformer.cu runs the image- and text-stream linears of a block back to
+// back: at 4096 image tokens the N = 3072 linears are 192 tiles on 256 CUs,
+// and the text stream's 256 rows are one more tile row). Otherwise the two
+// run one after the other through launch_linear_prequantized. Each output
+// element is computed exactly as in a launch of its own.
+hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
+                              hipStream_t stream) {
+    auto single = [&](const LinearArgs& x) {
+        return launch_linear_prequantized(x.act_q, x.act_scales, x.M, x.K, x.w_q, x.w_scales, x.N, mode, x.bias,
+                                          x.out, out_dtype, gelu, stream);
+    };
+    bool pair = a.M > 0 && a.N > 0 && b.M > 0 && b.N > 0 &&
+                g_linear_kernel.load(std::memory_order_relaxed) == QIMG_LINEAR_AUTO && (a.K % BK) == 0 &&
+                (b.K % BK) == 0 && small_m_variant(a.M, a.N, a.K) == 0;
+    if (pair) {
+        const int cus = device_cu_count();
+        const int64_t ta = static_cast<int64_t>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+        const int64_t tb = static_cast<int64_t>((b.M + BM - 1) / BM) * ((b.N + BN - 1) / BN);
+        const int64_t rounds = cus > 0 ? (ta + cus - 1) / cus : 0;
+        const int64_t tail = ta - (rounds - 1) * cus;
+        // no extra round, and not a case for the tail-row split of a lone launch
+        pair = cus > 0 && ta + tb <= rounds * cus && !(rounds > 1 && tail * 2 < cus);
+    }
+    if (!pair) {
+        hipError_t e = a.M > 0 ? single(a) : hipSuccess;
+        return e != hipSuccess || b.M == 0 ? e : single(b);
+    }
+    const TileProblem p0 = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out);
+    const TileProblem p1 = tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out);
+    return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(p0, p1, out_dtype, gelu, stream)
+                                        : dispatch_tiled<false>(p0, p1, out_dtype, gelu, stream);
 }
 
 }  // namespace qimg

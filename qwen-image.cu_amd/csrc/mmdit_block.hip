@@ -54,6 +54,8 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
     w.txt_norm = reinterpret_cast<float*>(take(4 * rt * DIM));
     w.act_q = take(mmax * MLP);
     w.act_scales = reinterpret_cast<float*>(take(4 * mmax));
+    w.act_q_txt = take((rt > 1 ? rt : 1) * MLP);
+    w.act_scales_txt = reinterpret_cast<float*>(take(4 * (rt > 1 ? rt : 1)));
     for (int i = 0; i < 3; ++i) {
         w.img_qkv[i] = reinterpret_cast<float*>(take(4 * ri * DIM));
         w.txt_qkv[i] = reinterpret_cast<float*>(take(4 * rt * DIM));
@@ -103,6 +105,22 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         auto same_quant = [](const qimg_qlinear& a, const qimg_qlinear& c) {
             return a.K == c.K && a.hbs == c.hbs && a.mode == c.mode;
         };
+        // quantized activations of the image (act_q) and text (act_q_txt)
+        // streams live side by side, so that the two streams' linears can
+        // share a launch
+        auto quant_txt = [&](const float* x, int M, const qimg_qlinear& l) {
+            return launch_fwht_quant(x, QIMG_FP32, M, l.K, l.hbs, l.mode, w.act_q_txt, w.act_scales_txt, s);
+        };
+        auto gemm_pair = [&](int Mi_, const qimg_qlinear& li, float* oi, int Mt_, const qimg_qlinear& lt, float* ot,
+                             int gelu) -> hipError_t {
+            if (li.mode != lt.mode) {
+                hipError_t r = Mi_ ? gemm(w.act_q, w.act_scales, Mi_, li, oi, gelu) : hipSuccess;
+                return r != hipSuccess || !Mt_ ? r : gemm(w.act_q_txt, w.act_scales_txt, Mt_, lt, ot, gelu);
+            }
+            const LinearArgs a{w.act_q, w.act_scales, Mi_, li.K, li.w, li.scales, li.N, li.bias, oi};
+            const LinearArgs c{w.act_q_txt, w.act_scales_txt, Mt_, lt.K, lt.w, lt.scales, lt.N, lt.bias, ot};
+            return launch_linear_pair(a, c, li.mode, QIMG_FP32, gelu, s);
+        };
 
         // modulation: silu(t_emb) -> img_mod / txt_mod (transformer.cu:506-515)
         QIMG_TRY(mark(QIMG_PROF_MODULATION));
@@ -123,25 +141,20 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, Mi, DIM, EPS, s));
         QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
 
-        // QKV with one activation quant per stream (transformer.cu:557-606)
+        // QKV with one activation quant per stream (transformer.cu:557-606);
+        // the image and text linears of each of q, k, v share a launch
         QIMG_TRY(mark(QIMG_PROF_QKV_GEMM));
         {
             const qimg_qlinear* il[3] = {&b.to_q, &b.to_k, &b.to_v};
             const qimg_qlinear* tl[3] = {&b.add_q_proj, &b.add_k_proj, &b.add_v_proj};
-            for (int pass = 0; pass < 2; ++pass) {
-                const qimg_qlinear* const* L = pass == 0 ? il : tl;
-                const float* x = pass == 0 ? w.img_norm : w.txt_norm;
-                float* const* outs = pass == 0 ? w.img_qkv : w.txt_qkv;
-                const int M = pass == 0 ? Mi : Mt;
-                if (M == 0) continue;
-                const bool share = same_quant(*L[0], *L[1]) && same_quant(*L[0], *L[2]);
-                if (share) QIMG_TRY(quant(x, M, *L[0]));
-                for (int i = 0; i < 3; ++i) {
-                    if (share)
-                        QIMG_TRY(gemm(w.act_q, w.act_scales, M, *L[i], outs[i], 0));
-                    else
-                        QIMG_TRY(linear(x, M, *L[i], outs[i], 0));
-                }
+            const bool share_i = same_quant(*il[0], *il[1]) && same_quant(*il[0], *il[2]);
+            const bool share_t = same_quant(*tl[0], *tl[1]) && same_quant(*tl[0], *tl[2]);
+            if (share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[0]));
+            if (share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[0]));
+            for (int i = 0; i < 3; ++i) {
+                if (!share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[i]));
+                if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i]));
+                QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], Mt, *tl[i], w.txt_qkv[i], 0));
             }
         }
 
@@ -179,8 +192,9 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(mark(QIMG_PROF_OUT_GEMM));
         float* img_proj = w.img_qkv[1];
         float* txt_proj = w.txt_qkv[1];
-        QIMG_TRY(linear(img_attn, Mi, b.to_out, img_proj, 0));
-        QIMG_TRY(linear(txt_attn, Mt, b.to_add_out, txt_proj, 0));
+        if (Mi) QIMG_TRY(quant(img_attn, Mi, b.to_out));
+        if (Mt) QIMG_TRY(quant_txt(txt_attn, Mt, b.to_add_out));
+        QIMG_TRY(gemm_pair(Mi, b.to_out, img_proj, Mt, b.to_add_out, txt_proj, 0));
 
         // residual with gate1 (transformer.cu:740-746)
         QIMG_TRY(mark(QIMG_PROF_GATE_ATTN));
@@ -196,10 +210,15 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));
         float* img_out = w.img_qkv[2];
         float* txt_out = w.txt_qkv[2];
+        // fc1 of each stream on its own, then both fc2 in one launch
         QIMG_TRY(linear(w.img_norm, Mi, b.img_mlp_fc1, w.img_mlp, 1));
-        QIMG_TRY(linear(w.img_mlp, Mi, b.img_mlp_fc2, img_out, 0));
-        QIMG_TRY(linear(w.txt_norm, Mt, b.txt_mlp_fc1, w.txt_mlp, 1));
-        QIMG_TRY(linear(w.txt_mlp, Mt, b.txt_mlp_fc2, txt_out, 0));
+        if (Mi) QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
+        if (Mt) {
+            QIMG_TRY(quant_txt(w.txt_norm, Mt, b.txt_mlp_fc1));
+            QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1));
+            QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2));
+        }
+        QIMG_TRY(gemm_pair(Mi, b.img_mlp_fc2, img_out, Mt, b.txt_mlp_fc2, txt_out, 0));
 
         // residual with gate2 (transformer.cu:812-818)
         QIMG_TRY(mark(QIMG_PROF_GATE_MLP));

@@ -17,6 +17,19 @@ hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, 
 hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t stream);
 
 // gemm_w8a8.hip
+// One linear of launch_linear_pair.
+struct LinearArgs {
+    const void* act_q;
+    const float* act_scales;
+    int M, K;
+    const void* w_q;
+    const float* w_scales;
+    int N;
+    const uint16_t* bias;
+    void* out;
+};
+hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
+                              hipStream_t stream);
 hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
                                       const void* w_q, const float* w_scales, int N, int mode,
                                       const uint16_t* bias, void* out, int out_dtype, int gelu,
@@ -80,8 +93,10 @@ struct BlockScratch {
     float* txt_mods;
     float* img_norm;
     float* txt_norm;
-    uint8_t* act_q;
+    uint8_t* act_q;  // image stream (and the modulation input)
     float* act_scales;
+    uint8_t* act_q_txt;  // text stream
+    float* act_scales_txt;
     float* img_qkv[3];
     float* txt_qkv[3];
     uint16_t* qkv16[3];

@@ -309,6 +309,49 @@ def test_mmdit_blocks_rejects_bad_arguments(qimg, int8_block):
         qimg.mmdit_blocks_forward(qimg.BlockTable([(bad, B, N)]), img, txt, t_emb, pe)
 
 
+def _gpu_block(qimg, seed, mode=0):
+    """Random N(0,0.02) block weights drawn on the GPU (no oracle copy)."""
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    shapes = {"img_mod": (18432, 3072), "txt_mod": (18432, 3072)}
+    for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
+        shapes[n] = (3072, 3072)
+    for s in ("img", "txt"):
+        shapes[f"{s}_mlp_fc1"] = (12288, 3072)
+        shapes[f"{s}_mlp_fc2"] = (3072, 12288)
+    W = {n: qimg.quantize_weight_tensor((torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16),
+                                        mode=mode) for n, (N, K) in shapes.items()}
+    B = {n: (torch.randn(N, generator=g, device=DEV) * 0.01).to(torch.bfloat16) for n, (N, K) in shapes.items()}
+    nr = {n: (1 + 0.1 * torch.randn(128, generator=g, device=DEV)).to(torch.bfloat16)
+          for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k")}
+    return W, B, nr
+
+
+@pytest.mark.parametrize("n_img,n_txt,batch", [(4096, 256, 1), (1024, 512, 2)])
+def test_mmdit_block_same_for_every_kernel_choice(qimg, n_img, n_txt, batch):
+    """At full block sizes the dispatcher pairs the image- and text-stream
+    linears in one launch, splits tail tile rows off to the small-tile kernel
+    and takes the small-M kernels for the modulation; forcing the large-tile
+    kernel everywhere must give the same bits (int8 accumulation is exact)."""
+    W, B, nr = _gpu_block(qimg, 3)
+    table = qimg.BlockTable([(W, B, nr)])
+    g = torch.Generator(device=DEV).manual_seed(4)
+    img = torch.randn(batch, n_img, 3072, generator=g, device=DEV)
+    txt = torch.randn(batch, n_txt, 3072, generator=g, device=DEV)
+    t_emb = torch.randn(3072, generator=g, device=DEV)
+    side = int(np.sqrt(n_img)) * 2
+    pe = _dev(qimg.qwen_image_pe(side, side, 2, n_txt))
+    outs = []
+    for choice in (qimg.LINEAR_AUTO, qimg.LINEAR_LARGE_TILE):
+        i, t = img.clone(), txt.clone()
+        with qimg.linear_kernel(choice):
+            qimg.mmdit_blocks_forward(table, i, t, t_emb, pe)
+        torch.cuda.synchronize()
+        outs.append((i, t))
+    assert torch.isfinite(outs[0][0]).all()
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+
+
 def test_mmdit_block_fp8_runs_close_to_int8(qimg, oracle, int8_block):
     """e4m3 weights through the same block: finite, deterministic, and close
     to the int8 block (both approximate the same bf16 weights). The fp8 linear
