@@ -195,6 +195,14 @@ int qimg_silu(const float* x, float* out, int64_t n, void* stream);
 int qimg_layernorm_modulate(const float* x, const float* shift, const float* scale, float* out,
                             int rows, int dim, float eps, void* stream);
 
+/* qimg_layernorm_modulate followed by the FWHT + quantization of
+ * qimg_quantize_activation (fwht_quantize_fp32, cuda_kernels.cu:2493-2601)
+ * in one pass, for a LayerNorm whose only consumer is a quantized linear
+ * (transformer.cu:526-606, 754-785): q_out int8 or e4m3 [rows, dim],
+ * q_scales fp32 [rows], bit-identical to the two calls. */
+int qimg_layernorm_modulate_quant(const float* x, const float* shift, const float* scale, int rows, int dim,
+                                  int hbs, int mode, float eps, void* q_out, float* q_scales, void* stream);
+
 /* rms_norm_fp32 on the per-head Q or K rows (cuda_kernels.cu:1656-1692)
  * + concat_transpose_fused_fp32 (transformer.cu:106-130, text tokens
  * first) + rope_apply_fp32_to_fp16 (cuda_kernels.cu:1935-1971), fused:

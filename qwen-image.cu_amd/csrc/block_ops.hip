@@ -32,60 +32,16 @@ __global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ x, 
     }
 }
 
-// layer_norm_modulate_fp32_kernel (cuda_kernels.cu:1799-1853): per row,
-// mean, then the variance about it, inv_std = rsqrt(var/dim + eps),
-// out = (x - mean) * inv_std * (1 + scale) + shift. One workgroup per row;
-// the row stays in registers between the passes.
-constexpr int LN_THR = 256;
-constexpr int LN_MAXV = 4;  // float4 per thread -> dim <= 4096
-
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();  // red may still be read by a previous call
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.0f;
-#pragma unroll
-    for (int w = 0; w < LN_THR / 64; ++w) t += red[w];
-    return t;
-}
-
+// layer_norm_modulate_fp32_kernel (cuda_kernels.cu:1799-1853), one
+// workgroup per row (ln_modulate_row).
 __global__ __launch_bounds__(LN_THR) void layernorm_modulate_kernel(const float* __restrict__ x,
                                                                     const float* __restrict__ shift,
                                                                     const float* __restrict__ scale,
                                                                     float* __restrict__ out, int dim, float eps) {
     __shared__ float red[LN_THR / 64];
     const int64_t row = blockIdx.x;
-    const v4f* xr = reinterpret_cast<const v4f*>(x + row * dim);
-    const int nv = dim >> 2;
-    v4f v[LN_MAXV];
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < LN_MAXV; ++j) {
-        const int c = threadIdx.x + j * LN_THR;
-        v[j] = c < nv ? xr[c] : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-        s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-    }
-    const float mean = block_sum(s, red) / dim;
-    float q = 0.0f;
-#pragma unroll
-    for (int j = 0; j < LN_MAXV; ++j) {
-        const int c = threadIdx.x + j * LN_THR;
-        if (c < nv) {
-            const v4f d = v[j] - mean;
-            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-        }
-    }
-    const float inv_std = rsqrtf(block_sum(q, red) / dim + eps);
-    const v4f* sh = reinterpret_cast<const v4f*>(shift);
-    const v4f* sc = reinterpret_cast<const v4f*>(scale);
     v4f* o = reinterpret_cast<v4f*>(out + row * dim);
-#pragma unroll
-    for (int j = 0; j < LN_MAXV; ++j) {
-        const int c = threadIdx.x + j * LN_THR;
-        if (c < nv) o[c] = (v[j] - mean) * inv_std * (1.0f + sc[c]) + sh[c];
-    }
+    ln_modulate_row(x + row * dim, shift, scale, dim, eps, red, [&](int c, v4f v) { o[c] = v; });
 }
 
 // One wave per (sequence b, token s, head h) of the joint sequences (txt
@@ -178,7 +134,7 @@ hipError_t launch_silu(const float* x, float* out, int64_t n, hipStream_t stream
 hipError_t launch_layernorm_modulate(const float* x, const float* shift, const float* scale, float* out, int rows,
                                      int dim, float eps, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    if ((dim & 3) != 0 || dim > LN_THR * 4 * LN_MAXV) return hipErrorInvalidValue;
+    if ((dim & 3) != 0 || dim > LN_MAX_DIM) return hipErrorInvalidValue;
     hipLaunchKernelGGL(layernorm_modulate_kernel, dim3(rows), dim3(LN_THR), 0, stream, x, shift, scale, out, dim, eps);
     return hipGetLastError();
 }

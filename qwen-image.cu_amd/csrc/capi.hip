@@ -327,6 +327,23 @@ int qimg_layernorm_modulate(const float* x, const float* shift, const float* sca
                       fn);
 }
 
+int qimg_layernorm_modulate_quant(const float* x, const float* shift, const float* scale, int rows, int dim, int hbs,
+                                  int mode, float eps, void* q_out, float* q_scales, void* stream) {
+    const char* fn = "qimg_layernorm_modulate_quant";
+    QIMG_REQUIRE(rows >= 0 && dim > 0 && dim % 4 == 0 && dim <= 4096,
+                 "%s: need rows >= 0 and dim a multiple of 4 in (0, 4096] (rows=%d dim=%d)", fn, rows, dim);
+    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
+    QIMG_REQUIRE(hbs >= 1 && (hbs & (hbs - 1)) == 0 && dim % hbs == 0,
+                 "%s: hbs=%d must be a power of two dividing dim=%d", fn, hbs, dim);
+    if (rows == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && shift && scale && q_out && q_scales, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(x) && aligned16(shift) && aligned16(scale) && aligned16(q_out),
+                 "%s: buffers must be 16-byte aligned", fn);
+    return hip_status(qimg::launch_ln_fwht_quant(x, shift, scale, rows, dim, hbs, mode, eps, q_out, q_scales,
+                                                 static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
 static int check_heads(const char* fn, int n_txt, int n_img, int H) {
     QIMG_REQUIRE(n_txt >= 0 && n_img >= 0 && H > 0, "%s: bad sizes n_txt=%d n_img=%d H=%d", fn, n_txt, n_img, H);
     QIMG_REQUIRE(static_cast<int64_t>(n_txt + n_img) * H * 128 < (int64_t{1} << 31), "%s: too many elements", fn);

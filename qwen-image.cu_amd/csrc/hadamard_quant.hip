@@ -116,52 +116,13 @@ __device__ __forceinline__ float load1<float>(const float* p) { return *p; }
 template <>
 __device__ __forceinline__ float load1<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
 
-// grid.x = rows, blockDim.x = 64..256 (multiple of 64).
-// hbs_log2 = log2(hbs) (0 = no transform). K % 16 == 0 and hbs >= 16 take
-// the vector path (first 4 stages in registers straight from global).
-template <typename InT, RowOut OUT>
-__global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
-    const InT* x, void* out, float* __restrict__ scales, int M, int K,
-    int hbs_log2, float norm) {
-    extern __shared__ float lds[];
-    float* red = lds + lds_pad(K) + 1;  // 4 floats for the cross-wave max
-    const int row = blockIdx.x;
-    if (row >= M) return;
-    const InT* xin = x + static_cast<int64_t>(row) * K;
+// The remaining butterfly stages (from bit `lo`) on the row in LDS, then the
+// row's output: fp32 as is, or per-row scale amax/QMAX and int8/e4m3 values.
+template <RowOut OUT>
+__device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, int hbs_log2, float norm, int lo,
+                                                float amax, void* out, float* __restrict__ scales, int row) {
     const int tid = threadIdx.x;
     const int nthr = blockDim.x;
-
-    const bool vec = (hbs_log2 >= 4) && ((K & 15) == 0);
-    float amax = 0.0f;
-    int lo;  // first stage bit still to do
-
-    if (vec) {
-        const bool only = (hbs_log2 == 4);
-        for (int c = tid; c < (K >> 4); c += nthr) {
-            float v[16];
-            load16<InT>(xin + 16 * c, v);
-            butterfly<4>(v);
-            if (only) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    v[i] = v[i] * norm;
-                    amax = fmaxf(amax, fabsf(v[i]));
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) lds[lds_pad(16 * c + i)] = v[i];
-        }
-        lo = 4;
-    } else {
-        for (int i = tid; i < K; i += nthr) {
-            float v = load1<InT>(xin + i);
-            if (hbs_log2 == 0) amax = fmaxf(amax, fabsf(v));
-            lds[lds_pad(i)] = v;
-        }
-        lo = 0;
-    }
-    __syncthreads();
-
     while (lo < hbs_log2) {
         const int rem = hbs_log2 - lo;
         const int rb = rem >= 8 ? 4 : (rem > 4 ? (rem + 1) / 2 : rem);
@@ -218,6 +179,104 @@ __global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
     }
 }
 
+// grid.x = rows, blockDim.x = 64..256 (multiple of 64).
+// hbs_log2 = log2(hbs) (0 = no transform). K % 16 == 0 and hbs >= 16 take
+// the vector path (first 4 stages in registers straight from global).
+template <typename InT, RowOut OUT>
+__global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
+    const InT* x, void* out, float* __restrict__ scales, int M, int K,
+    int hbs_log2, float norm) {
+    extern __shared__ float lds[];
+    float* red = lds + lds_pad(K) + 1;  // 4 floats for the cross-wave max
+    const int row = blockIdx.x;
+    if (row >= M) return;
+    const InT* xin = x + static_cast<int64_t>(row) * K;
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+
+    const bool vec = (hbs_log2 >= 4) && ((K & 15) == 0);
+    float amax = 0.0f;
+    int lo;  // first stage bit still to do
+
+    if (vec) {
+        const bool only = (hbs_log2 == 4);
+        for (int c = tid; c < (K >> 4); c += nthr) {
+            float v[16];
+            load16<InT>(xin + 16 * c, v);
+            butterfly<4>(v);
+            if (only) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    v[i] = v[i] * norm;
+                    amax = fmaxf(amax, fabsf(v[i]));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lds[lds_pad(16 * c + i)] = v[i];
+        }
+        lo = 4;
+    } else {
+        for (int i = tid; i < K; i += nthr) {
+            float v = load1<InT>(xin + i);
+            if (hbs_log2 == 0) amax = fmaxf(amax, fabsf(v));
+            lds[lds_pad(i)] = v;
+        }
+        lo = 0;
+    }
+    __syncthreads();
+
+    fwht_quant_tail<OUT>(lds, red, K, hbs_log2, norm, lo, amax, out, scales, row);
+}
+
+// LayerNorm + modulate (ln_modulate_row) feeding the FWHT + row quant of
+// the next linear's input in one pass: the normalized row goes to LDS
+// instead of HBM. One LN_THR-thread workgroup per row, K <= LN_MAX_DIM.
+// Each element sees the same operations as layernorm_modulate followed by
+// fwht_quant_rows_kernel, so the int8/e4m3 values and scales are the same.
+template <RowOut OUT>
+__global__ __launch_bounds__(LN_THR) void ln_fwht_quant_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ shift,
+                                                               const float* __restrict__ scale, float eps,
+                                                               void* out, float* __restrict__ scales, int K,
+                                                               int hbs_log2, float norm) {
+    extern __shared__ float lds[];
+    float* red = lds + lds_pad(K) + 1;
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    ln_modulate_row(x + static_cast<int64_t>(row) * K, shift, scale, K, eps, red, [&](int c, v4f v) {
+        lds[lds_pad(4 * c + 0)] = v.x;
+        lds[lds_pad(4 * c + 1)] = v.y;
+        lds[lds_pad(4 * c + 2)] = v.z;
+        lds[lds_pad(4 * c + 3)] = v.w;
+    });
+    __syncthreads();
+    float amax = 0.0f;
+    int lo = 0;
+    if (hbs_log2 >= 4 && (K & 15) == 0) {
+        const bool only = (hbs_log2 == 4);
+        for (int c = tid; c < (K >> 4); c += LN_THR) {
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = lds[lds_pad(16 * c + e)];
+            butterfly<4>(v);
+            if (only) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    v[e] = v[e] * norm;
+                    amax = fmaxf(amax, fabsf(v[e]));
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) lds[lds_pad(16 * c + e)] = v[e];
+        }
+        lo = 4;
+        __syncthreads();
+    } else if (hbs_log2 == 0) {
+        for (int e = tid; e < K; e += LN_THR) amax = fmaxf(amax, fabsf(lds[lds_pad(e)]));
+    }
+    fwht_quant_tail<OUT>(lds, red, K, hbs_log2, norm, lo, amax, out, scales, row);
+}
+
 static int ilog2(int v) {
     int r = 0;
     while ((1 << r) < v) ++r;
@@ -258,6 +317,22 @@ hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, 
     const float* xf = static_cast<const float*>(x);
     return fp8 ? launch_rows<float, RowOut::Fp8>(xf, q_out, scales, M, K, hbs, stream)
                : launch_rows<float, RowOut::Int8>(xf, q_out, scales, M, K, hbs, stream);
+}
+
+hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float* scale, int M, int K, int hbs,
+                                int mode, float eps, void* q_out, float* scales, hipStream_t stream) {
+    if (M == 0) return hipSuccess;
+    if ((K & 3) != 0 || K > LN_MAX_DIM || hbs < 1 || (hbs & (hbs - 1)) != 0 || K % hbs != 0)
+        return hipErrorInvalidValue;
+    const size_t lds = rows_lds_bytes(K);
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    if (mode == QIMG_QM_FP8_HADAMARD)
+        hipLaunchKernelGGL(ln_fwht_quant_kernel<RowOut::Fp8>, dim3(M), dim3(LN_THR), lds, stream, x, shift, scale,
+                           eps, q_out, scales, K, ilog2(hbs), norm);
+    else
+        hipLaunchKernelGGL(ln_fwht_quant_kernel<RowOut::Int8>, dim3(M), dim3(LN_THR), lds, stream, x, shift, scale,
+                           eps, q_out, scales, K, ilog2(hbs), norm);
+    return hipGetLastError();
 }
 
 hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t stream) {

@@ -136,26 +136,33 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         const float* im = w.img_mods;
         const float* tm = w.txt_mods;
 
-        // LayerNorm + modulate (transformer.cu:526-540)
+        // LayerNorm + modulate (transformer.cu:526-540), then QKV with one
+        // activation quant per stream (transformer.cu:557-606). When the
+        // three linears of a stream share the quantization (always, for the
+        // reference's weights) the LayerNorm writes their int8 input
+        // directly. The image and text linears of each of q, k, v share a
+        // launch.
+        const qimg_qlinear* il[3] = {&b.to_q, &b.to_k, &b.to_v};
+        const qimg_qlinear* tl[3] = {&b.add_q_proj, &b.add_k_proj, &b.add_v_proj};
+        const bool share_i = same_quant(*il[0], *il[1]) && same_quant(*il[0], *il[2]);
+        const bool share_t = same_quant(*tl[0], *tl[1]) && same_quant(*tl[0], *tl[2]);
         QIMG_TRY(mark(QIMG_PROF_ATTN_NORM));
-        QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, Mi, DIM, EPS, s));
-        QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
+        if (share_i)
+            QIMG_TRY(launch_ln_fwht_quant(img, im + 0 * DIM, im + 1 * DIM, Mi, DIM, il[0]->hbs, il[0]->mode, EPS,
+                                          w.act_q, w.act_scales, s));
+        else
+            QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, Mi, DIM, EPS, s));
+        if (share_t)
+            QIMG_TRY(launch_ln_fwht_quant(txt, tm + 0 * DIM, tm + 1 * DIM, Mt, DIM, tl[0]->hbs, tl[0]->mode, EPS,
+                                          w.act_q_txt, w.act_scales_txt, s));
+        else
+            QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
 
-        // QKV with one activation quant per stream (transformer.cu:557-606);
-        // the image and text linears of each of q, k, v share a launch
         QIMG_TRY(mark(QIMG_PROF_QKV_GEMM));
-        {
-            const qimg_qlinear* il[3] = {&b.to_q, &b.to_k, &b.to_v};
-            const qimg_qlinear* tl[3] = {&b.add_q_proj, &b.add_k_proj, &b.add_v_proj};
-            const bool share_i = same_quant(*il[0], *il[1]) && same_quant(*il[0], *il[2]);
-            const bool share_t = same_quant(*tl[0], *tl[1]) && same_quant(*tl[0], *tl[2]);
-            if (share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[0]));
-            if (share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[0]));
-            for (int i = 0; i < 3; ++i) {
-                if (!share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[i]));
-                if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i]));
-                QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], Mt, *tl[i], w.txt_qkv[i], 0));
-            }
+        for (int i = 0; i < 3; ++i) {
+            if (!share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[i]));
+            if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i]));
+            QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], Mt, *tl[i], w.txt_qkv[i], 0));
         }
 
         // RMSNorm + concat + transpose + RoPE -> fp16 (transformer.cu:617-666)
@@ -201,20 +208,24 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(launch_gate_add(img, im + 2 * DIM, img_proj, img, Mi, DIM, s));
         QIMG_TRY(launch_gate_add(txt, tm + 2 * DIM, txt_proj, txt, Mt, DIM, s));
 
-        // LayerNorm + modulate (transformer.cu:754-764)
+        // LayerNorm + modulate (transformer.cu:754-764) straight into the
+        // fc1 input quantization
         QIMG_TRY(mark(QIMG_PROF_MLP_NORM));
-        QIMG_TRY(launch_layernorm_modulate(img, im + 3 * DIM, im + 4 * DIM, w.img_norm, Mi, DIM, EPS, s));
-        QIMG_TRY(launch_layernorm_modulate(txt, tm + 3 * DIM, tm + 4 * DIM, w.txt_norm, Mt, DIM, EPS, s));
+        QIMG_TRY(launch_ln_fwht_quant(img, im + 3 * DIM, im + 4 * DIM, Mi, DIM, b.img_mlp_fc1.hbs, b.img_mlp_fc1.mode,
+                                      EPS, w.act_q, w.act_scales, s));
+        QIMG_TRY(launch_ln_fwht_quant(txt, tm + 3 * DIM, tm + 4 * DIM, Mt, DIM, b.txt_mlp_fc1.hbs, b.txt_mlp_fc1.mode,
+                                      EPS, w.act_q_txt, w.act_scales_txt, s));
 
-        // GELU MLP (transformer.cu:780-808), output into the v buffers
+        // GELU MLP (transformer.cu:780-808), output into the v buffers: fc1
+        // of each stream on its own, then both fc2 in one launch
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));
         float* img_out = w.img_qkv[2];
         float* txt_out = w.txt_qkv[2];
-        // fc1 of each stream on its own, then both fc2 in one launch
-        QIMG_TRY(linear(w.img_norm, Mi, b.img_mlp_fc1, w.img_mlp, 1));
-        if (Mi) QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
+        if (Mi) {
+            QIMG_TRY(gemm(w.act_q, w.act_scales, Mi, b.img_mlp_fc1, w.img_mlp, 1));
+            QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
+        }
         if (Mt) {
-            QIMG_TRY(quant_txt(w.txt_norm, Mt, b.txt_mlp_fc1));
             QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1));
             QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2));
         }

@@ -163,4 +163,63 @@ __device__ __forceinline__ float dequant_elem(float acc, float sa, float sw, boo
     return t;
 }
 
+
+// ---- LayerNorm + modulate of one row (layer_norm_modulate_fp32_kernel,
+// cuda_kernels.cu:1799-1853): mean, then the variance about it,
+// inv_std = rsqrt(var/dim + eps), out = (x - mean) * inv_std * (1 + scale)
+// + shift. A workgroup of LN_THR threads owns the row, held in registers
+// between the passes (float4 chunk c = tid + j * LN_THR); emit(c, v) receives
+// each modulated chunk. Every kernel that normalizes a row calls this, so
+// the reduction order, and the result, is the same in all of them.
+constexpr int LN_THR = 256;
+constexpr int LN_MAXV = 4;  // float4 chunks per thread
+constexpr int LN_MAX_DIM = LN_THR * 4 * LN_MAXV;
+
+__device__ __forceinline__ float ln_block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();  // red may still be read by a previous call
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < LN_THR / 64; ++w) t += red[w];
+    return t;
+}
+
+template <class Emit>
+__device__ __forceinline__ void ln_modulate_row(const float* __restrict__ xrow, const float* __restrict__ shift,
+                                                const float* __restrict__ scale, int dim, float eps, float* red,
+                                                Emit emit) {
+#pragma clang fp contract(off)
+    const v4f* xr = reinterpret_cast<const v4f*>(xrow);
+    const int nv = dim >> 2;
+    v4f v[LN_MAXV];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < LN_MAXV; ++j) {
+        const int c = threadIdx.x + j * LN_THR;
+        v[j] = c < nv ? xr[c] : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+        s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    }
+    const float mean = ln_block_sum(s, red) / dim;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < LN_MAXV; ++j) {
+        const int c = threadIdx.x + j * LN_THR;
+        if (c < nv) {
+            const v4f d = v[j] - mean;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+    }
+    const float inv_std = rsqrtf(ln_block_sum(q, red) / dim + eps);
+    const v4f* sh = reinterpret_cast<const v4f*>(shift);
+    const v4f* sc = reinterpret_cast<const v4f*>(scale);
+#pragma unroll
+    for (int j = 0; j < LN_MAXV; ++j) {
+        const int c = threadIdx.x + j * LN_THR;
+        if (c < nv) emit(c, (v[j] - mean) * inv_std * (1.0f + sc[c]) + sh[c]);
+    }
+}
+
 }  // namespace qimg

@@ -14,6 +14,10 @@ namespace qimg {
 size_t rows_lds_bytes(int K);
 hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, int mode,
                              void* q_out, float* scales, hipStream_t stream);
+// LayerNorm + modulate of fp32 rows [M, K] (K <= 4096) straight into the
+// FWHT + int8/e4m3 quantization of launch_fwht_quant (same values).
+hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float* scale, int M, int K, int hbs,
+                                int mode, float eps, void* q_out, float* scales, hipStream_t stream);
 hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t stream);
 
 // gemm_w8a8.hip

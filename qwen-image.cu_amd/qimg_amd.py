@@ -51,6 +51,7 @@ _SIGS = {
     "qimg_sage_attention": (_I, [_P, _P, _P, _P, _I, _F, _I, _I, _I, _I, _P, _I64, _P]),
     "qimg_silu": (_I, [_P, _P, _I64, _P]),
     "qimg_layernorm_modulate": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "qimg_layernorm_modulate_quant": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P]),
     "qimg_joint_heads_f16": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "qimg_split_heads": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "qimg_gate_add": (_I, [_P, _P, _P, _P, _I, _I, _P]),
@@ -344,6 +345,19 @@ def layer_norm_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tenso
     _check(_lib.qimg_layernorm_modulate(_ptr(x), _ptr(shift), _ptr(scale), _ptr(out), rows, dim, float(eps),
                                         _stream()))
     return out
+
+
+def layer_norm_modulate_quant(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, had_block_size: int,
+                              mode: int = INT8_HADAMARD, eps: float = 1e-6):
+    """layer_norm_modulate_fp32 then fwht_quantize_fp32 (cuda_kernels.cu:1799-1859,
+    2493-2601) in one pass: (int8 or e4m3 bytes [rows, dim], fp32 scales [rows])."""
+    _dev(x, "x")
+    rows, dim = x.shape
+    q = torch.empty((rows, dim), dtype=torch.int8 if mode == INT8_HADAMARD else torch.uint8, device=x.device)
+    s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    _check(_lib.qimg_layernorm_modulate_quant(_ptr(x), _ptr(shift), _ptr(scale), rows, dim, int(had_block_size),
+                                              int(mode), float(eps), _ptr(q), _ptr(s), _stream()))
+    return q, s
 
 
 def joint_heads_f16(txt: torch.Tensor, img: torch.Tensor, norm_txt=None, norm_img=None, pe=None,

@@ -56,6 +56,20 @@ def test_layer_norm_modulate(qimg, blk, rows, dim):
     np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-5)
 
 
+@pytest.mark.parametrize("rows,dim,hbs,mode", [(300, 3072, 1024, 0), (257, 3072, 1024, 1), (5, 4096, 4096, 0),
+                                               (7, 1024, 16, 0), (9, 512, 8, 0), (4, 3072, 1, 1), (0, 3072, 1024, 0)])
+def test_layer_norm_modulate_quant_equals_two_passes(qimg, rows, dim, hbs, mode):
+    """The fused LayerNorm + FWHT quant gives the bits of the two kernels."""
+    g = torch.Generator(device=DEV).manual_seed(rows + dim + hbs)
+    x = torch.randn(rows, dim, generator=g, device=DEV) * 3 + 0.5
+    shift = torch.randn(dim, generator=g, device=DEV)
+    scale = torch.randn(dim, generator=g, device=DEV) * 0.3
+    q, s = qimg.layer_norm_modulate_quant(x, shift, scale, hbs, mode)
+    rq, rs = qimg.quantize_activation_hadamard(qimg.layer_norm_modulate(x, shift, scale), hbs, mode)
+    torch.cuda.synchronize()
+    assert torch.equal(q, rq) and torch.equal(s, rs)
+
+
 @pytest.mark.parametrize("n_txt,n_img", [(64, 256), (0, 96), (7, 0), (256, 4096)])
 def test_joint_heads_norm_rope_and_split(qimg, blk, n_txt, n_img):
     rng = np.random.default_rng(n_txt * 7 + n_img)
