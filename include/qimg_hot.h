@@ -254,7 +254,11 @@ typedef struct {
  * reference's PROFILE_BLOCK report (transformer.cu:843-857). RMSNorm,
  * concat/transpose and RoPE of Q/K run as one fused kernel here: its time
  * is reported under QK_NORM, the V concat/transpose under
- * CONCAT_TRANSPOSE, and ROPE stays 0. */
+ * CONCAT_TRANSPOSE, and ROPE stays about 0. The LayerNorms write the
+ * quantized input of the next linear (their time includes that
+ * quantization), and the gated residuals run in the epilogues of the
+ * out-projection and fc2, so GATE_ATTN and GATE_MLP stay about 0 and their
+ * work is counted in OUT_GEMM and MLP_GEMM. */
 enum {
     QIMG_PROF_MODULATION = 0,
     QIMG_PROF_ATTN_NORM,

@@ -110,7 +110,8 @@ __global__ __launch_bounds__(256) void split_heads_kernel(const uint16_t* __rest
 }
 
 // gate_add_fp32f_kernel (cuda_kernels.cu:2181-2189): out = x + gate[c] * y
-// (out may alias x).
+// as one fused multiply-add per element, the operation the large-tile GEMM
+// epilogue applies when it takes the gate itself (out may alias x).
 __global__ __launch_bounds__(256) void gate_add_kernel(const float* x, const float* __restrict__ gate,
                                                        const float* __restrict__ y, float* out, int64_t n4,
                                                        int dim4) {
@@ -118,7 +119,10 @@ __global__ __launch_bounds__(256) void gate_add_kernel(const float* x, const flo
     if (i >= n4) return;
     const int c = static_cast<int>(i % dim4);
     const v4f g = reinterpret_cast<const v4f*>(gate)[c];
-    reinterpret_cast<v4f*>(out)[i] = reinterpret_cast<const v4f*>(x)[i] + g * reinterpret_cast<const v4f*>(y)[i];
+    const v4f a = reinterpret_cast<const v4f*>(x)[i];
+    const v4f b = reinterpret_cast<const v4f*>(y)[i];
+    reinterpret_cast<v4f*>(out)[i] = (v4f){__builtin_fmaf(g.x, b.x, a.x), __builtin_fmaf(g.y, b.y, a.y),
+                                           __builtin_fmaf(g.z, b.z, a.z), __builtin_fmaf(g.w, b.w, a.w)};
 }
 
 inline int div_up_i(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }

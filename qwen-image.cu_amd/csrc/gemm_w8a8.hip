@@ -74,7 +74,7 @@ constexpr int OP_BYTES = BM * BK;              // one operand's share of a stage
 constexpr int LDS_BYTES = 2 * NSLOT * OP_BYTES;
 // Epilogue scales and bias reuse the end of the ring once the main loop is
 // done (the bf16 output staging uses its start).
-constexpr int SCALE_OFF = LDS_BYTES - 3 * 256 * 4;
+constexpr int SCALE_OFF = LDS_BYTES - 4 * 256 * 4;  // as, ws, bias, gate
 constexpr int GROUP_M = 4;  // tile rows per group in the tile order
 // Cache policy of the operand DMA: sc0 (measured ~10% faster than the
 // default policy at the MMDiT shapes; the non-temporal policy is slower).
@@ -119,6 +119,7 @@ struct TileProblem {
     const float* ws;
     const uint16_t* bias;
     void* out;
+    const float* gate;  // non-null: out = out + gate[n] * value (fp32 out)
     int M, N, K, tiles;
 };
 
@@ -128,6 +129,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
     float* s_ws = s_as + 256;
     float* s_bias = s_ws + 256;
+    float* s_gate = s_bias + 256;
 
     // Two problems share the grid: tiles [0, p0.tiles) are problem 0, the
     // rest problem 1 (e.g. the text-stream linear in the CUs the image-stream
@@ -141,6 +143,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     const float* __restrict__ ws = second ? p1.ws : p0.ws;
     const uint16_t* __restrict__ bias = second ? p1.bias : p0.bias;
     void* __restrict__ out = second ? p1.out : p0.out;
+    const float* __restrict__ gate = second ? p1.gate : p0.gate;
     const int M = second ? p1.M : p0.M;
     const int N = second ? p1.N : p0.N;
     const int K = second ? p1.K : p0.K;
@@ -164,6 +167,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     const int wm = wave / WAVES_N;
     const int wn = wave % WAVES_N;
     const bool has_bias = bias != nullptr;
+    const bool has_gate = gate != nullptr;
 
     // epilogue operands for this tile (clamped indices; only stored
     // outputs use them)
@@ -175,6 +179,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     const float e_ws = ws[e_n];
     const uint16_t* bsrc = has_bias ? bias : reinterpret_cast<const uint16_t*>(ws);
     const uint16_t e_braw = bsrc[e_n];
+    const float e_gate = (has_gate ? gate : ws)[e_n];
 
     // DMA assignment: wave w, instruction i fills LDS rows
     // DMA_ROWS*(NWAVES*i + w) .. +DMA_ROWS of the A tile (and the same rows
@@ -366,6 +371,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
         s_as[tid] = e_as;
         s_ws[tid] = e_ws;
         s_bias[tid] = has_bias ? bf16_to_f32(e_braw) : 0.0f;
+        s_gate[tid] = e_gate;
     }
     __syncthreads();
 
@@ -376,7 +382,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     // one 16-byte (fp32) or 8-byte (bf16) write per run. Interior tiles
     // (the common case) take a path with no per-element bounds checks.
     const bool interior = (m0 + BM <= M) && (n0 + BN <= N) && ((N & 3) == 0);
-    if (interior && OUT_DT == QIMG_BF16) {
+    if (interior && OUT_DT == QIMG_BF16) {  // (no gate with bf16 outputs)
         // Interior bf16 tiles: each wave stages one 32x128 block at a time in a
         // private LDS buffer (rows padded by 16 bytes: conflict-free for both
         // the row-per-lane writes and the row-major reads), then stores it
@@ -444,7 +450,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int nj = n0 + wn * WTN + j * 32 + 4 * half;
-        float wsv[16], bv[16];
+        float wsv[16], bv[16], gv[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -452,7 +458,28 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                 const int nl = nj - n0 + 8 * g + c;
                 wsv[4 * g + c] = s_ws[nl];
                 bv[4 * g + c] = s_bias[nl];
+                gv[4 * g + c] = s_gate[nl];
             }
+        // Gated residual (gate_add_fp32f, cuda_kernels.cu:2181-2189): the
+        // tile's residual values are all loaded before its first store.
+        v4f res[TM][4];
+        if (OUT_DT == QIMG_FP32 && has_gate) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int m = m0 + wm * WTM + i * 32 + (lane & 31);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int nb = nj + 8 * g;
+                    const float* o = reinterpret_cast<const float*>(out) + static_cast<int64_t>(m) * N + nb;
+                    if (interior) {
+                        res[i][g] = *reinterpret_cast<const v4f*>(o);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) res[i][g][c] = (m < M && nb + c < N) ? o[c] : 0.0f;
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int m = m0 + wm * WTM + i * 32 + (lane & 31);
@@ -471,6 +498,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                         if (has_bias) t = t + bv[4 * g + c];
                     }
                     if (GELU) t = gelu_tanh_fast(t);
+                    if (OUT_DT == QIMG_FP32 && has_gate) t = __builtin_fmaf(gv[4 * g + c], t, res[i][g][c]);
                     v[c] = t;
                 }
                 if (OUT_DT == QIMG_FP32) {
@@ -558,8 +586,8 @@ hipError_t launch_tiled(const TileProblem& p0, const TileProblem& p1, hipStream_
 }
 
 TileProblem tile_problem(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
-                         const uint16_t* bias, void* out) {
-    return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, M, N, K,
+                         const uint16_t* bias, void* out, const float* gate) {
+    return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, gate, M, N, K,
             ((M + BM - 1) / BM) * ((N + BN - 1) / BN)};
 }
 
@@ -606,9 +634,17 @@ hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float*
 hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
                                       const void* w_q, const float* w_scales, int N, int mode,
                                       const uint16_t* bias, void* out, int out_dtype, int gelu,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, const float* gate, float* tmp) {
     if (M == 0 || N == 0) return hipSuccess;
+    if (gate != nullptr && (out_dtype != QIMG_FP32 || tmp == nullptr)) return hipErrorInvalidValue;
     const bool fp8 = (mode == QIMG_QM_FP8_HADAMARD);
+    // Rows [r0, M) computed by a kernel without the gated epilogue: into
+    // tmp, then out = out + gate * tmp.
+    auto gate_rest = [&](int r0) -> hipError_t {
+        const int64_t off = static_cast<int64_t>(r0) * N;
+        float* o = static_cast<float*>(out) + off;
+        return launch_gate_add(o, gate, tmp + off, o, M - r0, N, stream);
+    };
     const int choice = g_linear_kernel.load(std::memory_order_relaxed);
     int small = small_m_variant(M, N, K);
     if ((K % 64) == 0 && choice != QIMG_LINEAR_AUTO)
@@ -618,9 +654,11 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
                                                  : 0;
     // the large tiles need K % 128 == 0; other multiples of 64 take 64x64 tiles
     if (small == 0 && (K % BK) != 0 && small_m_fits(M, N, K)) small = 2;
-    if (small != 0)
-        return launch_linear_small_m(act_q, act_scales, M, K, w_q, w_scales, N, mode, bias, out, out_dtype, gelu,
-                                     small, stream);
+    if (small != 0) {
+        hipError_t e = launch_linear_small_m(act_q, act_scales, M, K, w_q, w_scales, N, mode, bias,
+                                             gate ? tmp : out, out_dtype, gelu, small, stream);
+        return e != hipSuccess || !gate ? e : gate_rest(0);
+    }
     if ((K % BK) == 0) {
         // Tile rounds: one 256x256 tile per CU at a time. When the last
         // round would be mostly idle, the trailing tile rows (at most two)
@@ -645,24 +683,27 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
             }
             if (m_big < M && !small_m_fits(M - m_big, N, K)) m_big = M;
         }
-        const TileProblem p0 = tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out);
+        const TileProblem p0 = tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate);
         const TileProblem none{};
         hipError_t e = fp8 ? dispatch_tiled<true>(p0, none, out_dtype, gelu, stream)
                            : dispatch_tiled<false>(p0, none, out_dtype, gelu, stream);
         if (e != hipSuccess || m_big == M) return e;
         const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
-        return launch_linear_small_m(static_cast<const uint8_t*>(act_q) + static_cast<int64_t>(m_big) * K,
-                                     act_scales + m_big, M - m_big, K, w_q, w_scales, N, mode, bias,
-                                     static_cast<uint8_t*>(out) + static_cast<int64_t>(m_big) * N * esz,
-                                     out_dtype, gelu, 2, stream);
+        void* rest = gate ? static_cast<void*>(tmp + static_cast<int64_t>(m_big) * N)
+                          : static_cast<void*>(static_cast<uint8_t*>(out) + static_cast<int64_t>(m_big) * N * esz);
+        e = launch_linear_small_m(static_cast<const uint8_t*>(act_q) + static_cast<int64_t>(m_big) * K,
+                                  act_scales + m_big, M - m_big, K, w_q, w_scales, N, mode, bias, rest, out_dtype,
+                                  gelu, 2, stream);
+        return e != hipSuccess || !gate ? e : gate_rest(m_big);
     }
     const int64_t total = static_cast<int64_t>(M) * N;
     const int blocks = static_cast<int>((total + 255) / 256);
     if (fp8) return hipErrorInvalidValue;  // e4m3 needs K % 64 == 0 (checked by the caller) and fitting sizes
     hipLaunchKernelGGL(gemm_i8_simple_kernel, dim3(blocks), dim3(256), 0, stream,
                        static_cast<const int8_t*>(act_q), static_cast<const int8_t*>(w_q),
-                       act_scales, w_scales, bias, out, M, N, K, out_dtype, gelu);
-    return hipGetLastError();
+                       act_scales, w_scales, bias, gate ? static_cast<void*>(tmp) : out, M, N, K, out_dtype, gelu);
+    hipError_t e = hipGetLastError();
+    return e != hipSuccess || !gate ? e : gate_rest(0);
 }
 
 // Two linears of the same mode, output type and epilogue in one launch
@@ -676,7 +717,7 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
                               hipStream_t stream) {
     auto single = [&](const LinearArgs& x) {
         return launch_linear_prequantized(x.act_q, x.act_scales, x.M, x.K, x.w_q, x.w_scales, x.N, mode, x.bias,
-                                          x.out, out_dtype, gelu, stream);
+                                          x.out, out_dtype, gelu, stream, x.gate, x.tmp);
     };
     bool pair = a.M > 0 && a.N > 0 && b.M > 0 && b.N > 0 &&
                 g_linear_kernel.load(std::memory_order_relaxed) == QIMG_LINEAR_AUTO && (a.K % BK) == 0 &&
@@ -694,8 +735,9 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
         hipError_t e = a.M > 0 ? single(a) : hipSuccess;
         return e != hipSuccess || b.M == 0 ? e : single(b);
     }
-    const TileProblem p0 = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out);
-    const TileProblem p1 = tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out);
+    if ((a.gate || b.gate) && out_dtype != QIMG_FP32) return hipErrorInvalidValue;
+    const TileProblem p0 = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate);
+    const TileProblem p1 = tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out, b.gate);
     return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(p0, p1, out_dtype, gelu, stream)
                                         : dispatch_tiled<false>(p0, p1, out_dtype, gelu, stream);
 }

@@ -11,6 +11,12 @@
 //    reference also writes feeds nothing on the Sage path);
 //  - the attention writes fp16 and the split reads it (the reference
 //    widens to fp32 first; fp16 -> fp32 is exact);
+//  - the LayerNorm + modulate before QKV and before fc1 writes the int8
+//    input of those linears directly (no fp32 copy of the normalized rows);
+//  - the gated residuals after the out-projection and after fc2 are applied
+//    in the GEMM epilogue (one fused multiply-add, as the gate-add kernel);
+//  - the image- and text-stream linears of q, k, v, out-proj and fc2 share
+//    a launch when the text tiles fit the image GEMM's last tile round;
 //  - buffers whose producer has been consumed are reused (q/k/v of each
 //    stream hold the attention output, the projection and the MLP output);
 //  - `batch` sequences of equal lengths that share t_emb and pe (the two
@@ -111,15 +117,17 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         auto quant_txt = [&](const float* x, int M, const qimg_qlinear& l) {
             return launch_fwht_quant(x, QIMG_FP32, M, l.K, l.hbs, l.mode, w.act_q_txt, w.act_scales_txt, s);
         };
-        auto gemm_pair = [&](int Mi_, const qimg_qlinear& li, float* oi, int Mt_, const qimg_qlinear& lt, float* ot,
-                             int gelu) -> hipError_t {
-            if (li.mode != lt.mode) {
-                hipError_t r = Mi_ ? gemm(w.act_q, w.act_scales, Mi_, li, oi, gelu) : hipSuccess;
-                return r != hipSuccess || !Mt_ ? r : gemm(w.act_q_txt, w.act_scales_txt, Mt_, lt, ot, gelu);
-            }
-            const LinearArgs a{w.act_q, w.act_scales, Mi_, li.K, li.w, li.scales, li.N, li.bias, oi};
-            const LinearArgs c{w.act_q_txt, w.act_scales_txt, Mt_, lt.K, lt.w, lt.scales, lt.N, lt.bias, ot};
-            return launch_linear_pair(a, c, li.mode, QIMG_FP32, gelu, s);
+        // One linear of each stream over the stream's quantized activations;
+        // gate != nullptr adds the gated residual into `out` (the stream
+        // itself), with `tmp` for rows computed without the fused epilogue.
+        auto gemm_pair = [&](int Mi_, const qimg_qlinear& li, float* oi, const float* gi, float* ti, int Mt_,
+                             const qimg_qlinear& lt, float* ot, const float* gt, float* tt, int gelu) -> hipError_t {
+            const LinearArgs a{w.act_q, w.act_scales, Mi_, li.K, li.w, li.scales, li.N, li.bias, oi, gi, ti};
+            const LinearArgs c{w.act_q_txt, w.act_scales_txt, Mt_, lt.K, lt.w, lt.scales, lt.N, lt.bias, ot, gt, tt};
+            if (li.mode == lt.mode) return launch_linear_pair(a, c, li.mode, QIMG_FP32, gelu, s);
+            const LinearArgs none{};
+            hipError_t r = launch_linear_pair(a, none, li.mode, QIMG_FP32, gelu, s);
+            return r != hipSuccess ? r : launch_linear_pair(none, c, lt.mode, QIMG_FP32, gelu, s);
         };
 
         // modulation: silu(t_emb) -> img_mod / txt_mod (transformer.cu:506-515)
@@ -162,7 +170,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         for (int i = 0; i < 3; ++i) {
             if (!share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[i]));
             if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i]));
-            QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], Mt, *tl[i], w.txt_qkv[i], 0));
+            QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], nullptr, nullptr, Mt, *tl[i], w.txt_qkv[i], nullptr, nullptr,
+                               0));
         }
 
         // RMSNorm + concat + transpose + RoPE -> fp16 (transformer.cu:617-666)
@@ -195,18 +204,15 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         float* txt_attn = w.txt_qkv[0];
         QIMG_TRY(launch_split_heads(w.attn16, txt_attn, img_attn, n_txt, n_img, batch, HEADS, s));
 
-        // out projections (transformer.cu:723-732), into the k buffers
+        // out projections (transformer.cu:723-732) with the gate1 residual
+        // (transformer.cu:740-746) in their epilogue; the k buffers take
+        // rows a kernel without that epilogue computes
         QIMG_TRY(mark(QIMG_PROF_OUT_GEMM));
-        float* img_proj = w.img_qkv[1];
-        float* txt_proj = w.txt_qkv[1];
         if (Mi) QIMG_TRY(quant(img_attn, Mi, b.to_out));
         if (Mt) QIMG_TRY(quant_txt(txt_attn, Mt, b.to_add_out));
-        QIMG_TRY(gemm_pair(Mi, b.to_out, img_proj, Mt, b.to_add_out, txt_proj, 0));
-
-        // residual with gate1 (transformer.cu:740-746)
+        QIMG_TRY(gemm_pair(Mi, b.to_out, img, im + 2 * DIM, w.img_qkv[1], Mt, b.to_add_out, txt, tm + 2 * DIM,
+                           w.txt_qkv[1], 0));
         QIMG_TRY(mark(QIMG_PROF_GATE_ATTN));
-        QIMG_TRY(launch_gate_add(img, im + 2 * DIM, img_proj, img, Mi, DIM, s));
-        QIMG_TRY(launch_gate_add(txt, tm + 2 * DIM, txt_proj, txt, Mt, DIM, s));
 
         // LayerNorm + modulate (transformer.cu:754-764) straight into the
         // fc1 input quantization
@@ -216,11 +222,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(launch_ln_fwht_quant(txt, tm + 3 * DIM, tm + 4 * DIM, Mt, DIM, b.txt_mlp_fc1.hbs, b.txt_mlp_fc1.mode,
                                       EPS, w.act_q_txt, w.act_scales_txt, s));
 
-        // GELU MLP (transformer.cu:780-808), output into the v buffers: fc1
-        // of each stream on its own, then both fc2 in one launch
+        // GELU MLP (transformer.cu:780-808): fc1 of each stream on its own
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));
-        float* img_out = w.img_qkv[2];
-        float* txt_out = w.txt_qkv[2];
         if (Mi) {
             QIMG_TRY(gemm(w.act_q, w.act_scales, Mi, b.img_mlp_fc1, w.img_mlp, 1));
             QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
@@ -229,12 +232,11 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1));
             QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2));
         }
-        QIMG_TRY(gemm_pair(Mi, b.img_mlp_fc2, img_out, Mt, b.txt_mlp_fc2, txt_out, 0));
-
-        // residual with gate2 (transformer.cu:812-818)
+        // both fc2 in one launch, with the gate2 residual (transformer.cu:
+        // 812-818) in their epilogue
+        QIMG_TRY(gemm_pair(Mi, b.img_mlp_fc2, img, im + 5 * DIM, w.img_qkv[2], Mt, b.txt_mlp_fc2, txt, tm + 5 * DIM,
+                           w.txt_qkv[2], 0));
         QIMG_TRY(mark(QIMG_PROF_GATE_MLP));
-        QIMG_TRY(launch_gate_add(img, im + 5 * DIM, img_out, img, Mi, DIM, s));
-        QIMG_TRY(launch_gate_add(txt, tm + 5 * DIM, txt_out, txt, Mt, DIM, s));
         QIMG_TRY(mark(QIMG_PROF_COUNT));
 
         if (prof) {

@@ -31,13 +31,19 @@ struct LinearArgs {
     int N;
     const uint16_t* bias;
     void* out;
+    // non-null: gated residual out = out + gate[n] * value (fp32 out), fused
+    // into the large-tile epilogue; rows another kernel computes go through
+    // tmp [M, N] and the gate-add kernel
+    const float* gate;
+    float* tmp;
 };
 hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
                               hipStream_t stream);
 hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
                                       const void* w_q, const float* w_scales, int N, int mode,
                                       const uint16_t* bias, void* out, int out_dtype, int gelu,
-                                      hipStream_t stream);
+                                      hipStream_t stream,
+                                      const float* gate = nullptr, float* tmp = nullptr);
 hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
                               float* out, int M, int N, int gelu, hipStream_t stream);
 
