@@ -277,6 +277,56 @@ __global__ __launch_bounds__(LN_THR) void ln_fwht_quant_kernel(const float* __re
     fwht_quant_tail<OUT>(lds, red, K, hbs_log2, norm, lo, amax, out, scales, row);
 }
 
+// The attention output fp16 [batch][H][S][128] read as the token rows of
+// one stream (transpose_split_fused_fp32, transformer.cu:84-104: sequence b,
+// token s0 + r of the joint sequence is row b * n + r), straight into the
+// FWHT + row quant of the out-projection input. fp16 -> fp32 is exact, so
+// the values are those of the split followed by fwht_quant_rows_kernel.
+// K = H * 128, hbs >= 16 (the first four stages run on the 16 values a
+// thread loads, as in fwht_quant_rows_kernel).
+template <RowOut OUT>
+__global__ __launch_bounds__(256) void heads_fwht_quant_kernel(const uint16_t* __restrict__ attn, int S, int H,
+                                                               int s0, int n, void* out,
+                                                               float* __restrict__ scales, int hbs_log2,
+                                                               float norm) {
+    extern __shared__ float lds[];
+    const int K = H * 128;
+    float* red = lds + lds_pad(K) + 1;
+    const int row = blockIdx.x;
+    const int b = row / n;
+    const int s = s0 + row - b * n;
+    const int tid = threadIdx.x;
+    const bool only = (hbs_log2 == 4);
+    float amax = 0.0f;
+    for (int c = tid; c < (K >> 4); c += blockDim.x) {
+        const int h = c >> 3;
+        const uint16_t* src = attn + ((static_cast<int64_t>(b) * H + h) * S + s) * 128 + 16 * (c & 7);
+        float v[16];
+        const u32x4* q = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const u32x4 t = q[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[8 * j + 2 * e] = f16_to_f32(static_cast<uint16_t>(t[e] & 0xffffu));
+                v[8 * j + 2 * e + 1] = f16_to_f32(static_cast<uint16_t>(t[e] >> 16));
+            }
+        }
+        butterfly<4>(v);
+        if (only) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                v[e] = v[e] * norm;
+                amax = fmaxf(amax, fabsf(v[e]));
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) lds[lds_pad(16 * c + e)] = v[e];
+    }
+    __syncthreads();
+    fwht_quant_tail<OUT>(lds, red, K, hbs_log2, norm, 4, amax, out, scales, row);
+}
+
 static int ilog2(int v) {
     int r = 0;
     while ((1 << r) < v) ++r;
@@ -332,6 +382,25 @@ hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float*
     else
         hipLaunchKernelGGL(ln_fwht_quant_kernel<RowOut::Int8>, dim3(M), dim3(LN_THR), lds, stream, x, shift, scale,
                            eps, q_out, scales, K, ilog2(hbs), norm);
+    return hipGetLastError();
+}
+
+hipError_t launch_heads_fwht_quant(const uint16_t* attn, int batch, int H, int S, int s0, int n, int hbs, int mode,
+                                   void* q_out, float* scales, hipStream_t stream) {
+    const int M = batch * n;
+    if (M == 0) return hipSuccess;
+    const int K = H * 128;
+    if (hbs < 16 || (hbs & (hbs - 1)) != 0 || K % hbs != 0 || s0 < 0 || s0 + n > S) return hipErrorInvalidValue;
+    int threads = ((K / 16 + kWave - 1) / kWave) * kWave;
+    threads = threads > 256 ? 256 : threads;
+    const size_t lds = rows_lds_bytes(K);
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    if (mode == QIMG_QM_FP8_HADAMARD)
+        hipLaunchKernelGGL(heads_fwht_quant_kernel<RowOut::Fp8>, dim3(M), dim3(threads), lds, stream, attn, S, H, s0,
+                           n, q_out, scales, ilog2(hbs), norm);
+    else
+        hipLaunchKernelGGL(heads_fwht_quant_kernel<RowOut::Int8>, dim3(M), dim3(threads), lds, stream, attn, S, H, s0,
+                           n, q_out, scales, ilog2(hbs), norm);
     return hipGetLastError();
 }
 

@@ -197,19 +197,33 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                                       HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, ss.v_t, s));
         }
 
-        // transpose + split back to the streams (transformer.cu:693-703);
-        // q buffers are free now
+        // transpose + split back to the streams (transformer.cu:693-703),
+        // read by the out-projection quantization straight from the fp16
+        // attention output; out projections (transformer.cu:723-732) with
+        // the gate1 residual (transformer.cu:740-746) in their epilogue, the
+        // k buffers taking rows a kernel without that epilogue computes
         QIMG_TRY(mark(QIMG_PROF_TRANSPOSE_SPLIT));
-        float* img_attn = w.img_qkv[0];
-        float* txt_attn = w.txt_qkv[0];
-        QIMG_TRY(launch_split_heads(w.attn16, txt_attn, img_attn, n_txt, n_img, batch, HEADS, s));
-
-        // out projections (transformer.cu:723-732) with the gate1 residual
-        // (transformer.cu:740-746) in their epilogue; the k buffers take
-        // rows a kernel without that epilogue computes
+        const bool heads_i = b.to_out.hbs >= 16 && b.to_out.K == DIM;
+        const bool heads_t = b.to_add_out.hbs >= 16 && b.to_add_out.K == DIM;
+        if (!heads_i || !heads_t) {
+            // q buffers are free now
+            QIMG_TRY(launch_split_heads(w.attn16, w.txt_qkv[0], w.img_qkv[0], n_txt, n_img, batch, HEADS, s));
+        }
         QIMG_TRY(mark(QIMG_PROF_OUT_GEMM));
-        if (Mi) QIMG_TRY(quant(img_attn, Mi, b.to_out));
-        if (Mt) QIMG_TRY(quant_txt(txt_attn, Mt, b.to_add_out));
+        if (Mi) {
+            if (heads_i)
+                QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, n_txt, n_img, b.to_out.hbs, b.to_out.mode,
+                                                 w.act_q, w.act_scales, s));
+            else
+                QIMG_TRY(quant(w.img_qkv[0], Mi, b.to_out));
+        }
+        if (Mt) {
+            if (heads_t)
+                QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, 0, n_txt, b.to_add_out.hbs,
+                                                 b.to_add_out.mode, w.act_q_txt, w.act_scales_txt, s));
+            else
+                QIMG_TRY(quant_txt(w.txt_qkv[0], Mt, b.to_add_out));
+        }
         QIMG_TRY(gemm_pair(Mi, b.to_out, img, im + 2 * DIM, w.img_qkv[1], Mt, b.to_add_out, txt, tm + 2 * DIM,
                            w.txt_qkv[1], 0));
         QIMG_TRY(mark(QIMG_PROF_GATE_ATTN));

@@ -18,6 +18,11 @@ hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, 
 // FWHT + int8/e4m3 quantization of launch_fwht_quant (same values).
 hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float* scale, int M, int K, int hbs,
                                 int mode, float eps, void* q_out, float* scales, hipStream_t stream);
+// Rows s0 .. s0+n of each of `batch` sequences of the fp16 attention
+// output [batch][H][S][128] (K = H * 128, hbs >= 16) quantized as
+// launch_fwht_quant quantizes their fp32 split copy.
+hipError_t launch_heads_fwht_quant(const uint16_t* attn, int batch, int H, int S, int s0, int n, int hbs, int mode,
+                                   void* q_out, float* scales, hipStream_t stream);
 hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t stream);
 
 // gemm_w8a8.hip
