@@ -17,6 +17,9 @@
 //    in the GEMM epilogue (one fused multiply-add, as the gate-add kernel);
 //  - the image- and text-stream linears of q, k, v, out-proj and fc2 share
 //    a launch when the text tiles fit the image GEMM's last tile round;
+//  - the K mean runs on a second stream, beside the Q and V preparation
+//    and the Q quantization (fork and join by events, which a graph
+//    capture of the calling stream records as dependencies);
 //  - buffers whose producer has been consumed are reused (q/k/v of each
 //    stream hold the attention output, the projection and the MLP output);
 //  - `batch` sequences of equal lengths that share t_emb and pe (the two
@@ -37,6 +40,36 @@ constexpr int MLP = 12288;
 constexpr float EPS = 1e-6f;
 
 inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t{255}; }
+
+// A second stream (default priority) and two events per device and host
+// thread, created on first use and kept for the life of the process: the K
+// mean (a sequential sum that keeps 48-96 CUs busy for tens of
+// microseconds) runs beside the Q/V preparation. Thread-local, so that
+// concurrent callers never share an event.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr;
+    hipEvent_t join = nullptr;
+};
+
+hipError_t side_stream(SideStream** out) {
+    constexpr int kMaxDev = 64;
+    thread_local SideStream per_dev[kMaxDev];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+    SideStream& f = per_dev[dev];
+    if (f.stream == nullptr) {
+        SideStream n;
+        if ((e = hipStreamCreateWithFlags(&n.stream, hipStreamNonBlocking)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming)) != hipSuccess) return e;
+        f = n;
+    }
+    *out = &f;
+    return hipSuccess;
+}
 
 }  // namespace
 
@@ -175,10 +208,20 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         }
 
         // RMSNorm + concat + transpose + RoPE -> fp16 (transformer.cu:617-666)
+        // K first: its mean (sageattention_sm80.cu:759-773) then runs on the
+        // side stream while Q, V and the Q quantization run here.
+        SideStream* side = nullptr;
+        QIMG_TRY(side_stream(&side));
+        SageScratch ss;
+        sage_scratch_layout(HEADS * batch, S, HEAD_DIM, w.sage, &ss);
         QIMG_TRY(mark(QIMG_PROF_QK_NORM));
-        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, w.qkv16[0], n_txt,
-                                        n_img, batch, HEADS, EPS, s));
         QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.qkv16[1], n_txt,
+                                        n_img, batch, HEADS, EPS, s));
+        QIMG_TRY(hipEventRecord(side->fork, s));
+        QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+        QIMG_TRY(launch_sage_k_mean(w.qkv16[1], ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
+        QIMG_TRY(hipEventRecord(side->join, side->stream));
+        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, w.qkv16[0], n_txt,
                                         n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_CONCAT_TRANSPOSE));
         QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[2], w.img_qkv[2], nullptr, nullptr, nullptr, w.qkv16[2], n_txt,
@@ -187,15 +230,11 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
 
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)
         QIMG_TRY(mark(QIMG_PROF_ATTENTION));
-        {
-            SageScratch ss;
-            sage_scratch_layout(HEADS * batch, S, HEAD_DIM, w.sage, &ss);
-            QIMG_TRY(launch_sage_k_mean(w.qkv16[1], ss.k_mean, HEADS * batch, S, HEAD_DIM, s));
-            QIMG_TRY(launch_sage_quant_q(w.qkv16[0], ss.q_i8, ss.q_scale, HEADS * batch, S, HEAD_DIM, s));
-            QIMG_TRY(launch_sage_quant_k(w.qkv16[1], ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
-            QIMG_TRY(launch_sage_attn(ss.q_i8, ss.k_i8, w.qkv16[2], ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
-                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, ss.v_t, s));
-        }
+        QIMG_TRY(launch_sage_quant_q(w.qkv16[0], ss.q_i8, ss.q_scale, HEADS * batch, S, HEAD_DIM, s));
+        QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
+        QIMG_TRY(launch_sage_quant_k(w.qkv16[1], ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
+        QIMG_TRY(launch_sage_attn(ss.q_i8, ss.k_i8, w.qkv16[2], ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
+                                  HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, ss.v_t, s));
 
         // transpose + split back to the streams (transformer.cu:693-703),
         // read by the out-projection quantization straight from the fp16

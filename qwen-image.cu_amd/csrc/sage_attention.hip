@@ -49,84 +49,115 @@ __host__ __device__ constexpr int div_up(int a, int b) { return (a + b - 1) / b;
 // ---------------------------------------------------------------- k mean
 // mean[h,d] = (sum over s of k[h,s,d], left to right in fp32) / max(S,1),
 // bit-equal to the reference's one-thread-per-(h,d) loop. The sum must stay
-// sequential, so the work is arranged to keep memory latency off that chain:
-// a 256-thread workgroup owns 64 (h,d) chains. Wave 0 only sums; waves 1-3
-// stream 512-token chunks of k[h, :, d0:d0+64] into LDS (16-byte coalesced
-// loads), stored transposed as [d][s] so the summing lane reads 8 consecutive
-// tokens of its chain with one ds_read_b128. Chunks are double-buffered: the
-// loads of chunk c+1 overlap the sums of chunk c, which take about as long as
-// one memory round trip.
+// sequential, so the work is arranged to keep everything else off that
+// chain: a 256-thread workgroup owns 64 (h,d) chains. Wave 0 only sums, one
+// chain per lane, one v_fma_mix_f32 (fp16 -> fp32 and the add, one
+// rounding: the same value as converting then adding) per token, with the
+// LDS reads of the next 32 tokens issued before the adds of the current
+// ones. Waves 1-3 stream 512-token chunks of k[h, :, d0:d0+64] (8 rows x 128
+// bytes per load instruction), transpose 4 tokens x 8 dims in registers and
+// store them to LDS as [d][s] with 8-byte writes. The 16-byte token chunk c
+// of row d sits at c ^ (2 * (d >> 4)) in a 260-dword row: conflict-free for
+// both the 8-byte writes (32 lanes per pass) and the 16-byte reads of the
+// summing wave (16 lanes per pass). Chunks are double-buffered.
 constexpr int KM_CHUNK = 512;                 // tokens per chunk
-constexpr int KM_PITCH = KM_CHUNK + 8;        // fp16 per LDS row (1040 B: 16-byte aligned rows)
-constexpr int KM_PIECES = KM_CHUNK * 8;       // 16-byte pieces per chunk (64 fp16 per token)
-constexpr int KM_LOADERS = 192;               // threads of waves 1-3
-constexpr int KM_BATCH = 22;                  // loads in flight per loader lane: a whole chunk
-static_assert(KM_BATCH * KM_LOADERS >= KM_PIECES, "one batch covers a chunk");
+constexpr int KM_PITCH = KM_CHUNK / 2 + 4;    // dwords per LDS row
+constexpr int KM_ROUNDS = KM_CHUNK / 32;      // loader rounds of 8 token quads x 8 dim groups
+constexpr int KM_MAXR = (KM_ROUNDS + 2) / 3;  // rounds per loader wave (at most)
+
+__device__ __forceinline__ int km_swz(int d) { return 2 * ((d >> 4) & 3); }
+
+__device__ __forceinline__ float km_add_lo(float acc, uint32_t v) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(v));
+    return acc;
+}
+__device__ __forceinline__ float km_add_hi(float acc, uint32_t v) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(v));
+    return acc;
+}
 
 __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean,
                                                      int S, int D) {
-    __shared__ __attribute__((aligned(16))) uint16_t tile[2][64][KM_PITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t tile[2][64 * KM_PITCH];
     const int slices = D / 64;
     const int h = blockIdx.x / slices;
     const int d0 = (blockIdx.x % slices) * 64;
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const uint16_t* src = k + static_cast<int64_t>(h) * S * D + d0;
     const int nchunk = div_up(S, KM_CHUNK);
 
-    // loader piece p: token p / 8 of the chunk, fp16 columns 8 * (p % 8) .. +8
+    // loader lane: dim group g = lane & 7, token quad 8 * round + (lane >> 3)
     auto load_chunk = [&](int c, int buf) {
-        const int lt = tid - 64;
-        {
-            constexpr int b = 0;
-            u32x4 v[KM_BATCH];
+        const int g = lane & 7;
+        u32x4 v[KM_MAXR][4];
 #pragma unroll
-            for (int j = 0; j < KM_BATCH; ++j) {
-                const int p = (b * KM_BATCH + j) * KM_LOADERS + lt;
-                const int s = c * KM_CHUNK + (p >> 3);
-                v[j] = (u32x4){0u, 0u, 0u, 0u};
-                if (p < KM_PIECES && s < S)
-                    v[j] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(s) * D + (p & 7) * 8);
+        for (int r = 0; r < KM_MAXR; ++r) {
+            const int round = (wave - 1) + 3 * r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int s = c * KM_CHUNK + 4 * (8 * round + (lane >> 3)) + i;
+                v[r][i] = (u32x4){0u, 0u, 0u, 0u};
+                if (round < KM_ROUNDS && s < S)
+                    v[r][i] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(s) * D + 8 * g);
             }
+        }
 #pragma unroll
-            for (int j = 0; j < KM_BATCH; ++j) {
-                const int p = (b * KM_BATCH + j) * KM_LOADERS + lt;
-                if (p >= KM_PIECES) continue;
-                const int sl = p >> 3;
-                const int col = (p & 7) * 8;
+        for (int r = 0; r < KM_MAXR; ++r) {
+            const int round = (wave - 1) + 3 * r;
+            if (round >= KM_ROUNDS) continue;
+            const int tq = 8 * round + (lane >> 3);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    tile[buf][col + 2 * e][sl] = static_cast<uint16_t>(v[j][e] & 0xffffu);
-                    tile[buf][col + 2 * e + 1][sl] = static_cast<uint16_t>(v[j][e] >> 16);
-                }
+            for (int e = 0; e < 8; ++e) {
+                // dim 8g + e of tokens 4tq .. 4tq+3: fp16 e of each 16-byte row piece
+                const int w = e >> 1;
+                const int sh = (e & 1) * 16;
+                const uint32_t t0 = (v[r][0][w] >> sh) & 0xffffu, t1 = (v[r][1][w] >> sh) & 0xffffu;
+                const uint32_t t2 = (v[r][2][w] >> sh) & 0xffffu, t3 = (v[r][3][w] >> sh) & 0xffffu;
+                const int d = 8 * g + e;
+                uint32_t* dst = &tile[buf][d * KM_PITCH + 4 * ((tq >> 1) ^ km_swz(d)) + 2 * (tq & 1)];
+                *reinterpret_cast<uint2*>(dst) = make_uint2(t0 | (t1 << 16), t2 | (t3 << 16));
             }
         }
     };
 
     float sum = 0.0f;
-    if (tid >= 64) load_chunk(0, 0);
+    if (wave > 0) load_chunk(0, 0);
     __syncthreads();
     for (int c = 0; c < nchunk; ++c) {
         const int buf = c & 1;
-        if (tid >= 64) {
+        if (wave > 0) {
             if (c + 1 < nchunk) load_chunk(c + 1, buf ^ 1);
         } else {
             const int n = min(KM_CHUNK, S - c * KM_CHUNK);
-            const uint16_t* row = &tile[buf][tid][0];
-            int s = 0;
-            // four 16-byte reads in flight ahead of the add chain
-            for (; s + 32 <= n; s += 32) {
-                u32x4 v[4];
+            const uint32_t* row = &tile[buf][lane * KM_PITCH];
+            const int sw = km_swz(lane);
+            auto rd = [&](int t8) { return *reinterpret_cast<const u32x4*>(row + 4 * (t8 ^ sw)); };
+            const int full = n >> 5;  // groups of 32 tokens
+            u32x4 cur[4], nxt[4];
+            if (full > 0) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = *reinterpret_cast<const u32x4*>(row + s + 8 * r);
+                for (int r = 0; r < 4; ++r) cur[r] = rd(r);
+            }
+            for (int gi = 0; gi < full; ++gi) {
+                const bool more = gi + 1 < full;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) nxt[r] = more ? rd(4 * (gi + 1) + r) : cur[r];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        sum += f16_to_f32(static_cast<uint16_t>(v[r][e] & 0xffffu));
-                        sum += f16_to_f32(static_cast<uint16_t>(v[r][e] >> 16));
+                        sum = km_add_lo(sum, cur[r][e]);
+                        sum = km_add_hi(sum, cur[r][e]);
                     }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) cur[r] = nxt[r];
             }
-            for (; s < n; ++s) sum += f16_to_f32(row[s]);
+            for (int t = full << 5; t < n; ++t) {
+                const uint32_t wv = row[4 * ((t >> 3) ^ sw) + ((t & 7) >> 1)];
+                sum = (t & 1) ? km_add_hi(sum, wv) : km_add_lo(sum, wv);
+            }
         }
         __syncthreads();
     }

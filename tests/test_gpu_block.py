@@ -366,6 +366,45 @@ def test_mmdit_block_same_for_every_kernel_choice(qimg, n_img, n_txt, batch):
     assert torch.equal(outs[0][1], outs[1][1])
 
 
+def test_mmdit_block_graph_replays_match_eager(qimg):
+    """The block (with its side-stream fork/join) captured in a HIP graph:
+    every replay, with eager work and synchronisations between replays,
+    gives the eager result bit for bit."""
+    W, B, nr = _gpu_block(qimg, 8)
+    table = qimg.BlockTable([(W, B, nr)])
+    g = torch.Generator(device=DEV).manual_seed(9)
+    n_img, n_txt = 1024, 128
+    img0 = torch.randn(n_img, 3072, generator=g, device=DEV)
+    txt0 = torch.randn(n_txt, 3072, generator=g, device=DEV)
+    t_emb = torch.randn(3072, generator=g, device=DEV)
+    pe = _dev(qimg.qwen_image_pe(64, 64, 2, n_txt))
+    scratch = torch.empty(qimg.mmdit_block_scratch_bytes(n_img, n_txt), dtype=torch.uint8, device=DEV)
+    ri, rt = img0.clone(), txt0.clone()
+    qimg.mmdit_blocks_forward(table, ri, rt, t_emb, pe, scratch=scratch)
+    torch.cuda.synchronize()
+    img, txt = img0.clone(), txt0.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream
+        qimg.mmdit_blocks_forward(table, img, txt, t_emb, pe, scratch=scratch)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qimg.mmdit_blocks_forward(table, img, txt, t_emb, pe, scratch=scratch)
+    for rep in range(3):
+        img.copy_(img0)
+        txt.copy_(txt0)
+        junk = torch.randn(1 << 20, device=DEV).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(img, ri), rep
+        assert torch.equal(txt, rt), rep
+        del junk
+    del graph
+
+
 def test_mmdit_block_fp8_runs_close_to_int8(qimg, oracle, int8_block):
     """e4m3 weights through the same block: finite, deterministic, and close
     to the int8 block (both approximate the same bf16 weights). The fp8 linear
