@@ -131,15 +131,17 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
 }
 
-// GELU with tanh(u) = 1 - 2 / (exp(2u) + 1) on the hardware exp2/rcp
-// (about 2e-7 absolute error in tanh; the reference evaluates tanhf under
-// fast-math approximation as well).
+// GELU-tanh, 0.5 v (1 + tanh(u)) with u = sqrt(2/pi) (v + 0.044715 v^3),
+// written as v - v / (exp(2u) + 1) (since 0.5 (1 + tanh u) = 1 - 1/(e^2u + 1))
+// with 2u log2(e) = v (C1 + C2 v^2): five full-rate operations and the
+// hardware exp2 / rcp (about 2e-7 absolute error in tanh; the reference
+// evaluates tanhf under fast-math approximation as well).
 __device__ __forceinline__ float gelu_tanh_fast(float v) {
-    const float c = 0.7978845608f;
-    const float u = c * (v + 0.044715f * v * v * v);
-    const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // exp(2u)
-    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-    return 0.5f * v * (1.0f + t);
+    constexpr float C1 = 2.3022082f;    // 2 sqrt(2/pi) log2(e)
+    constexpr float C2 = 0.10294324f;   // C1 * 0.044715
+    const float x = v * __builtin_fmaf(C2, v * v, C1);
+    const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(x) + 1.0f);
+    return __builtin_fmaf(-v, r, v);
 }
 
 __device__ __forceinline__ float gelu_tanh(float v) {

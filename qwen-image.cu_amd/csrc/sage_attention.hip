@@ -376,7 +376,9 @@ struct AttnCfg {
     static constexpr int V_INSTR = V_BYTES / 1024;
     static constexpr int NI = K_INSTR + V_INSTR;
     static constexpr int PER_WAVE = (NI + AWAVES - 1) / AWAVES;
-    static constexpr int KEEP = (ANSLOT - 2) * PER_WAVE;  // DMA instructions in flight at a hand-off
+    // DMA instructions left in flight at a hand-off: step kt reads tiles kt
+    // and kt+1, so at the end of step kt-1 only tile kt+2 may be missing
+    static constexpr int KEEP = (ANSLOT - 3) * PER_WAVE;
 };
 
 // physical 16-byte chunk of logical chunk c in row `row` (involution).
@@ -499,7 +501,7 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
 
 #pragma unroll
     for (int p = 0; p < ANSLOT - 1; ++p) issue_tile(p, p);
-    attn_wait_vmcnt<C::KEEP>();  // tile 0 has landed
+    attn_wait_vmcnt<C::KEEP>();  // tiles 0 and 1 have landed
     __builtin_amdgcn_s_barrier();
 
     // One 64-key tile. Fragment reads are issued in batches ahead of the
@@ -509,14 +511,10 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     // while the PV MFMAs of group t run. MASKED tiles (the tail past S, and
     // for causal the tiles that reach the block's diagonal) evaluate the
     // per-key validity; the others skip it.
-    auto step = [&](int kt, auto masked_c) {
-        constexpr bool MASKED = decltype(masked_c)::value;
-        issue_tile(kt + ANSLOT - 1, (kt + ANSLOT - 1) % ANSLOT);
-        const uint8_t* kb_lds = lds + (kt % ANSLOT) * C::STAGE;
-        const uint8_t* vb_lds = kb_lds + C::K_BYTES;
-        __builtin_amdgcn_sched_barrier(0);
-
-        // ---- S^T = K Q^T: blocks of keys 32*kb + (8*(r/4) + 4*half + r%4), query l32
+    // S^T = K Q^T of the tile in ring slot `slot`: blocks of keys
+    // 32*kb + (8*(r/4) + 4*half + r%4), query l32.
+    auto qk = [&](int slot, v16i (&acc)[2]) {
+        const uint8_t* kb_lds = lds + slot * C::STAGE;
         v4i kf[2 * C::KSTEPS];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -528,15 +526,33 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        v16i sacc[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0;
+            for (int r = 0; r < 16; ++r) acc[kb][r] = 0;
 #pragma unroll
             for (int s = 0; s < C::KSTEPS; ++s)
-                sacc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[kb * C::KSTEPS + s], qf[s], sacc[kb], 0, 0, 0);
+                acc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[kb * C::KSTEPS + s], qf[s], acc[kb], 0, 0, 0);
         }
+    };
+
+    // Scores of the tile being processed; the first tile's are computed
+    // before the loop, and each step issues the next tile's QK^T MFMAs
+    // before this tile's softmax, so the MFMA pipe works on them while the
+    // VALU computes P (tiles kt and kt+1 are both resident at the start of
+    // step kt; past the last tile the slot holds a re-fetched valid tile
+    // whose scores are not used).
+    v16i sacc[2];
+    qk(0, sacc);
+
+    auto step = [&](int kt, auto masked_c) {
+        constexpr bool MASKED = decltype(masked_c)::value;
+        issue_tile(kt + ANSLOT - 1, (kt + ANSLOT - 1) % ANSLOT);
+        const uint8_t* kb_lds = lds + (kt % ANSLOT) * C::STAGE;
+        const uint8_t* vb_lds = kb_lds + C::K_BYTES;
+        __builtin_amdgcn_sched_barrier(0);
+        v16i sacc_next[2];
+        qk((kt + 1) % ANSLOT, sacc_next);
         // first V fragments (groups 0 and 1) are read while QK^T runs
         v8h vf[2][C::DT];
         auto read_v = [&](int t, v8h* dst) {
@@ -637,10 +653,13 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
             if (t + 1 < 4) p_cur = make_p(t + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) sacc[kb] = sacc_next[kb];
 
-        // hand-off: this wave's reads of slot kt are done and its share of
-        // tile kt+1 has landed; the barrier makes every wave's share visible
-        // and frees slot kt for the DMA issued at the start of step kt+1.
+        // hand-off: this wave's reads of slots kt and kt+1 are done and its
+        // share of tile kt+2 has landed; the barrier makes every wave's share
+        // visible and frees slot kt for the DMA issued at the start of step
+        // kt+1.
         attn_wait_vmcnt_lgkm0<C::KEEP>();
         __builtin_amdgcn_s_barrier();
     };
