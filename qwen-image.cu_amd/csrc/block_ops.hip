@@ -44,13 +44,17 @@ __global__ __launch_bounds__(LN_THR) void layernorm_modulate_kernel(const float*
     ln_modulate_row(x + row * dim, shift, scale, dim, eps, red, [&](int c, v4f v) { o[c] = v; });
 }
 
-// One wave per (sequence b, token s, head h) of the joint sequences (txt
-// tokens first; the pe table is shared by the sequences):
-// optional RMSNorm over the head's 128 values with a bf16 weight
+// One workgroup of four waves per (sequence b, token s) of the joint
+// sequences (txt tokens first; the pe table is shared by the sequences);
+// wave w takes heads w, w + 4, ..., with the loads of up to JH_BATCH heads
+// in flight at once and the token's RoPE row read once. Per head:
+// optional RMSNorm over its 128 values with a bf16 weight
 // (rms_norm_fp32_kernel, cuda_kernels.cu:1656-1687), optional RoPE on the
 // pair (2l, 2l+1) held by lane l with pe[s][l] = (cos, -sin, sin, cos)
-// (rope_apply_fp32_to_fp16_kernel, :1935-1962), fp16 out at [h][s][:]
+// (rope_apply_fp32_to_fp16_kernel, :1935-1962), fp16 out at [b][h][s][:]
 // (concat_transpose_fused_fp32, transformer.cu:106-130).
+constexpr int JH_BATCH = 6;
+
 template <bool NORM_ROPE>
 __global__ __launch_bounds__(256) void joint_heads_f16_kernel(const float* __restrict__ txt,
                                                               const float* __restrict__ img,
@@ -60,31 +64,47 @@ __global__ __launch_bounds__(256) void joint_heads_f16_kernel(const float* __res
                                                               uint16_t* __restrict__ out, int n_txt, int n_img,
                                                               int batch, int H, float eps) {
     const int S = n_txt + n_img;
-    const int64_t gw = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-    if (gw >= static_cast<int64_t>(batch) * S * H) return;  // wave-uniform
+    const int b = blockIdx.x / S;
+    const int s = blockIdx.x - b * S;
     const int lane = threadIdx.x & 63;
-    const int b = static_cast<int>(gw / (static_cast<int64_t>(S) * H));
-    const int sh = static_cast<int>(gw - static_cast<int64_t>(b) * S * H);
-    const int s = sh / H;
-    const int h = sh - s * H;
+    const int wave = threadIdx.x >> 6;
     const bool is_txt = s < n_txt;
-    const float* src = is_txt ? txt + ((static_cast<int64_t>(b) * n_txt + s) * H + h) * HD
-                              : img + ((static_cast<int64_t>(b) * n_img + s - n_txt) * H + h) * HD;
-    float2 x = reinterpret_cast<const float2*>(src)[lane];
+    const float* src = is_txt ? txt + (static_cast<int64_t>(b) * n_txt + s) * H * HD
+                              : img + (static_cast<int64_t>(b) * n_img + s - n_txt) * H * HD;
+    v4f p = {0.0f, 0.0f, 0.0f, 0.0f};
+    float w0 = 0.0f, w1 = 0.0f;
     if constexpr (NORM_ROPE) {
-        const float ss = wave_sum(x.x * x.x + x.y * x.y);
-        const float rms = rsqrtf(ss / HD + eps);
-        const uint16_t* w = is_txt ? w_txt : w_img;
-        const uint32_t wp = reinterpret_cast<const uint32_t*>(w)[lane];
-        x.x = x.x * rms * bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
-        x.y = x.y * rms * bf16_to_f32(static_cast<uint16_t>(wp >> 16));
-        const v4f p = reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(s) * (HD / 2) + lane];
-        const float o0 = x.x * p.x + x.y * p.y;
-        const float o1 = x.x * p.z + x.y * p.w;
-        x = make_float2(o0, o1);
+        p = reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(s) * (HD / 2) + lane];
+        const uint32_t wp = reinterpret_cast<const uint32_t*>(is_txt ? w_txt : w_img)[lane];
+        w0 = bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
+        w1 = bf16_to_f32(static_cast<uint16_t>(wp >> 16));
     }
-    const uint32_t packed = static_cast<uint32_t>(f32_to_f16(x.x)) | (static_cast<uint32_t>(f32_to_f16(x.y)) << 16);
-    reinterpret_cast<uint32_t*>(out + ((static_cast<int64_t>(b) * H + h) * S + s) * HD)[lane] = packed;
+    for (int h0 = wave; h0 < H; h0 += 4 * JH_BATCH) {
+        float2 x[JH_BATCH];
+#pragma unroll
+        for (int k = 0; k < JH_BATCH; ++k) {
+            const int h = h0 + 4 * k;
+            x[k] = h < H ? reinterpret_cast<const float2*>(src + h * HD)[lane] : make_float2(0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < JH_BATCH; ++k) {
+            const int h = h0 + 4 * k;
+            if (h >= H) break;  // wave-uniform
+            float2 y = x[k];
+            if constexpr (NORM_ROPE) {
+                const float ss = wave_sum(y.x * y.x + y.y * y.y);
+                const float rms = rsqrtf(ss / HD + eps);
+                y.x = y.x * rms * w0;
+                y.y = y.y * rms * w1;
+                const float o0 = y.x * p.x + y.y * p.y;
+                const float o1 = y.x * p.z + y.y * p.w;
+                y = make_float2(o0, o1);
+            }
+            const uint32_t packed =
+                static_cast<uint32_t>(f32_to_f16(y.x)) | (static_cast<uint32_t>(f32_to_f16(y.y)) << 16);
+            reinterpret_cast<uint32_t*>(out + ((static_cast<int64_t>(b) * H + h) * S + s) * HD)[lane] = packed;
+        }
+    }
 }
 
 // transpose_split_fused_fp32 (transformer.cu:84-104) on the fp16
@@ -146,9 +166,9 @@ hipError_t launch_layernorm_modulate(const float* x, const float* shift, const f
 hipError_t launch_joint_heads_f16(const float* txt, const float* img, const uint16_t* w_txt, const uint16_t* w_img,
                                   const float* pe, uint16_t* out, int n_txt, int n_img, int batch, int H, float eps,
                                   hipStream_t stream) {
-    const int64_t waves = static_cast<int64_t>(n_txt + n_img) * H * batch;
-    if (waves == 0) return hipSuccess;
-    const int blocks = div_up_i(waves, 4);
+    const int64_t tokens = static_cast<int64_t>(n_txt + n_img) * batch;
+    if (tokens == 0 || H == 0) return hipSuccess;
+    const int blocks = static_cast<int>(tokens);
     if (w_txt != nullptr)
         hipLaunchKernelGGL(joint_heads_f16_kernel<true>, dim3(blocks), dim3(256), 0, stream, txt, img, w_txt, w_img,
                            pe, out, n_txt, n_img, batch, H, eps);

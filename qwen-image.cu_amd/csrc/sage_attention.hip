@@ -59,7 +59,8 @@ __host__ __device__ constexpr int div_up(int a, int b) { return (a + b - 1) / b;
 // store them to LDS as [d][s] with 8-byte writes. The 16-byte token chunk c
 // of row d sits at c ^ (2 * (d >> 4)) in a 260-dword row: conflict-free for
 // both the 8-byte writes (32 lanes per pass) and the 16-byte reads of the
-// summing wave (16 lanes per pass). Chunks are double-buffered.
+// summing wave (16 lanes per pass). Chunks are double-buffered in LDS, and
+// the loads run one chunk ahead of the LDS writes.
 constexpr int KM_CHUNK = 512;                 // tokens per chunk
 constexpr int KM_PITCH = KM_CHUNK / 2 + 4;    // dwords per LDS row
 constexpr int KM_ROUNDS = KM_CHUNK / 32;      // loader rounds of 8 token quads x 8 dim groups
@@ -88,10 +89,14 @@ __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict_
     const uint16_t* src = k + static_cast<int64_t>(h) * S * D + d0;
     const int nchunk = div_up(S, KM_CHUNK);
 
-    // loader lane: dim group g = lane & 7, token quad 8 * round + (lane >> 3)
-    auto load_chunk = [&](int c, int buf) {
-        const int g = lane & 7;
-        u32x4 v[KM_MAXR][4];
+    // loader lane: dim group g = lane & 7, token quad 8 * round + (lane >> 3).
+    // issue() starts the loads of a chunk into registers, commit() writes
+    // them transposed to an LDS buffer; chunk c+2 is issued right after
+    // chunk c+1 is committed, so its memory latency overlaps a whole chunk
+    // of the sum.
+    const int g = lane & 7;
+    u32x4 v[KM_MAXR][4];
+    auto issue = [&](int c) {
 #pragma unroll
         for (int r = 0; r < KM_MAXR; ++r) {
             const int round = (wave - 1) + 3 * r;
@@ -103,6 +108,8 @@ __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict_
                     v[r][i] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(s) * D + 8 * g);
             }
         }
+    };
+    auto commit = [&](int buf) {
 #pragma unroll
         for (int r = 0; r < KM_MAXR; ++r) {
             const int round = (wave - 1) + 3 * r;
@@ -123,12 +130,19 @@ __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict_
     };
 
     float sum = 0.0f;
-    if (wave > 0) load_chunk(0, 0);
+    if (wave > 0) {
+        issue(0);
+        commit(0);
+        if (nchunk > 1) issue(1);
+    }
     __syncthreads();
     for (int c = 0; c < nchunk; ++c) {
         const int buf = c & 1;
         if (wave > 0) {
-            if (c + 1 < nchunk) load_chunk(c + 1, buf ^ 1);
+            if (c + 1 < nchunk) {
+                commit(buf ^ 1);                 // chunk c+1, issued one chunk ago
+                if (c + 2 < nchunk) issue(c + 2);
+            }
         } else {
             const int n = min(KM_CHUNK, S - c * KM_CHUNK);
             const uint32_t* row = &tile[buf][lane * KM_PITCH];
