@@ -382,6 +382,9 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     // one 16-byte (fp32) or 8-byte (bf16) write per run. Interior tiles
     // (the common case) take a path with no per-element bounds checks.
     const bool interior = (m0 + BM <= M) && (n0 + BN <= N) && ((N & 3) == 0);
+    // edge tiles still store whole 4-column groups with one vector store
+    // when the row is in range (rows past M are skipped below)
+    const bool vec_n = (N & 3) == 0;
     if (interior && OUT_DT == QIMG_BF16) {  // (no gate with bf16 outputs)
         // Interior bf16 tiles: each wave stages one 32x128 block at a time in a
         // private LDS buffer (rows padded by 16 bytes: conflict-free for both
@@ -471,7 +474,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                 for (int g = 0; g < 4; ++g) {
                     const int nb = nj + 8 * g;
                     const float* o = reinterpret_cast<const float*>(out) + static_cast<int64_t>(m) * N + nb;
-                    if (interior) {
+                    if (interior || (m < M && vec_n && nb + 4 <= N)) {
                         res[i][g] = *reinterpret_cast<const v4f*>(o);
                     } else {
 #pragma unroll
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                 }
                 if (OUT_DT == QIMG_FP32) {
                     float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(m) * N + nb;
-                    if (interior) {
+                    if (interior || (vec_n && nb + 4 <= N)) {
                         *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
                     } else {
 #pragma unroll
@@ -512,7 +515,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                     }
                 } else {
                     uint16_t* o = reinterpret_cast<uint16_t*>(out) + static_cast<int64_t>(m) * N + nb;
-                    if (interior) {
+                    if (interior || (vec_n && nb + 4 <= N)) {
                         *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
                     } else {
 #pragma unroll
