@@ -366,6 +366,100 @@ def test_mmdit_block_same_for_every_kernel_choice(qimg, n_img, n_txt, batch):
     assert torch.equal(outs[0][1], outs[1][1])
 
 
+def test_mmdit_block_full_size_sampled(qimg, oracle, blk):
+    """The C4 block at its full size (4096 image + 256 text tokens): every
+    stage run through the C-ABI operations on the GPU, checked against the
+    oracle on the GPU's own inputs of that stage, on sampled rows where the
+    operation is row-wise (linears and LayerNorms: each output row depends
+    only on its input row) and on a 128-query window of every head for the
+    attention (whose Q/K int8 values and scales are compared in full); then
+    the fused block entry point must reproduce the full-size composition bit
+    for bit."""
+    n_img, n_txt, D = 4096, 256, 3072
+    W, B, N = _gpu_block(qimg, 21)
+    g = torch.Generator(device=DEV).manual_seed(22)
+    img = torch.randn(n_img, D, generator=g, device=DEV)
+    txt = torch.randn(n_txt, D, generator=g, device=DEV)
+    t_emb = torch.randn(D, generator=g, device=DEV)
+    pe_np = qimg.qwen_image_pe(128, 128, 2, n_txt)
+    pe = _dev(pe_np)
+    rng = np.random.default_rng(23)
+    h = lambda t: t.cpu().numpy()
+    ref = {n: (h(w.data), h(w.scales), w.had_block_size, h(B[n].view(torch.int16)).view(np.uint16), 0)
+           for n, w in W.items()}
+    norm_bits = {n: h(v.view(torch.int16)).view(np.uint16) for n, v in N.items()}
+
+    def rows_of(M, k=24):
+        return np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, k)]))
+
+    def lin(x, name, gelu=False):
+        got = qimg.linear_forward_quantized(x, W[name], B[name], apply_gelu=gelu)
+        idx = rows_of(x.shape[0])
+        _close(h(got)[idx], blk.qlinear(ref[name], h(x)[idx], gelu), 1e-5, 0.9999999, name)
+        return got
+
+    def ln(x, shift, scale):
+        got = qimg.layer_norm_modulate(x, shift.contiguous(), scale.contiguous())
+        idx = rows_of(x.shape[0])
+        np.testing.assert_allclose(h(got)[idx], blk.layer_norm_modulate(h(x)[idx], h(shift), h(scale)),
+                                   rtol=2e-5, atol=2e-5)
+        return got
+
+    def gate(x, gt, y):
+        got = qimg.gate_add(x, gt.contiguous(), y)
+        np.testing.assert_allclose(h(got), blk.gate_add(h(x), h(gt), h(y)), rtol=1e-6, atol=1e-6)
+        return got
+
+    ts = qimg.silu(t_emb)
+    np.testing.assert_allclose(h(ts), blk.silu(h(t_emb)), rtol=2e-6, atol=1e-7)
+    streams = {"img": (img, "img_mod", ("to_q", "to_k", "to_v"), "to_out", "img_mlp"),
+               "txt": (txt, "txt_mod", ("add_q_proj", "add_k_proj", "add_v_proj"), "to_add_out", "txt_mlp")}
+    mods, qkv = {}, {}
+    for s_, (x, mod, names, _, _) in streams.items():
+        mods[s_] = lin(ts.view(1, D), mod).view(6, D)
+        xn = ln(x, mods[s_][0], mods[s_][1])
+        qkv[s_] = [lin(xn, n) for n in names]
+    heads = []
+    for i, (wt, wi) in enumerate((("norm_added_q", "norm_q"), ("norm_added_k", "norm_k"))):
+        got = qimg.joint_heads_f16(qkv["txt"][i], qkv["img"][i], N[wt], N[wi], pe)
+        want = blk.rope_f16(blk.concat_transpose(blk.rms_norm_heads(h(qkv["txt"][i]), norm_bits[wt]),
+                                                 blk.rms_norm_heads(h(qkv["img"][i]), norm_bits[wi])), pe_np)
+        gg, r = h(got).astype(np.float64), want.astype(np.float64)
+        assert np.all(np.abs(gg - r) <= 2.0 ** -10 * np.abs(r) + 2.0 ** -14 * np.abs(r).max())
+        heads.append(got)
+    v16 = qimg.joint_heads_f16(qkv["txt"][2], qkv["img"][2])
+    np.testing.assert_array_equal(h(v16), blk.concat_transpose(h(qkv["txt"][2]), h(qkv["img"][2])).astype(np.float16))
+    # attention: Q/K int8 values and scales in full, output on a query window
+    qh, kh = h(heads[0]), h(heads[1])
+    km = qimg.sage_k_mean(heads[1])
+    qi, qs = qimg.sage_quant_q(heads[0])
+    ki, ks = qimg.sage_quant_k(heads[1], km)
+    rq, rqs = oracle.sage_quant_q(qh)
+    rkm = oracle.sage_k_mean(kh)
+    rk, rks = oracle.sage_quant_k(kh, rkm)
+    np.testing.assert_array_equal(h(km), rkm)
+    np.testing.assert_array_equal(h(qi), rq)
+    np.testing.assert_array_equal(h(qs), rqs)
+    np.testing.assert_array_equal(h(ki), rk)
+    np.testing.assert_array_equal(h(ks), rks)
+    att = qimg.attention_forward_sage_fp16io(heads[0], heads[1], v16, 1 / np.sqrt(128.0), out_dtype=torch.float16)
+    q0, q1 = 2048, 2176
+    want = oracle.sage_attn(rq, rk, h(v16), rqs, rks, 1 / np.sqrt(128.0), False, rows=(q0, q1))[:, q0:q1]
+    _close(h(att)[:, q0:q1].astype(np.float32), want.astype(np.float32), 2e-2, 0.999, "attention")
+    split = dict(zip(("txt", "img"), qimg.split_heads(att, n_txt)))
+    final = {}
+    for s_, (x, _, _, out_name, mlp) in streams.items():
+        m = mods[s_]
+        x1 = gate(x, m[2], lin(split[s_], out_name))
+        y = lin(lin(ln(x1, m[3], m[4]), f"{mlp}_fc1", gelu=True), f"{mlp}_fc2")
+        final[s_] = gate(x1, m[5], y)
+    img_d, txt_d = img.clone(), txt.clone()
+    qimg.mmdit_block_forward(W, B, N, img_d, txt_d, t_emb, pe)
+    torch.cuda.synchronize()
+    assert torch.equal(img_d, final["img"])
+    assert torch.equal(txt_d, final["txt"])
+
+
 def test_mmdit_block_graph_replays_match_eager(qimg):
     """The block (with its side-stream fork/join) captured in a HIP graph:
     every replay, with eager work and synchronisations between replays,
