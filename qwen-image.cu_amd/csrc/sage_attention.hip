@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
 // ------------------------------------------------------------ attention
 // A workgroup is 8 waves (two per SIMD) over AQ = 256 queries; wave w owns
 // queries 32w .. 32w+31 of the block. K (int8 [64][D]) and V^T (fp16
-// [D][64]) tiles stream through a 4-slot LDS ring filled by direct
+// [D][64]) tiles stream through a 5-slot LDS ring filled by direct
 // global->LDS DMA (global_load_lds_dwordx4), three tiles ahead of the
 // compute, so each 64-key tile is fetched once for 256 queries. Rows are
 // unpadded; a per-row XOR swizzle of the 16-byte chunks keeps the fragment
@@ -376,7 +376,11 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
 constexpr int AQ = 256;          // queries per workgroup
 constexpr float kRescaleSlack = 8.0f;  // lazy-rescale threshold of the running max (log2 units)
 constexpr int AWAVES = AQ / 32;  // 8
-constexpr int ANSLOT = 4;        // LDS ring depth (tiles)
+constexpr int ANSLOT = 5;        // LDS ring depth (tiles)
+constexpr int AHEAD = 3;         // tiles in the ring ahead of the current one
+// step kt reads tiles kt-1 (V), kt and kt+1 (K); kt+2 is in flight and the
+// DMA issued at its start fills the slot of tile kt-2
+static_assert(ANSLOT == AHEAD + 2, "ring depth");
 
 template <int D>
 struct AttnCfg {
@@ -390,9 +394,10 @@ struct AttnCfg {
     static constexpr int V_INSTR = V_BYTES / 1024;
     static constexpr int NI = K_INSTR + V_INSTR;
     static constexpr int PER_WAVE = (NI + AWAVES - 1) / AWAVES;
-    // DMA instructions left in flight at a hand-off: step kt reads tiles kt
-    // and kt+1, so at the end of step kt-1 only tile kt+2 may be missing
-    static constexpr int KEEP = (ANSLOT - 3) * PER_WAVE;
+    // DMA instructions left in flight at a hand-off: tiles are issued three
+    // steps ahead and step kt reads the K of tile kt+1, so at the end of step
+    // kt-1 only tile kt+2 may be missing
+    static constexpr int KEEP = PER_WAVE;
 };
 
 // physical 16-byte chunk of logical chunk c in row `row` (involution).
@@ -514,17 +519,10 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     float dsum = 0.0f;      // this lane-half's share of the row sum
 
 #pragma unroll
-    for (int p = 0; p < ANSLOT - 1; ++p) issue_tile(p, p);
+    for (int p = 0; p < AHEAD; ++p) issue_tile(p, p);
     attn_wait_vmcnt<C::KEEP>();  // tiles 0 and 1 have landed
     __builtin_amdgcn_s_barrier();
 
-    // One 64-key tile. Fragment reads are issued in batches ahead of the
-    // MFMAs that use them (sched_barrier fences keep each batch together,
-    // so an MFMA waits on a read issued several MFMAs earlier rather than on
-    // the one just before it), and P of group t+1 is computed on the VALU
-    // while the PV MFMAs of group t run. MASKED tiles (the tail past S, and
-    // for causal the tiles that reach the block's diagonal) evaluate the
-    // per-key validity; the others skip it.
     // S^T = K Q^T of the tile in ring slot `slot`: blocks of keys
     // 32*kb + (8*(r/4) + 4*half + r%4), query l32.
     auto qk = [&](int slot, v16i (&acc)[2]) {
@@ -550,37 +548,27 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
         }
     };
 
-    // Scores of the tile being processed; the first tile's are computed
-    // before the loop, and each step issues the next tile's QK^T MFMAs
-    // before this tile's softmax, so the MFMA pipe works on them while the
-    // VALU computes P (tiles kt and kt+1 are both resident at the start of
-    // step kt; past the last tile the slot holds a re-fetched valid tile
-    // whose scores are not used).
+    // Each 64-key step is two phases. Softmax(kt): the tile max, the lazy
+    // rescale of O and the row sum, P = exp2(s * mult - m) as fp16 for the
+    // four 16-key groups (VALU), then QK^T of tile kt+1 into the same score
+    // registers (MFMA). PV(kt): O^T += V^T P^T for the four groups (MFMA).
+    // Waves 0-3 run softmax(kt) then PV(kt) in step kt; waves 4-7 run
+    // PV(kt-1) then softmax(kt), so on every SIMD (one wave of each group)
+    // one wave's MFMAs overlap the other's VALU. Each wave applies the same
+    // operations to O, the row sum and P in the same order either way (the
+    // rescale for tile kt after the PV of tile kt-1, before that of kt), so
+    // both groups compute what a single sequence of steps computes. Tiles
+    // kt-1 (V, for waves 4-7), kt and kt+1 are resident during step kt.
     v16i sacc[2];
     qk(0, sacc);
+    const bool lag = wave >= AWAVES / 2;  // waves 4-7 run PV one step late
+    v8h p[4];
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
-    auto step = [&](int kt, auto masked_c) {
+    auto softmax = [&](int kt, auto masked_c) {
         constexpr bool MASKED = decltype(masked_c)::value;
-        issue_tile(kt + ANSLOT - 1, (kt + ANSLOT - 1) % ANSLOT);
-        const uint8_t* kb_lds = lds + (kt % ANSLOT) * C::STAGE;
-        const uint8_t* vb_lds = kb_lds + C::K_BYTES;
-        __builtin_amdgcn_sched_barrier(0);
-        v16i sacc_next[2];
-        qk((kt + 1) % ANSLOT, sacc_next);
-        // first V fragments (groups 0 and 1) are read while QK^T runs
-        v8h vf[2][C::DT];
-        auto read_v = [&](int t, v8h* dst) {
-#pragma unroll
-            for (int dt = 0; dt < C::DT; ++dt) {
-                const int row = dt * 32 + l32;
-                const int chunk = swz_chunk<8>(row, 2 * t + half);
-                dst[dt] = *reinterpret_cast<const v8h*>(vb_lds + row * (2 * KTILE) + chunk * 16);
-            }
-        };
-        read_v(0, vf[0]);
-        read_v(1, vf[1]);
-
-        // ---- softmax statistics of the tile
         const float4 ks4 = *reinterpret_cast<const float4*>(ksh + kt * 4);
         const float ks_lo = half ? ks4.z : ks4.x;
         const float ks_hi = half ? ks4.w : ks4.y;
@@ -628,17 +616,13 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[t][r] *= o_scale;
         }
-
-        // ---- P = exp2(acc * mult - m) -> fp16 (round to nearest, in pairs)
-        // per 16-key group t, and O^T += V^T P^T for that group. The row sum
-        // of the fp16 P is accumulated in fp32 with v_dot2_f32_f16.
+        // P = exp2(acc * mult - m) -> fp16 (round to nearest, in pairs) per
+        // 16-key group t; the row sum of the fp16 P accumulates in fp32 with
+        // v_dot2_f32_f16.
         const float neg_m = -m_new;
-        typedef float f2 __attribute__((ext_vector_type(2)));
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-        auto make_p = [&](int t) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
             const int kb = t >> 1;
-            v8h pt;
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const int r = 8 * (t & 1) + e;
@@ -650,30 +634,54 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
                     if (!key_ok(kb, r + 1)) p1 = 0.0f;
                 }
                 const h2 ph = __builtin_convertvector((f2){p0, p1}, h2);
-                pt[e] = ph.x;
-                pt[e + 1] = ph.y;
+                p[t][e] = ph.x;
+                p[t][e + 1] = ph.y;
                 dsum = __builtin_amdgcn_fdot2(ph, ones, dsum, false);
             }
-            return pt;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // the next tile's scores (past the last tile the slot holds a
+        // re-fetched valid tile whose scores are not used)
+        qk((kt + 1) % ANSLOT, sacc);
+    };
+
+    auto pv = [&](int kt) {
+        const uint8_t* vb_lds = lds + (kt % ANSLOT) * C::STAGE + C::K_BYTES;
+        v8h vf[2][C::DT];
+        auto read_v = [&](int t, v8h* dst) {
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) {
+                const int row = dt * 32 + l32;
+                const int chunk = swz_chunk<8>(row, 2 * t + half);
+                dst[dt] = *reinterpret_cast<const v8h*>(vb_lds + row * (2 * KTILE) + chunk * 16);
+            }
         };
-        v8h p_cur = make_p(0);
+        read_v(0, vf[0]);
+        read_v(1, vf[1]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int dt = 0; dt < C::DT; ++dt)
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t & 1][dt], p_cur, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t & 1][dt], p[t], o[dt], 0, 0, 0);
             if (t + 2 < 4) read_v(t + 2, vf[t & 1]);
-            if (t + 1 < 4) p_cur = make_p(t + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) sacc[kb] = sacc_next[kb];
+    };
 
-        // hand-off: this wave's reads of slots kt and kt+1 are done and its
-        // share of tile kt+2 has landed; the barrier makes every wave's share
-        // visible and frees slot kt for the DMA issued at the start of step
-        // kt+1.
+    // MASKED tiles (the tail past S, and for causal the tiles that reach
+    // the block's diagonal) evaluate the per-key validity; the others skip
+    // it.
+    auto step = [&](int kt, auto masked_c) {
+        issue_tile(kt + AHEAD, (kt + AHEAD) % ANSLOT);
+        __builtin_amdgcn_sched_barrier(0);
+        if (lag && kt > 0) pv(kt - 1);
+        softmax(kt, masked_c);
+        if (!lag) pv(kt);
+        // hand-off: this wave's LDS reads are done and its share of tile
+        // kt+2 has landed; the barrier makes every wave's share visible and
+        // frees slot kt-1 (last read by waves 4-7 in this step) for the DMA
+        // issued at the start of step kt+1.
         attn_wait_vmcnt_lgkm0<C::KEEP>();
         __builtin_amdgcn_s_barrier();
     };
@@ -686,6 +694,7 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     int kt = 0;
     for (; kt < kt_full; ++kt) step(kt, std::false_type{});
     for (; kt < kt_end; ++kt) step(kt, std::true_type{});
+    if (lag) pv(kt_end - 1);
     attn_wait_vmcnt<0>();  // drain the re-fetches issued by the last steps
 
     // combine the two lane-halves' row sums, normalise, store.
