@@ -373,6 +373,14 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
 // unpadded; a per-row XOR swizzle of the 16-byte chunks keeps the fragment
 // reads of 8 consecutive rows on distinct LDS banks (the DMA source address
 // of each lane applies the same swizzle).
+// max(v, v of lane ^ 32): v_permlane32_swap gives every lane the values of
+// both lane halves at its position (no LDS round trip)
+__device__ __forceinline__ float max_lane_halves(float v) {
+    const unsigned u = __float_as_uint(v);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
 constexpr int AQ = 256;          // queries per workgroup
 constexpr float kRescaleSlack = 8.0f;  // lazy-rescale threshold of the running max (log2 units)
 constexpr int AWAVES = AQ / 32;  // 8
@@ -567,9 +575,13 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 
+    // K scales of the tile being processed: each step loads the next tile's
+    // after its own softmax, so the load is in flight during the PV phase
+    // and the hand-off rather than in front of the tile max.
+    float4 ks_cur = *reinterpret_cast<const float4*>(ksh);
     auto softmax = [&](int kt, auto masked_c) {
         constexpr bool MASKED = decltype(masked_c)::value;
-        const float4 ks4 = *reinterpret_cast<const float4*>(ksh + kt * 4);
+        const float4 ks4 = ks_cur;
         const float ks_lo = half ? ks4.z : ks4.x;
         const float ks_hi = half ? ks4.w : ks4.y;
         const float mul_lo = sm_log2 * (qsc * ks_lo);
@@ -598,7 +610,7 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
         float mt = -5000000.0f;
         if (mx_lo != INT32_MIN) mt = fmaxf(mt, static_cast<float>(mx_lo) * mul_lo);
         if (mx_hi != INT32_MIN) mt = fmaxf(mt, static_cast<float>(mx_hi) * mul_hi);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = max_lane_halves(mt);
         // Lazy rescale: the reference max m moves (and O, d are rescaled) only
         // when the tile max exceeds it by more than kRescaleSlack (log2
         // units). Otherwise P = exp2(s - m) <= 2^kRescaleSlack, exact in fp16
@@ -677,6 +689,7 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
         __builtin_amdgcn_sched_barrier(0);
         if (lag && kt > 0) pv(kt - 1);
         softmax(kt, masked_c);
+        ks_cur = *reinterpret_cast<const float4*>(ksh + (kt + 1 < nkt ? kt + 1 : nkt - 1) * 4);
         if (!lag) pv(kt);
         // hand-off: this wave's LDS reads are done and its share of tile
         // kt+2 has landed; the barrier makes every wave's share visible and
