@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void joint_heads_f16_kernel(const float* __res
             if (h >= H) break;  // wave-uniform
             float2 y = x[k];
             if constexpr (NORM_ROPE) {
-                const float ss = wave_sum(y.x * y.x + y.y * y.y);
+                const float ss = wave_sum_dpp(y.x * y.x + y.y * y.y);
                 const float rms = rsqrtf(ss / HD + eps);
                 y.x = y.x * rms * w0;
                 y.y = y.y * rms * w1;

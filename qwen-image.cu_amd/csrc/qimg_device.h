@@ -122,6 +122,33 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// Wave64 fp32 sum without LDS round trips: DPP quad_perm [1,0,3,2] and
+// [2,3,0,1] (pairs, quads), row_half_mirror (lane i with 7-i: 8 lanes),
+// row_mirror (i with 15-i: a row of 16), v_permlane16_swap (rows 0+1, 2+3)
+// and v_permlane32_swap (the two halves). Every lane ends with the same
+// value (each step adds two partial sums in either order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm:[1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm:[2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    {
+        const unsigned u = __float_as_uint(v);
+        const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    {
+        const unsigned u = __float_as_uint(v);
+        const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    return v;
+}
+
 // Two fp32 values -> packed bf16x2 bits with the hardware RNE conversion
 // (v_cvt_pk_bf16_f32); same result as f32_to_bf16 on each.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
