@@ -182,7 +182,9 @@ __device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, i
 // grid.x = rows, blockDim.x = 64..256 (multiple of 64).
 // hbs_log2 = log2(hbs) (0 = no transform). K % 16 == 0 and hbs >= 16 take
 // the vector path (first 4 stages in registers straight from global).
-template <typename InT, RowOut OUT>
+// RPT: chunks a thread loads before transforming them (4 when a row has
+// more 16-value chunks than the workgroup has threads, else 1).
+template <typename InT, RowOut OUT, int RPT>
 __global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
     const InT* x, void* out, float* __restrict__ scales, int M, int K,
     int hbs_log2, float norm) {
@@ -200,19 +202,30 @@ __global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
 
     if (vec) {
         const bool only = (hbs_log2 == 4);
-        for (int c = tid; c < (K >> 4); c += nthr) {
-            float v[16];
-            load16<InT>(xin + 16 * c, v);
-            butterfly<4>(v);
-            if (only) {
+        // up to RPT chunks per thread per pass, all loads issued before the
+        // first transform (a K = 12288 row is 3 chunks per thread)
+        const int nch = K >> 4;
+        for (int c0 = tid; c0 < nch; c0 += RPT * nthr) {
+            float v[RPT][16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    v[i] = v[i] * norm;
-                    amax = fmaxf(amax, fabsf(v[i]));
+            for (int j = 0; j < RPT; ++j)
+                if (c0 + j * nthr < nch) load16<InT>(xin + 16 * (c0 + j * nthr), v[j]);
+#pragma unroll
+            for (int j = 0; j < RPT; ++j) {
+                const int c = c0 + j * nthr;
+                if (c < nch) {
+                    butterfly<4>(v[j]);
+                    if (only) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            v[j][i] = v[j][i] * norm;
+                            amax = fmaxf(amax, fabsf(v[j][i]));
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) lds[lds_pad(16 * c + i)] = v[j][i];
                 }
             }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) lds[lds_pad(16 * c + i)] = v[i];
         }
         lo = 4;
     } else {
@@ -343,7 +356,7 @@ static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int
     int threads = ((chunks + kWave - 1) / kWave) * kWave;
     threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
     const size_t lds = rows_lds_bytes(K);
-    auto kern = fwht_quant_rows_kernel<InT, OUT>;
+    auto kern = chunks > threads ? fwht_quant_rows_kernel<InT, OUT, 4> : fwht_quant_rows_kernel<InT, OUT, 1>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
