@@ -638,7 +638,7 @@ __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int q = 0; q < RW; ++q) {
-            const int tot = wave_sum(acc[m][q]);
+            const int tot = wave_sum_dpp(acc[m][q]);
             mine = lane == m * RW + q ? tot : mine;
         }
     if (lane < MR * RW && e_m < M && e_n < N) {

@@ -137,7 +137,7 @@ __device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, i
         for (int i = tid; i < K; i += nthr) o[i] = lds[lds_pad(i)];
         return;
     } else {
-        amax = wave_max(amax);
+        amax = wave_max_dpp(amax);
         if ((tid & (kWave - 1)) == 0) red[tid / kWave] = amax;
         __syncthreads();
         amax = red[0];

@@ -122,31 +122,42 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
-// Wave64 fp32 sum without LDS round trips: DPP quad_perm [1,0,3,2] and
+// Wave64 all-reduce without LDS round trips: DPP quad_perm [1,0,3,2] and
 // [2,3,0,1] (pairs, quads), row_half_mirror (lane i with 7-i: 8 lanes),
 // row_mirror (i with 15-i: a row of 16), v_permlane16_swap (rows 0+1, 2+3)
 // and v_permlane32_swap (the two halves). Every lane ends with the same
-// value (each step adds two partial sums in either order).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+// value (each step combines two partial results in either order).
+template <int CTRL, typename T>
+__device__ __forceinline__ T dpp32(T v) {
+    static_assert(sizeof(T) == 4, "32-bit lanes");
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v += dpp_f32<0xB1>(v);   // quad_perm:[1,0,3,2]
-    v += dpp_f32<0x4E>(v);   // quad_perm:[2,3,0,1]
-    v += dpp_f32<0x141>(v);  // row_half_mirror
-    v += dpp_f32<0x140>(v);  // row_mirror
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce_dpp(T v, Op op) {
+    v = op(v, dpp32<0xB1>(v));   // quad_perm:[1,0,3,2]
+    v = op(v, dpp32<0x4E>(v));   // quad_perm:[2,3,0,1]
+    v = op(v, dpp32<0x141>(v));  // row_half_mirror
+    v = op(v, dpp32<0x140>(v));  // row_mirror
     {
-        const unsigned u = __float_as_uint(v);
+        const unsigned u = __builtin_bit_cast(unsigned, v);
         const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        v = op(__builtin_bit_cast(T, static_cast<unsigned>(sw[0])), __builtin_bit_cast(T, static_cast<unsigned>(sw[1])));
     }
     {
-        const unsigned u = __float_as_uint(v);
+        const unsigned u = __builtin_bit_cast(unsigned, v);
         const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        v = op(__builtin_bit_cast(T, static_cast<unsigned>(sw[0])), __builtin_bit_cast(T, static_cast<unsigned>(sw[1])));
     }
     return v;
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    return wave_reduce_dpp(v, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+    return wave_reduce_dpp(v, [](int a, int b) { return a + b; });
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    return wave_reduce_dpp(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Two fp32 values -> packed bf16x2 bits with the hardware RNE conversion
@@ -205,7 +216,7 @@ constexpr int LN_MAXV = 4;  // float4 chunks per thread
 constexpr int LN_MAX_DIM = LN_THR * 4 * LN_MAXV;
 
 __device__ __forceinline__ float ln_block_sum(float v, float* red) {
-    v = wave_sum(v);
+    v = wave_sum_dpp(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();  // red may still be read by a previous call
     if (lane == 0) red[wave] = v;
