@@ -152,16 +152,15 @@ __device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, i
                 u32x4 pk;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    uint32_t word = 0;
+                    float v[4];
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        float v = lds[lds_pad(16 * c + 4 * w + b)] * inv;
-                        uint32_t byte;
-                        if constexpr (OUT == RowOut::Int8)
-                            byte = static_cast<uint8_t>(sat_rne_i8(v));
-                        else
-                            byte = f32_to_e4m3(v);
-                        word |= byte << (8 * b);
+                    for (int b = 0; b < 4; ++b) v[b] = lds[lds_pad(16 * c + 4 * w + b)] * inv;
+                    uint32_t word = 0;
+                    if constexpr (OUT == RowOut::Int8) {
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) word |= static_cast<uint32_t>(static_cast<uint8_t>(sat_rne_i8(v[b]))) << (8 * b);
+                    } else {
+                        word = e4m3x4(v[0], v[1], v[2], v[3]);
                     }
                     pk[w] = word;
                 }
@@ -173,7 +172,7 @@ __device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, i
                 if constexpr (OUT == RowOut::Int8)
                     o[i] = static_cast<uint8_t>(sat_rne_i8(v));
                 else
-                    o[i] = static_cast<uint8_t>(f32_to_e4m3(v));
+                    o[i] = static_cast<uint8_t>(e4m3x4(v, 0.0f, 0.0f, 0.0f) & 0xffu);
             }
         }
     }

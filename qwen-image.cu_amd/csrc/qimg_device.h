@@ -53,27 +53,14 @@ __device__ __forceinline__ int8_t sat_rne_i8(float v) {
     return static_cast<int8_t>(static_cast<int>(r));
 }
 
-// fp32 -> OCP E4M3FN bits, round to nearest even, saturating to +-448.
-// Integer-only so the result does not depend on conversion-instruction modes.
-__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
-    uint32_t u = __float_as_uint(f);
-    uint32_t s = (u >> 24) & 0x80u;
-    float a = fabsf(f);
-    if (a != a) return 0x7fu;
-    if (a >= 448.0f) return s | 0x7eu;
-    if (a < 0.015625f) {  // subnormal quantum 2^-9
-        float r = __builtin_rintf(a * 512.0f);
-        return s | static_cast<uint32_t>(r);
-    }
-    uint32_t au = __float_as_uint(a);
-    uint32_t e = (au >> 23) - 120u;  // rebias 127 -> 7
-    uint32_t m = au & 0x7fffffu;
-    uint32_t hm = m >> 20;
-    uint32_t rem = m & 0xfffffu;
-    uint32_t out = (e << 3) | hm;
-    out += (rem > 0x80000u || (rem == 0x80000u && (hm & 1u))) ? 1u : 0u;
-    out = out > 0x7eu ? 0x7eu : out;
-    return s | out;
+// Four fp32 values -> OCP E4M3FN bytes (a in the low byte) with
+// v_cvt_pk_fp8_f32: round to nearest even, subnormals kept (quantum 2^-9).
+// The quantizers call it on values already scaled to |v| <= 448 (plus one
+// rounding, which still rounds to 448), so no input reaches the NaN code.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return static_cast<uint32_t>(w);
 }
 
 // Address-space pointer types of the global -> LDS DMA builtin

@@ -53,6 +53,41 @@ def test_activation_quant_fp8_bit_exact(qimg, oracle, M, K):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
+def test_e4m3_rounding_at_every_tie(qimg, oracle):
+    """The e4m3 conversion of the quantizers against the oracle's, on values
+    chosen to decide the rounding: every midpoint between adjacent e4m3
+    magnitudes (ties go to the even code), one fp32 ulp either side of each
+    midpoint, the subnormal range (quantum 2^-9, ties at odd multiples of
+    2^-10), values just under 448, zeros and random magnitudes, both signs.
+    Each row's first value is 448, so the row scale is exactly 1 and the
+    stored code is the conversion of the value itself (hbs = 1: no
+    transform)."""
+    codes = oracle.e4m3_to_f32(np.arange(0, 0x7f, dtype=np.uint8)).astype(np.float64)  # +0 .. 448
+    mids = (codes[:-1] + codes[1:]) / 2
+    m32 = mids.astype(np.float32)
+    vals = np.concatenate([m32, np.nextafter(m32, np.float32(0)), np.nextafter(m32, np.float32(np.inf)),
+                           codes.astype(np.float32), np.float32([2.0 ** -10, 3 * 2.0 ** -10, 2.0 ** -11, 1e-30, 0.0,
+                                                                 447.9, 447.99997, 448.0])])
+    rng = np.random.default_rng(4)
+    vals = np.concatenate([vals, (rng.random(2000) * 448).astype(np.float32),
+                           (2.0 ** rng.uniform(-12, 8.8, 2000)).astype(np.float32)])
+    vals = np.concatenate([vals, -vals])
+    K = 4096
+    rows = -(-vals.size // (K - 1))
+    x = np.zeros((rows, K), np.float32)
+    x[:, 0] = 448.0
+    x.reshape(-1)[np.flatnonzero(np.tile(np.arange(K) > 0, rows))[:vals.size]] = vals
+    q_ref, s_ref = oracle.quantize_activation_fp8(x, 1)
+    assert np.all(s_ref == np.float32(1.0))
+    q, s = qimg.quantize_activation_hadamard(torch.from_numpy(x).to(DEV), 1, mode=qimg.FP8_HADAMARD)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    # ties really are ties and round to the even code in the oracle
+    tie_codes = q_ref.reshape(-1)[np.flatnonzero(np.tile(np.arange(K) > 0, rows))[:m32.size]]
+    assert np.all((tie_codes & 1) == 0)
+
+
 def test_activation_quant_special_rows(qimg, oracle):
     K = 3072
     x = np.zeros((4, K), np.float32)
