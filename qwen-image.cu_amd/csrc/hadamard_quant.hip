@@ -157,8 +157,7 @@ __device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, i
                     for (int b = 0; b < 4; ++b) v[b] = lds[lds_pad(16 * c + 4 * w + b)] * inv;
                     uint32_t word = 0;
                     if constexpr (OUT == RowOut::Int8) {
-#pragma unroll
-                        for (int b = 0; b < 4; ++b) word |= static_cast<uint32_t>(static_cast<uint8_t>(sat_rne_i8(v[b]))) << (8 * b);
+                        word = i8x4_rne_sat(v[0], v[1], v[2], v[3]);
                     } else {
                         word = e4m3x4(v[0], v[1], v[2], v[3]);
                     }

@@ -53,6 +53,24 @@ __device__ __forceinline__ int8_t sat_rne_i8(float v) {
     return static_cast<int8_t>(static_cast<int>(r));
 }
 
+// Four fp32 values -> saturating round-half-to-even int8 bytes (a in the
+// low byte), the same values as sat_rne_i8 on each: clamp to [-128, 127]
+// (v_med3_f32; clamping first gives the same integer as rounding first),
+// add 1.5 * 2^23 so the addition rounds to an integer (ulp 1) and the low
+// mantissa byte is its two's-complement byte, then gather the four low
+// bytes with v_perm_b32. NaN gives 0.
+__device__ __forceinline__ uint32_t i8x4_rne_sat(float a, float b, float c, float d) {
+    constexpr float kRound = 12582912.0f;  // 1.5 * 2^23
+    const uint32_t ra = __float_as_uint(__builtin_amdgcn_fmed3f(a, -128.0f, 127.0f) + kRound);
+    const uint32_t rb = __float_as_uint(__builtin_amdgcn_fmed3f(b, -128.0f, 127.0f) + kRound);
+    const uint32_t rc = __float_as_uint(__builtin_amdgcn_fmed3f(c, -128.0f, 127.0f) + kRound);
+    const uint32_t rd = __float_as_uint(__builtin_amdgcn_fmed3f(d, -128.0f, 127.0f) + kRound);
+    // v_perm_b32(s0, s1, sel): byte i = byte sel_i of {s1 (0-3), s0 (4-7)}, 0x0c -> 0
+    const uint32_t ab = __builtin_amdgcn_perm(rb, ra, 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(rd, rc, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
 // Four fp32 values -> OCP E4M3FN bytes (a in the low byte) with
 // v_cvt_pk_fp8_f32: round to nearest even, subnormals kept (quantum 2^-9).
 // The quantizers call it on values already scaled to |v| <= 448 (plus one

@@ -234,15 +234,11 @@ __global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict
         u32x4 pk;
 #pragma unroll
         for (int wd = 0; wd < 4; ++wd) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
-                const uint32_t r = raw[8 * c + 2 * wd + bb];
-                const uint32_t lo = static_cast<uint8_t>(sat_rne_i8(f16_to_f32(static_cast<uint16_t>(r & 0xffffu)) * inv));
-                const uint32_t hi = static_cast<uint8_t>(sat_rne_i8(f16_to_f32(static_cast<uint16_t>(r >> 16)) * inv));
-                word |= (lo | (hi << 8)) << (16 * bb);
-            }
-            pk[wd] = word;
+            const uint32_t r0 = raw[8 * c + 2 * wd], r1 = raw[8 * c + 2 * wd + 1];
+            pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(r0 & 0xffffu)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r0 >> 16)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r1 & 0xffffu)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r1 >> 16)) * inv);
         }
         reinterpret_cast<u32x4*>(dst)[c] = pk;
     }
@@ -307,11 +303,8 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const uint16_t* __restrict
         u32x4 pk;
 #pragma unroll
         for (int wd = 0; wd < 4; ++wd) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb)
-                word |= static_cast<uint32_t>(static_cast<uint8_t>(sat_rne_i8(v[16 * c + 4 * wd + bb] * inv))) << (8 * bb);
-            pk[wd] = word;
+            const int e = 16 * c + 4 * wd;
+            pk[wd] = i8x4_rne_sat(v[e] * inv, v[e + 1] * inv, v[e + 2] * inv, v[e + 3] * inv);
         }
         reinterpret_cast<u32x4*>(dst)[c] = pk;
     }

@@ -88,6 +88,34 @@ def test_e4m3_rounding_at_every_tie(qimg, oracle):
     assert np.all((tie_codes & 1) == 0)
 
 
+def test_int8_rounding_at_every_tie(qimg, oracle):
+    """The int8 conversion of the quantizers (clamp, round half to even)
+    against the oracle on every half-integer in range, one fp32 ulp either
+    side of each, the integers and random values, both signs. Each row's
+    first value is 127, so the row scale is exactly 1 and the stored value is
+    the rounding of the value itself (hbs = 1: no transform)."""
+    half = np.arange(-127, 127, dtype=np.float64) + 0.5
+    h32 = half.astype(np.float32)
+    vals = np.concatenate([h32, np.nextafter(h32, np.float32(-np.inf)), np.nextafter(h32, np.float32(np.inf)),
+                           np.arange(-127, 128, dtype=np.float32), np.float32([126.99999, -126.99999, 0.0, -0.0, 1e-30])])
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([vals, ((rng.random(3000) * 2 - 1) * 127).astype(np.float32)])
+    K = 4096
+    rows = -(-vals.size // (K - 1))
+    x = np.zeros((rows, K), np.float32)
+    x[:, 0] = 127.0
+    idx = np.flatnonzero(np.tile(np.arange(K) > 0, rows))[:vals.size]
+    x.reshape(-1)[idx] = vals
+    q_ref, s_ref = oracle.quantize_activation(x, 1, is_bf16=False)
+    assert np.all(s_ref == np.float32(1.0))
+    q, s = qimg.quantize_activation_hadamard(torch.from_numpy(x).to(DEV), 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+    ties = q_ref.reshape(-1)[idx[:h32.size]].astype(np.int64)
+    assert np.all(ties % 2 == 0)
+
+
 def test_activation_quant_special_rows(qimg, oracle):
     K = 3072
     x = np.zeros((4, K), np.float32)
