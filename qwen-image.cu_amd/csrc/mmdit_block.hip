@@ -129,9 +129,10 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
     }
     {
         auto mark = [&](int c) -> hipError_t { return prof ? hipEventRecord(ev[c], s) : hipSuccess; };
-        auto gemm = [&](const uint8_t* qa, const float* sa, int M, const qimg_qlinear& l, float* out, int gelu) {
+        auto gemm = [&](const uint8_t* qa, const float* sa, int M, const qimg_qlinear& l, float* out, int gelu,
+                        hipStream_t st) {
             return launch_linear_prequantized(qa, sa, M, l.K, l.w, l.scales, l.N, l.mode, l.bias, out, QIMG_FP32,
-                                              gelu, s);
+                                              gelu, st);
         };
         auto quant = [&](const float* x, int M, const qimg_qlinear& l) {
             return launch_fwht_quant(x, QIMG_FP32, M, l.K, l.hbs, l.mode, w.act_q, w.act_scales, s);
@@ -139,7 +140,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         auto linear = [&](const float* x, int M, const qimg_qlinear& l, float* out, int gelu) -> hipError_t {
             if (M == 0) return hipSuccess;
             hipError_t r = quant(x, M, l);
-            return r != hipSuccess ? r : gemm(w.act_q, w.act_scales, M, l, out, gelu);
+            return r != hipSuccess ? r : gemm(w.act_q, w.act_scales, M, l, out, gelu, s);
         };
         auto same_quant = [](const qimg_qlinear& a, const qimg_qlinear& c) {
             return a.K == c.K && a.hbs == c.hbs && a.mode == c.mode;
@@ -147,8 +148,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // quantized activations of the image (act_q) and text (act_q_txt)
         // streams live side by side, so that the two streams' linears can
         // share a launch
-        auto quant_txt = [&](const float* x, int M, const qimg_qlinear& l) {
-            return launch_fwht_quant(x, QIMG_FP32, M, l.K, l.hbs, l.mode, w.act_q_txt, w.act_scales_txt, s);
+        auto quant_txt = [&](const float* x, int M, const qimg_qlinear& l, hipStream_t st) {
+            return launch_fwht_quant(x, QIMG_FP32, M, l.K, l.hbs, l.mode, w.act_q_txt, w.act_scales_txt, st);
         };
         // One linear of each stream over the stream's quantized activations;
         // gate != nullptr adds the gated residual into `out` (the stream
@@ -167,9 +168,9 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(mark(QIMG_PROF_MODULATION));
         QIMG_TRY(launch_silu(t_emb, w.t_silu, DIM, s));
         QIMG_TRY(quant(w.t_silu, 1, b.img_mod));
-        QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.img_mod, w.img_mods, 0));
+        QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.img_mod, w.img_mods, 0, s));
         if (same_quant(b.img_mod, b.txt_mod)) {
-            QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.txt_mod, w.txt_mods, 0));
+            QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.txt_mod, w.txt_mods, 0, s));
         } else {
             QIMG_TRY(linear(w.t_silu, 1, b.txt_mod, w.txt_mods, 0));
         }
@@ -202,7 +203,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(mark(QIMG_PROF_QKV_GEMM));
         for (int i = 0; i < 3; ++i) {
             if (!share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[i]));
-            if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i]));
+            if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i], s));
             QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], nullptr, nullptr, Mt, *tl[i], w.txt_qkv[i], nullptr, nullptr,
                                0));
         }
@@ -261,7 +262,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                 QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, 0, n_txt, b.to_add_out.hbs,
                                                  b.to_add_out.mode, w.act_q_txt, w.act_scales_txt, s));
             else
-                QIMG_TRY(quant_txt(w.txt_qkv[0], Mt, b.to_add_out));
+                QIMG_TRY(quant_txt(w.txt_qkv[0], Mt, b.to_add_out, s));
         }
         QIMG_TRY(gemm_pair(Mi, b.to_out, img, im + 2 * DIM, w.img_qkv[1], Mt, b.to_add_out, txt, tm + 2 * DIM,
                            w.txt_qkv[1], 0));
@@ -277,14 +278,24 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
 
         // GELU MLP (transformer.cu:780-808): fc1 of each stream on its own
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));
-        if (Mi) {
-            QIMG_TRY(gemm(w.act_q, w.act_scales, Mi, b.img_mlp_fc1, w.img_mlp, 1));
-            QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
-        }
+        // The text stream's fc1 and fc2-input quantization run on the side
+        // stream beside the image fc2-input quantization, which is HBM-bound
+        // and leaves the matrix cores idle (they start once the image fc1,
+        // which fills every CU, is done).
+        if (Mi) QIMG_TRY(gemm(w.act_q, w.act_scales, Mi, b.img_mlp_fc1, w.img_mlp, 1, s));
         if (Mt) {
-            QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1));
-            QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2));
+            hipStream_t st = s;
+            if (Mi) {
+                QIMG_TRY(hipEventRecord(side->fork, s));
+                QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+                st = side->stream;
+            }
+            QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1, st));
+            QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2, st));
+            if (Mi) QIMG_TRY(hipEventRecord(side->join, side->stream));
         }
+        if (Mi) QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
+        if (Mt && Mi) QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
         // both fc2 in one launch, with the gate2 residual (transformer.cu:
         // 812-818) in their epilogue
         QIMG_TRY(gemm_pair(Mi, b.img_mlp_fc2, img, im + 5 * DIM, w.img_qkv[2], Mt, b.txt_mlp_fc2, txt, tm + 5 * DIM,
