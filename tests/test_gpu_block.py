@@ -340,12 +340,15 @@ def _gpu_block(qimg, seed, mode=0):
     return W, B, nr
 
 
-@pytest.mark.parametrize("n_img,n_txt,batch", [(4096, 256, 1), (1024, 512, 2)])
+@pytest.mark.parametrize("n_img,n_txt,batch", [(4096, 256, 1), (1024, 512, 2), (4356, 512, 1)])
 def test_mmdit_block_same_for_every_kernel_choice(qimg, n_img, n_txt, batch):
     """At full block sizes the dispatcher pairs the image- and text-stream
     linears in one launch, splits tail tile rows off to the small-tile kernel
     and takes the small-M kernels for the modulation; forcing the large-tile
-    kernel everywhere must give the same bits (int8 accumulation is exact)."""
+    kernel everywhere must give the same bits (int8 accumulation is exact).
+    At 4356 + 512 tokens the image fc1 splits its tail rows off while the
+    text fc1 (two tile rows) runs on the side stream beside the image
+    fc2-input quantization."""
     W, B, nr = _gpu_block(qimg, 3)
     table = qimg.BlockTable([(W, B, nr)])
     g = torch.Generator(device=DEV).manual_seed(4)
