@@ -225,8 +225,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, w.qkv16[0], n_txt,
                                         n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_CONCAT_TRANSPOSE));
-        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[2], w.img_qkv[2], nullptr, nullptr, nullptr, w.qkv16[2], n_txt,
-                                        n_img, batch, HEADS, EPS, s));
+        // V: fp16 straight into the attention's Vt tile layout
+        QIMG_TRY(launch_heads_v_relayout(w.txt_qkv[2], w.img_qkv[2], ss.v_t, n_txt, n_img, batch, HEADS, s));
         QIMG_TRY(mark(QIMG_PROF_ROPE));
 
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)
@@ -234,8 +234,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(launch_sage_quant_q(w.qkv16[0], ss.q_i8, ss.q_scale, HEADS * batch, S, HEAD_DIM, s));
         QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
         QIMG_TRY(launch_sage_quant_k(w.qkv16[1], ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
-        QIMG_TRY(launch_sage_attn(ss.q_i8, ss.k_i8, w.qkv16[2], ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
-                                  HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, ss.v_t, s));
+        QIMG_TRY(launch_sage_attn_vt(ss.q_i8, ss.k_i8, ss.v_t, ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
+                                     HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, s));
 
         // transpose + split back to the streams (transformer.cu:693-703),
         // read by the out-projection quantization straight from the fp16

@@ -87,6 +87,14 @@ hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
                             const float* q_scale, const float* k_scale, void* out, int out_dtype,
                             int BH, int S, int D, float sm_scale, int causal, uint16_t* v_t,
                             hipStream_t stream);
+// launch_sage_attn with V already in the Vt layout (no re-layout pass).
+hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t* v_t, const float* q_scale,
+                               const float* k_scale, void* out, int out_dtype, int BH, int S, int D, float sm_scale,
+                               int causal, hipStream_t stream);
+// The joint block's V (fp32 text and image linear outputs, H heads of 128)
+// -> fp16 in the Vt layout of launch_sage_attn_vt.
+hipError_t launch_heads_v_relayout(const float* txt, const float* img, uint16_t* v_t, int n_txt, int n_img,
+                                   int batch, int H, hipStream_t stream);
 
 
 // block_ops.hip

@@ -357,6 +357,55 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
     }
 }
 
+// The V of the joint block straight from the text and image linears' fp32
+// outputs (token s < n_txt of sequence b is txt[b][s], the rest img[b][s -
+// n_txt], head hh at columns hh*D..): the fp16 values of the V concat +
+// transpose (concat_transpose_fused_fp32, transformer.cu:106-130) laid out
+// as v_relayout_kernel lays them out, in one pass. Grid (ceil(S/64),
+// batch * H); Vt is [batch * H][ceil(S/64)][D][64].
+template <int D>
+__global__ __launch_bounds__(256) void heads_v_relayout_kernel(const float* __restrict__ txt,
+                                                               const float* __restrict__ img,
+                                                               uint16_t* __restrict__ vt, int n_txt, int n_img,
+                                                               int H) {
+    __shared__ uint16_t tile[KTILE][D + 2];
+    const int S = n_txt + n_img;
+    const int kt = blockIdx.x;
+    const int bh = blockIdx.y;
+    const int b = bh / H, hh = bh - b * H;
+    const int tid = threadIdx.x;
+    constexpr int PIECES = KTILE * D / 4;  // 4 fp32 per piece
+#pragma unroll 4
+    for (int pc = tid; pc < PIECES; pc += 256) {
+        const int key = pc / (D / 4);
+        const int c = pc % (D / 4);
+        const int tok = kt * KTILE + key;
+        v4f val = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (tok < S) {
+            const float* row = tok < n_txt ? txt + (static_cast<int64_t>(b) * n_txt + tok) * H * D
+                                           : img + (static_cast<int64_t>(b) * n_img + tok - n_txt) * H * D;
+            val = reinterpret_cast<const v4f*>(row + hh * D)[c];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[key][4 * c + e] = f32_to_f16(val[e]);
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (static_cast<int64_t>(bh) * div_up(S, KTILE) + kt) * D * KTILE;
+    constexpr int OPIECES = KTILE * D / 8;
+    for (int pc = tid; pc < OPIECES; pc += 256) {
+        const int d = pc / 8;
+        const int c = pc % 8;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = tile[vt_key_of_pos(8 * c + 2 * e)][d];
+            const uint32_t hi = tile[vt_key_of_pos(8 * c + 2 * e + 1)][d];
+            o[e] = lo | (hi << 16);
+        }
+        reinterpret_cast<u32x4*>(dst + d * KTILE)[c] = o;
+    }
+}
+
 // ------------------------------------------------------------ attention
 // A workgroup is 8 waves (two per SIMD) over AQ = 256 queries; wave w owns
 // queries 32w .. 32w+31 of the block. K (int8 [64][D]) and V^T (fp16
@@ -816,6 +865,15 @@ hipError_t launch_sage_quant_k(const uint16_t* k, const float* mean, int8_t* k_o
     return hipGetLastError();
 }
 
+hipError_t launch_heads_v_relayout(const float* txt, const float* img, uint16_t* v_t, int n_txt, int n_img,
+                                   int batch, int H, hipStream_t stream) {
+    const int S = n_txt + n_img;
+    if (S == 0 || batch == 0 || H == 0) return hipSuccess;
+    hipLaunchKernelGGL(heads_v_relayout_kernel<128>, dim3(div_up(S, KTILE), batch * H), dim3(256), 0, stream, txt,
+                       img, v_t, n_txt, n_img, H);
+    return hipGetLastError();
+}
+
 hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
                             const float* q_scale, const float* k_scale, void* out, int out_dtype,
                             int BH, int S, int D, float sm_scale, int causal, uint16_t* v_t,
@@ -827,6 +885,12 @@ hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
         hipLaunchKernelGGL(v_relayout_kernel<64>, vgrid, dim3(256), 0, stream, v, v_t, S);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    return launch_sage_attn_vt(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, D, sm_scale, causal, stream);
+}
+
+hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t* v_t, const float* q_scale,
+                               const float* k_scale, void* out, int out_dtype, int BH, int S, int D, float sm_scale,
+                               int causal, hipStream_t stream) {
     const float sm_log2 = sm_scale * 1.44269504088896340736f;
     if (D == 128)
         return causal ? launch_attn_dt<128, true>(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, sm_log2, stream)
