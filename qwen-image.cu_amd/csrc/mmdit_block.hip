@@ -98,8 +98,9 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
     for (int i = 0; i < 3; ++i) {
         w.img_qkv[i] = reinterpret_cast<float*>(take(4 * ri * DIM));
         w.txt_qkv[i] = reinterpret_cast<float*>(take(4 * rt * DIM));
-        w.qkv16[i] = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
     }
+    // fp16 Q and K (V goes straight to the attention's Vt layout)
+    for (int i = 0; i < 2; ++i) w.qkv16[i] = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
     w.attn16 = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
     w.img_mlp = reinterpret_cast<float*>(take(4 * ri * MLP));
     w.txt_mlp = reinterpret_cast<float*>(take(4 * rt * MLP));

@@ -122,7 +122,7 @@ struct BlockScratch {
     float* act_scales_txt;
     float* img_qkv[3];
     float* txt_qkv[3];
-    uint16_t* qkv16[3];
+    uint16_t* qkv16[2];  // fp16 Q, K
     uint16_t* attn16;
     float* img_mlp;
     float* txt_mlp;
