@@ -92,12 +92,14 @@ __global__ __launch_bounds__(256) void joint_heads_f16_kernel(const float* __res
             if (h >= H) break;  // wave-uniform
             float2 y = x[k];
             if constexpr (NORM_ROPE) {
-                const float ss = wave_sum_dpp(y.x * y.x + y.y * y.y);
+                // (explicit fused multiply-adds: the fused Q quantization in
+                // sage_attention.hip repeats this arithmetic bit for bit)
+                const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
                 const float rms = rsqrtf(ss / HD + eps);
                 y.x = y.x * rms * w0;
                 y.y = y.y * rms * w1;
-                const float o0 = y.x * p.x + y.y * p.y;
-                const float o1 = y.x * p.z + y.y * p.w;
+                const float o0 = __builtin_fmaf(y.x, p.x, y.y * p.y);
+                const float o1 = __builtin_fmaf(y.x, p.z, y.y * p.w);
                 y = make_float2(o0, o1);
             }
             const uint32_t packed =

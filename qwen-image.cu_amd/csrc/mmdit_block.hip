@@ -99,8 +99,9 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
         w.img_qkv[i] = reinterpret_cast<float*>(take(4 * ri * DIM));
         w.txt_qkv[i] = reinterpret_cast<float*>(take(4 * rt * DIM));
     }
-    // fp16 Q and K (V goes straight to the attention's Vt layout)
-    for (int i = 0; i < 2; ++i) w.qkv16[i] = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
+    // fp16 K for its mean and quantization (Q goes straight to int8, V to
+    // the attention's Vt layout)
+    w.k16 = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
     w.attn16 = reinterpret_cast<uint16_t*>(take(int64_t{2} * batch * S * DIM));
     w.img_mlp = reinterpret_cast<float*>(take(4 * ri * MLP));
     w.txt_mlp = reinterpret_cast<float*>(take(4 * rt * MLP));
@@ -202,29 +203,35 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
 
         QIMG_TRY(mark(QIMG_PROF_QKV_GEMM));
-        for (int i = 0; i < 3; ++i) {
-            if (!share_i && Mi) QIMG_TRY(quant(w.img_norm, Mi, *il[i]));
-            if (!share_t && Mt) QIMG_TRY(quant_txt(w.txt_norm, Mt, *tl[i], s));
-            QIMG_TRY(gemm_pair(Mi, *il[i], w.img_qkv[i], nullptr, nullptr, Mt, *tl[i], w.txt_qkv[i], nullptr, nullptr,
-                               0));
-        }
-
-        // RMSNorm + concat + transpose + RoPE -> fp16 (transformer.cu:617-666)
-        // K first: its mean (sageattention_sm80.cu:759-773) then runs on the
-        // side stream while Q, V and the Q quantization run here.
+        auto qkv_gemm = [&](int i) -> hipError_t {
+            hipError_t r = hipSuccess;
+            if (!share_i && Mi) r = quant(w.img_norm, Mi, *il[i]);
+            if (r == hipSuccess && !share_t && Mt) r = quant_txt(w.txt_norm, Mt, *tl[i], s);
+            return r != hipSuccess ? r
+                                   : gemm_pair(Mi, *il[i], w.img_qkv[i], nullptr, nullptr, Mt, *tl[i], w.txt_qkv[i],
+                                               nullptr, nullptr, 0);
+        };
+        // K first: its RMSNorm + concat + transpose + RoPE -> fp16
+        // (transformer.cu:617-666), then its mean (sageattention_sm80.cu:
+        // 759-773) on the side stream beside the q and v linears (their 204
+        // tiles at 4096 + 256 tokens leave CUs idle) and the Q / V preparation.
         SideStream* side = nullptr;
         QIMG_TRY(side_stream(&side));
         SageScratch ss;
         sage_scratch_layout(HEADS * batch, S, HEAD_DIM, w.sage, &ss);
-        QIMG_TRY(mark(QIMG_PROF_QK_NORM));
-        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.qkv16[1], n_txt,
+        QIMG_TRY(qkv_gemm(1));
+        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.k16, n_txt,
                                         n_img, batch, HEADS, EPS, s));
         QIMG_TRY(hipEventRecord(side->fork, s));
         QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
-        QIMG_TRY(launch_sage_k_mean(w.qkv16[1], ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
+        QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
         QIMG_TRY(hipEventRecord(side->join, side->stream));
-        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, w.qkv16[0], n_txt,
-                                        n_img, batch, HEADS, EPS, s));
+        QIMG_TRY(qkv_gemm(0));
+        QIMG_TRY(qkv_gemm(2));
+        // Q: RMSNorm + RoPE + fp16 and the Sage int8 quantization in one pass
+        QIMG_TRY(mark(QIMG_PROF_QK_NORM));
+        QIMG_TRY(launch_heads_quant_q(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, ss.q_i8, ss.q_scale,
+                                      n_txt, n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_CONCAT_TRANSPOSE));
         // V: fp16 straight into the attention's Vt tile layout
         QIMG_TRY(launch_heads_v_relayout(w.txt_qkv[2], w.img_qkv[2], ss.v_t, n_txt, n_img, batch, HEADS, s));
@@ -232,9 +239,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
 
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)
         QIMG_TRY(mark(QIMG_PROF_ATTENTION));
-        QIMG_TRY(launch_sage_quant_q(w.qkv16[0], ss.q_i8, ss.q_scale, HEADS * batch, S, HEAD_DIM, s));
         QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
-        QIMG_TRY(launch_sage_quant_k(w.qkv16[1], ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
+        QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
         QIMG_TRY(launch_sage_attn_vt(ss.q_i8, ss.k_i8, ss.v_t, ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, s));
 

@@ -95,6 +95,11 @@ hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t*
 // -> fp16 in the Vt layout of launch_sage_attn_vt.
 hipError_t launch_heads_v_relayout(const float* txt, const float* img, uint16_t* v_t, int n_txt, int n_img,
                                    int batch, int H, hipStream_t stream);
+// The joint block's Q (fp32 text and image linear outputs) -> RMSNorm +
+// RoPE + fp16 rounding -> the int8 Q and scales of launch_sage_quant_q.
+hipError_t launch_heads_quant_q(const float* txt, const float* img, const uint16_t* w_txt, const uint16_t* w_img,
+                                const float* pe, int8_t* q_out, float* q_scale, int n_txt, int n_img, int batch, int H,
+                                float eps, hipStream_t stream);
 
 
 // block_ops.hip
@@ -122,7 +127,7 @@ struct BlockScratch {
     float* act_scales_txt;
     float* img_qkv[3];
     float* txt_qkv[3];
-    uint16_t* qkv16[2];  // fp16 Q, K
+    uint16_t* k16;  // fp16 K
     uint16_t* attn16;
     float* img_mlp;
     float* txt_mlp;

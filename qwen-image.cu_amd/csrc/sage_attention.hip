@@ -310,6 +310,125 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const uint16_t* __restrict
     }
 }
 
+// The joint block's Q straight from the text and image linears' fp32
+// outputs to int8: the RMSNorm + RoPE + fp16 of joint_heads_f16_kernel
+// (block_ops.hip), then quant_q_kernel, without the fp16 Q in HBM. A
+// workgroup owns one 128-token block of one head (quant_q_kernel's grid).
+// Phase 1: wave w takes tokens 32w .. 32w+31 one at a time with the heads
+// kernel's lane layout (lane l holds dims 2l, 2l+1; the same wave sum, FMAs
+// and fp16 rounding), writing the fp16 row to LDS. Phase 2: quant_q_kernel
+// reading those rows from LDS. The int8 values and scales are those of the
+// two kernels run one after the other. D = 128.
+constexpr int HQ_BATCH = 8;  // tokens whose loads a wave keeps in flight
+
+__global__ __launch_bounds__(256) void heads_quant_q_kernel(const float* __restrict__ txt,
+                                                            const float* __restrict__ img,
+                                                            const uint16_t* __restrict__ w_txt,
+                                                            const uint16_t* __restrict__ w_img,
+                                                            const float* __restrict__ pe, int8_t* __restrict__ q_out,
+                                                            float* __restrict__ q_scale, int n_txt, int n_img, int H,
+                                                            float eps) {
+    constexpr int D = 128, HD = D / 2;
+    // fp16 pairs of the block's tokens; rows padded by one word, so the
+    // phase-2 reads (32 rows x 2 halves per wave instruction) hit 64 banks
+    __shared__ uint32_t rowbuf[QBLK][D / 2 + 1];
+    __shared__ float red[QBLK][2];
+    __shared__ float inv_s[32];
+    const int S = n_txt + n_img;
+    const int blk = blockIdx.x;
+    const int bh = blockIdx.y;
+    const int b = bh / H, hh = bh - b * H;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    // phase 1
+    const uint32_t wpt = reinterpret_cast<const uint32_t*>(w_txt)[lane];
+    const uint32_t wpi = reinterpret_cast<const uint32_t*>(w_img)[lane];
+    for (int t0 = 0; t0 < 32; t0 += HQ_BATCH) {
+        float2 x[HQ_BATCH];
+        v4f p[HQ_BATCH];
+#pragma unroll
+        for (int k = 0; k < HQ_BATCH; ++k) {
+            const int tok = blk * QBLK + wave * 32 + t0 + k;
+            x[k] = make_float2(0.0f, 0.0f);
+            p[k] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+            if (tok < S) {
+                const float* row = tok < n_txt ? txt + (static_cast<int64_t>(b) * n_txt + tok) * H * D
+                                               : img + (static_cast<int64_t>(b) * n_img + tok - n_txt) * H * D;
+                x[k] = reinterpret_cast<const float2*>(row + hh * D)[lane];
+                p[k] = reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(tok) * HD + lane];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < HQ_BATCH; ++k) {
+            const int tl = wave * 32 + t0 + k;
+            const int tok = blk * QBLK + tl;
+            const uint32_t wp = tok < n_txt ? wpt : wpi;
+            const float w0 = bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
+            const float w1 = bf16_to_f32(static_cast<uint16_t>(wp >> 16));
+            float2 y = x[k];
+            const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
+            const float rms = rsqrtf(ss / D + eps);
+            y.x = y.x * rms * w0;
+            y.y = y.y * rms * w1;
+            const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
+            const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
+            rowbuf[tl][lane] = static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
+        }
+    }
+    __syncthreads();
+
+    // phase 2: quant_q_kernel on the LDS rows
+    const int tok = blk * QBLK + (tid >> 1);
+    const int part = tid & 1;
+    const bool valid = tok < S;
+    uint32_t raw[HD / 2];
+    float amax = 0.0f;
+    if (valid) {
+#pragma unroll
+        for (int i = 0; i < HD / 2; ++i) raw[i] = rowbuf[tid >> 1][part * (HD / 2) + i];
+#pragma unroll
+        for (int i = 0; i < HD / 2; ++i) {
+            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] & 0xffffu))));
+            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] >> 16))));
+        }
+    }
+    red[tid >> 1][part] = amax;
+    __syncthreads();
+    if (tid < 32) {
+        const int w = tid >> 3, g = tid & 7;
+        float a = 1e-7f;  // the reference starts its max at 1e-7
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int lt = w * 32 + g + 8 * i;
+            a = fmaxf(a, fmaxf(red[lt][0], red[lt][1]));
+        }
+        const float scale = a / 127.0f + 1e-7f;
+        const int nq = div_up(S, QBLK) * 32;
+        q_scale[static_cast<int64_t>(bh) * nq + blk * 32 + w * 8 + g] = scale;
+        inv_s[tid] = 1.0f / scale;
+    }
+    __syncthreads();
+    if (!valid) return;
+    const int lt = tid >> 1;
+    const float inv = inv_s[((lt % QBLK) / 32) * 8 + (lt & 7)];
+    int8_t* dst = q_out + (static_cast<int64_t>(bh) * S + tok) * D + part * HD;
+#pragma unroll
+    for (int c = 0; c < HD / 16; ++c) {
+        u32x4 pk;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            const uint32_t r0 = raw[8 * c + 2 * wd], r1 = raw[8 * c + 2 * wd + 1];
+            pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(r0 & 0xffffu)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r0 >> 16)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r1 & 0xffffu)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r1 >> 16)) * inv);
+        }
+        reinterpret_cast<u32x4*>(dst)[c] = pk;
+    }
+}
+
 // ------------------------------------------------------------ V re-layout
 // V fp16 [BH][S][D] -> Vt [BH][ceil(S/64)][D][64]: for each 64-key tile the
 // head dim becomes rows, and inside each 16-key group position p holds key
@@ -862,6 +981,16 @@ hipError_t launch_sage_quant_k(const uint16_t* k, const float* mean, int8_t* k_o
         hipLaunchKernelGGL(quant_k_kernel<128>, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
     else
         hipLaunchKernelGGL(quant_k_kernel<64>, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
+    return hipGetLastError();
+}
+
+hipError_t launch_heads_quant_q(const float* txt, const float* img, const uint16_t* w_txt, const uint16_t* w_img,
+                                const float* pe, int8_t* q_out, float* q_scale, int n_txt, int n_img, int batch, int H,
+                                float eps, hipStream_t stream) {
+    const int S = n_txt + n_img;
+    if (S == 0 || batch == 0 || H == 0) return hipSuccess;
+    hipLaunchKernelGGL(heads_quant_q_kernel, dim3(div_up(S, QBLK), batch * H), dim3(256), 0, stream, txt, img, w_txt,
+                       w_img, pe, q_out, q_scale, n_txt, n_img, H, eps);
     return hipGetLastError();
 }
 
