@@ -539,17 +539,33 @@ hipError_t launch_small_dma(const void* a, const float* as, int M, int K, const 
 // chunks read as zero through buffer loads, as in the MFMA kernel.
 constexpr int GV_MAXM = 4;
 
+// The weight-side operands of one GEMV of a launch.
+struct GemvOut {
+    const uint8_t* W;
+    const float* ws;
+    const uint16_t* bias;
+    void* out;
+    int N;
+};
+
+// Workgroups [0, split) compute GEMV g0, the rest g1 (two linears of the
+// same activation in one launch, e.g. a block's image and text modulation).
 // ONE: the whole row fits in IU chunks per lane (K <= IU*1024): all loads
 // are issued at once and nothing is loaded past K; otherwise steps of IU
 // chunks alternate between two register sets.
 template <int MR, int RW, int IU, bool ONE, int OUT_DT, bool GELU>
-__global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(
-    const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
-    const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
-    int N, int K) {
+__global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(const uint8_t* __restrict__ A, const float* __restrict__ as,
+                                                         int M, int K, GemvOut g0, GemvOut g1, int split) {
+    const bool second = static_cast<int>(blockIdx.x) >= split;
+    const uint8_t* __restrict__ W = second ? g1.W : g0.W;
+    const float* __restrict__ ws = second ? g1.ws : g0.ws;
+    const uint16_t* __restrict__ bias = second ? g1.bias : g0.bias;
+    void* __restrict__ out = second ? g1.out : g0.out;
+    const int N = second ? g1.N : g0.N;
+    const int bid = second ? static_cast<int>(blockIdx.x) - split : static_cast<int>(blockIdx.x);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n0 = (blockIdx.x * (SM_THR / 64) + wave) * RW;
+    const int n0 = (bid * (SM_THR / 64) + wave) * RW;
     if (n0 >= N) return;  // wave-uniform; no barriers below
     constexpr uint32_t kOob = 0x80000000u;
     const __amdgpu_buffer_rsrc_t ra =
@@ -651,15 +667,18 @@ __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(
 }
 
 template <int MR, int RW, int IU, bool ONE>
-hipError_t launch_gemv(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
-                       const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
-    const int waves = (N + RW - 1) / RW;
-    const int blocks = (waves + SM_THR / 64 - 1) / (SM_THR / 64);
+hipError_t launch_gemv(const void* a, const float* as, int M, int K, const GemvOut& g0, const GemvOut& g1,
+                       int out_dt, int gelu, hipStream_t stream) {
+    auto blocks_of = [](int N) {
+        const int waves = (N + RW - 1) / RW;
+        return (waves + SM_THR / 64 - 1) / (SM_THR / 64);
+    };
+    const int split = blocks_of(g0.N);
+    const int blocks = split + (g1.N > 0 ? blocks_of(g1.N) : 0);
     const uint8_t* A = static_cast<const uint8_t*>(a);
-    const uint8_t* Wq = static_cast<const uint8_t*>(w);
-#define QIMG_GEMV_LAUNCH(ODT, GL)                                                                        \
-    hipLaunchKernelGGL((gemv_i8_kernel<MR, RW, IU, ONE, ODT, GL>), dim3(blocks), dim3(SM_THR), 0, stream, A, Wq, \
-                       as, ws, bias, out, M, N, K)
+#define QIMG_GEMV_LAUNCH(ODT, GL)                                                                              \
+    hipLaunchKernelGGL((gemv_i8_kernel<MR, RW, IU, ONE, ODT, GL>), dim3(blocks), dim3(SM_THR), 0, stream, A, as, M, \
+                       K, g0, g1, split)
     if (out_dt == QIMG_FP32) {
         if (gelu)
             QIMG_GEMV_LAUNCH(QIMG_FP32, true);
@@ -675,11 +694,11 @@ hipError_t launch_gemv(const void* a, const float* as, int M, int K, const void*
     return hipGetLastError();
 }
 
-hipError_t dispatch_gemv(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
-                         const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
+hipError_t dispatch_gemv(const void* a, const float* as, int M, int K, const GemvOut& g0, const GemvOut& g1,
+                         int out_dt, int gelu, hipStream_t stream) {
     const int chunks = ((K >> 4) + 63) >> 6;  // 16-byte chunks per lane
 #define QIMG_GEMV(MR_, RW_, IU_, ONE_) \
-    return launch_gemv<MR_, RW_, IU_, ONE_>(a, as, M, K, w, ws, N, bias, out, out_dt, gelu, stream)
+    return launch_gemv<MR_, RW_, IU_, ONE_>(a, as, M, K, g0, g1, out_dt, gelu, stream)
     if (M <= 2 && chunks <= 4) {
         if (M == 1) {
             if (chunks == 1) QIMG_GEMV(1, 8, 1, true);
@@ -704,6 +723,21 @@ bool small_m_fits(int M, int N, int K) {
            static_cast<int64_t>(N) * K < (int64_t{1} << 31);
 }
 
+// Two int8 linears of the same M <= GV_MAXM activation in one GEMV launch
+// (false: not that case; the caller then runs them one at a time).
+bool launch_gemv_pair(const void* act_q, const float* act_scales, int M, int K, const LinearArgs& a,
+                      const LinearArgs& b, int out_dtype, hipStream_t stream, hipError_t* err) {
+    if (!(get_linear_kernel() == QIMG_LINEAR_AUTO && M >= 1 && M <= GV_MAXM && small_m_fits(M, a.N, K) &&
+          small_m_fits(M, b.N, K) && a.K == K && b.K == K &&
+          small_m_variant(M, a.N, K) == 3 && small_m_variant(M, b.N, K) == 3))
+        return false;
+    *err = dispatch_gemv(act_q, act_scales, M, K,
+                         GemvOut{static_cast<const uint8_t*>(a.w_q), a.w_scales, a.bias, a.out, a.N},
+                         GemvOut{static_cast<const uint8_t*>(b.w_q), b.w_scales, b.bias, b.out, b.N}, out_dtype, 0,
+                         stream);
+    return true;
+}
+
 int small_m_variant(int M, int N, int K) {
     if (!small_m_fits(M, N, K)) return 0;
     if (M <= GV_MAXM) return 3;
@@ -720,7 +754,9 @@ hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int
     // The LDS-staged kernels split K exactly over four waves.
     const bool lds_staged = (K % (SM_KB * (SM_THR / 64))) == 0;
     if (variant == 3 && !fp8 && M <= GV_MAXM)
-        return dispatch_gemv(act_q, act_scales, M, K, w_q, w_scales, N, bias, out, out_dtype, gelu, stream);
+        return dispatch_gemv(act_q, act_scales, M, K,
+                             GemvOut{static_cast<const uint8_t*>(w_q), w_scales, bias, out, N}, GemvOut{}, out_dtype,
+                             gelu, stream);
     if (variant == 3) variant = 1;  // e4m3, or more rows than the GEMV takes
     if (variant == 1 && lds_staged)
         return fp8 ? launch_small_dma<true, 1, 1, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,

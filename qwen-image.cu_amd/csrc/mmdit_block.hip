@@ -170,11 +170,24 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(mark(QIMG_PROF_MODULATION));
         QIMG_TRY(launch_silu(t_emb, w.t_silu, DIM, s));
         QIMG_TRY(quant(w.t_silu, 1, b.img_mod));
-        QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.img_mod, w.img_mods, 0, s));
-        if (same_quant(b.img_mod, b.txt_mod)) {
-            QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.txt_mod, w.txt_mods, 0, s));
-        } else {
-            QIMG_TRY(linear(w.t_silu, 1, b.txt_mod, w.txt_mods, 0));
+        // both modulation linears in one GEMV launch where they share the
+        // activation quantization (int8, the reference's weights)
+        bool mods_done = false;
+        if (same_quant(b.img_mod, b.txt_mod) && b.img_mod.mode == QIMG_QM_INT8_HADAMARD) {
+            const LinearArgs mi{w.act_q, w.act_scales, 1, b.img_mod.K, b.img_mod.w, b.img_mod.scales, b.img_mod.N,
+                                b.img_mod.bias, w.img_mods, nullptr, nullptr};
+            const LinearArgs mt{w.act_q, w.act_scales, 1, b.txt_mod.K, b.txt_mod.w, b.txt_mod.scales, b.txt_mod.N,
+                                b.txt_mod.bias, w.txt_mods, nullptr, nullptr};
+            mods_done = launch_gemv_pair(w.act_q, w.act_scales, 1, b.img_mod.K, mi, mt, QIMG_FP32, s, &e);
+            if (mods_done && e != hipSuccess) goto done;
+        }
+        if (!mods_done) {
+            QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.img_mod, w.img_mods, 0, s));
+            if (same_quant(b.img_mod, b.txt_mod)) {
+                QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.txt_mod, w.txt_mods, 0, s));
+            } else {
+                QIMG_TRY(linear(w.t_silu, 1, b.txt_mod, w.txt_mods, 0));
+            }
         }
         // chunks: shift1, scale1, gate1, shift2, scale2, gate2
         const float* im = w.img_mods;
