@@ -89,6 +89,75 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+# ---- quantized checkpoint files (include/qimg_ckpt.h, libqimg_host.so) ----
+HOST_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libqimg_host.so")
+_CS = ctypes.c_char_p
+_CKPT_SIGS = {
+    "qimg_st_writer_new": (_P, []),
+    "qimg_st_writer_add": (_I, [_P, _CS, _CS, _P, _I, _P, ctypes.c_size_t]),
+    "qimg_st_writer_write": (_I, [_P, _CS]),
+    "qimg_st_writer_free": (None, [_P]),
+    "qimg_checkpoint_kind": (_I, [_CS, _CS, _I]),
+    "qimg_quantize_checkpoint": (_I, [_CS, _CS, _I, _I, _CS, _I]),
+}
+CKPT_EXPORTED = tuple(_CKPT_SIGS)
+CHECKPOINT_KINDS = {0: "bf16", 1: "int8", 2: "fp8"}
+_host = None
+
+
+def host_lib() -> ctypes.CDLL:
+    global _host
+    if _host is None:
+        if not os.path.exists(HOST_LIB_PATH):
+            raise ImportError(f"{HOST_LIB_PATH} is missing: build it with qwen-image.cu_amd/build.py")
+        h = ctypes.CDLL(HOST_LIB_PATH)
+        for name, (res, args) in _CKPT_SIGS.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _host = h
+    return _host
+
+
+def write_safetensors(path: str, tensors) -> None:
+    """tensors: iterable of (name, dtype string, shape, bytes-like), written
+    in that order with the reference's safetensors writer layout."""
+    h = host_lib()
+    w = h.qimg_st_writer_new()
+    if not w:
+        raise MemoryError("qimg_st_writer_new")
+    try:
+        for name, dtype, shape, data in tensors:
+            buf = bytes(data)
+            shp = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+            if h.qimg_st_writer_add(w, name.encode(), dtype.encode(), shp, len(shape), buf, len(buf)) != 0:
+                raise ValueError(f"qimg_st_writer_add rejected {name!r}")
+        if h.qimg_st_writer_write(w, path.encode()) != 0:
+            raise OSError(f"failed to write {path}")
+    finally:
+        h.qimg_st_writer_free(w)
+
+
+def checkpoint_kind(path: str) -> str:
+    """'bf16', 'int8' or 'fp8' (transformer.h:146-156); raises ValueError on
+    an unreadable or malformed checkpoint or an unknown dtype."""
+    err = ctypes.create_string_buffer(512)
+    k = host_lib().qimg_checkpoint_kind(path.encode(), err, len(err))
+    if k < 0:
+        raise ValueError(err.value.decode())
+    return CHECKPOINT_KINDS[k]
+
+
+def quantize_checkpoint(in_path: str, out_path: str, mode: int = INT8_HADAMARD,
+                        num_blocks: int = 60) -> None:
+    """The offline quantizer (quantize.cu): BF16 checkpoint -> I8 / F8_E4M3 +
+    .__scales__ on the current device."""
+    err = ctypes.create_string_buffer(1024)
+    if host_lib().qimg_quantize_checkpoint(in_path.encode(), out_path.encode(), mode, num_blocks, err,
+                                           len(err)) != 0:
+        raise ValueError(err.value.decode())
+
+
 def _check(status: int) -> None:
     if status != QIMG_OK:
         raise QimgError(status, _lib.qimg_last_error().decode())
