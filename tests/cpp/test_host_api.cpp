@@ -9,11 +9,14 @@
 //                                    process then exits 1 with a message, as
 //                                    the reference's asserts do); no GPU needed
 #include <cmath>
+#include <cstdlib>
+#include <unistd.h>
 #include <cstdio>
 #include <cstring>
 #include <string>
 #include <vector>
 
+#include "checkpoint.h"
 #include "kernels.h"
 #include "qimg_oracle.h"
 
@@ -410,6 +413,50 @@ int expect_error(const std::string& c) {
 
 }  // namespace
 
+// Quantized weights through the checkpoint format (transformer.h:146-199):
+// written with SafeTensorsWriter, read back with SafeTensorsLoader and
+// load_quantized_weight, the device bytes, scales, mode and Hadamard block
+// must be those that were written; a BF16 weight loads as BF16 or, when
+// asked, quantized as quantize_weight_tensor quantizes it.
+void case_checkpoint_roundtrip() {
+    Rng r(11);
+    const int N = 64, K = 3072;
+    std::vector<uint16_t> w = bf16_normal(r, static_cast<size_t>(N) * K, 0.02f);
+    Tensor wt = upload(w, {N, K}, DType::BF16);
+    QuantizedWeight q8 = quantize_weight_tensor(wt);
+    QuantizedWeight qf = quantize_weight_tensor_fp8(wt);
+    const std::vector<uint8_t> d8 = download<uint8_t>(q8.data), df = download<uint8_t>(qf.data);
+    const std::vector<float> s8 = download<float>(q8.scales), sf = download<float>(qf.scales);
+    SafeTensorsWriter wr;
+    wr.add("transformer_blocks.0.attn.to_q.weight", "I8", {N, K}, d8.data(), d8.size());
+    wr.add("transformer_blocks.0.attn.to_q.weight.__scales__", "F32", {N}, s8.data(), s8.size() * 4);
+    wr.add("fp8.weight", "F8_E4M3", {N, K}, df.data(), df.size());
+    wr.add("fp8.weight.__scales__", "F32", {N}, sf.data(), sf.size() * 4);
+    wr.add("img_in.weight", "BF16", {N, K}, w.data(), w.size() * 2);
+    const char* tmp = getenv("TMPDIR");
+    const std::string path = std::string(tmp ? tmp : "/tmp") + "/qimg_ckpt_roundtrip_" + std::to_string(getpid()) +
+                             ".safetensors";
+    bool ok = wr.write(path);
+    SafeTensorsLoader ld;
+    ok = ok && ld.load_file(path);
+    if (ok) {
+        ok = detect_checkpoint(ld) == CheckpointKind::INT8 && ld.names().size() == 5;
+        QuantizedWeight a = load_quantized_weight(ld, "transformer_blocks.0.attn.to_q.weight");
+        QuantizedWeight b = load_quantized_weight(ld, "fp8.weight");
+        QuantizedWeight c = load_quantized_weight(ld, "img_in.weight");
+        QuantizedWeight d = load_quantized_weight(ld, "img_in.weight", false);
+        ok = ok && a.mode == QuantMode::INT8_HADAMARD && a.had_block_size == 1024 && a.data.dtype == DType::INT8 &&
+             download<uint8_t>(a.data) == d8 && download<float>(a.scales) == s8;
+        ok = ok && b.mode == QuantMode::FP8_HADAMARD && b.had_block_size == 1024 &&
+             b.data.dtype == DType::FP8_E4M3 && download<uint8_t>(b.data) == df && download<float>(b.scales) == sf;
+        ok = ok && c.mode == QuantMode::BF16 && download<uint16_t>(c.data) == w;
+        ok = ok && d.mode == QuantMode::INT8_HADAMARD && download<uint8_t>(d.data) == d8 &&
+             download<float>(d.scales) == s8;
+    }
+    remove(path.c_str());
+    report("checkpoint_roundtrip", ok);
+}
+
 int main(int argc, char** argv) {
     if (argc == 3 && std::string(argv[1]) == "--expect-error") return expect_error(argv[2]);
     case_tensor_api();
@@ -426,6 +473,7 @@ int main(int argc, char** argv) {
     case_sage(2, 300, 128, false);
     case_sage(3, 129, 64, true);
     case_block_loop();
+    case_checkpoint_roundtrip();
     printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "PASSED", g_fail);
     return g_fail ? 1 : 0;
 }
