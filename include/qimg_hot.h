@@ -23,7 +23,7 @@ extern "C" {
 typedef enum {
     QIMG_OK = 0,
     QIMG_ERR_INVALID_ARG = 1,  /* null pointer, bad size, bad enum */
-    QIMG_ERR_UNSUPPORTED = 2,  /* valid request this build does not implement */
+    QIMG_ERR_UNSUPPORTED = 2,  /* valid request this library does not implement */
     QIMG_ERR_SCRATCH = 3,      /* caller scratch smaller than required */
     QIMG_ERR_HIP = 4           /* a HIP runtime call failed */
 } qimg_status;

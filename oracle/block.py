@@ -1,7 +1,7 @@
 """CPU restatement of one MMDiT joint block (transformer.cu:506-817).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/ and the bench's CPU-baseline leg
-as the checker. Product code never imports it.
+to produce expected values. Product code never imports it.
 
 The element-wise / per-row operations are restated in numpy float32 with
 float64 reductions (the reference reduces in fp32 trees; the difference is a

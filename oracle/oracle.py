@@ -1,7 +1,7 @@
 """numpy front end of the CPU oracle (oracle/qimg_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and the bench's
-CPU-baseline leg as the checker. Product code never imports it.
+CPU-baseline leg to produce expected values. Product code never imports it.
 
 Each wrapper names the reference function it restates (file:line relative to
 the qwen-image.cu tree); the C source holds the arithmetic.

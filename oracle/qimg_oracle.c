@@ -1,7 +1,7 @@
 /*
  * qimg_oracle.c — CPU restatement of qwen-image.cu's quantized-linear and
- * SageAttention hot path. TEST INFRASTRUCTURE ONLY (the checker, never the
- * product). Built with -ffp-contract=off so every fp32 operation rounds
+ * SageAttention hot path. TEST INFRASTRUCTURE ONLY (expected values, never
+ * the product). Built with -ffp-contract=off so every fp32 operation rounds
  * exactly where the reference's source places it.
  */
 #include "qimg_oracle.h"

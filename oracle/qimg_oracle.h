@@ -2,7 +2,7 @@
  * qimg_oracle.h — CPU restatement of qwen-image.cu's quantized-linear and
  * SageAttention hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke
+ * TEST INFRASTRUCTURE ONLY. This library gives the expected values: tests, the smoke
  * check and the bench's CPU-baseline leg call it to produce expected values.
  * No product code path links or calls it.
  *

@@ -1,7 +1,7 @@
 // st_writer_ref.cpp — test infrastructure: writes a fixed set of tensors
 // with the reference's SafeTensorsWriter (safetensors_writer.h, compiled
 // from the reference sources by `make -C oracle ref`) so that the bytes of
-// this build's writer can be compared with it.
+// the library's writer can be compared with it.
 //
 //   st_writer_ref OUT.safetensors
 #include <cstdint>

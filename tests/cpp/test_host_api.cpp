@@ -1,7 +1,7 @@
 // test_host_api.cpp — exercises the reference-signature C++ layer
 // (qwen-image.cu_amd/host/kernels.h) the way the reference's forward pass
 // calls it (transformer.cu:563-606, 680-689, 785-807), and checks every
-// result against the CPU oracle (oracle/qimg_oracle.h, the checker).
+// result against the CPU oracle (oracle/qimg_oracle.h).
 //
 //   test_host_api                    GPU parity cases; exit 0 when all pass
 //   test_host_api --expect-error C   run case C, which must be rejected by the
