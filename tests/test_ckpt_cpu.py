@@ -144,3 +144,25 @@ def test_plan_fixture():
     assert len(glob) == 13 and len(blk) == 32
     assert sum(q for _, q in glob) == 2 and sum(q for _, q in blk) == 14
     assert all(n.endswith(".weight") for n, q in plan if q)
+
+
+def test_metadata_and_escaped_names(qimg, tmp_path):
+    """__metadata__ is skipped (safetensors.h:71); JSON escapes in names
+    (\\u sequences, written by the safetensors package for non-ASCII) are
+    decoded, so the probe name is found."""
+    from safetensors.torch import save_file
+    f = str(tmp_path / "m.safetensors")
+    save_file({"transformer_blocks.0.attn.to_q.weight": torch.zeros(2, 2, dtype=torch.int8),
+               "transformer_blocks.0.attn.to_q.weight.__scales__": torch.ones(2),
+               "café.weight": torch.zeros(1)}, f, metadata={"format": "pt", "quote": 'a"b'})
+    assert qimg.checkpoint_kind(f) == "int8"
+    # the same header hand-escaped with \u sequences
+    raw = open(f, "rb").read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    hdr = raw[8:8 + n].decode()
+    esc = hdr.replace("transformer_blocks.0", "\\u0074ransformer_blocks.0")
+    pad = (8 - (8 + len(esc.encode())) % 8) % 8
+    esc_b = (esc + " " * pad).encode()
+    g = str(tmp_path / "e.safetensors")
+    open(g, "wb").write(struct.pack("<Q", len(esc_b)) + esc_b + raw[8 + n:])
+    assert qimg.checkpoint_kind(g) == "int8"
