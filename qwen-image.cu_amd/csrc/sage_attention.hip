@@ -321,6 +321,7 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const uint16_t* __restrict
 // two kernels run one after the other. D = 128.
 constexpr int HQ_BATCH = 8;  // tokens whose loads a wave keeps in flight
 
+template <int HPW>
 __global__ __launch_bounds__(256) void heads_quant_q_kernel(const float* __restrict__ txt,
                                                             const float* __restrict__ img,
                                                             const uint16_t* __restrict__ w_txt,
@@ -331,13 +332,15 @@ __global__ __launch_bounds__(256) void heads_quant_q_kernel(const float* __restr
     constexpr int D = 128, HD = D / 2;
     // fp16 pairs of the block's tokens; rows padded by one word, so the
     // phase-2 reads (32 rows x 2 halves per wave instruction) hit 64 banks
-    __shared__ uint32_t rowbuf[QBLK][D / 2 + 1];
+    __shared__ uint32_t rowbuf[HPW][QBLK][D / 2 + 1];
     __shared__ float red[QBLK][2];
     __shared__ float inv_s[32];
     const int S = n_txt + n_img;
     const int blk = blockIdx.x;
-    const int bh = blockIdx.y;
-    const int b = bh / H, hh = bh - b * H;
+    // heads hh0 .. hh0 + HPW - 1 of sequence b (H % HPW == 0): each token's
+    // pe row is loaded once for all of them
+    const int b = static_cast<int>(blockIdx.y) * HPW / H;
+    const int hh0 = static_cast<int>(blockIdx.y) * HPW - b * H;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -346,17 +349,19 @@ __global__ __launch_bounds__(256) void heads_quant_q_kernel(const float* __restr
     const uint32_t wpt = reinterpret_cast<const uint32_t*>(w_txt)[lane];
     const uint32_t wpi = reinterpret_cast<const uint32_t*>(w_img)[lane];
     for (int t0 = 0; t0 < 32; t0 += HQ_BATCH) {
-        float2 x[HQ_BATCH];
+        float2 x[HPW][HQ_BATCH];
         v4f p[HQ_BATCH];
 #pragma unroll
         for (int k = 0; k < HQ_BATCH; ++k) {
             const int tok = blk * QBLK + wave * 32 + t0 + k;
-            x[k] = make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int hi = 0; hi < HPW; ++hi) x[hi][k] = make_float2(0.0f, 0.0f);
             p[k] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
             if (tok < S) {
                 const float* row = tok < n_txt ? txt + (static_cast<int64_t>(b) * n_txt + tok) * H * D
                                                : img + (static_cast<int64_t>(b) * n_img + tok - n_txt) * H * D;
-                x[k] = reinterpret_cast<const float2*>(row + hh * D)[lane];
+#pragma unroll
+                for (int hi = 0; hi < HPW; ++hi) x[hi][k] = reinterpret_cast<const float2*>(row + (hh0 + hi) * D)[lane];
                 p[k] = reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(tok) * HD + lane];
             }
         }
@@ -367,65 +372,74 @@ __global__ __launch_bounds__(256) void heads_quant_q_kernel(const float* __restr
             const uint32_t wp = tok < n_txt ? wpt : wpi;
             const float w0 = bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
             const float w1 = bf16_to_f32(static_cast<uint16_t>(wp >> 16));
-            float2 y = x[k];
-            const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
-            const float rms = rsqrtf(ss / D + eps);
-            y.x = y.x * rms * w0;
-            y.y = y.y * rms * w1;
-            const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
-            const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
-            rowbuf[tl][lane] = static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
+#pragma unroll
+            for (int hi = 0; hi < HPW; ++hi) {
+                float2 y = x[hi][k];
+                const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
+                const float rms = rsqrtf(ss / D + eps);
+                y.x = y.x * rms * w0;
+                y.y = y.y * rms * w1;
+                const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
+                const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
+                rowbuf[hi][tl][lane] =
+                    static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
+            }
         }
     }
     __syncthreads();
 
-    // phase 2: quant_q_kernel on the LDS rows
-    const int tok = blk * QBLK + (tid >> 1);
-    const int part = tid & 1;
-    const bool valid = tok < S;
-    uint32_t raw[HD / 2];
-    float amax = 0.0f;
-    if (valid) {
+    // phase 2: quant_q_kernel on the LDS rows, one head at a time
+    for (int hi = 0; hi < HPW; ++hi) {
+        const int bh = static_cast<int>(blockIdx.y) * HPW + hi;
+        if (hi) __syncthreads();  // red / inv_s of the previous head are read
+        const int tok = blk * QBLK + (tid >> 1);
+        const int part = tid & 1;
+        const bool valid = tok < S;
+        uint32_t raw[HD / 2];
+        float amax = 0.0f;
+        if (valid) {
 #pragma unroll
-        for (int i = 0; i < HD / 2; ++i) raw[i] = rowbuf[tid >> 1][part * (HD / 2) + i];
+            for (int i = 0; i < HD / 2; ++i) raw[i] = rowbuf[hi][tid >> 1][part * (HD / 2) + i];
 #pragma unroll
-        for (int i = 0; i < HD / 2; ++i) {
-            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] & 0xffffu))));
-            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] >> 16))));
+            for (int i = 0; i < HD / 2; ++i) {
+                amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] & 0xffffu))));
+                amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] >> 16))));
+            }
         }
-    }
-    red[tid >> 1][part] = amax;
-    __syncthreads();
-    if (tid < 32) {
-        const int w = tid >> 3, g = tid & 7;
-        float a = 1e-7f;  // the reference starts its max at 1e-7
+        red[tid >> 1][part] = amax;
+        __syncthreads();
+        if (tid < 32) {
+            const int w = tid >> 3, g = tid & 7;
+            float a = 1e-7f;  // the reference starts its max at 1e-7
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int lt = w * 32 + g + 8 * i;
-            a = fmaxf(a, fmaxf(red[lt][0], red[lt][1]));
+            for (int i = 0; i < 4; ++i) {
+                const int lt = w * 32 + g + 8 * i;
+                a = fmaxf(a, fmaxf(red[lt][0], red[lt][1]));
+            }
+            const float scale = a / 127.0f + 1e-7f;
+            const int nq = div_up(S, QBLK) * 32;
+            q_scale[static_cast<int64_t>(bh) * nq + blk * 32 + w * 8 + g] = scale;
+            inv_s[tid] = 1.0f / scale;
         }
-        const float scale = a / 127.0f + 1e-7f;
-        const int nq = div_up(S, QBLK) * 32;
-        q_scale[static_cast<int64_t>(bh) * nq + blk * 32 + w * 8 + g] = scale;
-        inv_s[tid] = 1.0f / scale;
-    }
-    __syncthreads();
-    if (!valid) return;
-    const int lt = tid >> 1;
-    const float inv = inv_s[((lt % QBLK) / 32) * 8 + (lt & 7)];
-    int8_t* dst = q_out + (static_cast<int64_t>(bh) * S + tok) * D + part * HD;
+        __syncthreads();
+        if (valid) {
+            const int lt = tid >> 1;
+            const float inv = inv_s[((lt % QBLK) / 32) * 8 + (lt & 7)];
+            int8_t* dst = q_out + (static_cast<int64_t>(bh) * S + tok) * D + part * HD;
 #pragma unroll
-    for (int c = 0; c < HD / 16; ++c) {
-        u32x4 pk;
+            for (int c = 0; c < HD / 16; ++c) {
+                u32x4 pk;
 #pragma unroll
-        for (int wd = 0; wd < 4; ++wd) {
-            const uint32_t r0 = raw[8 * c + 2 * wd], r1 = raw[8 * c + 2 * wd + 1];
-            pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(r0 & 0xffffu)) * inv,
-                                  f16_to_f32(static_cast<uint16_t>(r0 >> 16)) * inv,
-                                  f16_to_f32(static_cast<uint16_t>(r1 & 0xffffu)) * inv,
-                                  f16_to_f32(static_cast<uint16_t>(r1 >> 16)) * inv);
+                for (int wd = 0; wd < 4; ++wd) {
+                    const uint32_t r0 = raw[8 * c + 2 * wd], r1 = raw[8 * c + 2 * wd + 1];
+                    pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(r0 & 0xffffu)) * inv,
+                                          f16_to_f32(static_cast<uint16_t>(r0 >> 16)) * inv,
+                                          f16_to_f32(static_cast<uint16_t>(r1 & 0xffffu)) * inv,
+                                          f16_to_f32(static_cast<uint16_t>(r1 >> 16)) * inv);
+                }
+                reinterpret_cast<u32x4*>(dst)[c] = pk;
+            }
         }
-        reinterpret_cast<u32x4*>(dst)[c] = pk;
     }
 }
 
@@ -989,8 +1003,12 @@ hipError_t launch_heads_quant_q(const float* txt, const float* img, const uint16
                                 float eps, hipStream_t stream) {
     const int S = n_txt + n_img;
     if (S == 0 || batch == 0 || H == 0) return hipSuccess;
-    hipLaunchKernelGGL(heads_quant_q_kernel, dim3(div_up(S, QBLK), batch * H), dim3(256), 0, stream, txt, img, w_txt,
-                       w_img, pe, q_out, q_scale, n_txt, n_img, H, eps);
+    if (H % 2 == 0)
+        hipLaunchKernelGGL(heads_quant_q_kernel<2>, dim3(div_up(S, QBLK), batch * H / 2), dim3(256), 0, stream, txt,
+                           img, w_txt, w_img, pe, q_out, q_scale, n_txt, n_img, H, eps);
+    else
+        hipLaunchKernelGGL(heads_quant_q_kernel<1>, dim3(div_up(S, QBLK), batch * H), dim3(256), 0, stream, txt, img,
+                           w_txt, w_img, pe, q_out, q_scale, n_txt, n_img, H, eps);
     return hipGetLastError();
 }
 
