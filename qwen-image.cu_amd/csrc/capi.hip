@@ -14,10 +14,15 @@ namespace {
 
 thread_local char g_err[512] = "";
 
+int vfail(int status, const char* fmt, va_list ap) {
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    return status;
+}
+
 int fail(int status, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    vfail(status, fmt, ap);
     va_end(ap);
     return status;
 }
@@ -30,6 +35,14 @@ int hip_status(hipError_t e, const char* where) {
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Every device pointer an entry point takes must be 16-byte aligned (the
+// kernels use 16-byte vector and DMA accesses from the base); null pointers
+// (optional arguments) pass.
+template <typename... P>
+bool all_aligned16(const P*... p) {
+    return (aligned16(p) && ...);
+}
 
 int64_t align256(int64_t v) { return (v + 255) & ~static_cast<int64_t>(255); }
 
@@ -50,6 +63,51 @@ int check_rows(const char* fn, int M, int K, int hbs) {
 }
 
 }  // namespace
+
+namespace qimg {
+
+int api_fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vfail(status, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int api_hip_status(hipError_t e, const char* where) { return hip_status(e, where); }
+
+int check_linear(const char* fn, const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales,
+                 int N, int hbs, int mode, void* out, int out_dtype, int64_t* need) {
+    QIMG_REQUIRE(x_dtype == QIMG_FP32 || x_dtype == QIMG_BF16, "%s: x_dtype %d must be FP32 or BF16", fn,
+                 x_dtype);
+    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
+    QIMG_REQUIRE(out_dtype == QIMG_FP32 || out_dtype == QIMG_BF16, "%s: out_dtype %d must be FP32 or BF16",
+                 fn, out_dtype);
+    int st = check_rows(fn, M, K, hbs);
+    if (st) return st;
+    QIMG_REQUIRE(N >= 0, "%s: bad N=%d", fn, N);
+    *need = align256(static_cast<int64_t>(M) * K) + align256(static_cast<int64_t>(M) * 4);
+    if (M == 0 || N == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && w_q && w_scales && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(x, w_q, out), "%s: x, w_q and out must be 16-byte aligned", fn);
+    if (mode == QIMG_QM_FP8_HADAMARD && K % 64 != 0)
+        return fail(QIMG_ERR_UNSUPPORTED, "%s: e4m3 mode needs K %% 64 == 0 (K=%d)", fn, K);
+    return QIMG_OK;
+}
+
+int run_linear(const char* fn, const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales,
+               int N, int hbs, int mode, const uint16_t* bias_bf16, void* out, int out_dtype, int gelu, void* scratch,
+               hipStream_t s) {
+    uint8_t* qa = static_cast<uint8_t*>(scratch);
+    float* sa = reinterpret_cast<float*>(qa + align256(static_cast<int64_t>(M) * K));
+    int st = hip_status(qimg::launch_fwht_quant(x, x_dtype, M, K, hbs, mode, qa, sa, s), fn);
+    if (st) return st;
+    return hip_status(qimg::launch_linear_prequantized(qa, sa, M, K, w_q, w_scales, N, mode, bias_bf16, out,
+                                                       out_dtype, gelu, s),
+                      fn);
+}
+
+}  // namespace qimg
 
 extern "C" {
 
@@ -80,6 +138,7 @@ int qimg_fwht_inplace(float* data, int M, int K, int hbs, void* stream) {
     int st = check_rows("qimg_fwht_inplace", M, K, hbs);
     if (st) return st;
     QIMG_REQUIRE(data || M == 0, "qimg_fwht_inplace: data is null");
+    QIMG_REQUIRE(aligned16(data), "qimg_fwht_inplace: data must be 16-byte aligned");
     return hip_status(qimg::launch_fwht_inplace(data, M, K, hbs, static_cast<hipStream_t>(stream)),
                       "qimg_fwht_inplace");
 }
@@ -89,6 +148,7 @@ int qimg_quantize_per_row_fp32(const float* x, int8_t* out, float* scales, int M
     int st = check_rows("qimg_quantize_per_row_fp32", M, K, 1);
     if (st) return st;
     QIMG_REQUIRE(M == 0 || (x && out && scales), "qimg_quantize_per_row_fp32: null pointer");
+    QIMG_REQUIRE(all_aligned16(x, out), "qimg_quantize_per_row_fp32: x and out must be 16-byte aligned");
     return hip_status(qimg::launch_fwht_quant(x, QIMG_FP32, M, K, 1, QIMG_QM_INT8_HADAMARD, out, scales,
                                               static_cast<hipStream_t>(stream)),
                       "qimg_quantize_per_row_fp32");
@@ -103,6 +163,7 @@ int qimg_quantize_activation(const void* x, int x_dtype, int M, int K, int hbs, 
     int st = check_rows(fn, M, K, hbs);
     if (st) return st;
     QIMG_REQUIRE(M == 0 || (x && q_out && scales_out), "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(x, q_out), "%s: x and q_out must be 16-byte aligned", fn);
     return hip_status(qimg::launch_fwht_quant(x, x_dtype, M, K, hbs, mode, q_out, scales_out,
                                               static_cast<hipStream_t>(stream)),
                       fn);
@@ -119,6 +180,7 @@ int qimg_quantize_weight(const void* w, int w_dtype, int N, int K, int mode, voi
     int st = check_rows(fn, N, K, hbs);
     if (st) return st;
     QIMG_REQUIRE(w && q_out && scales_out, "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(w, q_out), "%s: w and q_out must be 16-byte aligned", fn);
     hipStream_t s = static_cast<hipStream_t>(stream);
     st = hip_status(qimg::launch_fwht_quant(w, w_dtype, N, K, hbs, mode, q_out, scales_out, s), fn);
     if (st) return st;
@@ -142,9 +204,8 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
     if (K % 64 != 0) {
         if (mode == QIMG_QM_FP8_HADAMARD)
             return fail(QIMG_ERR_UNSUPPORTED, "%s: e4m3 mode needs K %% 64 == 0 (K=%d)", fn, K);
-    } else {
-        QIMG_REQUIRE(aligned16(act_q) && aligned16(w_q), "%s: operands must be 16-byte aligned", fn);
     }
+    QIMG_REQUIRE(all_aligned16(act_q, w_q, out), "%s: act_q, w_q and out must be 16-byte aligned", fn);
     return hip_status(qimg::launch_linear_prequantized(act_q, act_scales, M, K, w_q, w_scales, N, mode,
                                                        bias_bf16, out, out_dtype, gelu,
                                                        static_cast<hipStream_t>(stream)),
@@ -177,32 +238,15 @@ int qimg_linear(const void* x, int x_dtype, int M, int K, const void* w_q, const
                 int hbs, int mode, const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                 void* scratch, int64_t scratch_bytes, void* stream) {
     const char* fn = "qimg_linear";
-    QIMG_REQUIRE(x_dtype == QIMG_FP32 || x_dtype == QIMG_BF16, "%s: x_dtype %d must be FP32 or BF16", fn,
-                 x_dtype);
-    QIMG_REQUIRE(mode == QIMG_QM_INT8_HADAMARD || mode == QIMG_QM_FP8_HADAMARD, "%s: bad mode %d", fn, mode);
-    QIMG_REQUIRE(out_dtype == QIMG_FP32 || out_dtype == QIMG_BF16, "%s: out_dtype %d must be FP32 or BF16",
-                 fn, out_dtype);
-    int st = check_rows(fn, M, K, hbs);
-    if (st) return st;
-    QIMG_REQUIRE(N >= 0, "%s: bad N=%d", fn, N);
-    if (M == 0 || N == 0) return QIMG_OK;
-    QIMG_REQUIRE(x && w_q && w_scales && out, "%s: null pointer", fn);
-    if (mode == QIMG_QM_FP8_HADAMARD && K % 64 != 0)
-        return fail(QIMG_ERR_UNSUPPORTED, "%s: e4m3 mode needs K %% 64 == 0 (K=%d)", fn, K);
-    const int64_t act_bytes = align256(static_cast<int64_t>(M) * K);
-    const int64_t need = act_bytes + align256(static_cast<int64_t>(M) * 4);
+    int64_t need = 0;
+    int st = qimg::check_linear(fn, x, x_dtype, M, K, w_q, w_scales, N, hbs, mode, out, out_dtype, &need);
+    if (st || M == 0 || N == 0) return st;
     if (!scratch || scratch_bytes < need)
         return fail(QIMG_ERR_SCRATCH, "%s: scratch %lld bytes < required %lld", fn,
                     static_cast<long long>(scratch_bytes), static_cast<long long>(need));
     QIMG_REQUIRE(aligned16(scratch), "%s: scratch must be 16-byte aligned", fn);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    uint8_t* qa = static_cast<uint8_t*>(scratch);
-    float* sa = reinterpret_cast<float*>(qa + act_bytes);
-    st = hip_status(qimg::launch_fwht_quant(x, x_dtype, M, K, hbs, mode, qa, sa, s), fn);
-    if (st) return st;
-    return hip_status(qimg::launch_linear_prequantized(qa, sa, M, K, w_q, w_scales, N, mode, bias_bf16, out,
-                                                       out_dtype, gelu, s),
-                      fn);
+    return qimg::run_linear(fn, x, x_dtype, M, K, w_q, w_scales, N, hbs, mode, bias_bf16, out, out_dtype, gelu, scratch,
+                      static_cast<hipStream_t>(stream));
 }
 
 int64_t qimg_sage_scratch_bytes(int BH, int S, int D) {
@@ -224,6 +268,7 @@ int qimg_sage_k_mean(const uint16_t* k_f16, float* mean, int BH, int S, int D, v
     int st = check_sage(fn, BH, S, D);
     if (st) return st;
     QIMG_REQUIRE(k_f16 && mean, "%s: null pointer", fn);
+    QIMG_REQUIRE(aligned16(k_f16), "%s: k must be 16-byte aligned", fn);
     return hip_status(qimg::launch_sage_k_mean(k_f16, mean, BH, S, D, static_cast<hipStream_t>(stream)), fn);
 }
 
@@ -310,6 +355,7 @@ int qimg_silu(const float* x, float* out, int64_t n, void* stream) {
     QIMG_REQUIRE(n >= 0, "%s: bad n=%lld", fn, static_cast<long long>(n));
     if (n == 0) return QIMG_OK;
     QIMG_REQUIRE(x && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(x, out), "%s: x and out must be 16-byte aligned", fn);
     return hip_status(qimg::launch_silu(x, out, n, static_cast<hipStream_t>(stream)), fn);
 }
 
@@ -359,6 +405,7 @@ int qimg_joint_heads_f16(const float* txt, const float* img, const uint16_t* nor
     QIMG_REQUIRE(out && (txt || n_txt == 0) && (img || n_img == 0), "%s: null pointer", fn);
     QIMG_REQUIRE((norm_txt == nullptr) == (norm_img == nullptr), "%s: give both RMSNorm weights or neither", fn);
     QIMG_REQUIRE(norm_txt == nullptr || pe != nullptr, "%s: RMSNorm + RoPE needs pe", fn);
+    QIMG_REQUIRE(all_aligned16(txt, img, pe, out), "%s: txt, img, pe and out must be 16-byte aligned", fn);
     return hip_status(qimg::launch_joint_heads_f16(txt, img, norm_txt, norm_img, pe, out, n_txt, n_img, 1, H, eps,
                                                    static_cast<hipStream_t>(stream)),
                       fn);
@@ -370,6 +417,7 @@ int qimg_split_heads(const uint16_t* attn_f16, float* txt, float* img, int n_txt
     if (st) return st;
     if (n_txt + n_img == 0) return QIMG_OK;
     QIMG_REQUIRE(attn_f16 && (txt || n_txt == 0) && (img || n_img == 0), "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(attn_f16, txt, img), "%s: attn, txt and img must be 16-byte aligned", fn);
     return hip_status(
         qimg::launch_split_heads(attn_f16, txt, img, n_txt, n_img, 1, H, static_cast<hipStream_t>(stream)), fn);
 }

@@ -10,6 +10,23 @@
 
 namespace qimg {
 
+// capi.hip: the C entry points' error reporting and the quantized linear's
+// checks and launch sequence, for entry points defined in other files.
+// api_fail sets the calling thread's qimg_last_error message and returns
+// `status`; api_hip_status maps a HIP error to QIMG_ERR_HIP (or QIMG_OK).
+int api_fail(int status, const char* fmt, ...);
+int api_hip_status(hipError_t e, const char* where);
+// Arguments of qimg_linear (without its scratch); on success *need holds the
+// scratch bytes: align256(M*K) quantized activations, then align256(4*M)
+// scales.
+int check_linear(const char* fn, const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales,
+                 int N, int hbs, int mode, void* out, int out_dtype, int64_t* need);
+// Activation FWHT + quantization into `scratch` (laid out as above), then
+// the fused GEMM, on stream s.
+int run_linear(const char* fn, const void* x, int x_dtype, int M, int K, const void* w_q, const float* w_scales,
+               int N, int hbs, int mode, const uint16_t* bias_bf16, void* out, int out_dtype, int gelu, void* scratch,
+               hipStream_t s);
+
 // hadamard_quant.hip
 size_t rows_lds_bytes(int K);
 hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, int mode,

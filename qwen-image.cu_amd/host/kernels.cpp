@@ -107,6 +107,15 @@ QuantizedWeight quantize_weight_common(const Tensor& w, QuantMode mode, const ch
 
 // Per-device SageAttention workspace, grown on demand (the reference keeps
 // a static SageAttentionWorkspace, sageattention_sm80.cu:679-757).
+//
+// A caller holds the workspace's lock from the size check until its kernels
+// are queued, so a second thread cannot free the buffer in between. Growing
+// synchronises the device before the old buffer is freed (work queued
+// earlier may still read it), so a call that grows the workspace must not be
+// made while a stream is being captured into a graph: make the first call at
+// the largest size before capturing. As with the reference's static
+// workspace, calls queued on different streams share one buffer, so their
+// kernels must not overlap in time.
 struct SageWorkspace {
     std::mutex mu;
     std::vector<void*> buf;
@@ -124,10 +133,17 @@ SageWorkspace& block_ws() {
     return ws;
 }
 
-void* grown(SageWorkspace& w, int64_t need) {
+// The workspace buffer of the current device, at least `need` bytes, with
+// its lock held for as long as the lease lives.
+struct WorkspaceLease {
+    std::unique_lock<std::mutex> lock;
+    void* ptr = nullptr;
+};
+
+WorkspaceLease grown(SageWorkspace& w, int64_t need) {
     int dev = 0;
     HIP_CHECK(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lock(w.mu);
+    WorkspaceLease lease{std::unique_lock<std::mutex>(w.mu), nullptr};
     if (static_cast<int>(w.buf.size()) <= dev) {
         w.buf.resize(dev + 1, nullptr);
         w.bytes.resize(dev + 1, 0);
@@ -136,10 +152,13 @@ void* grown(SageWorkspace& w, int64_t need) {
         // the previous buffer may still be read by work queued earlier
         HIP_CHECK(hipDeviceSynchronize());
         if (w.buf[dev]) HIP_CHECK(hipFree(w.buf[dev]));
+        w.buf[dev] = nullptr;
+        w.bytes[dev] = 0;
         HIP_CHECK(hipMalloc(&w.buf[dev], need));
         w.bytes[dev] = need;
     }
-    return w.buf[dev];
+    lease.ptr = w.buf[dev];
+    return lease;
 }
 
 }  // namespace
@@ -263,10 +282,10 @@ void attention_forward_sage_sm80_fp16io(const __half* q, const __half* k, const 
     REQUIRE(D == 64 || D == 128, fn, "head_dim %d not supported (64 or 128)", D);
     REQUIRE(BH > 0 && S > 0, fn, "need BH > 0 and S > 0 (BH=%d S=%d)", BH, S);
     const int64_t need = qimg_sage_scratch_bytes(BH, S, D);
-    void* ws = need > 0 ? grown(sage_ws(), need) : nullptr;
+    const WorkspaceLease ws = grown(sage_ws(), need);  // held until the kernels are queued
     check(qimg_sage_attention(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
                               reinterpret_cast<const uint16_t*>(v), out, QIMG_FP32, scale, BH, S, D, causal ? 1 : 0,
-                              ws, need, stream),
+                              ws.ptr, need, stream),
           fn);
 }
 
@@ -295,10 +314,10 @@ void mmdit_blocks_forward(const std::vector<qimg_mmdit_block>& table, Tensor& im
     REQUIRE(pe.numel() == static_cast<int64_t>(n_img + n_txt) * 256, fn, "pe must be [%d, 64, 4]", n_img + n_txt);
     const int64_t need = qimg_mmdit_blocks_scratch_bytes(n_img, n_txt, batch);
     REQUIRE(need > 0, fn, "bad token counts n_img=%d n_txt=%d", n_img, n_txt);
-    void* ws = grown(block_ws(), need);
+    const WorkspaceLease ws = grown(block_ws(), need);  // held until the kernels are queued
     check(qimg_mmdit_blocks_forward(table.data(), static_cast<int>(table.size()), static_cast<float*>(img.data),
                                     static_cast<float*>(txt.data), static_cast<const float*>(temb.data),
-                                    static_cast<const float*>(pe.data), n_img, n_txt, batch, ws, need, prof_ms,
+                                    static_cast<const float*>(pe.data), n_img, n_txt, batch, ws.ptr, need, prof_ms,
                                     stream),
           fn);
 }

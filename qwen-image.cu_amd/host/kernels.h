@@ -103,7 +103,11 @@ void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& wei
 // ---- SageAttention (cuda_kernels.cuh:558-562) --------------------------
 // FP16 q, k, v [BH, S, D] -> FP32 out [BH, S, D] (values rounded through
 // FP16, as the reference). D in {64, 128}. Uses a per-device workspace the
-// library grows on demand (the reference's SageAttentionWorkspace).
+// library grows on demand (the reference's SageAttentionWorkspace). Like the
+// reference's static workspace, one buffer serves every stream: calls whose
+// kernels could overlap (different streams, no ordering between them) race.
+// Growing synchronises the device, so a call that grows the workspace must
+// not be captured into a graph (make the largest call once before capture).
 void attention_forward_sage_sm80_fp16io(const __half* q, const __half* k, const __half* v, float* out,
                                         float scale, int BH, int S, int D, bool causal = false,
                                         hipStream_t stream = 0);
@@ -145,7 +149,8 @@ qimg_mmdit_block mmdit_block_view(const Block& b) {
 // and pe (batch 2 runs the two CFG forwards of main.cu:761-773 as one):
 // img FP32 [batch * n_img, 3072], txt FP32 [batch * n_txt, 3072], both
 // updated in place; temb FP32 [3072]; pe FP32 [n_txt + n_img, 64, 4], text
-// first (rope.h:154-160). The library grows a per-device workspace.
+// first (rope.h:154-160). The library grows a per-device workspace, with
+// the same sharing and graph-capture rules as the SageAttention wrapper.
 // prof_ms, if given, receives the QIMG_PROF_COUNT PROFILE_BLOCK categories
 // (transformer.cu:486-495) summed over the blocks.
 void mmdit_blocks_forward(const std::vector<qimg_mmdit_block>& table, Tensor& img, Tensor& txt, const Tensor& temb,

@@ -81,3 +81,34 @@ def test_rms_norm_rope_split_invariants(blk):
     st, si = blk.split(x, 3)
     np.testing.assert_array_equal(st, txt)
     np.testing.assert_array_equal(si, img)
+
+
+def test_silu_against_independent_forms(blk):
+    """silu(x) = x * sigmoid(x): against scipy's logistic function in float64,
+    the closed values at 0 and the large-|x| limits (x and 0), and the
+    symmetry silu(x) - silu(-x) = x."""
+    from scipy.special import expit
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(4096) * 4, [0.0, 30.0, -30.0, 1e-3, -1e-3]]).astype(np.float32)
+    y = blk.silu(x)
+    want = x.astype(np.float64) * expit(x.astype(np.float64))
+    np.testing.assert_allclose(y, want, rtol=3e-7, atol=1e-12)
+    assert y[-5] == 0.0 and y[-4] == np.float32(30.0) and abs(y[-3]) < 1e-11
+    np.testing.assert_allclose(y.astype(np.float64) - blk.silu(-x), x, rtol=1e-6, atol=1e-6)
+
+
+def test_gate_add_against_float64(blk):
+    """x + gate * y with one fp32 rounding of the product and one of the sum,
+    or fewer: within one fp32 ulp of each of the two operations of the
+    float64 result; gate 0 returns x and gate 1 is the plain sum."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((7, 3072)).astype(np.float32)
+    y = (rng.standard_normal((7, 3072)) * 3).astype(np.float32)
+    g = rng.standard_normal(3072).astype(np.float32)
+    got = blk.gate_add(x, g, y).astype(np.float64)
+    exact = x.astype(np.float64) + g.astype(np.float64)[None] * y.astype(np.float64)
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    prod_ulp = np.spacing(np.abs(g[None] * y)).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= ulp + prod_ulp)
+    np.testing.assert_array_equal(blk.gate_add(x, np.zeros(3072, np.float32), y), x)
+    np.testing.assert_array_equal(blk.gate_add(x, np.ones(3072, np.float32), y), x + y)

@@ -84,6 +84,15 @@ def test_quantize_rejects_bad_arguments(qimg):
     assert L.qimg_quantize_weight(FAKE, 1, 0, 64, 0, FAKE, FAKE, None, None) == 1
     assert L.qimg_fwht_inplace(None, 4, 64, 64, None) == 1
     assert L.qimg_quantize_per_row_fp32(FAKE, None, FAKE, 4, 64, None) == 1
+    # every device pointer must be 16-byte aligned
+    odd = ctypes.c_void_p(0x10004)
+    assert L.qimg_quantize_activation(odd, 0, 4, 64, 64, 0, FAKE, FAKE, None) == 1
+    assert "aligned" in _err(qimg)
+    assert L.qimg_quantize_weight(FAKE, 1, 8, 64, 0, odd, FAKE, None, None) == 1
+    assert L.qimg_linear(FAKE, 0, 4, 64, odd, FAKE, 8, 64, 0, None, FAKE, 0, 0, FAKE, 1 << 20, None) == 1
+    assert L.qimg_linear_prequantized(FAKE, FAKE, 4, 128, FAKE, FAKE, 8, 0, None, odd, 0, 0, None) == 1
+    assert L.qimg_sage_k_mean(odd, FAKE, 1, 64, 128, None) == 1
+    assert L.qimg_fwht_inplace(odd, 4, 64, 64, None) == 1
 
 
 def test_sage_rejects_bad_arguments(qimg):

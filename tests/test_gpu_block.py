@@ -13,6 +13,8 @@ import numpy as np
 import pytest
 import torch
 
+from blockutil import gpu_block
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
@@ -325,19 +327,7 @@ def test_mmdit_blocks_rejects_bad_arguments(qimg, int8_block):
 
 def _gpu_block(qimg, seed, mode=0):
     """Random N(0,0.02) block weights drawn on the GPU (no oracle copy)."""
-    g = torch.Generator(device=DEV).manual_seed(seed)
-    shapes = {"img_mod": (18432, 3072), "txt_mod": (18432, 3072)}
-    for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
-        shapes[n] = (3072, 3072)
-    for s in ("img", "txt"):
-        shapes[f"{s}_mlp_fc1"] = (12288, 3072)
-        shapes[f"{s}_mlp_fc2"] = (3072, 12288)
-    W = {n: qimg.quantize_weight_tensor((torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16),
-                                        mode=mode) for n, (N, K) in shapes.items()}
-    B = {n: (torch.randn(N, generator=g, device=DEV) * 0.01).to(torch.bfloat16) for n, (N, K) in shapes.items()}
-    nr = {n: (1 + 0.1 * torch.randn(128, generator=g, device=DEV)).to(torch.bfloat16)
-          for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k")}
-    return W, B, nr
+    return gpu_block(qimg, seed, mode)
 
 
 @pytest.mark.parametrize("n_img,n_txt,batch", [(4096, 256, 1), (1024, 512, 2), (4356, 512, 1)])
