@@ -144,6 +144,25 @@ int qimg_linear(const void* x, int x_dtype, int M, int K,
                 const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                 void* scratch, int64_t scratch_bytes, void* stream);
 
+/* Bytes of the static device array behind qimg_linear_noalloc (per GPU). */
+#define QIMG_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+/* qimg_linear without caller scratch and without any device allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The arguments and results are those of qimg_linear; the
+ * quantized activations and their scales go to a static device array of
+ * QIMG_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until
+ * the process ends. align256(M*K) + align256(4*M) must fit in it, else
+ * QIMG_ERR_SCRATCH (e.g. M = 4352 rows of K = 12288 fit, 8192 rows do not).
+ * Every call on one GPU shares that GPU's array and the array keeps the last
+ * call's contents: calls whose kernels can overlap on one GPU (different
+ * streams without ordering between them, or several host threads) race. */
+int qimg_linear_noalloc(const void* x, int x_dtype, int M, int K,
+                        const void* w_q, const float* w_scales, int N, int hbs, int mode,
+                        const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
+                        void* stream);
+
 /* ---- SageAttention ---------------------------------------------------- */
 
 /* Scratch needed by qimg_sage_attention for BH heads of S tokens, head dim D:

@@ -43,6 +43,7 @@ _SIGS = {
     "qimg_set_linear_kernel": (_I, [_I]),
     "qimg_get_linear_kernel": (_I, []),
     "qimg_linear": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I64, _P]),
+    "qimg_linear_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P]),
     "qimg_sage_scratch_bytes": (_I64, [_I, _I, _I]),
     "qimg_sage_k_mean": (_I, [_P, _P, _I, _I, _I, _P]),
     "qimg_sage_quant_q": (_I, [_P, _P, _P, _I, _I, _I, _P]),

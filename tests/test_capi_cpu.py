@@ -95,6 +95,15 @@ def test_quantize_rejects_bad_arguments(qimg):
     assert L.qimg_fwht_inplace(odd, 4, 64, 64, None) == 1
 
 
+def test_linear_noalloc_rejects_oversize_on_the_host(qimg):
+    """M*K beyond the static scratch is refused before any HIP call."""
+    L = qimg.lib()
+    assert L.qimg_linear_noalloc(FAKE, 1, 8192, 12288, FAKE, FAKE, 64, 4096, 0, None, FAKE, 0, 0, None) == 3
+    assert "static" in _err(qimg)
+    assert L.qimg_linear_noalloc(None, 1, 8, 64, FAKE, FAKE, 64, 64, 0, None, FAKE, 0, 0, None) == 1
+    assert L.qimg_linear_noalloc(FAKE, 1, 0, 64, FAKE, FAKE, 64, 64, 0, None, FAKE, 0, 0, None) == 0
+
+
 def test_sage_rejects_bad_arguments(qimg):
     L = qimg.lib()
     args = (FAKE, FAKE, FAKE, FAKE, 0)
