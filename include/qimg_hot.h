@@ -144,6 +144,18 @@ int qimg_linear(const void* x, int x_dtype, int M, int K,
                 const uint16_t* bias_bf16, void* out, int out_dtype, int gelu,
                 void* scratch, int64_t scratch_bytes, void* stream);
 
+/* linear_forward_bf16 / linear_forward_bf16_bf16in (cuda_kernels.cu:4534-4596),
+ * the QuantMode::BF16 path of linear_forward_quantized[_bf16in]
+ * (cuda_kernels.cu:4599-4635) for layers a checkpoint keeps in bf16
+ * (transformer.h:188-193: img_in, txt_in, norm_out, proj_out at
+ * transformer.cu:396-419, 874-895):
+ *   out[m,n] = sum_k bf16(x[m,k]) w[n,k] + bias[n]  (then GELU-tanh if gelu)
+ * x [M,K] QIMG_FP32 (rounded to bf16, nearest even, as fp32_to_bf16 at
+ * cuda_kernels.cu:33-42) or QIMG_BF16; w bf16 [N,K]; bias bf16 [N] or NULL;
+ * out fp32 [M,N]; fp32 accumulation. No scratch is needed. */
+int qimg_linear_bf16(const void* x, int x_dtype, int M, int K, const uint16_t* w_bf16, int N,
+                     const uint16_t* bias_bf16, float* out, int gelu, void* stream);
+
 /* Bytes of the static device array behind qimg_linear_noalloc (per GPU). */
 #define QIMG_NOALLOC_SCRATCH_BYTES (64ll << 20)
 

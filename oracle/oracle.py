@@ -182,6 +182,40 @@ def linear_w8a8(x, w_q, w_scales, hbs, bias_bits=None, gelu=False):
     return dequant_epilogue(c, s, w_scales, bias_bits, gelu)
 
 
+def gelu_tanh64(v):
+    """gelu_fp32 (cuda_kernels.cu:1863-1871): 0.5 v (1 + tanh(c (v + 0.044715 v^3))),
+    c = 0.7978845608, evaluated in float64."""
+    v = np.asarray(v, np.float64)
+    return 0.5 * v * (1.0 + np.tanh(0.7978845608 * (v + 0.044715 * v ** 3)))
+
+
+def linear_bf16(x, w_bits, bias_bits=None, gelu=False):
+    """linear_forward_bf16 / linear_forward_bf16_bf16in (cuda_kernels.cu:4534-4596).
+
+    x fp32 is rounded to bf16 (fp32_to_bf16, cuda_kernels.cu:33-42:
+    __float2bfloat16, nearest even); uint16 x is taken as bf16 bits. The
+    bf16 x bf16 products are summed exactly (float64) and rounded once to
+    fp32: cuBLAS's fp32 accumulation order is outside the reference's
+    sources, so the summation order is not pinned and callers compare within
+    a bound on the fp32 rounding of a K-term sum. Then + bias in fp32
+    (bias_add_fp32, :1510-1517) and GELU (gelu_fp32) when asked.
+    Returns (out float64 [M,N], sum_k |x_k w_k| [M,N] for error bounds)."""
+    if np.asarray(x).dtype == np.uint16:
+        xb = bf16_bits_to_f32(x).reshape(np.shape(x))
+    else:
+        xb = bf16_bits_to_f32(bf16_bits_from_f32(np.asarray(x, np.float32))).reshape(np.shape(x))
+    w = bf16_bits_to_f32(w_bits).reshape(np.shape(w_bits)).astype(np.float64)
+    xd = xb.astype(np.float64)
+    acc = (xd @ w.T).astype(np.float32)
+    mag = np.abs(xd) @ np.abs(w).T
+    if bias_bits is not None:
+        acc = (acc + bf16_bits_to_f32(bias_bits)[None, :]).astype(np.float32)
+    out = acc.astype(np.float64)
+    if gelu:
+        out = gelu_tanh64(out)
+    return out, mag
+
+
 # ---------------------------------------------------------------- fp8
 def quant_rows_fp8(x: np.ndarray):
     x = np.ascontiguousarray(x, dtype=np.float32)

@@ -42,7 +42,7 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function",
 ]
 
-SOURCES = ["hadamard_quant.hip", "gemm_w8a8.hip", "gemm_small_m.hip", "sage_attention.hip", "block_ops.hip",
+SOURCES = ["hadamard_quant.hip", "gemm_w8a8.hip", "gemm_small_m.hip", "gemm_bf16.hip", "sage_attention.hip", "block_ops.hip",
            "mmdit_block.hip", "capi.hip", "linear_noalloc.hip"]
 HOST_SOURCES = ["kernels.cpp", "checkpoint.cpp"]
 

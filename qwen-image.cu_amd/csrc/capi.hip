@@ -249,6 +249,20 @@ int qimg_linear(const void* x, int x_dtype, int M, int K, const void* w_q, const
                       static_cast<hipStream_t>(stream));
 }
 
+int qimg_linear_bf16(const void* x, int x_dtype, int M, int K, const uint16_t* w_bf16, int N,
+                     const uint16_t* bias_bf16, float* out, int gelu, void* stream) {
+    const char* fn = "qimg_linear_bf16";
+    QIMG_REQUIRE(x_dtype == QIMG_FP32 || x_dtype == QIMG_BF16, "%s: x_dtype %d must be FP32 or BF16", fn,
+                 x_dtype);
+    QIMG_REQUIRE(M >= 0 && N >= 0 && K > 0, "%s: bad sizes M=%d N=%d K=%d", fn, M, N, K);
+    if (M == 0 || N == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && w_bf16 && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(x, w_bf16, out), "%s: x, w and out must be 16-byte aligned", fn);
+    return hip_status(qimg::launch_linear_bf16(x, x_dtype, M, K, w_bf16, N, bias_bf16, out, gelu,
+                                               static_cast<hipStream_t>(stream)),
+                      fn);
+}
+
 int64_t qimg_sage_scratch_bytes(int BH, int S, int D) {
     if (BH <= 0 || S <= 0 || D <= 0) return 0;
     return qimg::sage_scratch_layout(BH, S, D, nullptr, nullptr);

@@ -69,6 +69,11 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
 hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
                               float* out, int M, int N, int gelu, hipStream_t stream);
 
+// gemm_bf16.hip: out fp32 [M, N] = bf16(x) . w^T + bias (GELU), x fp32
+// (rounded to bf16) or bf16 [M, K], w bf16 [N, K].
+hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const uint16_t* w, int N,
+                              const uint16_t* bias, float* out, int gelu, hipStream_t stream);
+
 // Kernel selection override for the quantized linear (QIMG_LINEAR_*);
 // returns the previous setting.
 int set_linear_kernel(int which);

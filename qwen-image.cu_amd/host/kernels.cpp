@@ -37,7 +37,8 @@ int qmode(QuantMode m, const char* fn) {
         case QuantMode::FP8_HADAMARD: return QIMG_QM_FP8_HADAMARD;
         case QuantMode::INT4_SVD: die(fn, "QuantMode::INT4_SVD is not part of this library");
         case QuantMode::INT4_AWQ: die(fn, "QuantMode::INT4_AWQ is not part of this library");
-        case QuantMode::BF16: die(fn, "QuantMode::BF16 is not part of this library");
+        case QuantMode::BF16:
+            die(fn, "QuantMode::BF16 weights are not quantized (linear_forward_quantized[_bf16in] take them)");
     }
     die(fn, "unknown QuantMode");
 }
@@ -69,6 +70,28 @@ void check_weight(const QuantizedWeight& w, int K, const char* fn) {
 void check_out(const Tensor& out, int M, int N, const char* fn) {
     REQUIRE(out.ndim == 2 && out.shape[0] == M && out.shape[1] == N, fn, "out is %s, expected [%d, %d]",
             out.shape_str().c_str(), M, N);
+}
+
+// QuantMode::BF16 (linear_forward_bf16 / _bf16in, cuda_kernels.cu:4534-4596):
+// x FP32 (rounded to BF16 by the kernel) or BF16, weight.data BF16 [N, K],
+// out FP32 (asserted by the reference, :4539, :4581).
+void linear_bf16(const Tensor& x, DType want, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                 bool apply_gelu, const char* fn) {
+    REQUIRE(x.ndim == 2, fn, "x must be 2-D [M, K] (got %s)", x.shape_str().c_str());
+    REQUIRE(x.dtype == want, fn, "x must be %s (got %s)", dtype_name(want), dtype_name(x.dtype));
+    REQUIRE(weight.data.ndim == 2 && weight.data.dtype == DType::BF16, fn,
+            "a QuantMode::BF16 weight must be BF16 [N, K] (got %s %s)", dtype_name(weight.data.dtype),
+            weight.data.shape_str().c_str());
+    const int M = static_cast<int>(x.shape[0]);
+    const int K = static_cast<int>(x.shape[1]);
+    REQUIRE(weight.data.shape[1] == K, fn, "weight K=%lld != input K=%d", (long long)weight.data.shape[1], K);
+    const int N = static_cast<int>(weight.data.shape[0]);
+    REQUIRE(out.dtype == DType::FP32, fn, "out must be FP32 (got %s)", dtype_name(out.dtype));
+    check_out(out, M, N, fn);
+    check(qimg_linear_bf16(x.data, want == DType::BF16 ? QIMG_BF16 : QIMG_FP32, M, K,
+                           static_cast<const uint16_t*>(weight.data.data), N, bias_ptr(bias, N, fn),
+                           static_cast<float*>(out.data), apply_gelu ? 1 : 0, nullptr),
+          fn);
 }
 
 void linear_common(const Tensor& x, DType want, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
@@ -263,13 +286,15 @@ QuantizedWeight quantize_weight_tensor_fp8(const Tensor& bf16_weight) {
 void linear_forward_quantized(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
                               Tensor& scratch, bool apply_gelu) {
     const char* fn = "linear_forward_quantized";
-    qmode(weight.mode, fn);  // INT4 / BF16 modes are reported here
+    if (weight.mode == QuantMode::BF16) return linear_bf16(x, DType::FP32, weight, bias, out, apply_gelu, fn);
+    qmode(weight.mode, fn);  // INT4 modes are reported here
     linear_common(x, DType::FP32, weight, bias, out, scratch, apply_gelu, fn);
 }
 
 void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
                                      Tensor& out, Tensor& scratch) {
     const char* fn = "linear_forward_quantized_bf16in";
+    if (weight.mode == QuantMode::BF16) return linear_bf16(x, DType::BF16, weight, bias, out, false, fn);
     qmode(weight.mode, fn);
     linear_common(x, DType::BF16, weight, bias, out, scratch, false, fn);
 }

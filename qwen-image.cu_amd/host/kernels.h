@@ -9,8 +9,11 @@
 //     weights/activations (scale = amax/448); QuantizedWeight::data is then
 //     DType::FP8_E4M3.
 //   * `out` may be FP32 (the reference's type) or BF16.
-//   * The INT4 / BF16 modes of the reference are not part of this library:
-//     dispatching one reports the mode and exits, like any other failed check.
+//   * QuantMode::BF16 weights (layers kept unquantized) run the library's
+//     BF16 kernel behind linear_forward_quantized[_bf16in], as the
+//     reference's linear_forward_bf16[_bf16in]; the INT4 modes are not part
+//     of this library: dispatching one reports the mode and exits, like any
+//     other failed check.
 //
 // Error behaviour follows the reference (assert / CUDA_CHECK -> exit(1)): a
 // rejected argument or failed HIP call prints "qimg: <function>: <reason>"
@@ -95,6 +98,8 @@ inline int64_t int8_scratch_bytes(int M, int K, int N) {
 }
 
 // Dispatch on weight.mode (cuda_kernels.cu:4599-4635): x FP32 resp. BF16.
+// QuantMode::BF16: weight.data BF16 [N, K], no scales, out FP32, scratch
+// unused (the fp32 -> bf16 rounding of x happens inside the kernel).
 void linear_forward_quantized(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
                               Tensor& out, Tensor& scratch, bool apply_gelu = false);
 void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,

@@ -44,6 +44,7 @@ _SIGS = {
     "qimg_get_linear_kernel": (_I, []),
     "qimg_linear": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I64, _P]),
     "qimg_linear_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P]),
+    "qimg_linear_bf16": (_I, [_P, _I, _I, _I, _P, _I, _P, _P, _I, _P]),
     "qimg_sage_scratch_bytes": (_I64, [_I, _I, _I]),
     "qimg_sage_k_mean": (_I, [_P, _P, _I, _I, _I, _P]),
     "qimg_sage_quant_q": (_I, [_P, _P, _P, _I, _I, _I, _P]),
@@ -324,6 +325,26 @@ def linear_forward_quantized(x: torch.Tensor, weight: QuantizedWeight, bias: tor
                             int(weight.had_block_size), int(weight.mode), _ptr(bias), _ptr(out),
                             _DT[out.dtype], int(bool(apply_gelu)), _ptr(scratch), scratch.numel(),
                             _stream()))
+    return out
+
+
+def linear_forward_bf16(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                        apply_gelu: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """linear_forward_bf16 / _bf16in (cuda_kernels.cu:4534-4596), the
+    QuantMode::BF16 path: x fp32 (rounded to bf16 in the kernel) or bf16
+    [M,K], weight bf16 [N,K], bias bf16 [N] -> fp32 [M,N] (+ GELU-tanh)."""
+    _dev(x, "x")
+    _dev(weight, "weight")
+    if weight.dtype != torch.bfloat16:
+        raise QimgError(QIMG_ERR_INVALID_ARG, "weight must be bfloat16")
+    M, K = x.shape
+    N = weight.shape[0]
+    if weight.shape[1] != K:
+        raise QimgError(QIMG_ERR_INVALID_ARG, f"weight K {weight.shape[1]} != activation K {K}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    _check(_lib.qimg_linear_bf16(_ptr(x), _DT[x.dtype], M, K, _ptr(weight), N, _ptr(bias), _ptr(out),
+                                 int(bool(apply_gelu)), _stream()))
     return out
 
 

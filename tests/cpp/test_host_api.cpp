@@ -383,6 +383,12 @@ int expect_error(const std::string& c) {
     } else if (c == "weight_k") {
         Tensor x2 = Tensor::wrap(fake, {4, 128}, DType::FP32);
         linear_forward_quantized(x2, w, nullptr, out, scratch);
+    } else if (c == "bf16_out_dtype") {
+        QuantizedWeight wb;
+        wb.mode = QuantMode::BF16;
+        wb.data = Tensor::wrap(fake, {8, 64}, DType::BF16);
+        Tensor out16 = Tensor::wrap(fake, {4, 8}, DType::BF16);
+        linear_forward_quantized(x, wb, nullptr, out16, scratch);
     } else if (c == "mode_int4") {
         w.mode = QuantMode::INT4_SVD;
         linear_forward_quantized(x, w, nullptr, out, scratch);
@@ -457,6 +463,48 @@ void case_checkpoint_roundtrip() {
     report("checkpoint_roundtrip", ok);
 }
 
+// QuantMode::BF16 weights through the dispatchers (transformer.cu:400, 418
+// call linear_forward_quantized_bf16in; :876, :894 linear_forward_quantized):
+// integer-valued operands, exact in bf16 and in any fp32 summation order, so
+// the output must equal the int64 product plus the bias.
+void case_bf16_mode(bool bf16_in, int M, int N, int K) {
+    Rng r(M + 5 * N + K + bf16_in);
+    std::vector<float> xf(static_cast<size_t>(M) * K), wf(static_cast<size_t>(N) * K);
+    for (auto& v : xf) v = static_cast<float>(static_cast<int>(r.next() % 9) - 4);
+    for (auto& v : wf) v = static_cast<float>(static_cast<int>(r.next() % 9) - 4);
+    std::vector<uint16_t> xb(xf.size()), wb(wf.size()), b(N);
+    for (size_t i = 0; i < xf.size(); ++i) xb[i] = or_f32_to_bf16(xf[i]);
+    for (size_t i = 0; i < wf.size(); ++i) wb[i] = or_f32_to_bf16(wf[i]);
+    for (auto& v : b) v = or_f32_to_bf16(static_cast<float>(static_cast<int>(r.next() % 17) - 8));
+    QuantizedWeight qw;
+    qw.mode = QuantMode::BF16;
+    qw.data = upload(wb, {N, K}, DType::BF16);
+    Tensor bias = upload(b, {N}, DType::BF16);
+    Tensor x = bf16_in ? upload(xb, {M, K}, DType::BF16) : upload(xf, {M, K}, DType::FP32);
+    Tensor out = Tensor::alloc({M, N}, DType::FP32);
+    Tensor scratch = Tensor::alloc({16}, DType::UINT8);  // the BF16 path needs none
+    if (bf16_in)
+        linear_forward_quantized_bf16in(x, qw, &bias, out, scratch);
+    else
+        linear_forward_quantized(x, qw, &bias, out, scratch);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> got = download<float>(out);
+    double d = 0;
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            int64_t acc = 0;
+            for (int k = 0; k < K; ++k)
+                acc += static_cast<int64_t>(xf[static_cast<size_t>(m) * K + k]) *
+                       static_cast<int64_t>(wf[static_cast<size_t>(n) * K + k]);
+            const double want = static_cast<double>(acc) + or_bf16_to_f32(b[n]);
+            d = std::fmax(d, std::fabs(got[static_cast<size_t>(m) * N + n] - want));
+        }
+    char name[96], det[64];
+    snprintf(name, sizeof(name), "bf16-mode linear %s M=%d N=%d K=%d", bf16_in ? "bf16in" : "fp32in", M, N, K);
+    snprintf(det, sizeof(det), "max|diff|=%.3g", d);
+    report(name, d == 0.0, det);
+}
+
 int main(int argc, char** argv) {
     if (argc == 3 && std::string(argv[1]) == "--expect-error") return expect_error(argv[2]);
     case_tensor_api();
@@ -470,6 +518,10 @@ int main(int argc, char** argv) {
     case_linear(true, 1, 18432 / 8, 3072, true, false);
     case_prequantized_and_dequant();
     case_fp8_linear();
+    case_bf16_mode(true, 64, 3072, 64);     // img_in
+    case_bf16_mode(true, 32, 512, 3584);    // txt_in (a slice of N)
+    case_bf16_mode(false, 1, 6144, 3072);   // norm_out
+    case_bf16_mode(false, 96, 64, 3072);    // proj_out
     case_sage(2, 300, 128, false);
     case_sage(3, 129, 64, true);
     case_block_loop();

@@ -20,6 +20,7 @@ REJECTIONS = {
     "x_dtype": "linear_forward_int8: x must be FP32",
     "weight_k": "linear_forward_quantized: weight K=64 != input K=128",
     "mode_int4": "QuantMode::INT4_SVD is not part of this library",
+    "bf16_out_dtype": "linear_forward_quantized: out must be FP32",
     "scratch": "scratch 16 bytes < required",
     "hbs": "hbs=48 is not a power of two",
     "sage_head_dim": "head_dim 96 not supported",

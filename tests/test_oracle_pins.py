@@ -312,3 +312,31 @@ def test_sage_attention_against_float64(oracle, S, D, causal):
     ref = _attn64(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), scale, causal)
     rel, cos = _metrics(out, ref)
     assert rel <= 2e-2 and cos >= 0.999, (rel, cos)
+
+
+def test_linear_bf16_oracle_pins(oracle):
+    """The BF16-mode linear's oracle: integer-valued operands (exact in bf16,
+    every partial sum exact in fp32) equal the int64 product plus the bias;
+    fp32 inputs are rounded as torch rounds to bfloat16 (an independent
+    implementation of nearest even); GELU is the tanh form at known points."""
+    import torch
+    rng = np.random.default_rng(41)
+    M, N, K = 9, 13, 3584
+    xi = rng.integers(-4, 5, (M, K))
+    wi = rng.integers(-4, 5, (N, K))
+    b = oracle.bf16_bits_from_f32(rng.integers(-8, 9, N).astype(np.float32))
+    out, mag = oracle.linear_bf16(xi.astype(np.float32), oracle.bf16_bits_from_f32(wi.astype(np.float32)), b)
+    np.testing.assert_array_equal(out, (xi @ wi.T + oracle.bf16_bits_to_f32(b)[None]).astype(np.float64))
+    np.testing.assert_array_equal(mag, np.abs(xi) @ np.abs(wi).T)
+    # one-hot weights pick bf16(x) exactly
+    x = rng.standard_normal((5, 64)).astype(np.float32) * 3
+    eye = oracle.bf16_bits_from_f32(np.eye(64, dtype=np.float32))
+    got, _ = oracle.linear_bf16(x, eye)
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(got.astype(np.float32), want)
+    # bf16 inputs are used as given
+    got16, _ = oracle.linear_bf16(oracle.bf16_bits_from_f32(x), eye)
+    np.testing.assert_array_equal(got16, got)
+    g = oracle.gelu_tanh64(np.array([0.0, 10.0, -10.0, 1.0]))
+    assert g[0] == 0.0 and abs(g[1] - 10.0) < 1e-12 and abs(g[2]) < 1e-12
+    assert abs(g[3] - 0.8411919906) < 1e-9  # 0.5 (1 + tanh(0.7978845608 * 1.044715))
