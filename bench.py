@@ -74,6 +74,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
+    ap.add_argument("--profile-set", choices=sorted(PROFILE_SETS),
+                    help="only run the named group of measured workloads a few times each, untimed, for "
+                         "rocprofv3 counter runs, and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -90,6 +93,12 @@ def main():
         return
 
     import qimg_amd as q
+
+    if args.profile_set:
+        PROFILE_SETS[args.profile_set](q, torch, torch.device("cuda:0"))
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_set": args.profile_set, "done": True}))
+        return
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -162,8 +171,10 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(stop)
-    ms_step = total_ms / K
-    per_kernel_ms = {n: float(np.mean([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K)]))
+    # medians over the K timed steps (per step, and per launch)
+    step_ms = [ev[i][0].elapsed_time(ev[i][len(launches)]) for i in range(K)]
+    ms_step = float(np.median(step_ms))
+    per_kernel_ms = {n: float(np.median([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K)]))
                      for j, n in enumerate(names)}
     gemm_ops = 2.0 * M * D * H
     total_ops = 2 * gemm_ops
@@ -192,8 +203,8 @@ def main():
                 "traffic": _traffic_from_profiles(dom), "bytes_per_launch": nbytes,
                 "avg_launch_ms": round(per_kernel_ms[dom], 4)}
 
-    extra = {"per_kernel_ms": {k: round(v, 4) for k, v in per_kernel_ms.items()},
-             "wall_s_timed": round(wall, 3)}
+    extra = {"per_kernel_ms_median": {k: round(v, 4) for k, v in per_kernel_ms.items()},
+             "ms_per_step_mean": round(total_ms / K, 4), "wall_s_timed": round(wall, 3)}
     if not args.no_extra:
         extra.update(_extra(q, torch, dev))
 
@@ -202,6 +213,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline(np, torch, x, w1, w2, b1, b2, y, M, D, H)
+        cpu["c3_attention"] = _cpu_baseline_sage(np, torch, q, dev)
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K,
@@ -532,17 +544,163 @@ def _cpu_baseline(np, torch, x, w1, w2, b1, b2, y_gpu, M, D, H, min_seconds=10.0
     y_ref_r = np.stack([o.bf16_bits_to_f32(o.bf16_bits_from_f32(y_ref[r])) for r in rows])
     y_got = y_gpu[rows].float().cpu().numpy()
     parity_rel = float(np.max(np.abs(y_got - y_ref_r)) / np.max(np.abs(y_ref_r)))
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": round(runs * ops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"full MLP pair (M={M}) through the C oracle, {runs} runs in {dt:.1f} s",
-            "cpu": cpu_model, "gpu_parity_max_rel_5rows": parity_rel}
+            "cpu": _cpu_model(), "gpu_parity_max_rel_5rows": parity_rel}
+
+
+def _cpu_model():
+    """The host CPU as /proc/cpuinfo and sysfs describe it: model name,
+    family/model/stepping, logical CPUs visible to this process, and the
+    widest x86 vector extension present."""
+    info = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = (t.strip() for t in line.split(":", 1))
+                info.setdefault(k, v)
+    except OSError:
+        return "unknown"
+    flags = info.get("flags", "").split()
+    vec = next((f for f in ("avx512f", "avx2", "avx") if f in flags), "none")
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        visible = os.cpu_count()
+    return (f"{info.get('model name', '?')} (family {info.get('cpu family', '?')} model {info.get('model', '?')} "
+            f"stepping {info.get('stepping', '?')}, {visible} logical CPUs visible, {vec})")
+
+
+def _cpu_baseline_sage(np, torch, q, dev, min_seconds=10.0, heads_per_run=2):
+    """The C3 attention (24 heads, S = 4352, D = 128, sm_scale 1/sqrt(128))
+    through the oracle's SageAttention (K mean, per-thread Q/K int8 quant,
+    integer QK^T, online softmax, fp16 PV) on the host cores, `heads_per_run`
+    heads at a time over successive heads until `min_seconds` of CPU work;
+    each sample's heads are also run on the GPU and compared."""
+    from oracle import oracle as o
+    BH, S, D = 24, 4352, 128
+    g = torch.Generator(device="cpu").manual_seed(3)
+    qh = torch.randn(BH, S, D, generator=g).to(torch.float16)
+    kh = torch.randn(BH, S, D, generator=g).to(torch.float16)
+    vh = torch.randn(BH, S, D, generator=g).to(torch.float16)
+    sc = 1.0 / math.sqrt(128.0)
+    heads, worst = 0, 0.0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_seconds and heads < BH:
+        h0, h1 = heads, min(BH, heads + heads_per_run)
+        ref = o.sage_attention_fp16io(qh[h0:h1].numpy(), kh[h0:h1].numpy(), vh[h0:h1].numpy(), sc)
+        heads = h1
+    dt = time.perf_counter() - t0
+    # GPU parity on the first sample's heads
+    got = q.attention_forward_sage_fp16io(qh[:heads_per_run].to(dev), kh[:heads_per_run].to(dev),
+                                          vh[:heads_per_run].to(dev), sc, out_dtype=torch.float16)
+    ref0 = o.sage_attention_fp16io(qh[:heads_per_run].numpy(), kh[:heads_per_run].numpy(),
+                                   vh[:heads_per_run].numpy(), sc).astype(np.float32)
+    worst = float(np.max(np.abs(got.float().cpu().numpy() - ref0)) / np.max(np.abs(ref0)))
+    flops = 4.0 * heads * S * S * D
+    return {"value": round(flops / dt / 1e9, 2), "unit": "GFLOP/s", "cores": o.get_threads(), "kind": "port",
+            "sample": f"{heads} of the 24 heads (S={S}, D={D}) through the C oracle's SageAttention in {dt:.1f} s",
+            "gpu_max_rel_vs_oracle": worst}
+
+
+# ---- workloads for rocprofv3 counter runs (bench.py --profile-set NAME):
+# each runs its kernels a few times, untimed; the counters per dispatch are
+# read from the profiler's output by kernel name and grid size.
+def _profile_gemm(q, torch, dev, reps=4):
+    """Large-tile GEMMs: C1 (4096 x 3072 x 3072, int8, fp32 out + bias), the
+    MLP pair at 4352 tokens (int8; fc1 GELU fp32 out, fc2 bf16 out), and the
+    batch-2 e4m3 fc1 / fc2 of the 1328x1328 step (13778 rows)."""
+    g = torch.Generator(device=dev).manual_seed(11)
+
+    def problem(M, N, K, mode):
+        a = torch.randn(M, K, generator=g, device=dev)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        qw = q.quantize_weight_tensor(w, mode=mode)
+        aq, asc = q.quantize_activation_hadamard(a, qw.had_block_size, mode)
+        b = (torch.randn(N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+        return aq, asc, qw, b
+
+    for (M, N, K, mode, gelu, odt) in ((4096, 3072, 3072, q.INT8_HADAMARD, False, torch.float32),
+                                       (4352, 12288, 3072, q.INT8_HADAMARD, True, torch.float32),
+                                       (4352, 3072, 12288, q.INT8_HADAMARD, False, torch.bfloat16),
+                                       (13778, 12288, 3072, q.FP8_HADAMARD, True, torch.float32),
+                                       (13778, 3072, 12288, q.FP8_HADAMARD, False, torch.float32)):
+        aq, asc, qw, b = problem(M, N, K, mode)
+        out = torch.empty(M, N, dtype=odt, device=dev)
+        for _ in range(reps):
+            q.linear_forward_prequantized(aq, asc, qw, b, apply_gelu=gelu, out=out)
+        torch.cuda.synchronize()
+        del aq, asc, qw, b, out
+
+
+def _profile_sage(q, torch, dev, reps=4):
+    """SageAttention at C3 (24 heads, S = 4352): K mean, Q/K quantization
+    and the attention kernel; and the K mean of the batch-2 1328x1328 block
+    (48 heads, S = 7401)."""
+    g = torch.Generator(device=dev).manual_seed(12)
+    for BH, S in ((24, 4352), (48, 7401)):
+        qh = torch.randn(BH, S, 128, generator=g, device=dev).half()
+        kh = torch.randn(BH, S, 128, generator=g, device=dev).half()
+        vh = torch.randn(BH, S, 128, generator=g, device=dev).half()
+        scratch = torch.empty(q.sage_scratch_bytes(BH, S, 128), dtype=torch.uint8, device=dev)
+        for _ in range(reps):
+            km = q.sage_k_mean(kh)
+            if BH == 24:
+                qi, qs = q.sage_quant_q(qh)
+                ki, ks = q.sage_quant_k(kh, km)
+                q.sage_attn_quantized(qi, ki, vh, qs, ks, 1.0 / math.sqrt(128.0), scratch=scratch)
+        torch.cuda.synchronize()
+        del qh, kh, vh, scratch
+
+
+def _profile_small_m(q, torch, dev, reps=3):
+    """The small-M linears (GEMM only) as bench.py's extra leg runs them:
+    modulation (M = 1 and 2, 18432 x 3072) and the text-stream linears at
+    M = 256, each over weight copies totalling > 600 MB so the weights come
+    from HBM."""
+    g = torch.Generator(device=dev).manual_seed(13)
+    for M, N, K, gelu in ((1, 18432, 3072, False), (2, 18432, 3072, False), (256, 3072, 3072, False),
+                          (256, 12288, 3072, True), (256, 3072, 12288, False)):
+        x = torch.randn(M, K, generator=g, device=dev)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        qw0 = q.quantize_weight_tensor(w)
+        b = (torch.randn(N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+        copies = max(2, -(-600_000_000 // (N * K)))
+        qws = [q.QuantizedWeight(qw0.data.clone(), qw0.scales.clone(), qw0.had_block_size, qw0.mode)
+               for _ in range(copies)]
+        aq, asc = q.quantize_activation_hadamard(x, qw0.had_block_size)
+        out = torch.empty(M, N, device=dev)
+        for _ in range(reps):
+            for qw in qws:
+                q.linear_forward_prequantized(aq, asc, qw, b, apply_gelu=gelu, out=out)
+        torch.cuda.synchronize()
+        del qws, qw0, w, out
+
+
+def _profile_quant(q, torch, dev, reps=4):
+    """Activation FWHT + quantization passes: the fc1 input (bf16 4352 x
+    3072, block 1024), the fc2 input (fp32 4352 x 12288, block 4096, int8)
+    and the batch-2 e4m3 fc2 input of the 1328x1328 block (13778 x 12288);
+    and the LayerNorm + modulate + quantization of 4096 x 3072 rows."""
+    g = torch.Generator(device=dev).manual_seed(14)
+    for M, K, hbs, mode, dt in ((4352, 3072, 1024, q.INT8_HADAMARD, torch.bfloat16),
+                                (4352, 12288, 4096, q.INT8_HADAMARD, torch.float32),
+                                (13778, 12288, 4096, q.FP8_HADAMARD, torch.float32)):
+        x = torch.randn(M, K, generator=g, device=dev).to(dt)
+        for _ in range(reps):
+            q.quantize_activation_hadamard(x, hbs, mode)
+        torch.cuda.synchronize()
+        del x
+    x = torch.randn(4096, 3072, generator=g, device=dev)
+    shift = torch.randn(3072, generator=g, device=dev)
+    scale = torch.randn(3072, generator=g, device=dev) * 0.1
+    for _ in range(reps):
+        q.layer_norm_modulate_quant(x, shift, scale, 1024, q.INT8_HADAMARD)
+    torch.cuda.synchronize()
+
+
+PROFILE_SETS = {"gemm": _profile_gemm, "sage": _profile_sage, "small_m": _profile_small_m,
+                "quant": _profile_quant}
 
 
 if __name__ == "__main__":
