@@ -50,80 +50,87 @@ __host__ __device__ constexpr int div_up(int a, int b) { return (a + b - 1) / b;
 // mean[h,d] = (sum over s of k[h,s,d], left to right in fp32) / max(S,1),
 // bit-equal to the reference's one-thread-per-(h,d) loop. The sum must stay
 // sequential, so the work is arranged to keep everything else off that
-// chain: a 256-thread workgroup owns 64 (h,d) chains. Wave 0 only sums, one
-// chain per lane, one v_fma_mix_f32 (fp16 -> fp32 and the add, one
-// rounding: the same value as converting then adding) per token, with the
-// LDS reads of the next 32 tokens issued before the adds of the current
-// ones. Waves 1-3 stream 512-token chunks of k[h, :, d0:d0+64] (8 rows x 128
-// bytes per load instruction), transpose 4 tokens x 8 dims in registers and
-// store them to LDS as [d][s] with 8-byte writes. The 16-byte token chunk c
-// of row d sits at c ^ (2 * (d >> 4)) in a 260-dword row: conflict-free for
-// both the 8-byte writes (32 lanes per pass) and the 16-byte reads of the
-// summing wave (16 lanes per pass). Chunks are double-buffered in LDS, and
-// the loads run one chunk ahead of the LDS writes.
-constexpr int KM_CHUNK = 512;                 // tokens per chunk
-constexpr int KM_PITCH = KM_CHUNK / 2 + 4;    // dwords per LDS row
-constexpr int KM_ROUNDS = KM_CHUNK / 32;      // loader rounds of 8 token quads x 8 dim groups
-constexpr int KM_MAXR = (KM_ROUNDS + 2) / 3;  // rounds per loader wave (at most)
+// chain: a 256-thread workgroup owns KM_DIMS (h,d) chains (one head, 32
+// dims), so that BH * D / 32 workgroups stream K from HBM together (the
+// chain, 4352 dependent adds at S = 4352, is the same length whatever the
+// slice width; a narrow slice spreads the loads over more CUs, and 32 dims
+// measured faster than 16, whose loads touch 32 rows for 32 bytes each,
+// and than 64). Wave 0 only
+// sums, one chain per lane (lanes past KM_DIMS repeat a chain and store
+// nothing), one fp32 add per token (the fp16 -> fp32 conversions stay off
+// the dependent chain), with the LDS reads of each group of 32 tokens
+// issued two groups ahead. Waves 1-3
+// stream KM_CHUNK-token chunks of k[h, :, d0:d0+32] (each lane 16 bytes =
+// 8 dims of 4 consecutive tokens), transpose 4 tokens x 8 dims in registers
+// and store them to LDS as [d][s] with 8-byte writes; rows are padded to a
+// pitch of 4 banks mod 64. Chunks are double-buffered in LDS,
+// and the loads run one chunk ahead of the LDS writes.
+constexpr int KM_DIMS = 32;                        // chains per workgroup
+constexpr int KM_G = KM_DIMS / 8;                  // 16-byte dim groups per token row
+constexpr int KM_CHUNK = 1024;                     // tokens per chunk
+constexpr int KM_PITCH = KM_CHUNK / 2 + 4;         // dwords per LDS row
+constexpr int KM_QPR = 64 / KM_G;                  // token quads per loader round
+constexpr int KM_ROUNDS = KM_CHUNK / 4 / KM_QPR;   // loader rounds per chunk
+constexpr int KM_MAXR = (KM_ROUNDS + 2) / 3;       // rounds per loader wave (at most)
 
-__device__ __forceinline__ int km_swz(int d) { return 2 * ((d >> 4) & 3); }
-
+// acc + (fp16 token in the low / high half of v): the fp16 -> fp32
+// conversion is exact, so the sum is rounded once per token, as the
+// reference's float add of the converted value.
 __device__ __forceinline__ float km_add_lo(float acc, uint32_t v) {
-    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(v));
-    return acc;
+    return acc + f16_to_f32(static_cast<uint16_t>(v & 0xffffu));
 }
 __device__ __forceinline__ float km_add_hi(float acc, uint32_t v) {
-    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(v));
-    return acc;
+    return acc + f16_to_f32(static_cast<uint16_t>(v >> 16));
 }
 
 __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean,
                                                      int S, int D) {
-    __shared__ __attribute__((aligned(16))) uint32_t tile[2][64 * KM_PITCH];
-    const int slices = D / 64;
+    __shared__ __attribute__((aligned(16))) uint32_t tile[2][KM_DIMS * KM_PITCH];
+    const int slices = D / KM_DIMS;
     const int h = blockIdx.x / slices;
-    const int d0 = (blockIdx.x % slices) * 64;
+    const int d0 = (blockIdx.x % slices) * KM_DIMS;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const uint16_t* src = k + static_cast<int64_t>(h) * S * D + d0;
     const int nchunk = div_up(S, KM_CHUNK);
 
-    // loader lane: dim group g = lane & 7, token quad 8 * round + (lane >> 3).
-    // issue() starts the loads of a chunk into registers, commit() writes
-    // them transposed to an LDS buffer; chunk c+2 is issued right after
-    // chunk c+1 is committed, so its memory latency overlaps a whole chunk
-    // of the sum.
-    const int g = lane & 7;
-    u32x4 v[KM_MAXR][4];
-    auto issue = [&](int c) {
+    // loader lane: dim group g = lane % KM_G, token quad KM_QPR * round +
+    // lane / KM_G. issue() starts the loads of a chunk into registers,
+    // commit() writes them transposed to an LDS buffer; chunk c+2 is issued
+    // right after chunk c+1 is committed, so its memory latency overlaps a
+    // whole chunk of the sum. (A second register set, two chunks in flight,
+    // measured slower: the compiler's in-order vmcnt waits drain both.)
+    const int g = lane % KM_G;
+    u32x4 v[1][KM_MAXR][4];
+    auto issue = [&](int c, int set) {
 #pragma unroll
         for (int r = 0; r < KM_MAXR; ++r) {
             const int round = (wave - 1) + 3 * r;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int s = c * KM_CHUNK + 4 * (8 * round + (lane >> 3)) + i;
-                v[r][i] = (u32x4){0u, 0u, 0u, 0u};
+                const int s = c * KM_CHUNK + 4 * (KM_QPR * round + lane / KM_G) + i;
+                v[set][r][i] = (u32x4){0u, 0u, 0u, 0u};
                 if (round < KM_ROUNDS && s < S)
-                    v[r][i] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(s) * D + 8 * g);
+                    v[set][r][i] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(s) * D + 8 * g);
             }
         }
     };
-    auto commit = [&](int buf) {
+    auto commit = [&](int buf, int set) {
 #pragma unroll
         for (int r = 0; r < KM_MAXR; ++r) {
             const int round = (wave - 1) + 3 * r;
             if (round >= KM_ROUNDS) continue;
-            const int tq = 8 * round + (lane >> 3);
+            const int tq = KM_QPR * round + lane / KM_G;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 // dim 8g + e of tokens 4tq .. 4tq+3: fp16 e of each 16-byte row piece
                 const int w = e >> 1;
                 const int sh = (e & 1) * 16;
-                const uint32_t t0 = (v[r][0][w] >> sh) & 0xffffu, t1 = (v[r][1][w] >> sh) & 0xffffu;
-                const uint32_t t2 = (v[r][2][w] >> sh) & 0xffffu, t3 = (v[r][3][w] >> sh) & 0xffffu;
+                const uint32_t t0 = (v[set][r][0][w] >> sh) & 0xffffu, t1 = (v[set][r][1][w] >> sh) & 0xffffu;
+                const uint32_t t2 = (v[set][r][2][w] >> sh) & 0xffffu, t3 = (v[set][r][3][w] >> sh) & 0xffffu;
                 const int d = 8 * g + e;
-                uint32_t* dst = &tile[buf][d * KM_PITCH + 4 * ((tq >> 1) ^ km_swz(d)) + 2 * (tq & 1)];
+                uint32_t* dst = &tile[buf][d * KM_PITCH + 2 * tq];
                 *reinterpret_cast<uint2*>(dst) = make_uint2(t0 | (t1 << 16), t2 | (t3 << 16));
             }
         }
@@ -131,33 +138,27 @@ __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict_
 
     float sum = 0.0f;
     if (wave > 0) {
-        issue(0);
-        commit(0);
-        if (nchunk > 1) issue(1);
+        issue(0, 0);
+        commit(0, 0);
+        if (nchunk > 1) issue(1, 0);
     }
     __syncthreads();
     for (int c = 0; c < nchunk; ++c) {
         const int buf = c & 1;
         if (wave > 0) {
             if (c + 1 < nchunk) {
-                commit(buf ^ 1);                 // chunk c+1, issued one chunk ago
-                if (c + 2 < nchunk) issue(c + 2);
+                commit(buf ^ 1, 0);              // chunk c+1, issued one chunk ago
+                if (c + 2 < nchunk) issue(c + 2, 0);
             }
         } else {
             const int n = min(KM_CHUNK, S - c * KM_CHUNK);
-            const uint32_t* row = &tile[buf][lane * KM_PITCH];
-            const int sw = km_swz(lane);
-            auto rd = [&](int t8) { return *reinterpret_cast<const u32x4*>(row + 4 * (t8 ^ sw)); };
-            const int full = n >> 5;  // groups of 32 tokens
-            u32x4 cur[4], nxt[4];
-            if (full > 0) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) cur[r] = rd(r);
-            }
-            for (int gi = 0; gi < full; ++gi) {
-                const bool more = gi + 1 < full;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) nxt[r] = more ? rd(4 * (gi + 1) + r) : cur[r];
+            const uint32_t* row = &tile[buf][(lane % KM_DIMS) * KM_PITCH];
+            auto rd = [&](int t8) { return *reinterpret_cast<const u32x4*>(row + 4 * t8); };
+            // groups of 32 tokens, read two groups ahead in two register
+            // sets; a read past the chunk's last full group re-reads group
+            // 0 (in bounds, unused)
+            const int full = n >> 5;
+            auto group = [&](int gi, u32x4 (&cur)[4]) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -165,17 +166,30 @@ __global__ __launch_bounds__(256) void k_mean_kernel(const uint16_t* __restrict_
                         sum = km_add_lo(sum, cur[r][e]);
                         sum = km_add_hi(sum, cur[r][e]);
                     }
+                const int nx = gi + 2 < full ? gi + 2 : 0;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) cur[r] = nxt[r];
+                for (int r = 0; r < 4; ++r) cur[r] = rd(4 * nx + r);
+            };
+            u32x4 ga[4], gb[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                ga[r] = rd(r);
+                gb[r] = rd(4 + r);
             }
+            int gi = 0;
+            for (; gi + 1 < full; gi += 2) {
+                group(gi, ga);
+                group(gi + 1, gb);
+            }
+            if (gi < full) group(gi, ga);
             for (int t = full << 5; t < n; ++t) {
-                const uint32_t wv = row[4 * ((t >> 3) ^ sw) + ((t & 7) >> 1)];
+                const uint32_t wv = row[t >> 1];
                 sum = (t & 1) ? km_add_hi(sum, wv) : km_add_lo(sum, wv);
             }
         }
         __syncthreads();
     }
-    if (tid < 64) mean[static_cast<int64_t>(h) * D + d0 + tid] = sum / fmaxf(static_cast<float>(S), 1.0f);
+    if (tid < KM_DIMS) mean[static_cast<int64_t>(h) * D + d0 + tid] = sum / fmaxf(static_cast<float>(S), 1.0f);
 }
 
 // ---------------------------------------------------------------- Q quant
@@ -974,7 +988,7 @@ int64_t sage_scratch_layout(int BH, int S, int D, void* base, SageScratch* out) 
 
 hipError_t launch_sage_k_mean(const uint16_t* k, float* mean, int BH, int S, int D,
                               hipStream_t stream) {
-    hipLaunchKernelGGL(k_mean_kernel, dim3(BH * (D / 64)), dim3(256), 0, stream, k, mean, S, D);
+    hipLaunchKernelGGL(k_mean_kernel, dim3(BH * (D / KM_DIMS)), dim3(256), 0, stream, k, mean, S, D);
     return hipGetLastError();
 }
 
