@@ -361,8 +361,19 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
             issue_stage(kt + 2, slot);
             read_frags(fa0, fw0, slot ^ 1, 0);
             mfma_all(fa1, fw1);
-            SGB(SG_VMEM, 2 * NDMA);
-            interleave();
+            // the refill DMAs spread over the first MFMAs (measured 2-5%
+            // faster than issuing them all before the first MFMA)
+#pragma unroll
+            for (int i = 0; i < TM + TN; ++i) {
+                SGB(SG_MFMA, 1);
+                SGB(SG_VMEM, 1);
+                SGB(SG_DS_READ, 2);
+            }
+            SGB(SG_MFMA, 1);
+            SGB(SG_VMEM, 1);
+            SGB(SG_MFMA, 1);
+            SGB(SG_VMEM, 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 

@@ -80,7 +80,7 @@ def test_sage_attention_vs_oracle(qimg, oracle, BH, S, D, causal):
     assert cos >= 0.99999, cos
     exact = _attn64(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), scale, causal)
     rel, cos = _metrics(got, exact)
-    assert cos >= 0.999, (rel, cos)
+    assert rel <= 2e-2 and cos >= 0.999, (rel, cos)
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
