@@ -239,6 +239,75 @@ __global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
     fwht_quant_tail<OUT>(lds, red, K, hbs_log2, norm, lo, amax, out, scales, row);
 }
 
+// Rows of NB Hadamard blocks of 4096 values (e.g. the fc2 input, K = 12288
+// = 3 x 4096), 256 threads. The blocks go through one block-sized LDS
+// buffer in turn (17 KB instead of the whole row's 52 KB, so twice as many
+// rows are in flight per CU). Per block: thread t transforms its chunk t
+// (16 consecutive values, stages 1-8) in registers straight from the load,
+// one LDS sweep does stages 16-128, and the last sweep (stages 256-2048)
+// leaves thread t holding values t + 256 i, i < 16, in registers until the
+// row's absmax is known; the quantized bytes are stored from there (each
+// store instruction writes 64 consecutive bytes per wave). Each value sees
+// the same butterfly stages in the same order as in fwht_quant_rows_kernel.
+template <typename InT, RowOut OUT, int NB>
+__global__ __launch_bounds__(256) void fwht_quant_blocks_kernel(const InT* x, void* out, float* __restrict__ scales,
+                                                                int M, int K, float norm) {
+    constexpr int HBS = 4096;
+    extern __shared__ float lds[];
+    float* red = lds + lds_pad(HBS) + 1;
+    const int row = blockIdx.x;
+    if (row >= M) return;
+    const InT* xin = x + static_cast<int64_t>(row) * K;
+    const int tid = threadIdx.x;
+
+    float v[NB][16];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load16<InT>(xin + b * HBS + 16 * tid, v[b]);
+    float amax = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        butterfly<4>(v[b]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lds[lds_pad(16 * tid + i)] = v[b][i];
+        __syncthreads();
+        lds_pass<4>(lds, HBS, 4, false, norm, amax);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[b][i] = lds[lds_pad(tid + (i << 8))];
+        butterfly<4>(v[b]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            v[b][i] = v[b][i] * norm;
+            amax = fmaxf(amax, fabsf(v[b][i]));
+        }
+        __syncthreads();  // the next block's chunks overwrite the buffer
+    }
+
+    amax = wave_max_dpp(amax);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    constexpr float QMAX = (OUT == RowOut::Int8) ? 127.0f : 448.0f;
+    if (tid == 0) scales[row] = amax / QMAX;
+    const float inv = (amax > 0.0f) ? QMAX / amax : 0.0f;
+    uint8_t* o = reinterpret_cast<uint8_t*>(out) + static_cast<int64_t>(row) * K + tid;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            // four values 256 apart converted together, stored byte by byte
+            const float q0 = v[b][i] * inv, q1 = v[b][i + 1] * inv;
+            const float q2 = v[b][i + 2] * inv, q3 = v[b][i + 3] * inv;
+            uint32_t w;
+            if constexpr (OUT == RowOut::Int8)
+                w = i8x4_rne_sat(q0, q1, q2, q3);
+            else
+                w = e4m3x4(q0, q1, q2, q3);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[b * HBS + ((i + c) << 8)] = static_cast<uint8_t>(w >> (8 * c));
+        }
+}
+
 // LayerNorm + modulate (ln_modulate_row) feeding the FWHT + row quant of
 // the next linear's input in one pass: the normalized row goes to LDS
 // instead of HBM. One LN_THR-thread workgroup per row, K <= LN_MAX_DIM.
@@ -350,6 +419,19 @@ template <typename InT, RowOut OUT>
 static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int K, int hbs,
                               hipStream_t stream) {
     if (M == 0) return hipSuccess;
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    if constexpr (OUT != RowOut::Fp32) {
+        // rows of 2-4 Hadamard blocks of 4096 values: block by block
+        const int nb = K / 4096;
+        if (hbs == 4096 && nb >= 2 && nb <= 4 && nb * 4096 == K) {
+            const size_t lds = sizeof(float) * (4096 + 4096 / 16 + 1 + 8);
+            auto kern = nb == 2 ? fwht_quant_blocks_kernel<InT, OUT, 2>
+                      : nb == 3 ? fwht_quant_blocks_kernel<InT, OUT, 3>
+                                : fwht_quant_blocks_kernel<InT, OUT, 4>;
+            hipLaunchKernelGGL(kern, dim3(M), dim3(256), lds, stream, x, out, scales, M, K, norm);
+            return hipGetLastError();
+        }
+    }
     int chunks = (K + 15) / 16;
     int threads = ((chunks + kWave - 1) / kWave) * kWave;
     threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
@@ -361,7 +443,6 @@ static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int
                                            static_cast<int>(lds));
         if (e != hipSuccess) return e;
     }
-    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
     hipLaunchKernelGGL(kern, dim3(M), dim3(threads), lds, stream, x, out, scales, M, K, ilog2(hbs),
                        norm);
     return hipGetLastError();

@@ -41,6 +41,33 @@ def test_activation_quant_int8_bit_exact(qimg, oracle, M, K, in_bf16):
     np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
 
 
+@pytest.mark.parametrize("M,K,in_bf16,fp8", [
+    (300, 12288, False, False),   # fc2 input: three 4096-blocks
+    (37, 12288, True, True),
+    (6, 8192, False, False),      # hbs 4096 given explicitly: two blocks
+    (3, 16384, True, False),      # four blocks
+    (5, 16384, False, True),
+])
+def test_activation_quant_4096_blocks_bit_exact(qimg, oracle, M, K, in_bf16, fp8):
+    """Rows of 2-4 Hadamard blocks of 4096 (the block-by-block kernel)."""
+    rng = np.random.default_rng(M * 7 + K + fp8)
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
+    x[0, :] = 0.0  # an all-zero row: scale 0, all-zero values
+    mode = qimg.FP8_HADAMARD if fp8 else qimg.INT8_HADAMARD
+    ref = oracle.quantize_activation_fp8 if fp8 else oracle.quantize_activation
+    if in_bf16:
+        bits = oracle.bf16_bits_from_f32(x)
+        q_ref, s_ref = ref(bits, 4096)
+        xd = _bf16_dev(bits)
+    else:
+        q_ref, s_ref = ref(x, 4096)
+        xd = torch.from_numpy(x).to(DEV)
+    q, s = qimg.quantize_activation_hadamard(xd, 4096, mode=mode)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
+
+
 @pytest.mark.parametrize("M,K", [(128, 3072), (16, 12288), (3, 64)])
 def test_activation_quant_fp8_bit_exact(qimg, oracle, M, K):
     rng = np.random.default_rng(K + 7)
