@@ -339,6 +339,118 @@ int qimg_mmdit_blocks_forward(const qimg_mmdit_block* blocks, int n_blocks, floa
                               const float* t_emb, const float* pe, int n_img, int n_txt, int batch, void* scratch,
                               int64_t scratch_bytes, float* prof_ms, void* stream);
 
+/* ---- INT4 paths (cuda_kernels.cu:2864-4532) ----------------------------
+ * Packed INT4 tensors hold two columns per byte, the even column in the
+ * low nibble. Nibbles are NF4 codes, offset-8 linear values (value = n - 8)
+ * or two's complement values, as each entry point states. The arithmetic of
+ * every entry point follows the reference's source order; as for the INT8
+ * path, its --use_fast_math approximations are not reproduced. */
+
+/* dequantize_int4_to_bf16 (cuda_kernels.cu:2876-2929): qweight [N, K/2] ->
+ * bf16 [N, K]; NF4_GRID[n]*s (nf4_grid), (signed n)*s (signed_int4) or
+ * (n-8)*s; scales fp32 [N, K/group_size] or, with scales_gn, [K/group_size, N].
+ * K % 8 == 0, K % group_size == 0. */
+int qimg_dequantize_int4_bf16(const uint8_t* qweight, const float* scales, uint16_t* out, int N, int K,
+                              int group_size, int nf4_grid, int scales_gn, int signed_int4, void* stream);
+
+/* quantize_int4_per_group (NF4, cuda_kernels.cu:3290-3368) or, with
+ * nf4_grid = 0, the linear quantizer (quantize_linear_int4_per_group_kernel,
+ * :3226-3288: scale = amax/7, q = clamp(roundf(v*7/amax), -7, 7) + 8).
+ * residual fp32 [N, K] -> qweight [N, K/2], scales fp32 [N, K/group_size]. */
+int qimg_quantize_int4_per_group(const float* residual, uint8_t* qweight, float* scales, int N, int K,
+                                 int group_size, int nf4_grid, void* stream);
+
+/* quantize_activation_int4 (cuda_kernels.cu:3575-3648): x fp32 [M, K] ->
+ * two's complement nibbles act_packed [M, K/2], act_scales fp32
+ * [K/group_size, M] (scale amax/7). group_size 32, 64 or 128. */
+int qimg_quantize_activation_int4(const float* x, uint8_t* act_packed, float* act_scales, int M, int K,
+                                  int group_size, void* stream);
+
+/* fused_smooth_bf16_quant (cuda_kernels.cu:3650-3730): v = x / smooth[k]
+ * (smooth may be NULL), bf16_out = bf16(v) [M, K], then
+ * qimg_quantize_activation_int4 of v. */
+int qimg_fused_smooth_bf16_quant(const float* x, const float* smooth, uint16_t* bf16_out, uint8_t* act_packed,
+                                 float* act_scales, int M, int K, int group_size, void* stream);
+
+/* w4a4_gemm (cuda_kernels.cu:4257-4313; kernels :3732-3854, :4117-4255):
+ * out[m,n] = sum over groups g in order of ((float)d_g[m,n] * act_scales[g,m])
+ * * wgt_scales[g,n] (d_g the exact int32 dot product of the group's signed
+ * nibbles), plus bias[n] (bf16, or NULL); accumulate != 0 adds the result to
+ * out. act_packed [M, K/2] and wgt_packed [N, K/2] two's complement nibbles,
+ * act_scales [G, M], wgt_scales [G, N] fp32, group_size % 64 == 0. The
+ * reference's register-direct kernel reads an mma.sync fragment order; this
+ * entry point reads the row-major packing (qweight_rowmajor). */
+int qimg_w4a4_gemm(const uint8_t* act_packed, const uint8_t* wgt_packed, const float* act_scales,
+                   const float* wgt_scales, float* out, int M, int N, int K, int group_size, int accumulate,
+                   const uint16_t* bias_bf16, void* stream);
+
+/* One INT4 linear layer: QuantizedWeight's INT4_SVD fields
+ * (cuda_kernels.cuh:194-213). The residual is W4A4 when w4a4_qweight is set
+ * (two's complement nibbles [N, K/2], w4a4_wscales fp32 [K/group_size, N]: the
+ * unswizzled nunchaku form), otherwise W4A16 over qweight [N, K/2] (NF4 or
+ * offset-8 codes, nf4_grid) and scales4 fp32 [N, K/group_size]. svd_up bf16
+ * [N, rank] and svd_down bf16 [K, rank] are the low-rank factors; smooth fp32
+ * [K] is optional; had_block_size > 1 rotates x before the W4A16 residual. */
+typedef struct qimg_int4_weight {
+    int N, K, rank, group_size;
+    int nf4_grid, had_block_size;
+    const uint8_t* qweight;
+    const float* scales4;
+    const uint8_t* w4a4_qweight;
+    const float* w4a4_wscales;
+    const uint16_t* svd_up;
+    const uint16_t* svd_down;
+    const float* smooth;
+} qimg_int4_weight;
+
+/* int4_scratch_bytes (cuda_kernels.cuh:475-487), or more where this
+ * library's layout needs it (rank > K/2). */
+int64_t qimg_int4_scratch_bytes(int M, int K, int N, int svd_rank);
+
+/* linear_forward_int4 (cuda_kernels.cu:4332-4532): x fp32 [M, K] ->
+ * out fp32 [M, N] = x_lr . svd_down . svd_up^T (x_lr = bf16 of x or of
+ * x / smooth; the low-rank product rounded to bf16) + the residual (W4A16:
+ * bf16 of the smoothed, rotated x times the dequantized weight; W4A4:
+ * qimg_w4a4_gemm of the INT4-quantized smoothed x) + bias, then GELU-tanh
+ * if gelu. scratch >= qimg_int4_scratch_bytes(M, K, N, rank). */
+int qimg_linear_int4(const float* x, int M, const qimg_int4_weight* w, const uint16_t* bias_bf16, float* out,
+                     int gelu, void* scratch, int64_t scratch_bytes, void* stream);
+
+/* repack_awq_to_transposed (cuda_kernels.cu:3059-3102): AWQ kInterleave=4
+ * qweight int32 [OC/4, IC/2] -> [IC/8, OC], word (i, oc) holding the nibbles
+ * of inputs 8i .. 8i+7, low first. */
+int qimg_awq_repack(const int32_t* qweight_awq, int32_t* qweight_out, int OC, int IC, void* stream);
+
+/* dequantize_awq_to_bf16 (cuda_kernels.cu:3002-3057): bf16 [OC, IC] in the
+ * de-interleaved channel order, q * wscales + wzeros (bf16 [IC/group_size, OC]). */
+int qimg_dequantize_awq_bf16(const int32_t* qweight_awq, const uint16_t* wscales, const uint16_t* wzeros,
+                             uint16_t* out, int OC, int IC, int group_size, int num_components, void* stream);
+
+/* linear_forward_awq (cuda_kernels.cu:3155-3179, awq_gemv_repacked_kernel
+ * :3106-3153): M = 1, x fp32 [IC], qweight from qimg_awq_repack, group_size
+ * 64; out fp32 [OC] in the de-interleaved order, + bias (bf16, de-interleaved
+ * order) if given. Each output is the sum over ic in order. */
+int qimg_linear_awq(const float* x, const int32_t* qweight_repacked, const uint16_t* wscales,
+                    const uint16_t* wzeros, const uint16_t* bias_bf16, float* out, int OC, int IC, int group_size,
+                    int num_components, void* stream);
+
+/* unswizzle_nunchaku_weights (cuda_kernels.cu:3431-3499): nunchaku's
+ * MMA-swizzled qweight [N, K/2] and bf16 wscales -> row-major nibbles
+ * [N, K/2] and fp32 scales [num_groups, N]. N % 128 == 0, K % 64 == 0. */
+int qimg_unswizzle_nunchaku_weights(const uint8_t* qweight_swizzled, const uint16_t* wscales_swizzled,
+                                    uint8_t* qweight_rowmajor, float* wscales_rowmajor, int N, int K,
+                                    int num_groups, void* stream);
+
+/* dequantize_nunchaku_to_bf16 (cuda_kernels.cu:2932-2998). */
+int qimg_dequantize_nunchaku_bf16(const uint8_t* qweight_swizzled, const uint16_t* wscales_swizzled,
+                                  uint16_t* out, int N, int K, int num_groups, void* stream);
+
+/* unswizzle_lora_weights (cuda_kernels.cu:3503-3572): nunchaku's packed
+ * low-rank factor -> row-major bf16 [rows, cols] (is_down: the [K, rank]
+ * down factor). rows % 16 == 0, cols % 16 == 0. */
+int qimg_unswizzle_lora_weights(const uint16_t* packed, uint16_t* out, int rows, int cols, int is_down,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,17 @@ _SIGS = {
     "or_sage_quant_k": (None, [_P, _P, _I, _I, _I, _P, _P]),
     "or_sage_attn": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _F, _I, _I, _I, _P]),
     "or_sage_attention_fp16io": (None, [_P, _P, _P, _I, _I, _I, _F, _I, _P]),
+    "or_dequant_int4_bf16": (None, [_P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "or_quant_int4_linear": (None, [_P, _I, _I, _I, _P, _P]),
+    "or_quant_int4_nf4": (None, [_P, _I, _I, _I, _P, _P]),
+    "or_quant_act_int4": (None, [_P, _P, _I, _I, _I, _P, _P, _P]),
+    "or_w4a4_gemm": (None, [_P, _P, _P, _P, _I64, _I, _I, _I, _I, _P, _I64, _I64, _P]),
+    "or_awq_repack": (None, [_P, _I, _I, _P]),
+    "or_dequant_awq_bf16": (None, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "or_awq_gemv": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "or_unswizzle_nunchaku": (None, [_P, _P, _I, _I, _I, _P, _P]),
+    "or_dequant_nunchaku_bf16": (None, [_P, _P, _I, _I, _I, _P]),
+    "or_unswizzle_lora": (None, [_P, _I, _I, _I, _P]),
     "or_set_threads": (None, [_I]),
     "or_get_threads": (_I, []),
 }
@@ -313,4 +324,114 @@ def sage_attention_fp16io(q, k, v, sm_scale, causal=False) -> np.ndarray:
     out = np.empty((BH, S, D), np.float16)
     lib().or_sage_attention_fp16io(_ptr(q), _ptr(k), _ptr(v), BH, S, D, float(sm_scale),
                                    int(bool(causal)), _ptr(out))
+    return out
+
+
+# ---- INT4 paths (cuda_kernels.cu:2864-4532; arithmetic in qimg_oracle_int4.c) ----
+
+NF4_GRID = np.array([-1.0, -0.6962, -0.5251, -0.3949, -0.2844, -0.1848, -0.0911, 0.0,
+                     0.0796, 0.1609, 0.2461, 0.3379, 0.4407, 0.5626, 0.7230, 1.0], np.float32)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def dequant_int4_bf16(qw, scales, K, group_size, nf4=True, scales_gn=False, signed_int4=False):
+    """dequantize_int4_to_bf16 (cuda_kernels.cu:2876-2929): bf16 bits [N, K]."""
+    qw = _c(qw, np.uint8); scales = _c(scales, np.float32)
+    N = qw.shape[0]
+    out = np.empty((N, K), np.uint16)
+    lib().or_dequant_int4_bf16(_ptr(qw), _ptr(scales), N, K, group_size, int(nf4), int(scales_gn),
+                               int(signed_int4), _ptr(out))
+    return out
+
+
+def quant_int4_weight(r, group_size, nf4=True):
+    """quantize_int4_per_group (NF4, cuda_kernels.cu:3290-3368) or the linear
+    INT4 quantizer (:3226-3288): packed [N, K/2], scales [N, K/gs]."""
+    r = _c(r, np.float32)
+    N, K = r.shape
+    qw = np.empty((N, K // 2), np.uint8)
+    sc = np.empty((N, K // group_size), np.float32)
+    (lib().or_quant_int4_nf4 if nf4 else lib().or_quant_int4_linear)(_ptr(r), N, K, group_size, _ptr(qw), _ptr(sc))
+    return qw, sc
+
+
+def quant_act_int4(x, group_size, smooth=None, want_bf16=False):
+    """quantize_activation_int4 (cuda_kernels.cu:3575-3648), or with smooth /
+    bf16 copy fused_smooth_bf16_quant (:3650-3730): packed [M, K/2], scales
+    [G, M] (and bf16 bits [M, K])."""
+    x = _c(x, np.float32)
+    M, K = x.shape
+    pk = np.empty((M, K // 2), np.uint8)
+    sc = np.empty((K // group_size, M), np.float32)
+    bf = np.empty((M, K), np.uint16) if want_bf16 else None
+    sm = None if smooth is None else _c(smooth, np.float32)
+    lib().or_quant_act_int4(_ptr(x), None if sm is None else _ptr(sm), M, K, group_size,
+                            None if bf is None else _ptr(bf), _ptr(pk), _ptr(sc))
+    return (pk, sc, bf) if want_bf16 else (pk, sc)
+
+
+def w4a4_gemm(act, wgt, a_scales, w_scales, K, group_size, bias_bits=None, out=None, rows=None):
+    """w4a4_gemm (cuda_kernels.cu:4257-4313, kernels :3732-3854 / :4117-4255).
+    out (fp32 [M, N] or the given rows) is accumulated into when given."""
+    act = _c(act, np.uint8); wgt = _c(wgt, np.uint8)
+    a_scales = _c(a_scales, np.float32); w_scales = _c(w_scales, np.float32)
+    M, N = act.shape[0], wgt.shape[0]
+    m0, m1 = rows if rows is not None else (0, M)
+    acc = out is not None
+    o = _c(out, np.float32).copy() if acc else np.empty((m1 - m0, N), np.float32)
+    b = None if bias_bits is None else _c(bias_bits, np.uint16)
+    lib().or_w4a4_gemm(_ptr(act), _ptr(wgt), _ptr(a_scales), _ptr(w_scales), M, N, K, group_size, int(acc),
+                       None if b is None else _ptr(b), m0, m1, _ptr(o))
+    return o
+
+
+def awq_repack(qw, OC, IC):
+    """repack_awq_to_transposed (cuda_kernels.cu:3059-3102): [IC/8, OC] int32."""
+    qw = _c(qw, np.int32)
+    out = np.empty((IC // 8, OC), np.int32)
+    lib().or_awq_repack(_ptr(qw), OC, IC, _ptr(out))
+    return out
+
+
+def dequant_awq_bf16(qw, wscales_bits, wzeros_bits, OC, IC, group_size, ncomp):
+    """dequantize_awq_to_bf16 (cuda_kernels.cu:3002-3057): bf16 bits [OC, IC]."""
+    out = np.empty((OC, IC), np.uint16)
+    lib().or_dequant_awq_bf16(_ptr(_c(qw, np.int32)), _ptr(_c(wscales_bits, np.uint16)),
+                              _ptr(_c(wzeros_bits, np.uint16)), OC, IC, group_size, ncomp, _ptr(out))
+    return out
+
+
+def awq_gemv(x, qw_rep, wscales_bits, wzeros_bits, OC, IC, group_size, ncomp, bias_bits=None):
+    """linear_forward_awq / awq_gemv_repacked_kernel (cuda_kernels.cu:3106-3179), x [IC]."""
+    out = np.empty(OC, np.float32)
+    b = None if bias_bits is None else _c(bias_bits, np.uint16)
+    lib().or_awq_gemv(_ptr(_c(x, np.float32)), _ptr(_c(qw_rep, np.int32)), _ptr(_c(wscales_bits, np.uint16)),
+                      _ptr(_c(wzeros_bits, np.uint16)), None if b is None else _ptr(b), OC, IC, group_size, ncomp,
+                      _ptr(out))
+    return out
+
+
+def unswizzle_nunchaku(q_sw, s_sw_bits, N, K, G):
+    """unswizzle_nunchaku_weights (cuda_kernels.cu:3431-3499): row-major
+    packed [N, K/2] and fp32 scales [G, N]."""
+    q = np.empty((N, K // 2), np.uint8)
+    s = np.empty((G, N), np.float32)
+    lib().or_unswizzle_nunchaku(_ptr(_c(q_sw, np.uint8)), _ptr(_c(s_sw_bits, np.uint16)), N, K, G, _ptr(q), _ptr(s))
+    return q, s
+
+
+def dequant_nunchaku_bf16(q_sw, s_sw_bits, N, K, G):
+    """dequantize_nunchaku_to_bf16 (cuda_kernels.cu:2932-2998): bf16 bits [N, K]."""
+    out = np.empty((N, K), np.uint16)
+    lib().or_dequant_nunchaku_bf16(_ptr(_c(q_sw, np.uint8)), _ptr(_c(s_sw_bits, np.uint16)), N, K, G, _ptr(out))
+    return out
+
+
+def unswizzle_lora(packed_bits, rows, cols, is_down):
+    """unswizzle_lora_weights (cuda_kernels.cu:3503-3572): bf16 bits [rows, cols]."""
+    out = np.empty((rows, cols), np.uint16)
+    lib().or_unswizzle_lora(_ptr(_c(packed_bits, np.uint16)), rows, cols, int(is_down), _ptr(out))
     return out

@@ -114,6 +114,37 @@ void or_sage_attention_fp16io(const uint16_t* q, const uint16_t* k, const uint16
 void or_set_threads(int n);
 int  or_get_threads(void);
 
+/* ---- INT4 paths (cuda_kernels.cu:2864-4532; qimg_oracle_int4.c) ------ */
+extern const float OR_NF4_GRID[16];
+/* :2876-2917 packed nibbles [N,K/2] (even column low) -> bf16 [N,K]:
+ * NF4_GRID[n]*s, (signed n)*s or (n-8)*s; scales [N,G] or [G,N]. */
+void or_dequant_int4_bf16(const uint8_t* qw, const float* scales, int N, int K, int gs, int nf4,
+                          int scales_gn, int signed_int4, uint16_t* out);
+/* :3226-3288 linear INT4 weight quantizer (offset 8, [-7,7]). */
+void or_quant_int4_linear(const float* r, int N, int K, int gs, uint8_t* qw, float* scales);
+/* :3290-3357 NF4 weight quantizer (nearest grid code, first on ties). */
+void or_quant_int4_nf4(const float* r, int N, int K, int gs, uint8_t* qw, float* scales);
+/* :3575-3636 / :3650-3705 activation INT4 quant, optional smooth divide and
+ * bf16 copy; scales [G, M]. */
+void or_quant_act_int4(const float* x, const float* smooth, int M, int K, int gs, uint16_t* bf16_out,
+                       uint8_t* packed, float* scales);
+/* :3732-3854, :4117-4255 W4A4 GEMM, rows [m0, m1) into out[(m1-m0), N]. */
+void or_w4a4_gemm(const uint8_t* act, const uint8_t* wgt, const float* as, const float* ws, int64_t M,
+                  int N, int K, int gs, int accumulate, const uint16_t* bias, int64_t m0, int64_t m1,
+                  float* out);
+/* :3059-3091 AWQ repack, :3002-3038 AWQ dequant, :3106-3153 AWQ GEMV. */
+void or_awq_repack(const int32_t* qw, int OC, int IC, int32_t* out);
+void or_dequant_awq_bf16(const int32_t* qw, const uint16_t* wscales, const uint16_t* wzeros, int OC, int IC,
+                         int gs, int ncomp, uint16_t* out);
+void or_awq_gemv(const float* x, const int32_t* qw_rep, const uint16_t* wscales, const uint16_t* wzeros,
+                 const uint16_t* bias, int OC, int IC, int gs, int ncomp, float* out);
+/* :3431-3487 nunchaku weight unswizzle, :2932-2978 nunchaku dequant,
+ * :3503-3562 LoRA unswizzle. */
+void or_unswizzle_nunchaku(const uint8_t* q_sw, const uint16_t* s_sw, int N, int K, int G, uint8_t* q_rm,
+                           float* s_rm);
+void or_dequant_nunchaku_bf16(const uint8_t* q_sw, const uint16_t* s_sw, int N, int K, int G, uint16_t* out);
+void or_unswizzle_lora(const uint16_t* packed, int rows, int cols, int is_down, uint16_t* out);
+
 #ifdef __cplusplus
 }
 #endif

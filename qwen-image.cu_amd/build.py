@@ -43,7 +43,7 @@ HIP_FLAGS = [
 ]
 
 SOURCES = ["hadamard_quant.hip", "gemm_w8a8.hip", "gemm_small_m.hip", "gemm_bf16.hip", "sage_attention.hip", "block_ops.hip",
-           "mmdit_block.hip", "capi.hip", "linear_noalloc.hip"]
+           "mmdit_block.hip", "capi.hip", "linear_noalloc.hip", "int4.hip", "capi_int4.hip"]
 HOST_SOURCES = ["kernels.cpp", "checkpoint.cpp"]
 
 

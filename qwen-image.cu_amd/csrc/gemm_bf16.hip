@@ -8,6 +8,9 @@
 // (cuda_kernels.cu:4534-4596: fp32_to_bf16, cublasGemmEx bf16 x bf16 -> fp32,
 // bias_add_fp32, gelu_fp32) with one kernel: the fp32 -> bf16 rounding
 // happens on the operand registers and the bias / GELU on the accumulators.
+// With `accumulate`, the product is added to the fp32 values already in out
+// before the bias (the INT4 linear's residual GEMM onto its low-rank term,
+// cublasGemmEx with beta = 1, cuda_kernels.cu:4488-4497).
 //
 // Shapes (M = tokens): img_in 3072 x 64, txt_in 3072 x 3584, norm_out
 // 6144 x 3072 at M = 1 (or 2), proj_out 64 x 3072. They are bound by reading
@@ -62,7 +65,7 @@ template <bool XF32, int TMW, int TNW, int DEPTH, bool GELU>
 __global__ __launch_bounds__(BF_THR) void gemm_bf16_kernel(const void* __restrict__ X,
                                                            const uint16_t* __restrict__ Wt,
                                                            const uint16_t* __restrict__ bias,
-                                                           float* __restrict__ out, int M, int N, int K) {
+                                                           float* out, int M, int N, int K, int accumulate) {
     constexpr int MB = 32 * TMW;
     constexpr int NB = 32 * TNW;
     constexpr int NBLK = TMW * TNW;
@@ -214,15 +217,27 @@ __global__ __launch_bounds__(BF_THR) void gemm_bf16_kernel(const void* __restric
         v4f sum = red[(blk * 4 + g) * 64 + ln];
 #pragma unroll
         for (int w = 1; w < NW; ++w) sum += red[((w * NBLK + blk) * 4 + g) * 64 + ln];
+        float* o = out + static_cast<int64_t>(m) * N + nb;
+        float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (accumulate) {
+            if (vec_ok) {
+                const v4f p4 = *reinterpret_cast<const v4f*>(o);
+                prev[0] = p4[0]; prev[1] = p4[1]; prev[2] = p4[2]; prev[3] = p4[3];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (nb + c < N) prev[c] = o[c];
+            }
+        }
         float v[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float t = sum[c];
+            if (accumulate) t = t + prev[c];
             if (bias != nullptr) t = t + epi.b[q][c];
             if (GELU) t = gelu_tanh(t);
             v[c] = t;
         }
-        float* o = out + static_cast<int64_t>(m) * N + nb;
         if (vec_ok) {
             *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
         } else {
@@ -243,7 +258,7 @@ template <bool XF32, bool GELU>
 __global__ __launch_bounds__(BF_THR) void gemm_bf16_shortk_kernel(const void* __restrict__ X,
                                                                   const uint16_t* __restrict__ Wt,
                                                                   const uint16_t* __restrict__ bias,
-                                                                  float* __restrict__ out, int M, int N, int K) {
+                                                                  float* out, int M, int N, int K, int accumulate) {
     constexpr int XE = XF32 ? 4 : 2;
     const int tiles_m = (M + 63) / 64;
     const int tiles_n = (N + 63) / 64;
@@ -297,15 +312,22 @@ __global__ __launch_bounds__(BF_THR) void gemm_bf16_shortk_kernel(const void* __
     for (int g = 0; g < 4; ++g) {
         const int nb = n0 + 8 * g + 4 * h;
         if (nb >= N) continue;
+        float* o = out + static_cast<int64_t>(m) * N + nb;
+        float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (accumulate) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (nb + c < N) prev[c] = o[c];
+        }
         float v[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float t = acc[4 * g + c];
+            if (accumulate) t = t + prev[c];
             if (bias != nullptr) t = t + bv[4 * g + c];
             if (GELU) t = gelu_tanh(t);
             v[c] = t;
         }
-        float* o = out + static_cast<int64_t>(m) * N + nb;
         if ((N & 3) == 0) {
             *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
         } else {
@@ -323,8 +345,8 @@ template <bool XF32>
 __global__ __launch_bounds__(256) void gemm_bf16_simple_kernel(const void* __restrict__ X,
                                                                const uint16_t* __restrict__ Wt,
                                                                const uint16_t* __restrict__ bias,
-                                                               float* __restrict__ out, int M, int N, int K,
-                                                               int gelu) {
+                                                               float* out, int M, int N, int K, int gelu,
+                                                               int accumulate) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= static_cast<int64_t>(M) * N) return;
     const int m = static_cast<int>(idx / N);
@@ -339,6 +361,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_simple_kernel(const void* __res
             xv = bf16_to_f32(static_cast<const uint16_t*>(X)[static_cast<int64_t>(m) * K + k]);
         s = __builtin_fmaf(xv, bf16_to_f32(w[k]), s);
     }
+    if (accumulate) s = s + out[idx];
     if (bias != nullptr) s = s + bf16_to_f32(bias[n]);
     if (gelu) s = gelu_tanh(s);
     out[idx] = s;
@@ -346,22 +369,22 @@ __global__ __launch_bounds__(256) void gemm_bf16_simple_kernel(const void* __res
 
 template <bool XF32, int TMW, int TNW>
 hipError_t launch_tiled_bf16(const void* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias, float* out,
-                             int gelu, hipStream_t stream) {
+                             int gelu, int accumulate, hipStream_t stream) {
     constexpr int DEPTH = 4;
     const int tiles = ((M + 32 * TMW - 1) / (32 * TMW)) * ((N + 32 * TNW - 1) / (32 * TNW));
     if (gelu)
         hipLaunchKernelGGL((gemm_bf16_kernel<XF32, TMW, TNW, DEPTH, true>), dim3(tiles), dim3(BF_THR), 0, stream, x,
-                           w, bias, out, M, N, K);
+                           w, bias, out, M, N, K, accumulate);
     else
         hipLaunchKernelGGL((gemm_bf16_kernel<XF32, TMW, TNW, DEPTH, false>), dim3(tiles), dim3(BF_THR), 0, stream, x,
-                           w, bias, out, M, N, K);
+                           w, bias, out, M, N, K, accumulate);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const uint16_t* w, int N,
-                              const uint16_t* bias, float* out, int gelu, hipStream_t stream) {
+                              const uint16_t* bias, float* out, int gelu, hipStream_t stream, int accumulate) {
     if (M == 0 || N == 0) return hipSuccess;
     const bool xf32 = x_dtype == QIMG_FP32;
     const int64_t xbytes = static_cast<int64_t>(M) * K * (xf32 ? 4 : 2);
@@ -372,10 +395,10 @@ hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const ui
         const int blocks = static_cast<int>((total + 255) / 256);
         if (xf32)
             hipLaunchKernelGGL(gemm_bf16_simple_kernel<true>, dim3(blocks), dim3(256), 0, stream, x, w, bias, out, M,
-                               N, K, gelu);
+                               N, K, gelu, accumulate);
         else
             hipLaunchKernelGGL(gemm_bf16_simple_kernel<false>, dim3(blocks), dim3(256), 0, stream, x, w, bias, out, M,
-                               N, K, gelu);
+                               N, K, gelu, accumulate);
         return hipGetLastError();
     }
     // 64x64 tiles when they give at least 256 workgroups, otherwise 32x32
@@ -386,7 +409,7 @@ hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const ui
         const int tiles = static_cast<int>(big);
 #define QIMG_SHORTK(XF, GL)                                                                                    \
     hipLaunchKernelGGL((gemm_bf16_shortk_kernel<XF, GL>), dim3(tiles), dim3(BF_THR), 0, stream, x, w, bias, out, M, \
-                       N, K)
+                       N, K, accumulate)
         if (xf32) {
             if (gelu)
                 QIMG_SHORTK(true, true);
@@ -402,10 +425,10 @@ hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const ui
         return hipGetLastError();
     }
     if (M > 32 && big >= 256)
-        return xf32 ? launch_tiled_bf16<true, 2, 2>(x, M, K, w, N, bias, out, gelu, stream)
-                    : launch_tiled_bf16<false, 2, 2>(x, M, K, w, N, bias, out, gelu, stream);
-    return xf32 ? launch_tiled_bf16<true, 1, 1>(x, M, K, w, N, bias, out, gelu, stream)
-                : launch_tiled_bf16<false, 1, 1>(x, M, K, w, N, bias, out, gelu, stream);
+        return xf32 ? launch_tiled_bf16<true, 2, 2>(x, M, K, w, N, bias, out, gelu, accumulate, stream)
+                    : launch_tiled_bf16<false, 2, 2>(x, M, K, w, N, bias, out, gelu, accumulate, stream);
+    return xf32 ? launch_tiled_bf16<true, 1, 1>(x, M, K, w, N, bias, out, gelu, accumulate, stream)
+                : launch_tiled_bf16<false, 1, 1>(x, M, K, w, N, bias, out, gelu, accumulate, stream);
 }
 
 }  // namespace qimg

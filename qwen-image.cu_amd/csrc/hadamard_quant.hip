@@ -23,7 +23,7 @@
 
 namespace qimg {
 
-enum class RowOut { Int8 = 0, Fp8 = 1, Fp32 = 2 };
+enum class RowOut { Int8 = 0, Fp8 = 1, Fp32 = 2, Bf16 = 3 };
 
 __device__ __forceinline__ int lds_pad(int i) { return i + (i >> 4); }
 
@@ -135,6 +135,10 @@ __device__ __forceinline__ void fwht_quant_tail(float* lds, float* red, int K, i
     if constexpr (OUT == RowOut::Fp32) {
         float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(row) * K;
         for (int i = tid; i < K; i += nthr) o[i] = lds[lds_pad(i)];
+        return;
+    } else if constexpr (OUT == RowOut::Bf16) {
+        uint16_t* o = reinterpret_cast<uint16_t*>(out) + static_cast<int64_t>(row) * K;
+        for (int i = tid; i < K; i += nthr) o[i] = f32_to_bf16(lds[lds_pad(i)]);
         return;
     } else {
         amax = wave_max_dpp(amax);
@@ -306,6 +310,52 @@ __global__ __launch_bounds__(256) void fwht_quant_blocks_kernel(const InT* x, vo
 #pragma unroll
             for (int c = 0; c < 4; ++c) o[b * HBS + ((i + c) << 8)] = static_cast<uint8_t>(w >> (8 * c));
         }
+}
+
+// The INT4 linear's input preparation (linear_forward_int4, cuda_kernels.cu:
+// 4378-4395 and 4452-4470): v = x / smooth[k] (apply_smooth_div, :2258-2264),
+// its bf16 copy for the low-rank branch, and bf16 of the block FWHT of v for
+// the residual GEMM (fwht_inplace / smooth_hadamard_inplace, :2209-2254,
+// :2275-2317; fp32_to_bf16), one row per workgroup in one pass.
+__global__ __launch_bounds__(256) void int4_prep_kernel(const float* __restrict__ x, const float* __restrict__ smooth,
+                                                        uint16_t* __restrict__ xs, uint16_t* __restrict__ xr, int K,
+                                                        int hbs_log2, float norm) {
+    extern __shared__ float lds[];
+    float* red = lds + lds_pad(K) + 1;
+    const int row = blockIdx.x;
+    const int64_t base = static_cast<int64_t>(row) * K;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+        float v = x[base + i];
+        if (smooth != nullptr) v = v / smooth[i];
+        const uint16_t b = f32_to_bf16(v);
+        if (xs != nullptr) xs[base + i] = b;
+        if (hbs_log2 == 0) xr[base + i] = b;
+        lds[lds_pad(i)] = v;
+    }
+    if (hbs_log2 == 0) return;
+    __syncthreads();
+    fwht_quant_tail<RowOut::Bf16>(lds, red, K, hbs_log2, norm, 0, 0.0f, xr, nullptr, row);
+}
+
+hipError_t launch_int4_prep(const float* x, const float* smooth, uint16_t* xs_bf16, uint16_t* xr_bf16, int M, int K,
+                            int hbs, hipStream_t stream) {
+    if (M == 0 || K == 0) return hipSuccess;
+    if (hbs < 1) hbs = 1;
+    if ((hbs & (hbs - 1)) != 0 || K % hbs != 0) return hipErrorInvalidValue;
+    const size_t lds = sizeof(float) * (static_cast<size_t>(K) + K / 16 + 1 + 8);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(int4_prep_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
+    int threads = ((K / 4 + kWave - 1) / kWave) * kWave;
+    threads = threads < 64 ? 64 : (threads > 256 ? 256 : threads);
+    int lg = 0;
+    while ((1 << lg) < hbs) ++lg;
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    hipLaunchKernelGGL(int4_prep_kernel, dim3(M), dim3(threads), lds, stream, x, smooth, xs_bf16, xr_bf16, K, lg, norm);
+    return hipGetLastError();
 }
 
 // LayerNorm + modulate (ln_modulate_row) feeding the FWHT + row quant of

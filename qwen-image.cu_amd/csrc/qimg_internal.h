@@ -71,8 +71,37 @@ hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float*
 
 // gemm_bf16.hip: out fp32 [M, N] = bf16(x) . w^T + bias (GELU), x fp32
 // (rounded to bf16) or bf16 [M, K], w bf16 [N, K].
+// accumulate != 0: out = out + x . w^T, then the bias and GELU
 hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const uint16_t* w, int N,
-                              const uint16_t* bias, float* out, int gelu, hipStream_t stream);
+                              const uint16_t* bias, float* out, int gelu, hipStream_t stream, int accumulate = 0);
+
+// ---- INT4 paths (int4.hip, hadamard_quant.hip) ----
+hipError_t launch_dequant_int4_bf16(const uint8_t* qw, const float* scales, uint16_t* out, int N, int K, int gs,
+                                    int nf4, int scales_gn, int signed_int4, hipStream_t stream);
+hipError_t launch_quant_int4_weight(const float* r, uint8_t* qw, float* scales, int N, int K, int gs, int nf4,
+                                    hipStream_t stream);
+hipError_t launch_quant_act_int4(const float* x, const float* smooth, uint16_t* bf16_out, uint8_t* packed,
+                                 float* scales, int M, int K, int gs, hipStream_t stream);
+hipError_t launch_w4a4_gemm(const uint8_t* act, const uint8_t* wgt, const float* as, const float* ws, float* out,
+                            int M, int N, int K, int gs, int accumulate, const uint16_t* bias, int gelu,
+                            hipStream_t stream);
+hipError_t launch_awq_repack(const int32_t* qw, int32_t* out, int OC, int IC, hipStream_t stream);
+hipError_t launch_awq_dequant(const int32_t* qw, const uint16_t* wscales, const uint16_t* wzeros, uint16_t* out,
+                              int OC, int IC, int gs, int ncomp, hipStream_t stream);
+hipError_t launch_awq_gemv(const float* x, const int32_t* qw_rep, const uint16_t* wscales, const uint16_t* wzeros,
+                           const uint16_t* bias, float* out, int OC, int IC, int gs, int ncomp, hipStream_t stream);
+hipError_t launch_nk_unswizzle(const uint8_t* q_sw, const uint16_t* s_sw, uint8_t* q_rm, float* s_rm, int N, int K,
+                               int G, hipStream_t stream);
+hipError_t launch_nk_dequant(const uint8_t* q_sw, const uint16_t* s_sw, uint16_t* out, int N, int K, int G,
+                             hipStream_t stream);
+hipError_t launch_lora_unswizzle(const uint16_t* packed, uint16_t* out, int rows, int cols, int is_down,
+                                 hipStream_t stream);
+hipError_t launch_transpose_u16(const uint16_t* in, uint16_t* out, int R, int C, hipStream_t stream);
+hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
+// Rows of x fp32 [M, K]: v = x (/ smooth[k]); xs_bf16 = bf16(v) (if
+// non-null); xr_bf16 = bf16(FWHT_hbs(v)) (hbs > 1; hbs <= 1: bf16(v)).
+hipError_t launch_int4_prep(const float* x, const float* smooth, uint16_t* xs_bf16, uint16_t* xr_bf16, int M, int K,
+                            int hbs, hipStream_t stream);
 
 // Kernel selection override for the quantized linear (QIMG_LINEAR_*);
 // returns the previous setting.

@@ -45,6 +45,19 @@ _SIGS = {
     "qimg_linear": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I64, _P]),
     "qimg_linear_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P]),
     "qimg_linear_bf16": (_I, [_P, _I, _I, _I, _P, _I, _P, _P, _I, _P]),
+    "qimg_dequantize_int4_bf16": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "qimg_quantize_int4_per_group": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "qimg_quantize_activation_int4": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "qimg_fused_smooth_bf16_quant": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "qimg_w4a4_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "qimg_int4_scratch_bytes": (_I64, [_I, _I, _I, _I]),
+    "qimg_linear_int4": (_I, [_P, _I, _P, _P, _P, _I, _P, _I64, _P]),
+    "qimg_awq_repack": (_I, [_P, _P, _I, _I, _P]),
+    "qimg_dequantize_awq_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "qimg_linear_awq": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "qimg_unswizzle_nunchaku_weights": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "qimg_dequantize_nunchaku_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "qimg_unswizzle_lora_weights": (_I, [_P, _P, _I, _I, _I, _P]),
     "qimg_sage_scratch_bytes": (_I64, [_I, _I, _I]),
     "qimg_sage_k_mean": (_I, [_P, _P, _I, _I, _I, _P]),
     "qimg_sage_quant_q": (_I, [_P, _P, _P, _I, _I, _I, _P]),
@@ -345,6 +358,171 @@ def linear_forward_bf16(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tenso
         out = torch.empty((M, N), dtype=torch.float32, device=x.device)
     _check(_lib.qimg_linear_bf16(_ptr(x), _DT[x.dtype], M, K, _ptr(weight), N, _ptr(bias), _ptr(out),
                                  int(bool(apply_gelu)), _stream()))
+    return out
+
+
+# ------------------------------------------------------------- INT4 paths
+def dequantize_int4_to_bf16(qweight: torch.Tensor, scales: torch.Tensor, K: int, group_size: int,
+                            nf4_grid: bool = True, scales_gn: bool = False, signed_int4: bool = False) -> torch.Tensor:
+    """dequantize_int4_to_bf16 (cuda_kernels.cu:2876-2929): packed [N, K/2]
+    uint8 -> bf16 [N, K]."""
+    _dev(qweight, "qweight")
+    N = qweight.shape[0]
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=qweight.device)
+    _check(_lib.qimg_dequantize_int4_bf16(_ptr(qweight), _ptr(scales), _ptr(out), N, K, group_size, int(nf4_grid),
+                                          int(scales_gn), int(signed_int4), _stream()))
+    return out
+
+
+def quantize_int4_per_group(residual: torch.Tensor, group_size: int, nf4_grid: bool = True):
+    """quantize_int4_per_group (NF4, cuda_kernels.cu:3290-3368) or the linear
+    INT4 quantizer (:3226-3288): fp32 [N, K] -> (packed [N, K/2], scales [N, K/gs])."""
+    _dev(residual, "residual")
+    N, K = residual.shape
+    qw = torch.empty((N, K // 2), dtype=torch.uint8, device=residual.device)
+    sc = torch.empty((N, K // group_size), dtype=torch.float32, device=residual.device)
+    _check(_lib.qimg_quantize_int4_per_group(_ptr(residual), _ptr(qw), _ptr(sc), N, K, group_size, int(nf4_grid),
+                                             _stream()))
+    return qw, sc
+
+
+def quantize_activation_int4(x: torch.Tensor, group_size: int, smooth: torch.Tensor | None = None,
+                             want_bf16: bool = False):
+    """quantize_activation_int4 (cuda_kernels.cu:3575-3648) or, with smooth /
+    the bf16 copy, fused_smooth_bf16_quant (:3650-3730): fp32 [M, K] ->
+    (packed [M, K/2], scales [K/gs, M][, bf16 [M, K]])."""
+    _dev(x, "x")
+    M, K = x.shape
+    pk = torch.empty((M, K // 2), dtype=torch.uint8, device=x.device)
+    sc = torch.empty((K // group_size, M), dtype=torch.float32, device=x.device)
+    if smooth is None and not want_bf16:
+        _check(_lib.qimg_quantize_activation_int4(_ptr(x), _ptr(pk), _ptr(sc), M, K, group_size, _stream()))
+        return pk, sc
+    bf = torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+    _check(_lib.qimg_fused_smooth_bf16_quant(_ptr(x), _ptr(smooth), _ptr(bf), _ptr(pk), _ptr(sc), M, K, group_size,
+                                             _stream()))
+    return pk, sc, bf
+
+
+def w4a4_gemm(act_packed: torch.Tensor, wgt_packed: torch.Tensor, act_scales: torch.Tensor, wgt_scales: torch.Tensor,
+              K: int, group_size: int, bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+              accumulate: bool = False) -> torch.Tensor:
+    """w4a4_gemm (cuda_kernels.cu:4257-4313) over row-major packed weights."""
+    _dev(act_packed, "act_packed")
+    M, N = act_packed.shape[0], wgt_packed.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=act_packed.device)
+    _check(_lib.qimg_w4a4_gemm(_ptr(act_packed), _ptr(wgt_packed), _ptr(act_scales), _ptr(wgt_scales), _ptr(out), M, N,
+                               K, group_size, int(bool(accumulate)), _ptr(bias), _stream()))
+    return out
+
+
+class _Int4Weight(ctypes.Structure):
+    _fields_ = [("N", _I), ("K", _I), ("rank", _I), ("group_size", _I), ("nf4_grid", _I), ("had_block_size", _I),
+                ("qweight", _P), ("scales4", _P), ("w4a4_qweight", _P), ("w4a4_wscales", _P), ("svd_up", _P),
+                ("svd_down", _P), ("smooth", _P)]
+
+
+class Int4Weight:
+    """The INT4_SVD fields of QuantizedWeight (cuda_kernels.cuh:194-213).
+    W4A4 when w4a4_qweight (two's complement [N, K/2]) and w4a4_wscales
+    ([K/gs, N]) are given, else W4A16 over qweight / scales4 ([N, K/gs])."""
+
+    def __init__(self, N, K, group_size, svd_up=None, svd_down=None, qweight=None, scales4=None, nf4_grid=True,
+                 had_block_size=1, w4a4_qweight=None, w4a4_wscales=None, smooth=None):
+        self.N, self.K, self.group_size = N, K, group_size
+        self.svd_up, self.svd_down = svd_up, svd_down
+        self.rank = 0 if svd_up is None else int(svd_up.shape[1])
+        self.qweight, self.scales4, self.nf4_grid, self.had_block_size = qweight, scales4, nf4_grid, had_block_size
+        self.w4a4_qweight, self.w4a4_wscales, self.smooth = w4a4_qweight, w4a4_wscales, smooth
+
+    def struct(self) -> _Int4Weight:
+        def p(t):
+            return None if t is None else t.data_ptr()
+        return _Int4Weight(self.N, self.K, self.rank, self.group_size, int(bool(self.nf4_grid)),
+                           int(self.had_block_size), p(self.qweight), p(self.scales4), p(self.w4a4_qweight),
+                           p(self.w4a4_wscales), p(self.svd_up), p(self.svd_down), p(self.smooth))
+
+
+def int4_scratch_bytes(M: int, K: int, N: int, svd_rank: int) -> int:
+    """int4_scratch_bytes (cuda_kernels.cuh:475-487), or more where needed."""
+    return int(_lib.qimg_int4_scratch_bytes(M, K, N, svd_rank))
+
+
+def linear_forward_int4(x: torch.Tensor, weight: Int4Weight, bias: torch.Tensor | None = None,
+                        apply_gelu: bool = False, out: torch.Tensor | None = None,
+                        scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """linear_forward_int4 (cuda_kernels.cu:4332-4532): x fp32 [M, K] -> fp32 [M, N]."""
+    _dev(x, "x")
+    if x.dtype != torch.float32:
+        raise QimgError(QIMG_ERR_INVALID_ARG, "x must be float32")
+    M, K = x.shape
+    if K != weight.K:
+        raise QimgError(QIMG_ERR_INVALID_ARG, f"weight K {weight.K} != activation K {K}")
+    if out is None:
+        out = torch.empty((M, weight.N), dtype=torch.float32, device=x.device)
+    if scratch is None:
+        scratch = torch.empty((int4_scratch_bytes(M, K, weight.N, weight.rank),), dtype=torch.uint8, device=x.device)
+    st = weight.struct()
+    _check(_lib.qimg_linear_int4(_ptr(x), M, ctypes.byref(st), _ptr(bias), _ptr(out), int(bool(apply_gelu)),
+                                 _ptr(scratch), scratch.numel(), _stream()))
+    return out
+
+
+def repack_awq_to_transposed(qweight_awq: torch.Tensor, OC: int, IC: int) -> torch.Tensor:
+    """repack_awq_to_transposed (cuda_kernels.cu:3059-3102): int32 [OC/4, IC/2] -> [IC/8, OC]."""
+    _dev(qweight_awq, "qweight_awq")
+    out = torch.empty((IC // 8, OC), dtype=torch.int32, device=qweight_awq.device)
+    _check(_lib.qimg_awq_repack(_ptr(qweight_awq), _ptr(out), OC, IC, _stream()))
+    return out
+
+
+def dequantize_awq_to_bf16(qweight_awq, wscales, wzeros, OC, IC, group_size=64, num_components=6) -> torch.Tensor:
+    """dequantize_awq_to_bf16 (cuda_kernels.cu:3002-3057): bf16 [OC, IC]."""
+    _dev(qweight_awq, "qweight_awq")
+    out = torch.empty((OC, IC), dtype=torch.bfloat16, device=qweight_awq.device)
+    _check(_lib.qimg_dequantize_awq_bf16(_ptr(qweight_awq), _ptr(wscales), _ptr(wzeros), _ptr(out), OC, IC,
+                                         group_size, num_components, _stream()))
+    return out
+
+
+def linear_forward_awq(x: torch.Tensor, qweight_repacked: torch.Tensor, wscales: torch.Tensor, wzeros: torch.Tensor,
+                       OC: int, IC: int, bias: torch.Tensor | None = None, group_size: int = 64,
+                       num_components: int = 6) -> torch.Tensor:
+    """linear_forward_awq (cuda_kernels.cu:3155-3179): x fp32 [IC] (or [1, IC]) -> fp32 [1, OC]."""
+    _dev(x, "x")
+    out = torch.empty((1, OC), dtype=torch.float32, device=x.device)
+    _check(_lib.qimg_linear_awq(_ptr(x), _ptr(qweight_repacked), _ptr(wscales), _ptr(wzeros), _ptr(bias), _ptr(out),
+                                OC, IC, group_size, num_components, _stream()))
+    return out
+
+
+def unswizzle_nunchaku_weights(qweight_swizzled: torch.Tensor, wscales_swizzled: torch.Tensor, N: int, K: int,
+                               num_groups: int):
+    """unswizzle_nunchaku_weights (cuda_kernels.cu:3431-3499): -> (packed
+    [N, K/2] uint8, fp32 scales [num_groups, N])."""
+    _dev(qweight_swizzled, "qweight_swizzled")
+    q = torch.empty((N, K // 2), dtype=torch.uint8, device=qweight_swizzled.device)
+    sc = torch.empty((num_groups, N), dtype=torch.float32, device=qweight_swizzled.device)
+    _check(_lib.qimg_unswizzle_nunchaku_weights(_ptr(qweight_swizzled), _ptr(wscales_swizzled), _ptr(q), _ptr(sc), N,
+                                                K, num_groups, _stream()))
+    return q, sc
+
+
+def dequantize_nunchaku_to_bf16(qweight_swizzled, wscales_swizzled, N, K, num_groups) -> torch.Tensor:
+    """dequantize_nunchaku_to_bf16 (cuda_kernels.cu:2932-2998): bf16 [N, K]."""
+    _dev(qweight_swizzled, "qweight_swizzled")
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=qweight_swizzled.device)
+    _check(_lib.qimg_dequantize_nunchaku_bf16(_ptr(qweight_swizzled), _ptr(wscales_swizzled), _ptr(out), N, K,
+                                              num_groups, _stream()))
+    return out
+
+
+def unswizzle_lora_weights(packed: torch.Tensor, rows: int, cols: int, is_down: bool) -> torch.Tensor:
+    """unswizzle_lora_weights (cuda_kernels.cu:3503-3572): bf16 [rows, cols]."""
+    _dev(packed, "packed")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=packed.device)
+    _check(_lib.qimg_unswizzle_lora_weights(_ptr(packed), _ptr(out), rows, cols, int(bool(is_down)), _stream()))
     return out
 
 
