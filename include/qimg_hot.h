@@ -416,6 +416,14 @@ int64_t qimg_int4_scratch_bytes(int M, int K, int N, int svd_rank);
 int qimg_linear_int4(const float* x, int M, const qimg_int4_weight* w, const uint16_t* bias_bf16, float* out,
                      int gelu, void* scratch, int64_t scratch_bytes, void* stream);
 
+/* bf16_to_fp32 (cuda_kernels.cu:22-31): exact widening of n values. */
+int qimg_bf16_to_fp32(const uint16_t* in, float* out, int64_t n, void* stream);
+
+/* apply_smooth_div (cuda_kernels.cu:2257-2271) and smooth_hadamard_inplace
+ * (:2273-2324): out = FWHT_hbs(x / smooth[k]) row by row, fp32 [M, K]
+ * (smooth may be NULL; hbs 1: no transform). out may be x. */
+int qimg_smooth_hadamard(const float* x, const float* smooth, float* out, int M, int K, int hbs, void* stream);
+
 /* repack_awq_to_transposed (cuda_kernels.cu:3059-3102): AWQ kInterleave=4
  * qweight int32 [OC/4, IC/2] -> [IC/8, OC], word (i, oc) holding the nibbles
  * of inputs 8i .. 8i+7, low first. */

@@ -210,6 +210,26 @@ int qimg_linear_int4(const float* x, int M, const qimg_int4_weight* w, const uin
     return api_hip_status(e, fn);
 }
 
+int qimg_bf16_to_fp32(const uint16_t* in, float* out, int64_t n, void* stream) {
+    const char* fn = "qimg_bf16_to_fp32";
+    QIMG_REQUIRE(n >= 0, "%s: bad n=%lld", fn, static_cast<long long>(n));
+    if (n == 0) return QIMG_OK;
+    QIMG_REQUIRE(in && out, "%s: null pointer", fn);
+    return api_hip_status(qimg::launch_bf16_to_f32(in, out, n, hs(stream)), fn);
+}
+
+int qimg_smooth_hadamard(const float* x, const float* smooth, float* out, int M, int K, int hbs, void* stream) {
+    const char* fn = "qimg_smooth_hadamard";
+    QIMG_REQUIRE(M >= 0 && K > 0, "%s: bad sizes M=%d K=%d", fn, M, K);
+    QIMG_REQUIRE(hbs >= 1 && (hbs & (hbs - 1)) == 0 && K % hbs == 0, "%s: hbs=%d must be a power of two dividing K=%d",
+                 fn, hbs, K);
+    if (K > 32768) return api_fail(QIMG_ERR_UNSUPPORTED, "%s: K=%d exceeds the row limit 32768", fn, K);
+    if (M == 0) return QIMG_OK;
+    QIMG_REQUIRE(x && out, "%s: null pointer", fn);
+    QIMG_REQUIRE(all_aligned16(x, smooth, out), "%s: pointers must be 16-byte aligned", fn);
+    return api_hip_status(qimg::launch_smooth_fwht_f32(x, smooth, out, M, K, hbs, hs(stream)), fn);
+}
+
 int qimg_awq_repack(const int32_t* qweight_awq, int32_t* qweight_out, int OC, int IC, void* stream) {
     const char* fn = "qimg_awq_repack";
     QIMG_REQUIRE(OC >= 0 && IC > 0 && OC % 4 == 0 && IC % 64 == 0, "%s: bad sizes OC=%d IC=%d", fn, OC, IC);

@@ -314,12 +314,14 @@ __global__ __launch_bounds__(256) void fwht_quant_blocks_kernel(const InT* x, vo
 
 // The INT4 linear's input preparation (linear_forward_int4, cuda_kernels.cu:
 // 4378-4395 and 4452-4470): v = x / smooth[k] (apply_smooth_div, :2258-2264),
-// its bf16 copy for the low-rank branch, and bf16 of the block FWHT of v for
-// the residual GEMM (fwht_inplace / smooth_hadamard_inplace, :2209-2254,
-// :2275-2317; fp32_to_bf16), one row per workgroup in one pass.
-__global__ __launch_bounds__(256) void int4_prep_kernel(const float* __restrict__ x, const float* __restrict__ smooth,
-                                                        uint16_t* __restrict__ xs, uint16_t* __restrict__ xr, int K,
-                                                        int hbs_log2, float norm) {
+// its bf16 copy for the low-rank branch, and the block FWHT of v for the
+// residual (fwht_inplace / smooth_hadamard_inplace, :2209-2254, :2275-2317),
+// as bf16 (fp32_to_bf16) or fp32, one row per workgroup in one pass. The row
+// is in LDS before anything is written, so xr may be x.
+template <RowOut OUT>
+__global__ __launch_bounds__(256) void smooth_fwht_rows_kernel(const float* x, const float* __restrict__ smooth,
+                                                               uint16_t* __restrict__ xs, void* xr, int K,
+                                                               int hbs_log2, float norm) {
     extern __shared__ float lds[];
     float* red = lds + lds_pad(K) + 1;
     const int row = blockIdx.x;
@@ -327,25 +329,23 @@ __global__ __launch_bounds__(256) void int4_prep_kernel(const float* __restrict_
     for (int i = threadIdx.x; i < K; i += blockDim.x) {
         float v = x[base + i];
         if (smooth != nullptr) v = v / smooth[i];
-        const uint16_t b = f32_to_bf16(v);
-        if (xs != nullptr) xs[base + i] = b;
-        if (hbs_log2 == 0) xr[base + i] = b;
+        if (xs != nullptr) xs[base + i] = f32_to_bf16(v);
         lds[lds_pad(i)] = v;
     }
-    if (hbs_log2 == 0) return;
     __syncthreads();
-    fwht_quant_tail<RowOut::Bf16>(lds, red, K, hbs_log2, norm, 0, 0.0f, xr, nullptr, row);
+    fwht_quant_tail<OUT>(lds, red, K, hbs_log2, norm, 0, 0.0f, xr, nullptr, row);
 }
 
-hipError_t launch_int4_prep(const float* x, const float* smooth, uint16_t* xs_bf16, uint16_t* xr_bf16, int M, int K,
-                            int hbs, hipStream_t stream) {
+template <RowOut OUT>
+static hipError_t launch_smooth_fwht(const float* x, const float* smooth, uint16_t* xs, void* xr, int M, int K,
+                                     int hbs, hipStream_t stream) {
     if (M == 0 || K == 0) return hipSuccess;
     if (hbs < 1) hbs = 1;
     if ((hbs & (hbs - 1)) != 0 || K % hbs != 0) return hipErrorInvalidValue;
     const size_t lds = sizeof(float) * (static_cast<size_t>(K) + K / 16 + 1 + 8);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(int4_prep_kernel),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(smooth_fwht_rows_kernel<OUT>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
     }
@@ -354,8 +354,19 @@ hipError_t launch_int4_prep(const float* x, const float* smooth, uint16_t* xs_bf
     int lg = 0;
     while ((1 << lg) < hbs) ++lg;
     const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
-    hipLaunchKernelGGL(int4_prep_kernel, dim3(M), dim3(threads), lds, stream, x, smooth, xs_bf16, xr_bf16, K, lg, norm);
+    hipLaunchKernelGGL(smooth_fwht_rows_kernel<OUT>, dim3(M), dim3(threads), lds, stream, x, smooth, xs, xr, K, lg,
+                       norm);
     return hipGetLastError();
+}
+
+hipError_t launch_int4_prep(const float* x, const float* smooth, uint16_t* xs_bf16, uint16_t* xr_bf16, int M, int K,
+                            int hbs, hipStream_t stream) {
+    return launch_smooth_fwht<RowOut::Bf16>(x, smooth, xs_bf16, xr_bf16, M, K, hbs, stream);
+}
+
+hipError_t launch_smooth_fwht_f32(const float* x, const float* smooth, float* out, int M, int K, int hbs,
+                                  hipStream_t stream) {
+    return launch_smooth_fwht<RowOut::Fp32>(x, smooth, nullptr, out, M, K, hbs, stream);
 }
 
 // LayerNorm + modulate (ln_modulate_row) feeding the FWHT + row quant of

@@ -158,7 +158,12 @@ __global__ __launch_bounds__(256) void quant_act_int4_kernel(const float* __rest
 }
 
 // ---- W4A4 GEMM ---------------------------------------------------------
-constexpr int W4_THR = 256;  // four waves, 2 x 2, each a 64 x 64 wave tile
+// A 512-thread workgroup owns a 128 x 128 output tile: eight waves in a 4 x 2
+// arrangement, each a 32 x 64 wave tile (two 32 x 32 blocks). The
+// per-group rescale is VALU work on every accumulator, so the kernel is
+// sized for occupancy (under 128 VGPRs: four waves per SIMD), letting one
+// wave's rescale run beside another's MFMAs and loads.
+constexpr int W4_THR = 512;
 constexpr int W4_BM = 128;
 constexpr int W4_BN = 128;
 
@@ -192,105 +197,95 @@ __global__ __launch_bounds__(W4_THR) void w4a4_gemm_kernel(const uint8_t* __rest
     const int KB = K / 2;
     const int G = K / gs;
 
-    int mrow[2], nrow[2];
-    const uint8_t* ap[2];
+    const int m = m0 + wm * 32 + (lane & 31);
+    const int mrow = m < M ? m : M - 1;  // rows past the end are computed, never stored
+    // Lane half h takes packed bytes [16h, 16h + 16) of each 32-byte
+    // (64-column) chunk of its row, one 16-byte load for two MFMA steps:
+    // bytes 16h + 8s .. +8 feed step s (a k order that both operands share).
+    const uint8_t* ap = act + static_cast<int64_t>(mrow) * KB + 16 * h;
     const uint8_t* wp[2];
+    int ncol[2][4];  // the 16 output columns of block j held by this lane, as 4 runs of 4
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int m = m0 + wm * 64 + 32 * i + (lane & 31);
-        mrow[i] = m < M ? m : M - 1;  // rows past the end are computed, never stored
-        ap[i] = act + static_cast<int64_t>(mrow[i]) * KB + 8 * h;
-        const int n = n0 + wn * 64 + 32 * i + (lane & 31);
-        nrow[i] = n < N ? n : N - 1;
-        wp[i] = wgt + static_cast<int64_t>(nrow[i]) * KB + 8 * h;
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + 32 * j + (lane & 31);
+        wp[j] = wgt + static_cast<int64_t>(n < N ? n : N - 1) * KB + 16 * h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ncol[j][q] = n0 + wn * 64 + 32 * j + 8 * q + 4 * h;
     }
-    // the 16 output columns n of block j held by this lane, as 4 runs of 4
-    int ncol[2][4];
+    const bool vec_ws = (N & 3) == 0;
+
+    float acc[2][16];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ncol[j][q] = n0 + wn * 64 + 32 * j + 8 * q + 4 * h;
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
 
-    float acc[2][2][16];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
+    const int chunks = gs / 64;  // 64-column chunks (two MFMA steps) per group
+    for (int g = 0; g < G; ++g) {
+        v16i d[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    const int steps = gs / 32;  // 32-column MFMA steps per group
-    for (int g = 0; g < G; ++g) {
-        v16i d[2][2];
+            for (int r = 0; r < 16; ++r) d[j][r] = 0;
+        for (int c = 0; c < chunks; ++c) {
+            const int off = g * (gs / 2) + 32 * c;
+            const uint4 pa = *reinterpret_cast<const uint4*>(ap + off);
+            uint4 pw[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int j = 0; j < 2; ++j) pw[j] = *reinterpret_cast<const uint4*>(wp[j] + off);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int s = 0; s < 2; ++s) {
+                const v4i fa = unpack16(s ? make_uint2(pa.z, pa.w) : make_uint2(pa.x, pa.y));
 #pragma unroll
-                for (int r = 0; r < 16; ++r) d[i][j][r] = 0;
-        for (int s = 0; s < steps; ++s) {
-            const int off = g * (gs / 2) + 16 * s;
-            v4i fa[2], fw[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                fa[i] = unpack16(*reinterpret_cast<const uint2*>(ap[i] + off));
-                fw[i] = unpack16(*reinterpret_cast<const uint2*>(wp[i] + off));
+                for (int j = 0; j < 2; ++j) {
+                    const v4i fw = unpack16(s ? make_uint2(pw[j].z, pw[j].w) : make_uint2(pw[j].x, pw[j].y));
+                    d[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw, fa, d[j], 0, 0, 0);
+                }
             }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    d[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], d[i][j], 0, 0, 0);
         }
-        float sa[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) sa[i] = as[static_cast<int64_t>(g) * M + mrow[i]];
+        const float sa = as[static_cast<int64_t>(g) * M + mrow];
         const float* wsg = ws + static_cast<int64_t>(g) * N;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                float sw[4];
+                const int n = ncol[j][q];
+                v4f sw;
+                if (vec_ws && n + 3 < N) {
+                    sw = *reinterpret_cast<const v4f*>(wsg + n);
+                } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int n = ncol[j][q] + c;
-                    sw[c] = wsg[n < N ? n : N - 1];
+                    for (int c = 0; c < 4; ++c) sw[c] = wsg[n + c < N ? n + c : N - 1];
                 }
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
+                for (int c = 0; c < 4; ++c) {
 #pragma clang fp contract(off)
-                        const float t = static_cast<float>(d[i][j][4 * q + c] >> 8) * sa[i];
-                        acc[i][j][4 * q + c] = acc[i][j][4 * q + c] + t * sw[c];
-                    }
+                    const float t = static_cast<float>(d[j][4 * q + c] >> 8) * sa;
+                    acc[j][4 * q + c] = acc[j][4 * q + c] + t * sw[c];
+                }
             }
     }
 
+    if (m >= M) return;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int m = m0 + wm * 64 + 32 * i + (lane & 31);
-        if (m >= M) continue;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int n = ncol[j][q] + c;
-                    if (n >= N) continue;
-                    const float b = bias != nullptr ? bf16_to_f32(bias[n]) : 0.0f;
-                    float* o = out + static_cast<int64_t>(m) * N + n;
-                    float v;
-                    {
+            for (int c = 0; c < 4; ++c) {
+                const int n = ncol[j][q] + c;
+                if (n >= N) continue;
+                const float b = bias != nullptr ? bf16_to_f32(bias[n]) : 0.0f;
+                float* o = out + static_cast<int64_t>(m) * N + n;
+                float v;
+                {
 #pragma clang fp contract(off)
-                        v = acc[i][j][4 * q + c] + b;
-                        if (accumulate) v = *o + v;
-                    }
-                    if (gelu) v = gelu_tanh(v);
-                    *o = v;
+                    v = acc[j][4 * q + c] + b;
+                    if (accumulate) v = *o + v;
                 }
-    }
+                if (gelu) v = gelu_tanh(v);
+                *o = v;
+            }
 }
 
 // ---- AWQ ----------------------------------------------------------------
@@ -341,8 +336,10 @@ __global__ __launch_bounds__(256) void awq_dequant_kernel(const int32_t* __restr
 
 // awq_gemv_repacked_kernel (cuda_kernels.cu:3106-3153), M = 1, gs = 64: one
 // lane per interleaved output channel, the input row in LDS, the sum over
-// ic in order. 64-lane workgroups spread the channels over the CUs (each
-// lane's sum is a dependent chain).
+// ic in order (a dependent chain per lane). The next group's eight weight
+// words and its scale and zero are loaded while the current group is
+// summed, so the chain waits on the memory latency once, not per group;
+// 64-lane workgroups spread the channels over the CUs.
 __global__ __launch_bounds__(64) void awq_gemv_kernel(const float* __restrict__ x, const int32_t* __restrict__ qw,
                                                       const uint16_t* __restrict__ wscales,
                                                       const uint16_t* __restrict__ wzeros,
@@ -351,25 +348,42 @@ __global__ __launch_bounds__(64) void awq_gemv_kernel(const float* __restrict__ 
     extern __shared__ float s_x[];
     for (int i = threadIdx.x; i < IC; i += blockDim.x) s_x[i] = x[i];
     __syncthreads();
-    const int nk = blockIdx.x * blockDim.x + threadIdx.x;
-    if (nk >= OC) return;
+    const int nk_raw = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = nk_raw < OC;
+    const int nk = live ? nk_raw : OC - 1;
     const int G = IC / 64;
-    float acc = 0.0f;
-    for (int g = 0; g < G; ++g) {
-        const float s = bf16_to_f32(wscales[static_cast<int64_t>(g) * OC + nk]);
-        const float z = bf16_to_f32(wzeros[static_cast<int64_t>(g) * OC + nk]);
-        uint32_t p[8];
+    auto load = [&](int g, uint32_t* p, uint16_t& s, uint16_t& z) {
 #pragma unroll
         for (int io = 0; io < 8; ++io) p[io] = static_cast<uint32_t>(qw[static_cast<int64_t>(g * 8 + io) * OC + nk]);
+        s = wscales[static_cast<int64_t>(g) * OC + nk];
+        z = wzeros[static_cast<int64_t>(g) * OC + nk];
+    };
+    uint32_t p[8], pn[8];
+    uint16_t s16, z16, sn16 = 0, zn16 = 0;
+    load(0, p, s16, z16);
+    float acc = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        if (g + 1 < G) load(g + 1, pn, sn16, zn16);
+        const float s = bf16_to_f32(s16);
+        const float z = bf16_to_f32(z16);
+        const v4f* xv = reinterpret_cast<const v4f*>(s_x + g * 64);
 #pragma unroll
-        for (int io = 0; io < 8; ++io)
+        for (int io = 0; io < 8; ++io) {
+            const v4f x0 = xv[2 * io], x1 = xv[2 * io + 1];
+            const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
 #pragma clang fp contract(off)
                 const float w = static_cast<float>((p[io] >> (4 * k)) & 0xF) * s + z;
-                acc = acc + w * s_x[(g * 8 + io) * 8 + k];
+                acc = acc + w * xs[k];
             }
+        }
+#pragma unroll
+        for (int io = 0; io < 8; ++io) p[io] = pn[io];
+        s16 = sn16;
+        z16 = zn16;
     }
+    if (!live) return;
     const int dim = OC / ncomp;
     const int so = (nk % ncomp) * dim + nk / ncomp;
     if (bias != nullptr) acc = acc + bf16_to_f32(bias[so]);
@@ -460,6 +474,14 @@ __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restric
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x)
         out[i] = f32_to_bf16(in[i]);
+}
+
+// bf16 -> fp32 (bf16_to_fp32, cuda_kernels.cu:22-31): exact widening.
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ in, float* __restrict__ out,
+                                                          int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        out[i] = bf16_to_f32(in[i]);
 }
 
 int grid_for(int64_t n, int per_block = 256) {
@@ -595,6 +617,12 @@ hipError_t launch_transpose_u16(const uint16_t* in, uint16_t* out, int R, int C,
 hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_bf16_to_f32(const uint16_t* in, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n);
     return hipGetLastError();
 }
 

@@ -98,10 +98,15 @@ hipError_t launch_lora_unswizzle(const uint16_t* packed, uint16_t* out, int rows
                                  hipStream_t stream);
 hipError_t launch_transpose_u16(const uint16_t* in, uint16_t* out, int R, int C, hipStream_t stream);
 hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
+hipError_t launch_bf16_to_f32(const uint16_t* in, float* out, int64_t n, hipStream_t stream);
 // Rows of x fp32 [M, K]: v = x (/ smooth[k]); xs_bf16 = bf16(v) (if
 // non-null); xr_bf16 = bf16(FWHT_hbs(v)) (hbs > 1; hbs <= 1: bf16(v)).
 hipError_t launch_int4_prep(const float* x, const float* smooth, uint16_t* xs_bf16, uint16_t* xr_bf16, int M, int K,
                             int hbs, hipStream_t stream);
+// out = FWHT_hbs(x / smooth[k]) fp32 (smooth may be null, hbs <= 1: no
+// transform); out may be x.
+hipError_t launch_smooth_fwht_f32(const float* x, const float* smooth, float* out, int M, int K, int hbs,
+                                  hipStream_t stream);
 
 // Kernel selection override for the quantized linear (QIMG_LINEAR_*);
 // returns the previous setting.

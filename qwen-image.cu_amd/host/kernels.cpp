@@ -35,8 +35,8 @@ int qmode(QuantMode m, const char* fn) {
     switch (m) {
         case QuantMode::INT8_HADAMARD: return QIMG_QM_INT8_HADAMARD;
         case QuantMode::FP8_HADAMARD: return QIMG_QM_FP8_HADAMARD;
-        case QuantMode::INT4_SVD: die(fn, "QuantMode::INT4_SVD is not part of this library");
-        case QuantMode::INT4_AWQ: die(fn, "QuantMode::INT4_AWQ is not part of this library");
+        case QuantMode::INT4_SVD: die(fn, "QuantMode::INT4_SVD weights take linear_forward_int4");
+        case QuantMode::INT4_AWQ: die(fn, "QuantMode::INT4_AWQ weights take linear_forward_awq");
         case QuantMode::BF16:
             die(fn, "QuantMode::BF16 weights are not quantized (linear_forward_quantized[_bf16in] take them)");
     }
@@ -283,11 +283,178 @@ QuantizedWeight quantize_weight_tensor_fp8(const Tensor& bf16_weight) {
     return quantize_weight_common(bf16_weight, QuantMode::FP8_HADAMARD, "quantize_weight_tensor_fp8");
 }
 
+// ---- INT4 paths ---------------------------------------------------------
+void dequantize_int4_to_bf16(const uint8_t* qweight, const float* scales, __hip_bfloat16* out, int N, int K,
+                             int group_size, hipStream_t stream, bool nf4_grid, bool scales_gn, bool signed_int4) {
+    check(qimg_dequantize_int4_bf16(qweight, scales, reinterpret_cast<uint16_t*>(out), N, K, group_size, nf4_grid,
+                                    scales_gn, signed_int4, stream),
+          "dequantize_int4_to_bf16");
+}
+
+void dequantize_nunchaku_to_bf16(const uint8_t* qweight, const __hip_bfloat16* wscales, __hip_bfloat16* out, int N,
+                                 int K, int num_groups, hipStream_t stream) {
+    check(qimg_dequantize_nunchaku_bf16(qweight, reinterpret_cast<const uint16_t*>(wscales),
+                                        reinterpret_cast<uint16_t*>(out), N, K, num_groups, stream),
+          "dequantize_nunchaku_to_bf16");
+}
+
+void quantize_int4_per_group(const float* residual, uint8_t* qweight, float* scales, int N, int K, int group_size,
+                             hipStream_t stream) {
+    check(qimg_quantize_int4_per_group(residual, qweight, scales, N, K, group_size, 1, stream),
+          "quantize_int4_per_group");
+}
+
+void repack_awq_to_transposed(const int32_t* qweight_awq, int32_t* qweight_out, int OC, int IC, hipStream_t stream) {
+    check(qimg_awq_repack(qweight_awq, qweight_out, OC, IC, stream), "repack_awq_to_transposed");
+}
+
+void dequantize_awq_to_bf16(const int32_t* qweight, const __hip_bfloat16* wscales, const __hip_bfloat16* wzeros,
+                            __hip_bfloat16* out, int OC, int IC, int group_size, int num_components,
+                            hipStream_t stream) {
+    check(qimg_dequantize_awq_bf16(qweight, reinterpret_cast<const uint16_t*>(wscales),
+                                   reinterpret_cast<const uint16_t*>(wzeros), reinterpret_cast<uint16_t*>(out), OC, IC,
+                                   group_size, num_components, stream),
+          "dequantize_awq_to_bf16");
+}
+
+void unswizzle_nunchaku_weights(const uint8_t* qweight_swizzled, const __hip_bfloat16* wscales_swizzled,
+                                uint8_t* qweight_rowmajor, float* wscales_rowmajor, int N, int K, int num_groups,
+                                hipStream_t stream) {
+    check(qimg_unswizzle_nunchaku_weights(qweight_swizzled, reinterpret_cast<const uint16_t*>(wscales_swizzled),
+                                          qweight_rowmajor, wscales_rowmajor, N, K, num_groups, stream),
+          "unswizzle_nunchaku_weights");
+}
+
+void unswizzle_lora_weights(const __hip_bfloat16* packed, __hip_bfloat16* standard, int rows, int cols, bool is_down,
+                            hipStream_t stream) {
+    check(qimg_unswizzle_lora_weights(reinterpret_cast<const uint16_t*>(packed), reinterpret_cast<uint16_t*>(standard),
+                                      rows, cols, is_down, stream),
+          "unswizzle_lora_weights");
+}
+
+void quantize_activation_int4(const float* x, uint8_t* act_packed, float* act_scales, int M, int K, int group_size,
+                              hipStream_t stream) {
+    check(qimg_quantize_activation_int4(x, act_packed, act_scales, M, K, group_size, stream),
+          "quantize_activation_int4");
+}
+
+void swizzle_w4a4_weights_mma(const uint8_t* wgt_rowmajor, uint32_t* wgt_mma, int N, int K, int group_size,
+                              hipStream_t stream) {
+    const char* fn = "swizzle_w4a4_weights_mma";
+    REQUIRE(N > 0 && K > 0 && group_size > 0 && K % group_size == 0, fn, "bad sizes N=%d K=%d group_size=%d", N, K,
+            group_size);
+    // [num_groups, ceil(N/8), 256 B] holds the N * K/2 row-major bytes
+    const size_t bytes = static_cast<size_t>(N) * (K / 2);
+    const hipError_t e = hipMemcpyAsync(wgt_mma, wgt_rowmajor, bytes, hipMemcpyDeviceToDevice, stream);
+    REQUIRE(e == hipSuccess, fn, "%s", hipGetErrorString(e));
+}
+
+void w4a4_gemm(const uint8_t* act_packed, const uint8_t* wgt_packed, const float* act_scales, const float* wgt_scales,
+               float* output, int M, int N, int K, int group_size, const uint32_t* wgt_mma, bool accumulate,
+               const __hip_bfloat16* bias, hipStream_t stream) {
+    const uint8_t* w = wgt_packed ? wgt_packed : reinterpret_cast<const uint8_t*>(wgt_mma);
+    check(qimg_w4a4_gemm(act_packed, w, act_scales, wgt_scales, output, M, N, K, group_size, accumulate,
+                         reinterpret_cast<const uint16_t*>(bias), stream),
+          "w4a4_gemm");
+}
+
+void fused_smooth_bf16_quant(const float* x, const float* smooth, __hip_bfloat16* bf16_out, uint8_t* act_packed,
+                             float* act_scales, int M, int K, int group_size, hipStream_t stream) {
+    check(qimg_fused_smooth_bf16_quant(x, smooth, reinterpret_cast<uint16_t*>(bf16_out), act_packed, act_scales, M, K,
+                                       group_size, stream),
+          "fused_smooth_bf16_quant");
+}
+
+void apply_smooth_div(const float* x, const float* smooth, float* out, int M, int K, hipStream_t stream) {
+    check(qimg_smooth_hadamard(x, smooth, out, M, K, 1, stream), "apply_smooth_div");
+}
+
+void smooth_hadamard_inplace(float* data, const float* smooth, int M, int K, int had_block_size, hipStream_t stream) {
+    check(qimg_smooth_hadamard(data, smooth, data, M, K, had_block_size, stream), "smooth_hadamard_inplace");
+}
+
+void linear_forward_int4(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                         Tensor& scratch, bool apply_gelu) {
+    const char* fn = "linear_forward_int4";
+    REQUIRE(x.dtype == DType::FP32 && x.ndim == 2, fn, "x must be FP32 [M, K] (got %s %s)", dtype_name(x.dtype),
+            x.shape_str().c_str());
+    REQUIRE(out.dtype == DType::FP32, fn, "out must be FP32 (got %s)", dtype_name(out.dtype));
+    REQUIRE(weight.mode == QuantMode::INT4_SVD, fn, "weight.mode must be INT4_SVD");
+    REQUIRE(weight.svd_up.ndim == 2 && weight.svd_down.ndim == 2 && weight.svd_up.dtype == DType::BF16 &&
+                weight.svd_down.dtype == DType::BF16,
+            fn, "svd_up [N, r] and svd_down [K, r] must be BF16");
+    // N and K from the low-rank factors (cuda_kernels.cu:4340-4342)
+    const int M = static_cast<int>(x.shape[0]);
+    const int N = static_cast<int>(weight.svd_up.shape[0]);
+    const int K = static_cast<int>(weight.svd_down.shape[0]);
+    const int r = static_cast<int>(weight.svd_up.shape[1]);
+    REQUIRE(x.shape[1] == K, fn, "x K=%lld != weight K=%d", (long long)x.shape[1], K);
+    REQUIRE(weight.svd_down.shape[1] == r, fn, "svd_down rank %lld != svd_up rank %d",
+            (long long)weight.svd_down.shape[1], r);
+    check_out(out, M, N, fn);
+    qimg_int4_weight w{};
+    w.N = N;
+    w.K = K;
+    w.rank = r;
+    w.group_size = weight.group_size;
+    w.nf4_grid = weight.nf4_grid ? 1 : 0;
+    w.had_block_size = weight.had_block_size;
+    w.svd_up = static_cast<const uint16_t*>(weight.svd_up.data);
+    w.svd_down = static_cast<const uint16_t*>(weight.svd_down.data);
+    w.smooth = static_cast<const float*>(weight.smooth.data);
+    const Tensor& w4 = weight.qweight_mma.data ? weight.qweight_mma : weight.qweight_rowmajor;
+    if (weight.nunchaku_swizzle && w4.data) {
+        REQUIRE(weight.wscales_rowmajor.dtype == DType::FP32 && weight.wscales_rowmajor.data, fn,
+                "W4A4 needs wscales_rowmajor FP32 [num_groups, N]");
+        w.w4a4_qweight = static_cast<const uint8_t*>(w4.data);
+        w.w4a4_wscales = static_cast<const float*>(weight.wscales_rowmajor.data);
+    } else {
+        REQUIRE(weight.qweight.data && weight.scales4.dtype == DType::FP32, fn,
+                "W4A16 needs qweight [N, K/2] and scales4 FP32 [N, K/group_size]");
+        w.qweight = static_cast<const uint8_t*>(weight.qweight.data);
+        w.scales4 = static_cast<const float*>(weight.scales4.data);
+    }
+    check(qimg_linear_int4(static_cast<const float*>(x.data), M, &w, bias_ptr(bias, N, fn),
+                           static_cast<float*>(out.data), apply_gelu ? 1 : 0, scratch.data,
+                           static_cast<int64_t>(scratch.nbytes()), nullptr),
+          fn);
+}
+
+void linear_forward_awq(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out) {
+    const char* fn = "linear_forward_awq";
+    REQUIRE(x.dtype == DType::FP32 && out.dtype == DType::FP32, fn, "x and out must be FP32");
+    REQUIRE(weight.mode == QuantMode::INT4_AWQ, fn, "weight.mode must be INT4_AWQ");
+    REQUIRE(x.shape[0] == 1, fn, "AWQ GEMV only supports M=1 (got %lld)", (long long)x.shape[0]);
+    const int OC = weight.awq_OC, IC = weight.awq_IC;
+    REQUIRE(x.numel() == IC && out.numel() == OC, fn, "x must hold IC=%d values and out OC=%d", IC, OC);
+    check(qimg_linear_awq(static_cast<const float*>(x.data), static_cast<const int32_t*>(weight.awq_qweight.data),
+                          static_cast<const uint16_t*>(weight.awq_wscales.data),
+                          static_cast<const uint16_t*>(weight.awq_wzeros.data), bias_ptr(bias, OC, fn),
+                          static_cast<float*>(out.data), OC, IC, weight.awq_group_size, weight.awq_num_components,
+                          nullptr),
+          fn);
+}
+
+namespace {
+
+// A BF16 input widened to FP32 in a temporary (the reference's bf16in
+// dispatch, cuda_kernels.cu:4616-4631).
+Tensor widen_bf16(const Tensor& x, const char* fn) {
+    REQUIRE(x.dtype == DType::BF16, fn, "x must be BF16 (got %s)", dtype_name(x.dtype));
+    Tensor f = Tensor::alloc(std::vector<int64_t>(x.shape, x.shape + x.ndim), DType::FP32);
+    check(qimg_bf16_to_fp32(static_cast<const uint16_t*>(x.data), static_cast<float*>(f.data), x.numel(), nullptr),
+          fn);
+    return f;
+}
+
+}  // namespace
+
 void linear_forward_quantized(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
                               Tensor& scratch, bool apply_gelu) {
     const char* fn = "linear_forward_quantized";
     if (weight.mode == QuantMode::BF16) return linear_bf16(x, DType::FP32, weight, bias, out, apply_gelu, fn);
-    qmode(weight.mode, fn);  // INT4 modes are reported here
+    if (weight.mode == QuantMode::INT4_AWQ) return linear_forward_awq(x, weight, bias, out);
+    if (weight.mode == QuantMode::INT4_SVD) return linear_forward_int4(x, weight, bias, out, scratch, apply_gelu);
     linear_common(x, DType::FP32, weight, bias, out, scratch, apply_gelu, fn);
 }
 
@@ -295,7 +462,15 @@ void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& wei
                                      Tensor& out, Tensor& scratch) {
     const char* fn = "linear_forward_quantized_bf16in";
     if (weight.mode == QuantMode::BF16) return linear_bf16(x, DType::BF16, weight, bias, out, false, fn);
-    qmode(weight.mode, fn);
+    if (weight.mode == QuantMode::INT4_AWQ || weight.mode == QuantMode::INT4_SVD) {
+        Tensor xf = widen_bf16(x, fn);
+        if (weight.mode == QuantMode::INT4_AWQ)
+            linear_forward_awq(xf, weight, bias, out);
+        else
+            linear_forward_int4(xf, weight, bias, out, scratch);
+        REQUIRE(hipDeviceSynchronize() == hipSuccess, fn, "device synchronisation failed");
+        return;
+    }
     linear_common(x, DType::BF16, weight, bias, out, scratch, false, fn);
 }
 

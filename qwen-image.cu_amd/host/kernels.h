@@ -11,9 +11,13 @@
 //   * `out` may be FP32 (the reference's type) or BF16.
 //   * QuantMode::BF16 weights (layers kept unquantized) run the library's
 //     BF16 kernel behind linear_forward_quantized[_bf16in], as the
-//     reference's linear_forward_bf16[_bf16in]; the INT4 modes are not part
-//     of this library: dispatching one reports the mode and exits, like any
-//     other failed check.
+//     reference's linear_forward_bf16[_bf16in].
+//   * INT4_SVD and INT4_AWQ run the library's INT4 kernels. The W4A4
+//     residual reads the row-major packing: swizzle_w4a4_weights_mma
+//     copies the row-major nibbles into qweight_mma (the buffer the
+//     reference's loader allocates has room for them), so
+//     TransformerWeights::load runs unchanged and w4a4_gemm /
+//     linear_forward_int4 read qweight_mma as [N, K/2] row-major.
 //
 // Error behaviour follows the reference (assert / CUDA_CHECK -> exit(1)): a
 // rejected argument or failed HIP call prints "qimg: <function>: <reason>"
@@ -32,20 +36,49 @@
 
 enum class QuantMode { INT8_HADAMARD, INT4_SVD, BF16, INT4_AWQ, FP8_HADAMARD };
 
-// cuda_kernels.cuh:187-245, INT8 fields (plus the e4m3 mode).
+// cuda_kernels.cuh:187-245 (plus the e4m3 mode). Unused fields stay null.
 struct QuantizedWeight {
     QuantMode mode = QuantMode::INT8_HADAMARD;
-    Tensor data;             // [N, K] INT8, or FP8_E4M3 for FP8_HADAMARD
+
+    // INT8 / FP8 / BF16
+    Tensor data;             // [N, K] INT8, FP8_E4M3 for FP8_HADAMARD, BF16 for BF16
     Tensor scales;           // [N] FP32
     int had_block_size = 0;  // Hadamard block size (power of 2)
+
+    // INT4 + SVD
+    Tensor qweight;          // [N, K/2] UINT8 packed INT4 (NF4 or offset-8 codes)
+    Tensor scales4;          // [N, K/group_size] FP32
+    Tensor svd_up;           // [N, r] BF16
+    Tensor svd_down;         // [K, r] BF16
+    Tensor smooth;           // [K] FP32, optional
+    int group_size = 128;
+    int svd_rank = 0;
+    bool nf4_grid = true;
+
+    // nunchaku INT4 (two's complement nibbles)
+    bool nunchaku_swizzle = false;
+    Tensor wscales_bf16;      // [num_groups, N] BF16, swizzled
+    Tensor qweight_rowmajor;  // [N, K/2] UINT8
+    Tensor wscales_rowmajor;  // [num_groups, N] FP32
+    Tensor qweight_mma;       // row-major [N, K/2] nibbles here (see above)
+
+    // AWQ INT4 (modulation layers)
+    Tensor awq_qweight;   // [IC/8, OC] INT32 after repack_awq_to_transposed
+    Tensor awq_wscales;   // [num_groups, OC] BF16
+    Tensor awq_wzeros;    // [num_groups, OC] BF16
+    int awq_OC = 0;
+    int awq_IC = 0;
+    int awq_group_size = 64;
+    int awq_num_components = 6;
 
     QuantizedWeight() = default;
     QuantizedWeight(QuantizedWeight&&) = default;
     QuantizedWeight& operator=(QuantizedWeight&&) = default;
 
     void free_data() {
-        data.free_data();
-        scales.free_data();
+        for (Tensor* t : {&data, &scales, &qweight, &scales4, &svd_up, &svd_down, &smooth, &wscales_bf16,
+                          &qweight_rowmajor, &wscales_rowmajor, &qweight_mma, &awq_qweight, &awq_wscales, &awq_wzeros})
+            t->free_data();
     }
 };
 
@@ -100,10 +133,53 @@ inline int64_t int8_scratch_bytes(int M, int K, int N) {
 // Dispatch on weight.mode (cuda_kernels.cu:4599-4635): x FP32 resp. BF16.
 // QuantMode::BF16: weight.data BF16 [N, K], no scales, out FP32, scratch
 // unused (the fp32 -> bf16 rounding of x happens inside the kernel).
+// INT4_SVD: linear_forward_int4 (a BF16 x is widened to FP32 first, as the
+// reference does); INT4_AWQ: linear_forward_awq (M = 1).
 void linear_forward_quantized(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
                               Tensor& out, Tensor& scratch, bool apply_gelu = false);
 void linear_forward_quantized_bf16in(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias,
                                      Tensor& out, Tensor& scratch);
+
+// ---- INT4 paths (cuda_kernels.cuh:322-470) -----------------------------
+void dequantize_int4_to_bf16(const uint8_t* qweight, const float* scales, __hip_bfloat16* out, int N, int K,
+                             int group_size, hipStream_t stream = 0, bool nf4_grid = true, bool scales_gn = false,
+                             bool signed_int4 = false);
+void dequantize_nunchaku_to_bf16(const uint8_t* qweight, const __hip_bfloat16* wscales, __hip_bfloat16* out, int N,
+                                 int K, int num_groups, hipStream_t stream = 0);
+void quantize_int4_per_group(const float* residual, uint8_t* qweight, float* scales, int N, int K, int group_size,
+                             hipStream_t stream = 0);
+void linear_forward_awq(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out);
+void repack_awq_to_transposed(const int32_t* qweight_awq, int32_t* qweight_out, int OC, int IC,
+                              hipStream_t stream = 0);
+void dequantize_awq_to_bf16(const int32_t* qweight, const __hip_bfloat16* wscales, const __hip_bfloat16* wzeros,
+                            __hip_bfloat16* out, int OC, int IC, int group_size, int num_components,
+                            hipStream_t stream = 0);
+void unswizzle_nunchaku_weights(const uint8_t* qweight_swizzled, const __hip_bfloat16* wscales_swizzled,
+                                uint8_t* qweight_rowmajor, float* wscales_rowmajor, int N, int K, int num_groups,
+                                hipStream_t stream = 0);
+void unswizzle_lora_weights(const __hip_bfloat16* packed, __hip_bfloat16* standard, int rows, int cols, bool is_down,
+                            hipStream_t stream = 0);
+void quantize_activation_int4(const float* x, uint8_t* act_packed, float* act_scales, int M, int K, int group_size,
+                              hipStream_t stream = 0);
+// Keeps the row-major packing (copied into wgt_mma), which this library's
+// W4A4 GEMM reads.
+void swizzle_w4a4_weights_mma(const uint8_t* wgt_rowmajor, uint32_t* wgt_mma, int N, int K, int group_size,
+                              hipStream_t stream = 0);
+// wgt_packed, or wgt_mma when wgt_packed is null, is [N, K/2] row-major.
+void w4a4_gemm(const uint8_t* act_packed, const uint8_t* wgt_packed, const float* act_scales, const float* wgt_scales,
+               float* output, int M, int N, int K, int group_size, const uint32_t* wgt_mma = nullptr,
+               bool accumulate = false, const __hip_bfloat16* bias = nullptr, hipStream_t stream = 0);
+void fused_smooth_bf16_quant(const float* x, const float* smooth, __hip_bfloat16* bf16_out, uint8_t* act_packed,
+                             float* act_scales, int M, int K, int group_size, hipStream_t stream = 0);
+void apply_smooth_div(const float* x, const float* smooth, float* out, int M, int K, hipStream_t stream = 0);
+void smooth_hadamard_inplace(float* data, const float* smooth, int M, int K, int had_block_size,
+                             hipStream_t stream = 0);
+// x FP32 [M, K], out FP32 [M, N]; scratch >= int4_scratch_bytes(M, K, N, r).
+void linear_forward_int4(const Tensor& x, const QuantizedWeight& weight, const Tensor* bias, Tensor& out,
+                         Tensor& scratch, bool apply_gelu = false);
+inline int64_t int4_scratch_bytes(int M, int K, int N, int svd_rank) {
+    return qimg_int4_scratch_bytes(M, K, N, svd_rank);
+}
 
 // ---- SageAttention (cuda_kernels.cuh:558-562) --------------------------
 // FP16 q, k, v [BH, S, D] -> FP32 out [BH, S, D] (values rounded through

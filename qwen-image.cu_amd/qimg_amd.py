@@ -52,6 +52,8 @@ _SIGS = {
     "qimg_w4a4_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "qimg_int4_scratch_bytes": (_I64, [_I, _I, _I, _I]),
     "qimg_linear_int4": (_I, [_P, _I, _P, _P, _P, _I, _P, _I64, _P]),
+    "qimg_bf16_to_fp32": (_I, [_P, _P, _I64, _P]),
+    "qimg_smooth_hadamard": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "qimg_awq_repack": (_I, [_P, _P, _I, _I, _P]),
     "qimg_dequantize_awq_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "qimg_linear_awq": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
@@ -466,6 +468,18 @@ def linear_forward_int4(x: torch.Tensor, weight: Int4Weight, bias: torch.Tensor 
     st = weight.struct()
     _check(_lib.qimg_linear_int4(_ptr(x), M, ctypes.byref(st), _ptr(bias), _ptr(out), int(bool(apply_gelu)),
                                  _ptr(scratch), scratch.numel(), _stream()))
+    return out
+
+
+def smooth_hadamard(x: torch.Tensor, smooth: torch.Tensor | None, had_block_size: int,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """apply_smooth_div / smooth_hadamard_inplace (cuda_kernels.cu:2257-2324):
+    FWHT_hbs(x / smooth) fp32 [M, K] (out may be x)."""
+    _dev(x, "x")
+    M, K = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    _check(_lib.qimg_smooth_hadamard(_ptr(x), _ptr(smooth), _ptr(out), M, K, int(had_block_size), _stream()))
     return out
 
 

@@ -390,7 +390,12 @@ int expect_error(const std::string& c) {
         Tensor out16 = Tensor::wrap(fake, {4, 8}, DType::BF16);
         linear_forward_quantized(x, wb, nullptr, out16, scratch);
     } else if (c == "mode_int4") {
-        w.mode = QuantMode::INT4_SVD;
+        w.mode = QuantMode::INT4_SVD;  // no low-rank factors
+        linear_forward_quantized(x, w, nullptr, out, scratch);
+    } else if (c == "awq_m") {
+        w.mode = QuantMode::INT4_AWQ;
+        w.awq_OC = 8;
+        w.awq_IC = 64;
         linear_forward_quantized(x, w, nullptr, out, scratch);
     } else if (c == "scratch") {
         Tensor small = Tensor::wrap(fake, {16}, DType::UINT8);
@@ -505,6 +510,136 @@ void case_bf16_mode(bool bf16_in, int M, int N, int K) {
     report(name, d == 0.0, det);
 }
 
+// INT4_SVD through linear_forward_quantized[_bf16in] (cuda_kernels.cu:
+// 4599-4635). The low-rank up factor is zero, so the output is the residual
+// alone: W4A4 (nunchaku form, loaded as transformer.h:202-279 does: row-major
+// nibbles swizzled into qweight_mma) is then bit-exact against the oracle's
+// activation quant + W4A4 GEMM; W4A16 against float64 within an fp32
+// summation bound.
+void case_int4(bool w4a4, bool bf16_in, int M, int N, int K) {
+    Rng r(M * 7 + N + K + w4a4 * 2 + bf16_in);
+    const int gs = 64, G = K / gs, rank = 32;
+    std::vector<float> xf = f32_normal(r, static_cast<size_t>(M) * K, 1.0f);
+    std::vector<uint16_t> xb(xf.size());
+    for (size_t i = 0; i < xf.size(); ++i) {
+        xb[i] = or_f32_to_bf16(xf[i]);
+        xf[i] = or_bf16_to_f32(xb[i]);  // the same values either way
+    }
+    std::vector<uint16_t> b(N), up(static_cast<size_t>(N) * rank, 0);
+    for (auto& v : b) v = or_f32_to_bf16(r.normal() * 0.01f);
+    std::vector<uint16_t> down = bf16_normal(r, static_cast<size_t>(K) * rank, 0.05f);
+    std::vector<float> sm(K);
+    for (auto& v : sm) v = 0.5f + r.uniform();
+    QuantizedWeight qw;
+    qw.mode = QuantMode::INT4_SVD;
+    qw.group_size = gs;
+    qw.svd_rank = rank;
+    qw.svd_up = upload(up, {N, rank}, DType::BF16);
+    qw.svd_down = upload(down, {K, rank}, DType::BF16);
+    std::vector<float> want(static_cast<size_t>(M) * N, 0.0f);
+    double tol = 0;
+    if (w4a4) {
+        std::vector<uint8_t> wq(static_cast<size_t>(N) * K / 2);
+        for (auto& v : wq) v = static_cast<uint8_t>(r.next());
+        std::vector<float> ws(static_cast<size_t>(G) * N);
+        for (auto& v : ws) v = 0.001f + 0.01f * r.uniform();
+        qw.nunchaku_swizzle = true;
+        qw.had_block_size = 1;
+        qw.smooth = upload(sm, {K}, DType::FP32);
+        qw.qweight_rowmajor = upload(wq, {N, K / 2}, DType::UINT8);
+        qw.wscales_rowmajor = upload(ws, {G, N}, DType::FP32);
+        qw.qweight_mma = Tensor::alloc({static_cast<int64_t>(G) * ((N + 7) / 8) * 256}, DType::UINT8);
+        swizzle_w4a4_weights_mma(static_cast<const uint8_t*>(qw.qweight_rowmajor.data),
+                                 static_cast<uint32_t*>(qw.qweight_mma.data), N, K, gs);
+        HIP_CHECK(hipDeviceSynchronize());
+        qw.qweight_rowmajor.free_data();
+        std::vector<uint8_t> pk(static_cast<size_t>(M) * K / 2);
+        std::vector<float> as(static_cast<size_t>(G) * M);
+        or_quant_act_int4(xf.data(), sm.data(), M, K, gs, nullptr, pk.data(), as.data());
+        or_w4a4_gemm(pk.data(), wq.data(), as.data(), ws.data(), M, N, K, gs, 1, b.data(), 0, M, want.data());
+    } else {
+        std::vector<float> resid = f32_normal(r, static_cast<size_t>(N) * K, 0.02f);
+        std::vector<uint8_t> q4(static_cast<size_t>(N) * K / 2);
+        std::vector<float> s4(static_cast<size_t>(N) * G);
+        or_quant_int4_nf4(resid.data(), N, K, gs, q4.data(), s4.data());
+        const int hbs = K & -K;
+        qw.had_block_size = hbs;
+        qw.nf4_grid = true;
+        qw.qweight = upload(q4, {N, K / 2}, DType::UINT8);
+        qw.scales4 = upload(s4, {N, G}, DType::FP32);
+        std::vector<float> xr = xf;
+        or_fwht_rows(xr.data(), M, K, hbs);
+        std::vector<uint16_t> deq(static_cast<size_t>(N) * K);
+        or_dequant_int4_bf16(q4.data(), s4.data(), N, K, gs, 1, 0, 0, deq.data());
+        for (int m = 0; m < M; ++m)
+            for (int n = 0; n < N; ++n) {
+                double acc = 0, mag = 0;
+                for (int k = 0; k < K; ++k) {
+                    const double p = static_cast<double>(or_bf16_to_f32(or_f32_to_bf16(xr[static_cast<size_t>(m) * K + k]))) *
+                                     or_bf16_to_f32(deq[static_cast<size_t>(n) * K + k]);
+                    acc += p;
+                    mag += std::fabs(p);
+                }
+                want[static_cast<size_t>(m) * N + n] = static_cast<float>(acc + or_bf16_to_f32(b[n]));
+                tol = std::fmax(tol, 8 * std::sqrt(static_cast<double>(K)) * std::ldexp(mag, -24) + 1e-6);
+            }
+    }
+    Tensor bias = upload(b, {N}, DType::BF16);
+    Tensor x = bf16_in ? upload(xb, {M, K}, DType::BF16) : upload(xf, {M, K}, DType::FP32);
+    Tensor out = Tensor::alloc({M, N}, DType::FP32);
+    Tensor scratch = Tensor::alloc({int4_scratch_bytes(M, K, N, rank)}, DType::UINT8);
+    if (bf16_in)
+        linear_forward_quantized_bf16in(x, qw, &bias, out, scratch);
+    else
+        linear_forward_quantized(x, qw, &bias, out, scratch);
+    HIP_CHECK(hipDeviceSynchronize());
+    const double d = max_abs_diff(download<float>(out), want);
+    char name[96], det[64];
+    snprintf(name, sizeof(name), "int4 %s linear %s M=%d N=%d K=%d", w4a4 ? "W4A4" : "W4A16",
+             bf16_in ? "bf16in" : "fp32in", M, N, K);
+    snprintf(det, sizeof(det), "max|diff|=%.3g tol=%.3g", d, tol);
+    report(name, d <= tol, det);
+}
+
+// INT4_AWQ (M = 1) through linear_forward_quantized, loaded as
+// transformer.h:427-456 does (repack at load): bit-exact against the oracle.
+void case_awq(int OC, int IC) {
+    Rng r(OC + IC);
+    const int gs = 64, nc = 6;
+    std::vector<int32_t> q(static_cast<size_t>(OC / 4) * (IC / 2));
+    for (auto& v : q) v = static_cast<int32_t>(r.next());
+    std::vector<uint16_t> ws(static_cast<size_t>(IC / gs) * OC), wz(ws.size()), b(OC);
+    for (auto& v : ws) v = or_f32_to_bf16(0.001f + 0.01f * r.uniform());
+    for (auto& v : wz) v = or_f32_to_bf16(0.1f * r.normal());
+    for (auto& v : b) v = or_f32_to_bf16(0.01f * r.normal());
+    std::vector<float> x = f32_normal(r, IC, 1.0f);
+    QuantizedWeight qw;
+    qw.mode = QuantMode::INT4_AWQ;
+    Tensor raw = upload(q, {OC / 4, IC / 2}, DType::INT32);
+    qw.awq_wscales = upload(ws, {IC / gs, OC}, DType::BF16);
+    qw.awq_wzeros = upload(wz, {IC / gs, OC}, DType::BF16);
+    qw.awq_OC = OC;
+    qw.awq_IC = IC;
+    qw.awq_group_size = gs;
+    qw.awq_num_components = nc;
+    qw.awq_qweight = Tensor::alloc({IC / 8, OC}, DType::INT32);
+    repack_awq_to_transposed(static_cast<const int32_t*>(raw.data), static_cast<int32_t*>(qw.awq_qweight.data), OC, IC);
+    HIP_CHECK(hipDeviceSynchronize());
+    Tensor xt = upload(x, {1, IC}, DType::FP32), bias = upload(b, {OC}, DType::BF16);
+    Tensor out = Tensor::alloc({1, OC}, DType::FP32), scratch = Tensor::alloc({16}, DType::UINT8);
+    linear_forward_quantized(xt, qw, &bias, out, scratch);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<int32_t> rep(static_cast<size_t>(IC / 8) * OC);
+    or_awq_repack(q.data(), OC, IC, rep.data());
+    std::vector<float> want(OC);
+    or_awq_gemv(x.data(), rep.data(), ws.data(), wz.data(), b.data(), OC, IC, gs, nc, want.data());
+    const double d = max_abs_diff(download<float>(out), want);
+    char name[96], det[64];
+    snprintf(name, sizeof(name), "awq linear OC=%d IC=%d", OC, IC);
+    snprintf(det, sizeof(det), "max|diff|=%.3g", d);
+    report(name, d == 0.0, det);
+}
+
 int main(int argc, char** argv) {
     if (argc == 3 && std::string(argv[1]) == "--expect-error") return expect_error(argv[2]);
     case_tensor_api();
@@ -522,6 +657,12 @@ int main(int argc, char** argv) {
     case_bf16_mode(true, 32, 512, 3584);    // txt_in (a slice of N)
     case_bf16_mode(false, 1, 6144, 3072);   // norm_out
     case_bf16_mode(false, 96, 64, 3072);    // proj_out
+    case_int4(true, false, 96, 384, 3072);
+    case_int4(true, true, 33, 256, 1024);
+    case_int4(false, false, 40, 256, 3072);
+    case_int4(false, true, 17, 128, 1024);
+    case_awq(18432, 3072);                  // the modulation layer
+    case_awq(96, 128);
     case_sage(2, 300, 128, false);
     case_sage(3, 129, 64, true);
     case_block_loop();

@@ -19,7 +19,8 @@ REJECTIONS = {
     "out_shape": "linear_forward_int8: out is [4, 9], expected [4, 8]",
     "x_dtype": "linear_forward_int8: x must be FP32",
     "weight_k": "linear_forward_quantized: weight K=64 != input K=128",
-    "mode_int4": "QuantMode::INT4_SVD is not part of this library",
+    "mode_int4": "linear_forward_int4: svd_up [N, r] and svd_down [K, r] must be BF16",
+    "awq_m": "linear_forward_awq: AWQ GEMV only supports M=1 (got 4)",
     "bf16_out_dtype": "linear_forward_quantized: out must be FP32",
     "scratch": "scratch 16 bytes < required",
     "hbs": "hbs=48 is not a power of two",
