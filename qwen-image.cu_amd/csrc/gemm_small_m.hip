@@ -354,16 +354,26 @@ hipError_t launch_small(const void* a, const float* as, int M, int K, const void
 }
 
 
-// LDS-staged variant for K a multiple of 256. A load instruction whose 64
+// LDS-staged variant for K a multiple of 4 * BKB. A load instruction whose 64
 // lanes touch 32 different rows (the direct fragment loads above) costs the
-// address unit several times more than one whose lane quads read 64
+// address unit several times more than one whose lanes read whole rows of
 // contiguous bytes, so here each wave copies its K blocks into its own LDS
-// ring with global -> LDS DMA (16 rows x 64 bytes per instruction, the same
-// XOR swizzle as the large-tile kernel) and reads MFMA fragments from LDS.
-// The rings are private to their waves, so the main loop needs no barrier:
-// a wave waits only for its own DMA (vmcnt) and its own reads (lgkmcnt).
-// Rows past M or N are clamped (computed, never stored); K is split exactly.
-template <bool FP8, int TMW, int TNW, int D, int OUT_DT, bool GELU>
+// ring with global -> LDS DMA and reads MFMA fragments from LDS. BKB = 128
+// (K blocks of one whole 128-byte line per row, 8 rows per DMA instruction,
+// the large-tile kernel's swizzle) moves about twice the bytes per unit
+// time of BKB = 64 (half lines, 16 rows per instruction). The rings are
+// private to their waves, so the main loop needs no barrier: a wave waits
+// only for its own DMA (vmcnt) and its own reads (lgkmcnt). Rows past M or
+// N are clamped (computed, never stored); K is split exactly.
+template <int BKB>
+__device__ __forceinline__ int sm_swz(int row) {
+    if constexpr (BKB == 128)
+        return (row >> 1) & 7;
+    else
+        return swz_row(row);
+}
+
+template <bool FP8, int TMW, int TNW, int D, int OUT_DT, bool GELU, int BKB>
 __global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ as,
     const float* __restrict__ ws, const uint16_t* __restrict__ bias, void* __restrict__ out, int M,
@@ -373,13 +383,16 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
     constexpr int NB = 32 * TNW;
     constexpr int NBLK = TMW * TNW;
     constexpr int ROWS = MB + NB;
-    constexpr int SLOT = ROWS * SM_KB;  // one K block of the tile's rows
-    constexpr int NDMA = ROWS / 16;     // DMA instructions per block
+    constexpr int CPR = BKB / 16;       // 16-byte chunks per row of a block
+    constexpr int RPI = 1024 / BKB;     // rows per DMA instruction
+    constexpr int SLOT = ROWS * BKB;    // one K block of the tile's rows
+    constexpr int NDMA = ROWS / RPI;    // DMA instructions per block
     constexpr int RING = D * SLOT;      // per wave
     constexpr int LDS_RING = NW * RING;
     constexpr int LDS_RED = 4 * NBLK * 4 * 64 * 16;
     constexpr int LDS_BYTES = LDS_RING > LDS_RED ? LDS_RING : LDS_RED;
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+    static_assert(MB % RPI == 0, "A rows fill whole DMA instructions");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
     const int tiles_m = (M + MB - 1) / MB;
@@ -397,27 +410,27 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
     sm_prefetch<TMW, TNW>(epi, as, ws, bias, m0, n0, M, N);
 
     // Block t of this wave is K block NW*t + wave. DMA instruction i fills
-    // slot rows 16i .. 16i+15 (A rows first, then W rows); lane -> row
-    // 16i + lane/4 at physical chunk lane%4.
-    const int T = K / (SM_KB * NW);
+    // slot rows RPI*i .. RPI*i + RPI-1 (A rows first, then W rows); lane ->
+    // row RPI*i + lane/CPR at physical chunk lane%CPR.
+    const int T = K / (BKB * NW);
     const uint8_t* src[NDMA];
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-        const int row = 16 * i + (lane >> 2);
-        const int c = (lane & 3) ^ swz_row(row);
+        const int row = RPI * i + lane / CPR;
+        const int c = (lane % CPR) ^ sm_swz<BKB>(row);
         const uint8_t* base;
-        if (16 * i < MB) {
+        if (RPI * i < MB) {
             const int gm = m0 + row < M ? m0 + row : M - 1;
             base = A + static_cast<int64_t>(gm) * K;
         } else {
             const int gn = n0 + row - MB < N ? n0 + row - MB : N - 1;
             base = W + static_cast<int64_t>(gn) * K;
         }
-        src[i] = base + wave * SM_KB + c * 16;
+        src[i] = base + wave * BKB + c * 16;
     }
     uint8_t* ring = lds + wave * RING;
     auto issue = [&](int t, int slot) {
-        const int64_t koff = static_cast<int64_t>(t) * (NW * SM_KB);
+        const int64_t koff = static_cast<int64_t>(t) * (NW * BKB);
         uint8_t* dst = ring + slot * SLOT;
 #pragma unroll
         for (int i = 0; i < NDMA; ++i)
@@ -434,18 +447,21 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
     auto frag = [&](const uint8_t* base, int row, int chunk) {
-        return *reinterpret_cast<const v4i*>(base + row * SM_KB + ((chunk ^ swz_row(row)) << 4));
+        return *reinterpret_cast<const v4i*>(base + row * BKB + ((chunk ^ sm_swz<BKB>(row)) << 4));
     };
+    // Lane half h takes chunks [h*CPR/2, (h+1)*CPR/2) of every row: int8
+    // steps of one chunk each, e4m3 steps of two (both operands alike, so
+    // each dot product covers every k of the block once).
     auto compute = [&](int slot) {
         const uint8_t* base = ring + slot * SLOT;
         if constexpr (!FP8) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
+            for (int s = 0; s < CPR / 2; ++s) {
                 v4i fa[TMW], fw[TNW];
 #pragma unroll
-                for (int i = 0; i < TMW; ++i) fa[i] = frag(base, 32 * i + r, 2 * h + s);
+                for (int i = 0; i < TMW; ++i) fa[i] = frag(base, 32 * i + r, (CPR / 2) * h + s);
 #pragma unroll
-                for (int j = 0; j < TNW; ++j) fw[j] = frag(base, MB + 32 * j + r, 2 * h + s);
+                for (int j = 0; j < TNW; ++j) fw[j] = frag(base, MB + 32 * j + r, (CPR / 2) * h + s);
 #pragma unroll
                 for (int i = 0; i < TMW; ++i)
 #pragma unroll
@@ -453,23 +469,27 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
                         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
             }
         } else {
-            v8i fa[TMW], fw[TNW];
 #pragma unroll
-            for (int i = 0; i < TMW; ++i) {
-                const v4i lo = frag(base, 32 * i + r, 2 * h), hi = frag(base, 32 * i + r, 2 * h + 1);
-                fa[i] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            for (int s = 0; s < CPR / 4; ++s) {
+                const int c0 = (CPR / 2) * h + 2 * s;
+                v8i fa[TMW], fw[TNW];
+#pragma unroll
+                for (int i = 0; i < TMW; ++i) {
+                    const v4i lo = frag(base, 32 * i + r, c0), hi = frag(base, 32 * i + r, c0 + 1);
+                    fa[i] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                }
+#pragma unroll
+                for (int j = 0; j < TNW; ++j) {
+                    const v4i lo = frag(base, MB + 32 * j + r, c0), hi = frag(base, MB + 32 * j + r, c0 + 1);
+                    fw[j] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                }
+#pragma unroll
+                for (int i = 0; i < TMW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TNW; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], 0, 0,
+                                                                                    0, 127, 0, 127);
             }
-#pragma unroll
-            for (int j = 0; j < TNW; ++j) {
-                const v4i lo = frag(base, MB + 32 * j + r, 2 * h), hi = frag(base, MB + 32 * j + r, 2 * h + 1);
-                fw[j] = (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            }
-#pragma unroll
-            for (int i = 0; i < TMW; ++i)
-#pragma unroll
-                for (int j = 0; j < TNW; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fw[j], fa[i], acc[i][j], 0, 0, 0,
-                                                                                127, 0, 127);
         }
     };
 
@@ -505,14 +525,14 @@ __global__ __launch_bounds__(SM_THR) void gemm_small_dma_kernel(
                                                m0, n0, M, N);
 }
 
-template <bool FP8, int TMW, int TNW, int D>
+template <bool FP8, int TMW, int TNW, int D, int BKB = SM_KB>
 hipError_t launch_small_dma(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
                             const uint16_t* bias, void* out, int out_dt, int gelu, hipStream_t stream) {
     const int tiles = ((M + 32 * TMW - 1) / (32 * TMW)) * ((N + 32 * TNW - 1) / (32 * TNW));
     const uint8_t* A = static_cast<const uint8_t*>(a);
     const uint8_t* Wq = static_cast<const uint8_t*>(w);
 #define QIMG_SMALL_DMA_LAUNCH(ODT, GL)                                                                            \
-    hipLaunchKernelGGL((gemm_small_dma_kernel<FP8, TMW, TNW, D, ODT, GL>), dim3(tiles), dim3(SM_THR), 0, stream, A, \
+    hipLaunchKernelGGL((gemm_small_dma_kernel<FP8, TMW, TNW, D, ODT, GL, BKB>), dim3(tiles), dim3(SM_THR), 0, stream, A, \
                        Wq, as, ws, bias, out, M, N, K)
     if (out_dt == QIMG_FP32) {
         if (gelu)
@@ -753,6 +773,10 @@ hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int
     if (!small_m_fits(M, N, K)) return hipErrorInvalidValue;
     // The LDS-staged kernels split K exactly over four waves.
     const bool lds_staged = (K % (SM_KB * (SM_THR / 64))) == 0;
+    // Whole-line K blocks where K is long (text fc2, K = 12288: 25.8 -> 20.7
+    // us at M = 256, in-process A/B, output identical); at K = 3072 they
+    // measured equal.
+    const bool whole_lines = (K % (128 * (SM_THR / 64))) == 0 && K >= 8192;
     if (variant == 3 && !fp8 && M <= GV_MAXM)
         return dispatch_gemv(act_q, act_scales, M, K,
                              GemvOut{static_cast<const uint8_t*>(w_q), w_scales, bias, out, N}, GemvOut{}, out_dtype,
@@ -763,6 +787,11 @@ hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int
                                                      out_dtype, gelu, stream)
                    : launch_small_dma<false, 1, 1, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
                                                       out_dtype, gelu, stream);
+    if (variant == 2 && whole_lines)
+        return fp8 ? launch_small_dma<true, 2, 2, 2, 128>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                          out_dtype, gelu, stream)
+                   : launch_small_dma<false, 2, 2, 2, 128>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
+                                                           out_dtype, gelu, stream);
     if (variant == 2 && lds_staged) {
         // two slots per wave (64 KB) leave room for two workgroups per CU
         // when there are enough tiles to use them
