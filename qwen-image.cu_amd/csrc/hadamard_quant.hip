@@ -312,6 +312,94 @@ __global__ __launch_bounds__(256) void fwht_quant_blocks_kernel(const InT* x, vo
         }
 }
 
+// LDS operations of one wave complete in order; this keeps the compiler
+// from moving a read of another lane's value above the write.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Rows of NB Hadamard blocks of 1024 values (K = 3072 linear inputs), one
+// wave per row and four rows per workgroup: with 4352 rows the whole
+// problem is about one round of rows, so the time is one row's latency, and
+// a wave-private row needs no workgroup barrier. Lane l transforms chunk l
+// (16 consecutive values) of each block in registers straight from the load
+// (stages 1-8), one radix-16 sweep through the wave's LDS buffer does
+// stages 16-128, and the last radix-4 sweep (stages 256, 512) leaves lane l
+// holding values l + 64 q + 256 i (q, i < 4) in registers until the row's
+// absmax is known. Each value sees the same butterfly stages in the same
+// order as in fwht_quant_rows_kernel.
+template <typename InT, RowOut OUT, int NB>
+__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(const InT* x, void* out,
+                                                                   float* __restrict__ scales, int M, int K,
+                                                                   float norm) {
+    constexpr int HBS = 1024;
+    constexpr int PADDED = HBS + HBS / 16;
+    __shared__ float lds_all[4 * PADDED];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= M) return;  // whole waves: no barrier below
+    float* lds = lds_all + wave * PADDED;
+    const InT* xin = x + static_cast<int64_t>(row) * K;
+
+    float v[NB][16];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load16<InT>(xin + b * HBS + 16 * lane, v[b]);
+    float amax = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        butterfly<4>(v[b]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lds[lds_pad(16 * lane + i)] = v[b][i];
+        wave_lds_order();
+        // stages 16-128: group lane = elements base + 16 i
+        {
+            const int base = (lane & 15) + ((lane >> 4) << 8);
+            float t[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t[i] = lds[lds_pad(base + (i << 4))];
+            butterfly<4>(t);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) lds[lds_pad(base + (i << 4))] = t[i];
+        }
+        wave_lds_order();
+        // stages 256, 512: groups lane + 64 q = elements (lane + 64 q) + 256 i
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float t[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t[i] = lds[lds_pad(lane + 64 * q + 256 * i)];
+            butterfly<2>(t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[b][4 * q + i] = t[i] * norm;
+                amax = fmaxf(amax, fabsf(v[b][4 * q + i]));
+            }
+        }
+        wave_lds_order();  // the next block's chunks overwrite the buffer
+    }
+    amax = wave_max_dpp(amax);
+    constexpr float QMAX = (OUT == RowOut::Int8) ? 127.0f : 448.0f;
+    if (lane == 0) scales[row] = amax / QMAX;
+    const float inv = (amax > 0.0f) ? QMAX / amax : 0.0f;
+    uint8_t* o = reinterpret_cast<uint8_t*>(out) + static_cast<int64_t>(row) * K + lane;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // four values 64 apart (q = 0..3) converted together
+            const float q0 = v[b][i] * inv, q1 = v[b][4 + i] * inv, q2 = v[b][8 + i] * inv, q3 = v[b][12 + i] * inv;
+            uint32_t w;
+            if constexpr (OUT == RowOut::Int8)
+                w = i8x4_rne_sat(q0, q1, q2, q3);
+            else
+                w = e4m3x4(q0, q1, q2, q3);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[b * HBS + 64 * c + 256 * i] = static_cast<uint8_t>(w >> (8 * c));
+        }
+}
+
 // The INT4 linear's input preparation (linear_forward_int4, cuda_kernels.cu:
 // 4378-4395 and 4452-4470): v = x / smooth[k] (apply_smooth_div, :2258-2264),
 // its bf16 copy for the low-rank branch, and the block FWHT of v for the
@@ -481,7 +569,30 @@ static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int
                               hipStream_t stream) {
     if (M == 0) return hipSuccess;
     const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
-    if constexpr (OUT != RowOut::Fp32) {
+    if constexpr (OUT == RowOut::Int8 || OUT == RowOut::Fp8) {
+        // rows of 1-4 Hadamard blocks of 1024 values: one wave per row
+        if (hbs == 1024 && K % 1024 == 0 && K / 1024 <= 4) {
+            const int blocks = (M + 3) / 4;
+            switch (K / 1024) {
+                case 1:
+                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 1>), dim3(blocks), dim3(256), 0, stream,
+                                       x, out, scales, M, K, norm);
+                    break;
+                case 2:
+                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 2>), dim3(blocks), dim3(256), 0, stream,
+                                       x, out, scales, M, K, norm);
+                    break;
+                case 3:
+                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 3>), dim3(blocks), dim3(256), 0, stream,
+                                       x, out, scales, M, K, norm);
+                    break;
+                default:
+                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 4>), dim3(blocks), dim3(256), 0, stream,
+                                       x, out, scales, M, K, norm);
+                    break;
+            }
+            return hipGetLastError();
+        }
         // rows of 2-4 Hadamard blocks of 4096 values: block by block
         const int nb = K / 4096;
         if (hbs == 4096 && nb >= 2 && nb <= 4 && nb * 4096 == K) {

@@ -68,6 +68,33 @@ def test_activation_quant_4096_blocks_bit_exact(qimg, oracle, M, K, in_bf16, fp8
     np.testing.assert_array_equal(q.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
 
 
+@pytest.mark.parametrize("M,K,in_bf16,fp8", [
+    (5, 1024, False, False),      # one 1024-block per row
+    (7, 2048, True, True),
+    (4353, 3072, True, True),     # rows not a multiple of four
+    (2, 4096, True, False),       # four blocks
+    (9, 4096, False, True),
+])
+def test_activation_quant_1024_blocks_bit_exact(qimg, oracle, M, K, in_bf16, fp8):
+    """Rows of 1-4 Hadamard blocks of 1024 (one wave per row)."""
+    rng = np.random.default_rng(M * 5 + K + fp8)
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
+    x[M - 1, :] = 0.0  # an all-zero row: scale 0, all-zero values
+    mode = qimg.FP8_HADAMARD if fp8 else qimg.INT8_HADAMARD
+    ref = oracle.quantize_activation_fp8 if fp8 else oracle.quantize_activation
+    if in_bf16:
+        bits = oracle.bf16_bits_from_f32(x)
+        q_ref, s_ref = ref(bits, 1024)
+        xd = _bf16_dev(bits)
+    else:
+        q_ref, s_ref = ref(x, 1024)
+        xd = torch.from_numpy(x).to(DEV)
+    q, s = qimg.quantize_activation_hadamard(xd, 1024, mode=mode)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(q.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
+
+
 @pytest.mark.parametrize("M,K", [(128, 3072), (16, 12288), (3, 64)])
 def test_activation_quant_fp8_bit_exact(qimg, oracle, M, K):
     rng = np.random.default_rng(K + 7)
