@@ -45,6 +45,7 @@
 // 64-byte k-steps). Both operands use the same assignment, so each dot
 // product covers every k exactly once and the int8 result is exact.
 #include <atomic>
+#include <type_traits>
 
 #include "qimg_device.h"
 #include "qimg_internal.h"
@@ -73,8 +74,10 @@ constexpr int OP_BYTES = BM * BK;              // one operand's share of a stage
 // operands' DMAs interleaved.)
 constexpr int LDS_BYTES = 2 * NSLOT * OP_BYTES;
 // Epilogue scales and bias reuse the end of the ring once the main loop is
-// done (the bf16 output staging uses its start).
+// done (the output staging uses its start: 8 waves x 32 rows x 272 bytes).
 constexpr int SCALE_OFF = LDS_BYTES - 4 * 256 * 4;  // as, ws, bias, gate
+static_assert(NWAVES * 32 * (BN / WAVES_N * 4 + 16) <= SCALE_OFF, "output staging overlaps the scales");
+static_assert(2 * NDMA == TM * TN, "the int8 loop issues one refill DMA per MFMA of a k-step");
 constexpr int GROUP_M = 4;  // tile rows per group in the tile order
 // Cache policy of the operand DMA: sc0 (measured ~10% faster than the
 // default policy at the MMDiT shapes; the non-temporal policy is slower).
@@ -209,12 +212,11 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
 
     const int KT = K / BK;
 
-    // A stage past the end of K refetches the last one into an idle slot
-    // (the e4m3 loop issues them; the int8 loop refills nothing in its last
-    // two stages, which measured 1-2% faster for int8 and 2-3% slower for
-    // e4m3, whose schedule the branch disturbs).
+    // Both loops run their last two stages as a separate copy of the stage
+    // body with no refill, so no stage is fetched twice and no branch
+    // separates the refill DMAs from the MFMAs they are interleaved with.
     auto issue_stage = [&](int kt, int slot) {
-        kt = kt < KT ? kt : KT - 1;
+        kt = kt < KT ? kt : KT - 1;  // (the prologue's stage 1 when K is one stage)
         const int koff = kt * BK;
         uint8_t* abase = lds + slot * OP_BYTES;
         uint8_t* wbase = lds + (NSLOT + slot) * OP_BYTES;
@@ -294,8 +296,13 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
             SGB(SG_MFMA, TM * TN - (TM + TN));
             __builtin_amdgcn_sched_barrier(0);
         };
-        read_frags(fa0, fw0, 0, 0);
-        for (int kt = 0; kt < KT; ++kt) {
+        // One stage; REFILL (a std::bool_constant) says whether it refills
+        // its slot with stage kt + 2. The last two stages take the copy
+        // without it, so no branch separates the refill DMAs from the MFMAs
+        // and they are issued one after each MFMA of the last k-step instead
+        // of all at once after the barrier, where eight waves' 64 DMAs queue
+        // in front of the matrix core (measured 1-3% faster).
+        auto stage = [&](int kt, auto refill) {
             const int slot = kt & 1;
             read_frags(fa1, fw1, slot, 1);
             mfma_all(fa0, fw0);
@@ -307,12 +314,27 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
             mfma_all(fa0, fw0);
             interleave();
             handoff();
-            if (kt + 2 < KT) issue_stage(kt + 2, slot);
+            if constexpr (decltype(refill)::value) issue_stage(kt + 2, slot);
+            // (the compiler keeps these reads after the refill DMAs, which
+            // write LDS)
             read_frags(fa0, fw0, slot ^ 1, 0);
             mfma_all(fa1, fw1);
-            SGB(SG_VMEM, 2 * NDMA);
-            interleave();
-        }
+            if constexpr (decltype(refill)::value) {
+#pragma unroll
+                for (int i = 0; i < TM * TN; ++i) {
+                    SGB(SG_MFMA, 1);
+                    SGB(SG_VMEM, 2 * NDMA / (TM * TN));
+                    if (i < TM + TN) SGB(SG_DS_READ, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                interleave();
+            }
+        };
+        read_frags(fa0, fw0, 0, 0);
+        int kt = 0;
+        for (; kt + 2 < KT; ++kt) stage(kt, std::true_type{});
+        for (; kt < KT; ++kt) stage(kt, std::false_type{});
     } else {
         // Two 64-byte k-steps per stage (v_mfma_scale_f32_32x32x64_f8f6f4,
         // unit scales), with the same read-ahead and hand-off.
@@ -351,34 +373,41 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
             SGB(SG_MFMA, TM * TN - (TM + TN));
             __builtin_amdgcn_sched_barrier(0);
         };
-        read_frags(fa0, fw0, 0, 0);
-        for (int kt = 0; kt < KT; ++kt) {
+        auto stage = [&](int kt, auto refill) {
             const int slot = kt & 1;
             read_frags(fa1, fw1, slot, 1);
             mfma_all(fa0, fw0);
             interleave();
             handoff();
-            issue_stage(kt + 2, slot);
+            if constexpr (decltype(refill)::value) issue_stage(kt + 2, slot);
             read_frags(fa0, fw0, slot ^ 1, 0);
             mfma_all(fa1, fw1);
             // the refill DMAs spread over the first MFMAs (measured 2-5%
             // faster than issuing them all before the first MFMA)
+            if constexpr (decltype(refill)::value) {
 #pragma unroll
-            for (int i = 0; i < TM + TN; ++i) {
+                for (int i = 0; i < TM + TN; ++i) {
+                    SGB(SG_MFMA, 1);
+                    SGB(SG_VMEM, 1);
+                    SGB(SG_DS_READ, 2);
+                }
                 SGB(SG_MFMA, 1);
                 SGB(SG_VMEM, 1);
-                SGB(SG_DS_READ, 2);
+                SGB(SG_MFMA, 1);
+                SGB(SG_VMEM, 1);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                interleave();
             }
-            SGB(SG_MFMA, 1);
-            SGB(SG_VMEM, 1);
-            SGB(SG_MFMA, 1);
-            SGB(SG_VMEM, 1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        };
+        read_frags(fa0, fw0, 0, 0);
+        int kt = 0;
+        for (; kt + 2 < KT; ++kt) stage(kt, std::true_type{});
+        for (; kt < KT; ++kt) stage(kt, std::false_type{});
     }
 
-    // Drain the e4m3 loop's past-the-end refills and wait for every wave to
-    // leave the ring, then publish the epilogue operands in ring space.
+    // Wait for every wave to leave the ring, then publish the epilogue
+    // operands in ring space.
     wait_vmcnt<0>();
     __syncthreads();
     if (tid < 256) {
@@ -399,12 +428,14 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     // edge tiles still store whole 4-column groups with one vector store
     // when the row is in range (rows past M are skipped below)
     const bool vec_n = (N & 3) == 0;
-    if (interior && OUT_DT == QIMG_BF16) {  // (no gate with bf16 outputs)
-        // Interior bf16 tiles: each wave stages one 32x128 block at a time in a
-        // private LDS buffer (rows padded by 16 bytes: conflict-free for both
-        // the row-per-lane writes and the row-major reads), then stores it
-        // row-contiguously, 1 KB per store instruction. (For fp32 outputs the
-        // direct 16-byte stores below measured faster.)
+    if (interior && (OUT_DT == QIMG_BF16 || !has_gate)) {  // (no gate with bf16 outputs)
+        // Interior tiles without a gated residual: each wave stages one
+        // 32-row block at a time in a private LDS buffer (rows padded by 16
+        // bytes: conflict-free for both the row-per-lane writes and the
+        // row-major reads), then stores it row-contiguously, 1 KB (eight whole
+        // 128-byte lines) per store instruction. The direct stores below touch
+        // 32 rows per instruction; staging measured 3-6% faster for the whole
+        // fp32 GEMM at K = 3072, bit-identical.
         constexpr int ESZ = (OUT_DT == QIMG_FP32) ? 4 : 2;
         constexpr int ROWB = WTN * ESZ;
         constexpr int PITCH = ROWB + 16;
