@@ -413,7 +413,9 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     if (tid < 256) {
         s_as[tid] = e_as;
         s_ws[tid] = e_ws;
-        s_bias[tid] = has_bias ? bf16_to_f32(e_braw) : 0.0f;
+        // an absent bias is -0.0f: adding it leaves every value unchanged
+        // (-0.0 included), so the epilogue adds it without a select
+        s_bias[tid] = has_bias ? bf16_to_f32(e_braw) : -0.0f;
         s_gate[tid] = e_gate;
     }
     __syncthreads();
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                         {
 #pragma clang fp contract(off)
                             t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[j][4 * g + c];
-                            if (has_bias) t = t + bv[j][4 * g + c];
+                            t = t + bv[j][4 * g + c];
                         }
                         if (GELU) t = gelu_tanh_fast(t);
                         v[c] = t;
@@ -543,7 +545,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                     {
 #pragma clang fp contract(off)
                         t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[4 * g + c];
-                        if (has_bias) t = t + bv[4 * g + c];
+                        t = t + bv[4 * g + c];
                     }
                     if (GELU) t = gelu_tanh_fast(t);
                     if (OUT_DT == QIMG_FP32 && has_gate) t = __builtin_fmaf(gv[4 * g + c], t, res[i][g][c]);
