@@ -389,6 +389,12 @@ hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const ui
     const bool xf32 = x_dtype == QIMG_FP32;
     const int64_t xbytes = static_cast<int64_t>(M) * K * (xf32 ? 4 : 2);
     const int64_t wbytes = static_cast<int64_t>(N) * K * 2;
+    // Large problems with bf16 x (the INT4 linear's residual GEMM at 4096
+    // tokens): the quantized linear's 256x256 tiles with bf16 MFMA.
+    const int64_t tiles256 = static_cast<int64_t>((M + 255) / 256) * ((N + 255) / 256);
+    if (!xf32 && (K % 64) == 0 && tiles256 >= 128)
+        return launch_gemm_bf16_large(static_cast<const uint16_t*>(x), M, K, w, N, bias, out, gelu, accumulate,
+                                      stream);
     const bool tiled = (K % BF_KB) == 0 && xbytes < (int64_t{1} << 31) && wbytes < (int64_t{1} << 31);
     if (!tiled) {
         const int64_t total = static_cast<int64_t>(M) * N;

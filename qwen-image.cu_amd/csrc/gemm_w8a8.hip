@@ -102,15 +102,23 @@ constexpr int SG_DS_READ = 0x100;
 #define SGB(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
 
 
-template <bool FP8>
-struct Acc;
-template <>
-struct Acc<false> {
-    typedef v16i type;
+// Operand kinds: int8 (v_mfma_i32_32x32x32_i8), e4m3
+// (v_mfma_scale_f32_32x32x64_f8f6f4) and bf16 (v_mfma_f32_32x32x16_bf16;
+// a 32-byte k-step is 16 bf16, so the int8 loop, ring and fragment layout
+// serve it unchanged with K counted in bytes).
+constexpr int OP_I8 = 0;
+constexpr int OP_F8 = 1;
+constexpr int OP_BF16 = 2;
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+template <int OP>
+struct Acc {
+    typedef v16f type;
 };
 template <>
-struct Acc<true> {
-    typedef v16f type;
+struct Acc<OP_I8> {
+    typedef v16i type;
 };
 
 // One GEMM of a launch: out[M,N] = epilogue(A[M,K] . W[N,K]^T), `tiles` =
@@ -123,11 +131,14 @@ struct TileProblem {
     const uint16_t* bias;
     void* out;
     const float* gate;  // non-null: out = out + gate[n] * value (fp32 out)
-    int M, N, K, tiles;
+    int M, N, K, tiles;  // K in bytes
+    int accumulate;      // bf16 operands: out = out + product before the bias (fp32 out)
 };
 
-template <bool FP8, int OUT_DT, bool GELU>
+template <int OP, int OUT_DT, bool GELU>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, TileProblem p1) {
+    constexpr bool FP8 = OP == OP_F8;
+    constexpr bool BF = OP == OP_BF16;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
     float* s_ws = s_as + 256;
@@ -147,6 +158,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     const uint16_t* __restrict__ bias = second ? p1.bias : p0.bias;
     void* __restrict__ out = second ? p1.out : p0.out;
     const float* __restrict__ gate = second ? p1.gate : p0.gate;
+    const bool accumulate = BF && (second ? p1.accumulate : p0.accumulate);
     const int M = second ? p1.M : p0.M;
     const int N = second ? p1.N : p0.N;
     const int K = second ? p1.K : p0.K;
@@ -178,11 +190,17 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     // branch-free so it stays in flight behind the DMA stream)
     const int et = tid & 255;  // threads 0..255 own one row / column each
     const int e_n = n0 + et < N ? n0 + et : N - 1;
-    const float e_as = as[m0 + et < M ? m0 + et : M - 1];
-    const float e_ws = ws[e_n];
-    const uint16_t* bsrc = has_bias ? bias : reinterpret_cast<const uint16_t*>(ws);
-    const uint16_t e_braw = bsrc[e_n];
-    const float e_gate = (has_gate ? gate : ws)[e_n];
+    float e_as = 1.0f, e_ws = 1.0f, e_gate = 0.0f;
+    uint16_t e_braw = 0;
+    if constexpr (BF) {  // (no scales or gate with bf16 operands)
+        if (has_bias) e_braw = bias[e_n];
+    } else {
+        e_as = as[m0 + et < M ? m0 + et : M - 1];
+        e_ws = ws[e_n];
+        const uint16_t* bsrc = has_bias ? bias : reinterpret_cast<const uint16_t*>(ws);
+        e_braw = bsrc[e_n];
+        e_gate = (has_gate ? gate : ws)[e_n];
+    }
 
     // DMA assignment: wave w, instruction i fills LDS rows
     // DMA_ROWS*(NWAVES*i + w) .. +DMA_ROWS of the A tile (and the same rows
@@ -201,7 +219,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
         w_src[i] = W + static_cast<int64_t>(gn) * K + c * 16;
     }
 
-    typedef typename Acc<FP8>::type acc_t;
+    typedef typename Acc<OP>::type acc_t;
     acc_t acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -284,8 +302,14 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TN; ++j) {
+                    if constexpr (BF)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, fw[j]),
+                                                                             __builtin_bit_cast(v8bf, fa[i]),
+                                                                             acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[j], fa[i], acc[i][j], 0, 0, 0);
+                }
         };
         auto interleave = [&]() {
 #pragma unroll
@@ -430,7 +454,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
     // edge tiles still store whole 4-column groups with one vector store
     // when the row is in range (rows past M are skipped below)
     const bool vec_n = (N & 3) == 0;
-    if (interior && (OUT_DT == QIMG_BF16 || !has_gate)) {  // (no gate with bf16 outputs)
+    if (interior && (OUT_DT == QIMG_BF16 || !has_gate) && !accumulate) {  // (no gate with bf16 outputs)
         // Interior tiles without a gated residual: each wave stages one
         // 32-row block at a time in a private LDS buffer (rows padded by 16
         // bytes: conflict-free for both the row-per-lane writes and the
@@ -464,12 +488,17 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         float t;
-                        {
+                        if constexpr (BF) {
+                            t = acc[i][j][4 * g + c] + bv[j][4 * g + c];
+                            if (GELU) t = gelu_tanh(t);
+                        } else {
+                            {
 #pragma clang fp contract(off)
-                            t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[j][4 * g + c];
-                            t = t + bv[j][4 * g + c];
+                                t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[j][4 * g + c];
+                                t = t + bv[j][4 * g + c];
+                            }
+                            if (GELU) t = gelu_tanh_fast(t);
                         }
-                        if (GELU) t = gelu_tanh_fast(t);
                         v[c] = t;
                     }
                     uint8_t* dst = stage + row * PITCH + (j * 32 + 8 * g + 4 * half) * ESZ;
@@ -510,10 +539,11 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
                 bv[4 * g + c] = s_bias[nl];
                 gv[4 * g + c] = s_gate[nl];
             }
-        // Gated residual (gate_add_fp32f, cuda_kernels.cu:2181-2189): the
-        // tile's residual values are all loaded before its first store.
+        // Gated residual (gate_add_fp32f, cuda_kernels.cu:2181-2189), or the
+        // values a bf16 product accumulates onto: the tile's old values are
+        // all loaded before its first store.
         v4f res[TM][4];
-        if (OUT_DT == QIMG_FP32 && has_gate) {
+        if (OUT_DT == QIMG_FP32 && (has_gate || accumulate)) {
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int m = m0 + wm * WTM + i * 32 + (lane & 31);
@@ -542,13 +572,22 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblem p0, Tile
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     float t;
-                    {
-#pragma clang fp contract(off)
-                        t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[4 * g + c];
+                    if constexpr (BF) {
+                        // (linear_forward_bf16 order: GEMM with beta = 1,
+                        // then bias_add_fp32, then gelu_fp32)
+                        t = acc[i][j][4 * g + c];
+                        if (OUT_DT == QIMG_FP32 && accumulate) t = t + res[i][g][c];
                         t = t + bv[4 * g + c];
+                        if (GELU) t = gelu_tanh(t);
+                    } else {
+                        {
+#pragma clang fp contract(off)
+                            t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[4 * g + c];
+                            t = t + bv[4 * g + c];
+                        }
+                        if (GELU) t = gelu_tanh_fast(t);
+                        if (OUT_DT == QIMG_FP32 && has_gate) t = __builtin_fmaf(gv[4 * g + c], t, res[i][g][c]);
                     }
-                    if (GELU) t = gelu_tanh_fast(t);
-                    if (OUT_DT == QIMG_FP32 && has_gate) t = __builtin_fmaf(gv[4 * g + c], t, res[i][g][c]);
                     v[c] = t;
                 }
                 if (OUT_DT == QIMG_FP32) {
@@ -628,9 +667,9 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
     }
 }
 
-template <bool FP8, int OUT_DT, bool GELU>
+template <int OP, int OUT_DT, bool GELU>
 hipError_t launch_tiled(const TileProblem& p0, const TileProblem& p1, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_w8a8_kernel<FP8, OUT_DT, GELU>), dim3(p0.tiles + p1.tiles), dim3(NTHR), 0, stream, p0,
+    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU>), dim3(p0.tiles + p1.tiles), dim3(NTHR), 0, stream, p0,
                        p1);
     return hipGetLastError();
 }
@@ -638,18 +677,33 @@ hipError_t launch_tiled(const TileProblem& p0, const TileProblem& p1, hipStream_
 TileProblem tile_problem(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
                          const uint16_t* bias, void* out, const float* gate) {
     return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, gate, M, N, K,
-            ((M + BM - 1) / BM) * ((N + BN - 1) / BN)};
+            ((M + BM - 1) / BM) * ((N + BN - 1) / BN), 0};
 }
 
 template <bool FP8>
 hipError_t dispatch_tiled(const TileProblem& p0, const TileProblem& p1, int out_dt, int gelu, hipStream_t stream) {
+    constexpr int OP = FP8 ? OP_F8 : OP_I8;
     if (out_dt == QIMG_FP32)
-        return gelu ? launch_tiled<FP8, QIMG_FP32, true>(p0, p1, stream)
-                    : launch_tiled<FP8, QIMG_FP32, false>(p0, p1, stream);
-    return gelu ? launch_tiled<FP8, QIMG_BF16, true>(p0, p1, stream) : launch_tiled<FP8, QIMG_BF16, false>(p0, p1, stream);
+        return gelu ? launch_tiled<OP, QIMG_FP32, true>(p0, p1, stream)
+                    : launch_tiled<OP, QIMG_FP32, false>(p0, p1, stream);
+    return gelu ? launch_tiled<OP, QIMG_BF16, true>(p0, p1, stream) : launch_tiled<OP, QIMG_BF16, false>(p0, p1, stream);
 }
 
 }  // namespace
+
+// bf16 x [M, K] times w [N, K]^T into fp32 out with the large tiles (K %
+// 64 == 0), as linear_forward_bf16_bf16in computes it: out (+)= product,
+// then + bias, then GELU.
+hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias,
+                                  float* out, int gelu, int accumulate, hipStream_t stream) {
+    if (M == 0 || N == 0) return hipSuccess;
+    if ((K * 2) % BK != 0) return hipErrorInvalidValue;
+    TileProblem p0 = tile_problem(x, nullptr, M, K * 2, w, nullptr, N, bias, out, nullptr);
+    p0.accumulate = accumulate;
+    const TileProblem none{};
+    return gelu ? launch_tiled<OP_BF16, QIMG_FP32, true>(p0, none, stream)
+                : launch_tiled<OP_BF16, QIMG_FP32, false>(p0, none, stream);
+}
 
 static std::atomic<int> g_linear_kernel{QIMG_LINEAR_AUTO};
 

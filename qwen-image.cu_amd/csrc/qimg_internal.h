@@ -75,6 +75,12 @@ hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float*
 hipError_t launch_linear_bf16(const void* x, int x_dtype, int M, int K, const uint16_t* w, int N,
                               const uint16_t* bias, float* out, int gelu, hipStream_t stream, int accumulate = 0);
 
+// gemm_w8a8.hip: the same product for bf16 x with the 256x256 tiles of the
+// quantized linear (K % 64 == 0); launch_linear_bf16 takes it when the
+// problem has at least 128 such tiles.
+hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias,
+                                  float* out, int gelu, int accumulate, hipStream_t stream);
+
 // ---- INT4 paths (int4.hip, hadamard_quant.hip) ----
 hipError_t launch_dequant_int4_bf16(const uint8_t* qw, const float* scales, uint16_t* out, int N, int K, int gs,
                                     int nf4, int scales_gn, int signed_int4, hipStream_t stream);

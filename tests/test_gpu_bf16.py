@@ -31,6 +31,9 @@ LAYERS = [(4096, 3072, 64), (6889, 3072, 64), (13778, 3072, 64),
           (4096, 64, 3072), (6889, 64, 3072), (13778, 64, 3072)]
 # ragged tiles and K not a multiple of 32 (the one-thread-per-output kernel)
 RAGGED = [(7, 300, 96), (130, 70, 160), (33, 65, 32), (5, 17, 100), (3, 40, 8)]
+# bf16 x with at least 128 tiles of 256x256 (the large-tile kernel; the INT4
+# linear's residual GEMM): a full-tile shape and a ragged one
+LARGE = [(4096, 3072, 3072), (1000, 12288, 3072)]
 
 
 def _bf16_dev(bits):
@@ -41,7 +44,7 @@ def _rows(M, rng, k=48):
     return np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, k)]))
 
 
-@pytest.mark.parametrize("M,N,K", LAYERS + RAGGED)
+@pytest.mark.parametrize("M,N,K", LAYERS + RAGGED + LARGE)
 @pytest.mark.parametrize("x_fp32", [True, False])
 def test_linear_bf16_integer_operands_exact(qimg, oracle, M, N, K, x_fp32):
     rng = np.random.default_rng(M * 3 + N + K + x_fp32)
@@ -76,8 +79,10 @@ def test_linear_bf16_rounds_fp32_input_to_nearest_even(qimg, oracle, M, K):
     np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("M,N,K", LAYERS + RAGGED[:2])
-@pytest.mark.parametrize("x_fp32,gelu", [(True, False), (False, False), (True, True)])
+@pytest.mark.parametrize("M,N,K,x_fp32,gelu",
+                         [(M, N, K, xf, g) for (M, N, K) in LAYERS + RAGGED[:2]
+                          for (xf, g) in [(True, False), (False, False), (True, True)]]
+                         + [(M, N, K, False, g) for (M, N, K) in LARGE for g in (False, True)])
 def test_linear_bf16_random_vs_oracle(qimg, oracle, M, N, K, x_fp32, gelu):
     rng = np.random.default_rng(M + 7 * N + K + 2 * x_fp32 + gelu)
     g = torch.Generator(device=DEV).manual_seed(M + N + K)

@@ -230,6 +230,7 @@ def _int4_oracle(oracle, c, rows, N, K, r, gs, w4a4, nf4, hbs, gelu):
 
 @pytest.mark.parametrize("M,N,K,r,gs,w4a4,smooth,nf4,hbs,gelu", [
     (256, 3072, 3072, 32, 64, False, False, True, 1024, False),   # W4A16, NF4, Hadamard
+    (4096, 3072, 3072, 32, 64, False, True, True, 1024, True),    # W4A16 at 4096 tokens (large-tile residual)
     (300, 3072, 3072, 32, 64, False, True, False, 1024, True),    # linear INT4, smooth + Hadamard, GELU
     (64, 512, 1024, 16, 128, False, True, True, 1, False),        # smooth only
     (256, 3072, 3072, 32, 64, True, True, True, 1, False),        # W4A4 (nunchaku form)
