@@ -8,11 +8,15 @@ Workload (one "step"): the MMDiT MLP pair at M = 4352 tokens (4096 image +
     (+bias, bf16 out)
 with random N(0, 0.02) weights quantized by the library (W8A8 + Hadamard).
 Inputs are resident in HBM before timing. value = 2*M*N*K summed over both
-GEMMs (657.13 GOP) / measured time, in TFLOP/s (int8 ops).
+GEMMs (657.13 GOP) / measured time, in TFLOP/s (int8 ops). The K timed steps
+run twice: eagerly, with HIP events around each launch (the per-kernel
+times), then as K replays of the step captured in one HIP graph (the step
+time: the same launches without the host gaps between them; the output
+must equal the eager steps' bit for bit).
 
 Also printed in the same JSON line:
   roofline     the dominant kernel's achieved rate vs the int8 MFMA peak,
-               from HIP events recorded around each launch in the timed steps
+               from HIP events recorded around each launch in the eager steps
   cpu_baseline the CPU oracle (oracle/qimg_oracle.c, OpenMP) running the same
                MLP pair on the host cores
   extra        single linear (M=4096, 3072x3072), SageAttention (24 heads,
@@ -122,16 +126,16 @@ def main():
     s2 = torch.empty(M, dtype=torch.float32, device=dev)
     L = q.lib()
     stream = torch.cuda.current_stream(dev)
-    sp = q._stream(dev)
     P = q._ptr
 
+    # (the stream is read at each call, so the same launches can be captured)
     def quant(src, dt, K, hbs, dst, sc):
-        q._check(L.qimg_quantize_activation(P(src), dt, M, K, hbs, q.INT8_HADAMARD, P(dst), P(sc), sp))
+        q._check(L.qimg_quantize_activation(P(src), dt, M, K, hbs, q.INT8_HADAMARD, P(dst), P(sc), q._stream(dev)))
 
     def gemm(act, sc, w, bias, out, out_dt, gelu):
         q._check(L.qimg_linear_prequantized(P(act), P(sc), M, act.shape[1], P(w.data), P(w.scales),
                                             w.data.shape[0], q.INT8_HADAMARD, P(bias), P(out), out_dt,
-                                            gelu, sp))
+                                            gelu, q._stream(dev)))
 
     names = ["quant_fc1_in", "gemm_fc1", "quant_fc2_in", "gemm_fc2"]
     launches = [
@@ -173,9 +177,39 @@ def main():
     total_ms = start.elapsed_time(stop)
     # medians over the K timed steps (per step, and per launch)
     step_ms = [ev[i][0].elapsed_time(ev[i][len(launches)]) for i in range(K)]
-    ms_step = float(np.median(step_ms))
+    ms_step_eager = float(np.median(step_ms))
     per_kernel_ms = {n: float(np.median([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K)]))
                      for j, n in enumerate(names)}
+    y_eager = y.clone()
+
+    # ---- the same step as one HIP graph (the four launches without the host
+    # launch gaps between them), replayed K times with an event pair around
+    # each replay: ms_per_step and value are the median of these.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in launches:
+            f()
+    torch.cuda.synchronize()
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < min(args.ramp_s, 0.3):
+        for _ in range(20):
+            graph.replay()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    gev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        gev[i][0].record(stream)
+        graph.replay()
+        gev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall_graph = time.perf_counter() - t0
+    ms_step = float(np.median([a.elapsed_time(b) for a, b in gev]))
+    # every replay computes what the eager steps computed
+    graph_equals_eager = bool(torch.equal(y, y_eager))
+    del graph
     gemm_ops = 2.0 * M * D * H
     total_ops = 2 * gemm_ops
     value = total_ops / (ms_step * 1e-3) / 1e12
@@ -204,7 +238,10 @@ def main():
                 "avg_launch_ms": round(per_kernel_ms[dom], 4)}
 
     extra = {"per_kernel_ms_median": {k: round(v, 4) for k, v in per_kernel_ms.items()},
-             "ms_per_step_mean": round(total_ms / K, 4), "wall_s_timed": round(wall, 3)}
+             "step_timing": "median of K replays of the step captured as one HIP graph",
+             "ms_per_step_eager": round(ms_step_eager, 4), "ms_per_step_eager_mean": round(total_ms / K, 4),
+             "graph_equals_eager": graph_equals_eager,
+             "wall_s_timed_eager": round(wall, 3), "wall_s_timed_graph": round(wall_graph, 3)}
     if not args.no_extra:
         extra.update(_extra(q, torch, dev))
 
