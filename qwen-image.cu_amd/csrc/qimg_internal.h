@@ -61,6 +61,11 @@ struct LinearArgs {
 };
 hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
                               hipStream_t stream);
+// Up to six linears (same mode, output type and epilogue) in one launch of
+// the large tiles; hipErrorNotSupported (nothing launched) when they do not
+// all fit it or the kernel choice is forced.
+hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_dtype, int gelu,
+                               hipStream_t stream);
 hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
                                       const void* w_q, const float* w_scales, int N, int mode,
                                       const uint16_t* bias, void* out, int out_dtype, int gelu,
