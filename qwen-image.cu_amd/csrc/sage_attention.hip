@@ -324,138 +324,63 @@ __global__ __launch_bounds__(128) void quant_k_kernel(const uint16_t* __restrict
     }
 }
 
-// The joint block's Q straight from the text and image linears' fp32
-// outputs to int8: the RMSNorm + RoPE + fp16 of joint_heads_f16_kernel
-// (block_ops.hip), then quant_q_kernel, without the fp16 Q in HBM. A
-// workgroup owns one 128-token block of one head (quant_q_kernel's grid).
-// Phase 1: wave w takes tokens 32w .. 32w+31 one at a time with the heads
-// kernel's lane layout (lane l holds dims 2l, 2l+1; the same wave sum, FMAs
-// and fp16 rounding), writing the fp16 row to LDS. Phase 2: quant_q_kernel
-// reading those rows from LDS. The int8 values and scales are those of the
-// two kernels run one after the other. D = 128.
-constexpr int HQ_BATCH = 8;  // tokens whose loads a wave keeps in flight
-
-template <int HPW>
-__global__ __launch_bounds__(256) void heads_quant_q_kernel(const float* __restrict__ txt,
-                                                            const float* __restrict__ img,
-                                                            const uint16_t* __restrict__ w_txt,
-                                                            const uint16_t* __restrict__ w_img,
-                                                            const float* __restrict__ pe, int8_t* __restrict__ q_out,
-                                                            float* __restrict__ q_scale, int n_txt, int n_img, int H,
-                                                            float eps) {
-    constexpr int D = 128, HD = D / 2;
-    // fp16 pairs of the block's tokens; rows padded by one word, so the
-    // phase-2 reads (32 rows x 2 halves per wave instruction) hit 64 banks
-    __shared__ uint32_t rowbuf[HPW][QBLK][D / 2 + 1];
-    __shared__ float red[QBLK][2];
-    __shared__ float inv_s[32];
-    const int S = n_txt + n_img;
-    const int blk = blockIdx.x;
-    // heads hh0 .. hh0 + HPW - 1 of sequence b (H % HPW == 0): each token's
-    // pe row is loaded once for all of them
-    const int b = static_cast<int>(blockIdx.y) * HPW / H;
-    const int hh0 = static_cast<int>(blockIdx.y) * HPW - b * H;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    // phase 1
-    const uint32_t wpt = reinterpret_cast<const uint32_t*>(w_txt)[lane];
-    const uint32_t wpi = reinterpret_cast<const uint32_t*>(w_img)[lane];
-    for (int t0 = 0; t0 < 32; t0 += HQ_BATCH) {
-        float2 x[HPW][HQ_BATCH];
-        v4f p[HQ_BATCH];
+// K quant for head dim 128 with contiguous accesses: the 128 threads of a
+// (head, 64-token block) read the block's 16 KB in eight 2 KB steps, thread
+// t taking dims 8 (t % 16) .. +8 of tokens 8 c + t / 16 (c = 0..7). A
+// token's scale group (token % 8) / 2 is then t / 32: each group is one
+// half-wave, whose max needs lane exchanges only. Same per-element
+// arithmetic as quant_k_kernel (k - mean, max |.| from 1e-7, scale =
+// max / 127 + 1e-7, q = rne_sat(v * (1 / scale))).
+__global__ __launch_bounds__(128) void quant_k128_kernel(const uint16_t* __restrict__ k,
+                                                         const float* __restrict__ mean,
+                                                         int8_t* __restrict__ k_out,
+                                                         float* __restrict__ k_scale, int S) {
+    constexpr int D = 128;
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int t = threadIdx.x;
+    const int d0 = 8 * (t & 15);
+    const float* mu = mean + static_cast<int64_t>(h) * D + d0;
+    float m8[8];
 #pragma unroll
-        for (int k = 0; k < HQ_BATCH; ++k) {
-            const int tok = blk * QBLK + wave * 32 + t0 + k;
+    for (int e = 0; e < 8; ++e) m8[e] = mu[e];  // (the mean need not be 16-byte aligned)
+    const int64_t base = (static_cast<int64_t>(h) * S + b * KTILE) * D;
+    float v[8][8];
+    float amax = 0.0f;
 #pragma unroll
-            for (int hi = 0; hi < HPW; ++hi) x[hi][k] = make_float2(0.0f, 0.0f);
-            p[k] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-            if (tok < S) {
-                const float* row = tok < n_txt ? txt + (static_cast<int64_t>(b) * n_txt + tok) * H * D
-                                               : img + (static_cast<int64_t>(b) * n_img + tok - n_txt) * H * D;
+    for (int c = 0; c < 8; ++c) {
+        const int tok = b * KTILE + 8 * c + (t >> 4);
+        if (tok < S) {
+            const u32x4 r = *reinterpret_cast<const u32x4*>(k + base + (8 * c + (t >> 4)) * D + d0);
 #pragma unroll
-                for (int hi = 0; hi < HPW; ++hi) x[hi][k] = reinterpret_cast<const float2*>(row + (hh0 + hi) * D)[lane];
-                p[k] = reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(tok) * HD + lane];
+            for (int e = 0; e < 4; ++e) {
+                v[c][2 * e] = f16_to_f32(static_cast<uint16_t>(r[e] & 0xffffu)) - m8[2 * e];
+                v[c][2 * e + 1] = f16_to_f32(static_cast<uint16_t>(r[e] >> 16)) - m8[2 * e + 1];
             }
-        }
 #pragma unroll
-        for (int k = 0; k < HQ_BATCH; ++k) {
-            const int tl = wave * 32 + t0 + k;
-            const int tok = blk * QBLK + tl;
-            const uint32_t wp = tok < n_txt ? wpt : wpi;
-            const float w0 = bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
-            const float w1 = bf16_to_f32(static_cast<uint16_t>(wp >> 16));
-#pragma unroll
-            for (int hi = 0; hi < HPW; ++hi) {
-                float2 y = x[hi][k];
-                const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
-                const float rms = rsqrtf(ss / D + eps);
-                y.x = y.x * rms * w0;
-                y.y = y.y * rms * w1;
-                const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
-                const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
-                rowbuf[hi][tl][lane] =
-                    static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
-            }
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[c][e]));
         }
     }
-    __syncthreads();
-
-    // phase 2: quant_q_kernel on the LDS rows, one head at a time
-    for (int hi = 0; hi < HPW; ++hi) {
-        const int bh = static_cast<int>(blockIdx.y) * HPW + hi;
-        if (hi) __syncthreads();  // red / inv_s of the previous head are read
-        const int tok = blk * QBLK + (tid >> 1);
-        const int part = tid & 1;
-        const bool valid = tok < S;
-        uint32_t raw[HD / 2];
-        float amax = 0.0f;
-        if (valid) {
+    // max over the half-wave (the 16 tokens of scale group t / 32)
 #pragma unroll
-            for (int i = 0; i < HD / 2; ++i) raw[i] = rowbuf[hi][tid >> 1][part * (HD / 2) + i];
+    for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float a = fmaxf(1e-7f, amax);
+    const float scale = a / 127.0f + 1e-7f;
+    const int g = t >> 5;
+    if ((t & 31) == 0) k_scale[static_cast<int64_t>(h) * (div_up(S, KTILE) * 4) + b * 4 + g] = scale;
+    const float inv = 1.0f / scale;
 #pragma unroll
-            for (int i = 0; i < HD / 2; ++i) {
-                amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] & 0xffffu))));
-                amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i] >> 16))));
-            }
-        }
-        red[tid >> 1][part] = amax;
-        __syncthreads();
-        if (tid < 32) {
-            const int w = tid >> 3, g = tid & 7;
-            float a = 1e-7f;  // the reference starts its max at 1e-7
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int lt = w * 32 + g + 8 * i;
-                a = fmaxf(a, fmaxf(red[lt][0], red[lt][1]));
-            }
-            const float scale = a / 127.0f + 1e-7f;
-            const int nq = div_up(S, QBLK) * 32;
-            q_scale[static_cast<int64_t>(bh) * nq + blk * 32 + w * 8 + g] = scale;
-            inv_s[tid] = 1.0f / scale;
-        }
-        __syncthreads();
-        if (valid) {
-            const int lt = tid >> 1;
-            const float inv = inv_s[((lt % QBLK) / 32) * 8 + (lt & 7)];
-            int8_t* dst = q_out + (static_cast<int64_t>(bh) * S + tok) * D + part * HD;
-#pragma unroll
-            for (int c = 0; c < HD / 16; ++c) {
-                u32x4 pk;
-#pragma unroll
-                for (int wd = 0; wd < 4; ++wd) {
-                    const uint32_t r0 = raw[8 * c + 2 * wd], r1 = raw[8 * c + 2 * wd + 1];
-                    pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(r0 & 0xffffu)) * inv,
-                                          f16_to_f32(static_cast<uint16_t>(r0 >> 16)) * inv,
-                                          f16_to_f32(static_cast<uint16_t>(r1 & 0xffffu)) * inv,
-                                          f16_to_f32(static_cast<uint16_t>(r1 >> 16)) * inv);
-                }
-                reinterpret_cast<u32x4*>(dst)[c] = pk;
-            }
-        }
+    for (int c = 0; c < 8; ++c) {
+        const int tok = b * KTILE + 8 * c + (t >> 4);
+        if (tok >= S) continue;
+        uint2 pk;
+        pk.x = i8x4_rne_sat(v[c][0] * inv, v[c][1] * inv, v[c][2] * inv, v[c][3] * inv);
+        pk.y = i8x4_rne_sat(v[c][4] * inv, v[c][5] * inv, v[c][6] * inv, v[c][7] * inv);
+        *reinterpret_cast<uint2*>(k_out + base + (8 * c + (t >> 4)) * D + d0) = pk;
     }
 }
+
+constexpr int HQ_BATCH = 8;  // tokens whose loads a wave keeps in flight
 
 // ------------------------------------------------------------ V re-layout
 // V fp16 [BH][S][D] -> Vt [BH][ceil(S/64)][D][64]: for each 64-key tile the
@@ -939,6 +864,118 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     }
 }
 
+// The joint block's Q straight from the text and image linears' fp32
+// outputs to int8: the RMSNorm + RoPE + fp16 of joint_heads_f16_kernel
+// (block_ops.hip), then the Sage Q quantization of quant_q_kernel, without
+// the fp16 Q in HBM. One wave per (head, 32-token slice) and no workgroup
+// barriers: a Q scale group (tokens g, g + 8, g + 16, g + 24 of a slice)
+// never leaves its slice, so each wave quantizes its own. Phase 1 is the
+// heads kernel's per-token code (lane l holds dims 2l, 2l+1; the same wave
+// sum, FMAs and fp16 rounding) into a wave-private LDS buffer; in phase 2
+// lane 8g + j holds dims 16j .. +16 of group g's four tokens, and the
+// group's max is taken over its eight lanes. The int8 values and scales are
+// those of the two kernels run one after the other. (A workgroup per 128
+// tokens of two heads, with barriers between the phases, has half as many
+// waves in flight: the C4 block's qk_norm category measured 40 -> 35 us,
+// together with quant_k128_kernel for K.) D = 128.
+__global__ __launch_bounds__(256) void heads_quant_q_wave_kernel(const float* __restrict__ txt,
+                                                                 const float* __restrict__ img,
+                                                                 const uint16_t* __restrict__ w_txt,
+                                                                 const uint16_t* __restrict__ w_img,
+                                                                 const float* __restrict__ pe,
+                                                                 int8_t* __restrict__ q_out,
+                                                                 float* __restrict__ q_scale, int n_txt, int n_img,
+                                                                 int batch, int H, float eps) {
+    constexpr int D = 128, HD = D / 2, PITCH = HD + 1;
+    __shared__ uint32_t rows_all[4][32 * PITCH];
+    const int S = n_txt + n_img;
+    const int BH = batch * H;
+    const int nslice = div_up(S, QBLK) * 4;  // every slice of every 128-token block (their scales are written)
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int unit = blockIdx.x * 4 + wave;  // slice-major, head fastest: a workgroup's waves share pe rows
+    if (unit >= nslice * BH) return;         // whole waves; no barrier below
+    const int slice = unit / BH;
+    const int bh = unit - slice * BH;
+    const int b = bh / H, h = bh - b * H;
+    uint32_t* rows = rows_all[wave];
+
+    // phase 1
+    const uint32_t wpt = reinterpret_cast<const uint32_t*>(w_txt)[lane];
+    const uint32_t wpi = reinterpret_cast<const uint32_t*>(w_img)[lane];
+    for (int t0 = 0; t0 < 32; t0 += HQ_BATCH) {
+        float2 x[HQ_BATCH];
+        v4f p[HQ_BATCH];
+#pragma unroll
+        for (int k = 0; k < HQ_BATCH; ++k) {
+            const int tok = slice * 32 + t0 + k;
+            x[k] = make_float2(0.0f, 0.0f);
+            p[k] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+            if (tok < S) {
+                const float* row = tok < n_txt ? txt + (static_cast<int64_t>(b) * n_txt + tok) * H * D
+                                               : img + (static_cast<int64_t>(b) * n_img + tok - n_txt) * H * D;
+                x[k] = reinterpret_cast<const float2*>(row + h * D)[lane];
+                p[k] = reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(tok) * HD + lane];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < HQ_BATCH; ++k) {
+            const int tok = slice * 32 + t0 + k;
+            const uint32_t wp = tok < n_txt ? wpt : wpi;
+            const float w0 = bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
+            const float w1 = bf16_to_f32(static_cast<uint16_t>(wp >> 16));
+            float2 y = x[k];
+            const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
+            const float rms = rsqrtf(ss / D + eps);
+            y.x = y.x * rms * w0;
+            y.y = y.y * rms * w1;
+            const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
+            const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
+            rows[(t0 + k) * PITCH + lane] =
+                static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
+        }
+    }
+    // LDS operations of one wave complete in order; keep the compiler from
+    // moving the reads of other lanes' words above the writes
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+
+    // phase 2: group g = lane / 8, dims 16 j .. +16 with j = lane % 8
+    const int g = lane >> 3, j = lane & 7;
+    uint32_t raw[4][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            raw[i][c] = rows[(g + 8 * i) * PITCH + 8 * j + c];
+            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i][c] & 0xffffu))));
+            amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[i][c] >> 16))));
+        }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float a = fmaxf(1e-7f, amax);  // the reference starts its max at 1e-7
+    const float scale = a / 127.0f + 1e-7f;
+    const int nq = div_up(S, QBLK) * 32;
+    if (j == 0) q_scale[static_cast<int64_t>(bh) * nq + (slice >> 2) * 32 + (slice & 3) * 8 + g] = scale;
+    const float inv = 1.0f / scale;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = slice * 32 + g + 8 * i;
+        if (tok >= S) continue;
+        u32x4 pk;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            const uint32_t r0 = raw[i][2 * wd], r1 = raw[i][2 * wd + 1];
+            pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(r0 & 0xffffu)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r0 >> 16)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r1 & 0xffffu)) * inv,
+                                  f16_to_f32(static_cast<uint16_t>(r1 >> 16)) * inv);
+        }
+        *reinterpret_cast<u32x4*>(q_out + (static_cast<int64_t>(bh) * S + tok) * D + 16 * j) = pk;
+    }
+}
+
 template <int D, bool CAUSAL>
 hipError_t launch_attn_dt(const int8_t* q, const int8_t* k, const uint16_t* vt, const float* qs,
                           const float* ks, void* out, int out_dt, int BH, int S, float sm_log2,
@@ -1006,7 +1043,7 @@ hipError_t launch_sage_quant_k(const uint16_t* k, const float* mean, int8_t* k_o
                                float* k_scale, int BH, int S, int D, hipStream_t stream) {
     dim3 grid(div_up(S, KTILE), BH);
     if (D == 128)
-        hipLaunchKernelGGL(quant_k_kernel<128>, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
+        hipLaunchKernelGGL(quant_k128_kernel, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
     else
         hipLaunchKernelGGL(quant_k_kernel<64>, grid, dim3(128), 0, stream, k, mean, k_out, k_scale, S);
     return hipGetLastError();
@@ -1017,12 +1054,9 @@ hipError_t launch_heads_quant_q(const float* txt, const float* img, const uint16
                                 float eps, hipStream_t stream) {
     const int S = n_txt + n_img;
     if (S == 0 || batch == 0 || H == 0) return hipSuccess;
-    if (H % 2 == 0)
-        hipLaunchKernelGGL(heads_quant_q_kernel<2>, dim3(div_up(S, QBLK), batch * H / 2), dim3(256), 0, stream, txt,
-                           img, w_txt, w_img, pe, q_out, q_scale, n_txt, n_img, H, eps);
-    else
-        hipLaunchKernelGGL(heads_quant_q_kernel<1>, dim3(div_up(S, QBLK), batch * H), dim3(256), 0, stream, txt, img,
-                           w_txt, w_img, pe, q_out, q_scale, n_txt, n_img, H, eps);
+    const int64_t units = static_cast<int64_t>(div_up(S, QBLK)) * 4 * batch * H;
+    hipLaunchKernelGGL(heads_quant_q_wave_kernel, dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256), 0, stream,
+                       txt, img, w_txt, w_img, pe, q_out, q_scale, n_txt, n_img, batch, H, eps);
     return hipGetLastError();
 }
 
