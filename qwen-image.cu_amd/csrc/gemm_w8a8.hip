@@ -466,19 +466,36 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // edge tiles still store whole 4-column groups with one vector store
     // when the row is in range (rows past M are skipped below)
     const bool vec_n = (N & 3) == 0;
-    if (interior && (OUT_DT == QIMG_BF16 || !has_gate) && !accumulate) {  // (no gate with bf16 outputs)
-        // Interior tiles without a gated residual: each wave stages one
-        // 32-row block at a time in a private LDS buffer (rows padded by 16
-        // bytes: conflict-free for both the row-per-lane writes and the
-        // row-major reads), then stores it row-contiguously, 1 KB (eight whole
-        // 128-byte lines) per store instruction. The direct stores below touch
-        // 32 rows per instruction; staging measured 3-6% faster for the whole
-        // fp32 GEMM at K = 3072, bit-identical.
+    if (interior && (OUT_DT == QIMG_FP32 || !has_gate) && !accumulate) {  // (no gate with bf16 outputs)
+        // Interior tiles: each wave stages one 32-row block at a time in a
+        // private LDS buffer (rows padded by 16 bytes: conflict-free for both
+        // the row-per-lane writes and the row-major reads), then stores it
+        // row-contiguously, 1 KB (eight whole 128-byte lines) per store
+        // instruction. The direct stores below touch 32 rows per instruction;
+        // staging measured 3-6% faster for the whole fp32 GEMM at K = 3072,
+        // bit-identical. A gated residual is read the same way, row by row,
+        // each 32-row block's before its values are computed.
         constexpr int ESZ = (OUT_DT == QIMG_FP32) ? 4 : 2;
         constexpr int ROWB = WTN * ESZ;
         constexpr int PITCH = ROWB + 16;
         constexpr int CPR = ROWB / 16;  // 16-byte chunks per staged row
+        constexpr int NIT = 32 * CPR / 64;  // 16-byte chunks per lane per 32-row block
         uint8_t* stage = lds + wave * (32 * PITCH);
+        const bool gated = OUT_DT == QIMG_FP32 && has_gate;
+        auto block_base = [&](int i) {
+            return reinterpret_cast<uint8_t*>(out) +
+                   (static_cast<int64_t>(m0 + wm * WTM + i * 32) * N + n0 + wn * WTN) * ESZ;
+        };
+        v4f res[NIT];
+        auto load_res = [&](int i, v4f* r) {
+            const uint8_t* b = block_base(i);
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int idx = it * 64 + lane;
+                r[it] = *reinterpret_cast<const v4f*>(b + static_cast<int64_t>(idx / CPR) * N * ESZ + (idx % CPR) * 16);
+            }
+        };
+
         float wsv[TN][16], bv[TN][16];
 #pragma unroll
         for (int j = 0; j < TN; ++j)
@@ -491,6 +508,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         const int row = lane & 31;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
+            if (gated) load_res(i, res);
             const float sa = s_as[wm * WTM + i * 32 + row];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
@@ -523,15 +541,21 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             // LDS operations of one wave complete in order; the empty asm
             // keeps the compiler from moving the reads above the writes.
             asm volatile("" ::: "memory");
-            const int grow0 = m0 + wm * WTM + i * 32;
-            uint8_t* obase = reinterpret_cast<uint8_t*>(out) +
-                             (static_cast<int64_t>(grow0) * N + n0 + wn * WTN) * ESZ;
+            uint8_t* obase = block_base(i);
 #pragma unroll
-            for (int it = 0; it < 32 * CPR / 64; ++it) {
+            for (int it = 0; it < NIT; ++it) {
                 const int idx = it * 64 + lane;
                 const int r = idx / CPR;
                 const int c16 = idx % CPR;
-                const v4i val = *reinterpret_cast<const v4i*>(stage + r * PITCH + c16 * 16);
+                v4i val = *reinterpret_cast<const v4i*>(stage + r * PITCH + c16 * 16);
+                if (gated) {
+                    // gate_add_fp32f (cuda_kernels.cu:2181-2189): out + gate[n] * value
+                    const v4f t = __builtin_bit_cast(v4f, val);
+                    const v4f gv = *reinterpret_cast<const v4f*>(s_gate + wn * WTN + c16 * 4);
+                    const v4f rv = res[it];
+                    val = __builtin_bit_cast(v4i, (v4f){__builtin_fmaf(gv[0], t[0], rv[0]), __builtin_fmaf(gv[1], t[1], rv[1]),
+                                                        __builtin_fmaf(gv[2], t[2], rv[2]), __builtin_fmaf(gv[3], t[3], rv[3])});
+                }
                 *reinterpret_cast<v4i*>(obase + static_cast<int64_t>(r) * N * ESZ + c16 * 16) = val;
             }
             asm volatile("" ::: "memory");
