@@ -329,8 +329,40 @@ __device__ __forceinline__ void wave_lds_order() {
 // holding values l + 64 q + 256 i (q, i < 4) in registers until the row's
 // absmax is known. Each value sees the same butterfly stages in the same
 // order as in fwht_quant_rows_kernel.
-template <typename InT, RowOut OUT, int NB>
-__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(const InT* x, void* out,
+// Where a row's 16-value chunk c comes from: a row-major [M, K] matrix ...
+template <typename InT>
+struct RowsLoader {
+    const InT* x;
+    int K;
+    __device__ __forceinline__ void operator()(int row, int c, float* v) const {
+        load16<InT>(x + static_cast<int64_t>(row) * K + 16 * c, v);
+    }
+};
+// ... or the fp16 attention output [batch][H][S][128], read as the rows of
+// the out-projection's input (token s of sequence b: head h = c / 8, dims
+// 16 (c % 8) .. +16; the rows are tokens s0 .. s0 + n - 1 of each sequence).
+struct HeadsLoader {
+    const uint16_t* attn;
+    int S, H, s0, n;
+    __device__ __forceinline__ void operator()(int row, int c, float* v) const {
+        const int b = row / n;
+        const int s = s0 + row - b * n;
+        const uint16_t* src = attn + ((static_cast<int64_t>(b) * H + (c >> 3)) * S + s) * 128 + 16 * (c & 7);
+        const u32x4* q = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const u32x4 t = q[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[8 * j + 2 * e] = f16_to_f32(static_cast<uint16_t>(t[e] & 0xffffu));
+                v[8 * j + 2 * e + 1] = f16_to_f32(static_cast<uint16_t>(t[e] >> 16));
+            }
+        }
+    }
+};
+
+template <typename Loader, RowOut OUT, int NB>
+__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, void* out,
                                                                    float* __restrict__ scales, int M, int K,
                                                                    float norm) {
     constexpr int HBS = 1024;
@@ -341,11 +373,10 @@ __global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(const InT* x,
     const int row = blockIdx.x * 4 + wave;
     if (row >= M) return;  // whole waves: no barrier below
     float* lds = lds_all + wave * PADDED;
-    const InT* xin = x + static_cast<int64_t>(row) * K;
 
     float v[NB][16];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) load16<InT>(xin + b * HBS + 16 * lane, v[b]);
+    for (int b = 0; b < NB; ++b) ld(row, b * (HBS / 16) + lane, v[b]);
     float amax = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -564,6 +595,32 @@ static int ilog2(int v) {
 
 size_t rows_lds_bytes(int K) { return sizeof(float) * (static_cast<size_t>(K) + K / 16 + 1 + 8); }
 
+// Rows of 1-4 Hadamard blocks of 1024 (K / 1024 of them), one wave per row.
+template <RowOut OUT, typename Loader>
+static hipError_t launch_wave_rows(const Loader& ld, void* out, float* scales, int M, int K, float norm,
+                                   hipStream_t stream) {
+    const int blocks = (M + 3) / 4;
+    switch (K / 1024) {
+        case 1:
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 1>), dim3(blocks), dim3(256), 0, stream, ld,
+                               out, scales, M, K, norm);
+            break;
+        case 2:
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 2>), dim3(blocks), dim3(256), 0, stream, ld,
+                               out, scales, M, K, norm);
+            break;
+        case 3:
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 3>), dim3(blocks), dim3(256), 0, stream, ld,
+                               out, scales, M, K, norm);
+            break;
+        default:
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 4>), dim3(blocks), dim3(256), 0, stream, ld,
+                               out, scales, M, K, norm);
+            break;
+    }
+    return hipGetLastError();
+}
+
 template <typename InT, RowOut OUT>
 static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int K, int hbs,
                               hipStream_t stream) {
@@ -572,26 +629,7 @@ static hipError_t launch_rows(const InT* x, void* out, float* scales, int M, int
     if constexpr (OUT == RowOut::Int8 || OUT == RowOut::Fp8) {
         // rows of 1-4 Hadamard blocks of 1024 values: one wave per row
         if (hbs == 1024 && K % 1024 == 0 && K / 1024 <= 4) {
-            const int blocks = (M + 3) / 4;
-            switch (K / 1024) {
-                case 1:
-                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 1>), dim3(blocks), dim3(256), 0, stream,
-                                       x, out, scales, M, K, norm);
-                    break;
-                case 2:
-                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 2>), dim3(blocks), dim3(256), 0, stream,
-                                       x, out, scales, M, K, norm);
-                    break;
-                case 3:
-                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 3>), dim3(blocks), dim3(256), 0, stream,
-                                       x, out, scales, M, K, norm);
-                    break;
-                default:
-                    hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<InT, OUT, 4>), dim3(blocks), dim3(256), 0, stream,
-                                       x, out, scales, M, K, norm);
-                    break;
-            }
-            return hipGetLastError();
+            return launch_wave_rows<OUT>(RowsLoader<InT>{x, K}, out, scales, M, K, norm, stream);
         }
         // rows of 2-4 Hadamard blocks of 4096 values: block by block
         const int nb = K / 4096;
@@ -659,6 +697,13 @@ hipError_t launch_heads_fwht_quant(const uint16_t* attn, int batch, int H, int S
     threads = threads > 256 ? 256 : threads;
     const size_t lds = rows_lds_bytes(K);
     const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    // rows of 1-4 blocks of 1024 (the out-projection input, K = 3072): one
+    // wave per row, as for the activations in row-major layout
+    if (hbs == 1024 && K % 1024 == 0 && K / 1024 <= 4) {
+        const HeadsLoader ld{attn, S, H, s0, n};
+        return mode == QIMG_QM_FP8_HADAMARD ? launch_wave_rows<RowOut::Fp8>(ld, q_out, scales, M, K, norm, stream)
+                                            : launch_wave_rows<RowOut::Int8>(ld, q_out, scales, M, K, norm, stream);
+    }
     if (mode == QIMG_QM_FP8_HADAMARD)
         hipLaunchKernelGGL(heads_fwht_quant_kernel<RowOut::Fp8>, dim3(M), dim3(threads), lds, stream, attn, S, H, s0,
                            n, q_out, scales, ilog2(hbs), norm);
