@@ -329,33 +329,147 @@ __device__ __forceinline__ void wave_lds_order() {
 // holding values l + 64 q + 256 i (q, i < 4) in registers until the row's
 // absmax is known. Each value sees the same butterfly stages in the same
 // order as in fwht_quant_rows_kernel.
-// Where a row's 16-value chunk c comes from: a row-major [M, K] matrix ...
+// Where a row's 16-value chunk c comes from. fetch() issues the loads into
+// raw registers, unpack() turns them into fp32 once they are needed, so that
+// a wave can have its next row in flight while it transforms this one.
+// A row-major [M, K] matrix ...
 template <typename InT>
-struct RowsLoader {
-    const InT* x;
+struct RowsLoader;
+template <>
+struct RowsLoader<float> {
+    static constexpr bool kWholeRow = false;
+    typedef v4f Raw[4];
+    const float* x;
     int K;
-    __device__ __forceinline__ void operator()(int row, int c, float* v) const {
-        load16<InT>(x + static_cast<int64_t>(row) * K + 16 * c, v);
+    __device__ __forceinline__ void fetch(int row, int c, Raw& r) const {
+        const v4f* q = reinterpret_cast<const v4f*>(x + static_cast<int64_t>(row) * K + 16 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = q[j];
+    }
+    __device__ __forceinline__ static void unpack(const Raw& r, float* v) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[4 * j + 0] = r[j].x; v[4 * j + 1] = r[j].y; v[4 * j + 2] = r[j].z; v[4 * j + 3] = r[j].w;
+        }
+    }
+};
+template <>
+struct RowsLoader<uint16_t> {  // bf16
+    static constexpr bool kWholeRow = false;
+    typedef u32x4 Raw[2];
+    const uint16_t* x;
+    int K;
+    __device__ __forceinline__ void fetch(int row, int c, Raw& r) const {
+        const u32x4* q = reinterpret_cast<const u32x4*>(x + static_cast<int64_t>(row) * K + 16 * c);
+        r[0] = q[0];
+        r[1] = q[1];
+    }
+    __device__ __forceinline__ static void unpack(const Raw& r, float* v) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                v[8 * j + 2 * c + 0] = __uint_as_float(r[j][c] << 16);
+                v[8 * j + 2 * c + 1] = __uint_as_float(r[j][c] & 0xffff0000u);
+            }
     }
 };
 // ... or the fp16 attention output [batch][H][S][128], read as the rows of
 // the out-projection's input (token s of sequence b: head h = c / 8, dims
 // 16 (c % 8) .. +16; the rows are tokens s0 .. s0 + n - 1 of each sequence).
 struct HeadsLoader {
+    static constexpr bool kWholeRow = false;
+    typedef u32x4 Raw[2];
     const uint16_t* attn;
     int S, H, s0, n;
-    __device__ __forceinline__ void operator()(int row, int c, float* v) const {
+    __device__ __forceinline__ void fetch(int row, int c, Raw& r) const {
         const int b = row / n;
         const int s = s0 + row - b * n;
         const uint16_t* src = attn + ((static_cast<int64_t>(b) * H + (c >> 3)) * S + s) * 128 + 16 * (c & 7);
         const u32x4* q = reinterpret_cast<const u32x4*>(src);
+        r[0] = q[0];
+        r[1] = q[1];
+    }
+    __device__ __forceinline__ static void unpack(const Raw& r, float* v) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const u32x4 t = q[j];
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                v[8 * j + 2 * e] = f16_to_f32(static_cast<uint16_t>(t[e] & 0xffffu));
-                v[8 * j + 2 * e + 1] = f16_to_f32(static_cast<uint16_t>(t[e] >> 16));
+                v[8 * j + 2 * e] = f16_to_f32(static_cast<uint16_t>(r[j][e] & 0xffffu));
+                v[8 * j + 2 * e + 1] = f16_to_f32(static_cast<uint16_t>(r[j][e] >> 16));
+            }
+    }
+};
+
+// The 16-lane rows of a wave reduced with the first four levels of
+// wave_reduce_dpp (pairs, quads, eights, sixteens of lanes).
+__device__ __forceinline__ float row16_sum_dpp(float v) {
+    v = v + dpp32<0xB1>(v);
+    v = v + dpp32<0x4E>(v);
+    v = v + dpp32<0x141>(v);
+    v = v + dpp32<0x140>(v);
+    return v;
+}
+
+// ... or the LayerNorm + modulate of a row-major fp32 [M, K] matrix
+// (K = 1024 NB), normalized as a whole row (finish_row) before the
+// transform. The arithmetic is ln_modulate_row's, in its order: its thread
+// t = 4 lane + e holds float4 chunks t + 256 j, which are quarter e of this
+// lane's 16-value chunk j, so each lane keeps that thread's partial sums for
+// e = 0..3 (the same loop, including the zero chunks up to LN_MAXV). Its
+// reduction tree over 64 lanes is, level by level, the two lowest levels
+// inside this lane and the next four across this wave's 16-lane row w
+// (which stands for its wave w); the four row totals are then added in
+// order from zero, as its wave totals are.
+struct LnLoader : RowsLoader<float> {
+    static constexpr bool kWholeRow = true;
+    const float* shift;
+    const float* scale;
+    float eps;
+    __device__ __forceinline__ static float total(float part) {
+        const float r = row16_sum_dpp(part);
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < LN_THR / 64; ++w)
+            t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 16 * w));
+        return t;
+    }
+    template <int NB>
+    __device__ __forceinline__ void finish_row(int lane, float (&v)[NB][16]) const {
+#pragma clang fp contract(off)
+        static_assert(NB <= LN_MAXV && LN_THR == 256, "ln_modulate_row's thread layout");
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < LN_MAXV; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (j < NB)
+                    s[e] += (v[j][4 * e] + v[j][4 * e + 1]) + (v[j][4 * e + 2] + v[j][4 * e + 3]);
+                else
+                    s[e] += 0.0f;  // a chunk past the row reads as zeros there
+            }
+        const float mean = total((s[0] + s[1]) + (s[2] + s[3])) / K;
+        float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const v4f d = (v4f){v[j][4 * e], v[j][4 * e + 1], v[j][4 * e + 2], v[j][4 * e + 3]} - mean;
+                q[e] += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+        const float inv_std = rsqrtf(total((q[0] + q[1]) + (q[2] + q[3])) / K + eps);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const v4f* sh = reinterpret_cast<const v4f*>(shift + j * 1024 + 16 * lane);
+            const v4f* sc = reinterpret_cast<const v4f*>(scale + j * 1024 + 16 * lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const v4f xv = (v4f){v[j][4 * e], v[j][4 * e + 1], v[j][4 * e + 2], v[j][4 * e + 3]};
+                const v4f o = (xv - mean) * inv_std * (1.0f + sc[e]) + sh[e];
+                v[j][4 * e] = o.x;
+                v[j][4 * e + 1] = o.y;
+                v[j][4 * e + 2] = o.z;
+                v[j][4 * e + 3] = o.w;
             }
         }
     }
@@ -374,9 +488,13 @@ __global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, vo
     if (row >= M) return;  // whole waves: no barrier below
     float* lds = lds_all + wave * PADDED;
 
+    typename Loader::Raw raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ld.fetch(row, b * (HBS / 16) + lane, raw[b]);
     float v[NB][16];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) ld(row, b * (HBS / 16) + lane, v[b]);
+    for (int b = 0; b < NB; ++b) Loader::unpack(raw[b], v[b]);
+    if constexpr (Loader::kWholeRow) ld.template finish_row<NB>(lane, v);
     float amax = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -420,7 +538,8 @@ __global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, vo
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // four values 64 apart (q = 0..3) converted together
-            const float q0 = v[b][i] * inv, q1 = v[b][4 + i] * inv, q2 = v[b][8 + i] * inv, q3 = v[b][12 + i] * inv;
+            const float q0 = v[b][i] * inv, q1 = v[b][4 + i] * inv, q2 = v[b][8 + i] * inv,
+                        q3 = v[b][12 + i] * inv;
             uint32_t w;
             if constexpr (OUT == RowOut::Int8)
                 w = i8x4_rne_sat(q0, q1, q2, q3);
@@ -678,6 +797,17 @@ hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float*
         return hipErrorInvalidValue;
     const size_t lds = rows_lds_bytes(K);
     const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    // rows of 1-4 Hadamard blocks of 1024 values (the block's K = 3072
+    // linear inputs), at least 1024 of them: one wave per row, the row
+    // normalized in registers (4096 x 3072: 21.3 -> 18.9 us, 13778 x 3072
+    // e4m3: 53.1 -> 45.4 us; with 256 or 300 rows one workgroup per row is
+    // faster, 6.4 against 7.2 us)
+    if (hbs == 1024 && K % 1024 == 0 && M >= 1024) {
+        const LnLoader ld{{x, K}, shift, scale, eps};
+        return mode == QIMG_QM_FP8_HADAMARD
+                   ? launch_wave_rows<RowOut::Fp8>(ld, q_out, scales, M, K, norm, stream)
+                   : launch_wave_rows<RowOut::Int8>(ld, q_out, scales, M, K, norm, stream);
+    }
     if (mode == QIMG_QM_FP8_HADAMARD)
         hipLaunchKernelGGL(ln_fwht_quant_kernel<RowOut::Fp8>, dim3(M), dim3(LN_THR), lds, stream, x, shift, scale,
                            eps, q_out, scales, K, ilog2(hbs), norm);

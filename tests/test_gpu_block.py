@@ -59,13 +59,23 @@ def test_layer_norm_modulate(qimg, blk, rows, dim):
 
 
 @pytest.mark.parametrize("rows,dim,hbs,mode", [(300, 3072, 1024, 0), (257, 3072, 1024, 1), (5, 4096, 4096, 0),
-                                               (7, 1024, 16, 0), (9, 512, 8, 0), (4, 3072, 1, 1), (0, 3072, 1024, 0)])
+                                               (7, 1024, 16, 0), (9, 512, 8, 0), (4, 3072, 1, 1), (0, 3072, 1024, 0),
+                                               (1024, 3072, 1024, 0), (4099, 3072, 1024, 1), (1100, 4096, 1024, 0),
+                                               (1025, 1024, 1024, 1), (2050, 2048, 1024, 0)])
 def test_layer_norm_modulate_quant_equals_two_passes(qimg, rows, dim, hbs, mode):
-    """The fused LayerNorm + FWHT quant gives the bits of the two kernels."""
+    """The fused LayerNorm + FWHT quant gives the bits of the two kernels
+    (one workgroup per row, or from 1024 rows of 1024-blocks one wave per
+    row), also for rows of -0.0, constant rows and rows whose variance
+    overflows."""
     g = torch.Generator(device=DEV).manual_seed(rows + dim + hbs)
     x = torch.randn(rows, dim, generator=g, device=DEV) * 3 + 0.5
+    if rows > 8:
+        x[3] = -0.0
+        x[5] = 1.25
+        x[7, ::2] = 1e30
     shift = torch.randn(dim, generator=g, device=DEV)
     scale = torch.randn(dim, generator=g, device=DEV) * 0.3
+    shift[:5] = 0.0
     q, s = qimg.layer_norm_modulate_quant(x, shift, scale, hbs, mode)
     rq, rs = qimg.quantize_activation_hadamard(qimg.layer_norm_modulate(x, shift, scale), hbs, mode)
     torch.cuda.synchronize()
