@@ -133,7 +133,22 @@ struct TileProblem {
     const float* gate;  // non-null: out = out + gate[n] * value (fp32 out)
     int M, N, K, tiles;  // K in bytes
     int accumulate;      // bf16 operands: out = out + product before the bias (fp32 out)
+    // vt_heads > 0: `out` is the attention's V^T tile layout (VtLayout):
+    // fp16 values at vt_index, for an fp32-out launch
+    int vt_heads, vt_S, vt_off, vt_n;
 };
+
+// Element offset in the V^T tile layout [seq * heads + head][ceil(S/64)][128]
+// [64] of row r (token off + r % n of sequence r / n) and column c (dim
+// c % 128 of head c / 128): a key's position in its 64-key tile swaps bits 2
+// and 3 of the key (the layout the attention kernel's PV fragments read).
+__device__ __forceinline__ int64_t vt_index(int r, int c, int heads, int S, int off, int n) {
+    const int b = r / n;
+    const int s = off + (r - b * n);
+    const int key = s & 63;
+    const int pos = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+    return ((static_cast<int64_t>(b * heads + (c >> 7)) * ((S + 63) >> 6) + (s >> 6)) * 128 + (c & 127)) * 64 + pos;
+}
 
 // The GEMMs of one launch: tiles [0, p[0].tiles) are problem 0, the next
 // p[1].tiles problem 1, and so on (e.g. the image- and text-stream q, k and v
@@ -144,7 +159,9 @@ struct TileProblems {
     int n, total;
 };
 
-template <int OP, int OUT_DT, bool GELU>
+// VT: the launch may hold V^T-layout problems (an instance of its own, so
+// that the extra epilogue leaves the others' register allocation alone).
+template <int OP, int OUT_DT, bool GELU, bool VT = false>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr bool FP8 = OP == OP_F8;
     constexpr bool BF = OP == OP_BF16;
@@ -466,7 +483,78 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // edge tiles still store whole 4-column groups with one vector store
     // when the row is in range (rows past M are skipped below)
     const bool vec_n = (N & 3) == 0;
-    if (interior && (OUT_DT == QIMG_FP32 || !has_gate) && !accumulate) {  // (no gate with bf16 outputs)
+    const bool vt = VT && OUT_DT == QIMG_FP32 && !BF && pr.vt_heads > 0;
+    if (interior && (vt || ((OUT_DT == QIMG_FP32 || !has_gate) && !accumulate))) {  // (no gate with bf16 outputs)
+        float wsv[TN][16], bv[TN][16];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int nl = wn * WTN + j * 32 + 4 * half + 8 * (q >> 2) + (q & 3);
+                wsv[j][q] = s_ws[nl];
+                bv[j][q] = s_bias[nl];
+            }
+        if (vt) {
+            // V^T output: each wave stages a 32-row block as fp16 [row][column]
+            // in a private LDS buffer, then lane l reads column l (one head dim)
+            // down the 32 rows. When the rows are 32 consecutive keys of one
+            // sequence starting at a multiple of 32 they fill half of one key
+            // tile's 128-byte row for that dim: four 16-byte stores in position
+            // order. Otherwise each value is stored at its own position.
+            constexpr int PH = WTN + 4;  // staging pitch in fp16 elements (136 bytes)
+            uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * (32 * PH * 2));
+            uint16_t* vo = reinterpret_cast<uint16_t*>(out);
+            const int vh = pr.vt_heads, vS = pr.vt_S, voff = pr.vt_off, vn = pr.vt_n;
+            const int row = lane & 31;
+            const int col = n0 + wn * WTN + lane;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const float sa = s_as[wm * WTM + i * 32 + row];
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        uint16_t h[4];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            float t;
+                            {
+#pragma clang fp contract(off)
+                                t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[j][4 * g + c];
+                                t = t + bv[j][4 * g + c];
+                            }
+                            if (GELU) t = gelu_tanh_fast(t);
+                            h[c] = f32_to_f16(t);
+                        }
+                        *reinterpret_cast<uint2*>(stg + row * PH + j * 32 + 8 * g + 4 * half) =
+                            make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                    }
+                // LDS operations of one wave complete in order; the empty asm
+                // keeps the compiler from moving the reads above the writes.
+                asm volatile("" ::: "memory");
+                const int r0 = m0 + wm * WTM + i * 32;
+                const int b0 = r0 / vn;
+                const int s0 = voff + r0 - b0 * vn;
+                if ((r0 + 31) / vn == b0 && (s0 & 31) == 0) {
+                    uint16_t* dst = vo + vt_index(r0, col, vh, vS, voff, vn);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        u32x4 wv;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int p = 8 * q + 2 * e;
+                            const int k = (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);  // key at positions p, p + 1
+                            wv[e] = stg[k * PH + lane] | (static_cast<uint32_t>(stg[(k + 1) * PH + lane]) << 16);
+                        }
+                        *reinterpret_cast<u32x4*>(dst + 8 * q) = wv;
+                    }
+                } else {
+                    for (int t = 0; t < 32; ++t) vo[vt_index(r0 + t, col, vh, vS, voff, vn)] = stg[t * PH + lane];
+                }
+                asm volatile("" ::: "memory");  // the next block's writes go after these reads
+            }
+            return;
+        }
         // Interior tiles: each wave stages one 32-row block at a time in a
         // private LDS buffer (rows padded by 16 bytes: conflict-free for both
         // the row-per-lane writes and the row-major reads), then stores it
@@ -496,15 +584,6 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             }
         };
 
-        float wsv[TN][16], bv[TN][16];
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int nl = wn * WTN + j * 32 + 4 * half + 8 * (q >> 2) + (q & 3);
-                wsv[j][q] = s_ws[nl];
-                bv[j][q] = s_bias[nl];
-            }
         const int row = lane & 31;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -561,6 +640,16 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             asm volatile("" ::: "memory");
         }
         return;
+    }
+    // V^T output: each of this lane's rows' offset at dim 0 of the wave's
+    // head (the wave's WTN columns lie in one head)
+    int64_t vrow[TM];
+    if (vt) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int m = m0 + wm * WTM + i * 32 + (lane & 31);
+            vrow[i] = m < M ? vt_index(m, (n0 + wn * WTN) & ~127, pr.vt_heads, pr.vt_S, pr.vt_off, pr.vt_n) : 0;
+        }
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -626,7 +715,13 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                     }
                     v[c] = t;
                 }
-                if (OUT_DT == QIMG_FP32) {
+                if (vt) {
+                    // (nb .. nb + 3 lie in one head: row base + dim * 64)
+                    uint16_t* o = reinterpret_cast<uint16_t*>(out) + vrow[i] + static_cast<int64_t>(nb & 127) * 64;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (nb + c < N) o[64 * c] = f32_to_f16(v[c]);
+                } else if (OUT_DT == QIMG_FP32) {
                     float* o = reinterpret_cast<float*>(out) + static_cast<int64_t>(m) * N + nb;
                     if (interior || (vec_n && nb + 4 <= N)) {
                         *reinterpret_cast<v4f*>(o) = (v4f){v[0], v[1], v[2], v[3]};
@@ -705,7 +800,16 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
 
 template <int OP, int OUT_DT, bool GELU>
 hipError_t launch_tiled(const TileProblems& P, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU>), dim3(P.total), dim3(NTHR), 0, stream, P);
+    bool vt = false;
+    for (int i = 0; i < P.n; ++i) vt = vt || P.p[i].vt_heads > 0;
+    if (vt) {
+        if constexpr (OUT_DT == QIMG_FP32 && !GELU && OP != OP_BF16)
+            hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, true>), dim3(P.total), dim3(NTHR), 0, stream, P);
+        else
+            return hipErrorInvalidValue;
+    } else {
+        hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU>), dim3(P.total), dim3(NTHR), 0, stream, P);
+    }
     return hipGetLastError();
 }
 
@@ -907,8 +1011,19 @@ hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_
         const LinearArgs& a = list[i];
         if (a.M <= 0 || a.N <= 0 || (a.K % BK) != 0) return hipErrorNotSupported;
         if (a.gate && out_dtype != QIMG_FP32) return hipErrorInvalidValue;
-        P.p[P.n++] = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate);
-        P.total += P.p[P.n - 1].tiles;
+        TileProblem t = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate);
+        if (a.vt != nullptr) {
+            const VtLayout& v = *a.vt;
+            if (out_dtype != QIMG_FP32 || a.gate || v.heads <= 0 || a.N != 128 * v.heads || v.n <= 0 ||
+                a.M % v.n != 0 || v.off < 0 || v.off + v.n > v.S)
+                return hipErrorInvalidValue;
+            t.vt_heads = v.heads;
+            t.vt_S = v.S;
+            t.vt_off = v.off;
+            t.vt_n = v.n;
+        }
+        P.p[P.n++] = t;
+        P.total += t.tiles;
     }
     // the first linear must be one the large tiles serve on its own
     if (small_m_variant(list[0].M, list[0].N, list[0].K) != 0) return hipErrorNotSupported;

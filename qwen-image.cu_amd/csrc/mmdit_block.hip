@@ -237,6 +237,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // 2.4 rounds at 4096 + 256 tokens instead of three launches of 204
         // (then the K mean runs beside the Q and V preparation instead).
         bool merged = false;
+        // the V linears write the attention's V^T tiles from their epilogue
+        const VtLayout vt_img{HEADS, S, n_txt, n_img}, vt_txt{HEADS, S, 0, n_txt};
         if (share_i && share_t && Mi > 0 && Mt > 0) {
             LinearArgs six[6];
             bool same_mode = true;
@@ -247,6 +249,10 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                 six[2 * i + 1] = LinearArgs{w.act_q_txt, w.act_scales_txt, Mt, tl[i]->K, tl[i]->w, tl[i]->scales,
                                             tl[i]->N, tl[i]->bias, w.txt_qkv[i], nullptr, nullptr};
             }
+            six[4].out = ss.v_t;
+            six[4].vt = &vt_img;
+            six[5].out = ss.v_t;
+            six[5].vt = &vt_txt;
             if (same_mode) {
                 const hipError_t r = launch_linear_multi(six, 6, il[0]->mode, QIMG_FP32, 0, s);
                 if (r != hipSuccess && r != hipErrorNotSupported) {
@@ -272,8 +278,12 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(launch_heads_quant_q(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, ss.q_i8, ss.q_scale,
                                       n_txt, n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_CONCAT_TRANSPOSE));
-        // V: fp16 straight into the attention's Vt tile layout
-        QIMG_TRY(launch_heads_v_relayout(w.txt_qkv[2], w.img_qkv[2], ss.v_t, n_txt, n_img, batch, HEADS, s));
+        // V: fp16 straight into the attention's Vt tile layout (done by the
+        // merged linears' epilogue, which leaves the tail keys' zeros to set)
+        if (merged)
+            QIMG_TRY(launch_vt_zero_tail(ss.v_t, HEADS * batch, S, s));
+        else
+            QIMG_TRY(launch_heads_v_relayout(w.txt_qkv[2], w.img_qkv[2], ss.v_t, n_txt, n_img, batch, HEADS, s));
         QIMG_TRY(mark(QIMG_PROF_ROPE));
 
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)

@@ -44,6 +44,16 @@ hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t s
 
 // gemm_w8a8.hip
 // One linear of launch_linear_pair.
+// The attention's V^T tile layout as the output of a linear: row r of the
+// [M, N] product is token off + r % n of sequence r / n (n rows per
+// sequence, S tokens per sequence in all), column c is dim c % 128 of head
+// c / 128 (N = 128 heads); the fp16 value goes to [seq * heads + head]
+// [ceil(S/64)][128][64] where the attention kernel reads it. Positions of
+// keys past S are not written.
+struct VtLayout {
+    int heads, S, off, n;
+};
+
 struct LinearArgs {
     const void* act_q;
     const float* act_scales;
@@ -58,6 +68,9 @@ struct LinearArgs {
     // tmp [M, N] and the gate-add kernel
     const float* gate;
     float* tmp;
+    // non-null (launch_linear_multi, fp32 launches): this linear's output
+    // goes to `out` in the V^T tile layout instead
+    const VtLayout* vt = nullptr;
 };
 hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
                               hipStream_t stream);
@@ -167,6 +180,9 @@ hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t*
                                int causal, hipStream_t stream);
 // The joint block's V (fp32 text and image linear outputs, H heads of 128)
 // -> fp16 in the Vt layout of launch_sage_attn_vt.
+// Zeros at the Vt positions of the keys past S in each last key tile
+// (for a Vt written by a linear's V^T epilogue).
+hipError_t launch_vt_zero_tail(uint16_t* v_t, int BH, int S, hipStream_t stream);
 hipError_t launch_heads_v_relayout(const float* txt, const float* img, uint16_t* v_t, int n_txt, int n_img,
                                    int batch, int H, hipStream_t stream);
 // The joint block's Q (fp32 text and image linear outputs) -> RMSNorm +

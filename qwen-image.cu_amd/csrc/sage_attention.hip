@@ -429,6 +429,20 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
     }
 }
 
+// Zeros at the positions of keys S .. 64 ceil(S/64) - 1 of the last key
+// tile of every (sequence, head) of Vt [BH][ceil(S/64)][D][64], which the
+// relayout kernels write and a linear writing Vt directly does not (the
+// attention reads whole tiles and gives those keys zero weight). Grid BH,
+// one thread per dim.
+template <int D>
+__global__ __launch_bounds__(D) void vt_zero_tail_kernel(uint16_t* __restrict__ vt, int S) {
+    const int nt = div_up(S, KTILE);
+    const int rem = S - (nt - 1) * KTILE;
+    uint16_t* row = vt + ((static_cast<int64_t>(blockIdx.x) * nt + nt - 1) * D + threadIdx.x) * KTILE;
+    for (int p = 0; p < KTILE; ++p)
+        if (vt_key_of_pos(p) >= rem) row[p] = 0;
+}
+
 // The V of the joint block straight from the text and image linears' fp32
 // outputs (token s < n_txt of sequence b is txt[b][s], the rest img[b][s -
 // n_txt], head hh at columns hh*D..): the fp16 values of the V concat +
@@ -1057,6 +1071,12 @@ hipError_t launch_heads_quant_q(const float* txt, const float* img, const uint16
     const int64_t units = static_cast<int64_t>(div_up(S, QBLK)) * 4 * batch * H;
     hipLaunchKernelGGL(heads_quant_q_wave_kernel, dim3(static_cast<unsigned>((units + 3) / 4)), dim3(256), 0, stream,
                        txt, img, w_txt, w_img, pe, q_out, q_scale, n_txt, n_img, batch, H, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_vt_zero_tail(uint16_t* v_t, int BH, int S, hipStream_t stream) {
+    if (S % KTILE == 0 || BH == 0) return hipSuccess;
+    hipLaunchKernelGGL(vt_zero_tail_kernel<128>, dim3(BH), dim3(128), 0, stream, v_t, S);
     return hipGetLastError();
 }
 
