@@ -133,18 +133,24 @@ struct TileProblem {
     const float* gate;  // non-null: out = out + gate[n] * value (fp32 out)
     int M, N, K, tiles;  // K in bytes
     int accumulate;      // bf16 operands: out = out + product before the bias (fp32 out)
-    // vt_heads > 0: `out` is the attention's V^T tile layout (VtLayout):
-    // fp16 values at vt_index, for an fp32-out launch
-    int vt_heads, vt_S, vt_off, vt_n;
+    // hk > 0: the output goes to an attention operand layout (HeadsOut kind
+    // hk: heads hH, S tokens per sequence, rows are tokens hoff + r % hn of
+    // sequences hb0 + r / hn)
+    int hk, hH, hS, hoff, hn, hb0;
+    const uint16_t* hnorm;
+    const float* hpe;
+    float* hqs;
+    float heps;
 };
 
 // Element offset in the V^T tile layout [seq * heads + head][ceil(S/64)][128]
-// [64] of row r (token off + r % n of sequence r / n) and column c (dim
+// [64] of row r (token off + r % n of sequence b0 + r / n) and column c (dim
 // c % 128 of head c / 128): a key's position in its 64-key tile swaps bits 2
 // and 3 of the key (the layout the attention kernel's PV fragments read).
-__device__ __forceinline__ int64_t vt_index(int r, int c, int heads, int S, int off, int n) {
-    const int b = r / n;
-    const int s = off + (r - b * n);
+__device__ __forceinline__ int64_t vt_index(int r, int c, int heads, int S, int off, int n, int b0) {
+    const int q = r / n;
+    const int b = b0 + q;
+    const int s = off + (r - q * n);
     const int key = s & 63;
     const int pos = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
     return ((static_cast<int64_t>(b * heads + (c >> 7)) * ((S + 63) >> 6) + (s >> 6)) * 128 + (c & 127)) * 64 + pos;
@@ -153,15 +159,16 @@ __device__ __forceinline__ int64_t vt_index(int r, int c, int heads, int S, int 
 // The GEMMs of one launch: tiles [0, p[0].tiles) are problem 0, the next
 // p[1].tiles problem 1, and so on (e.g. the image- and text-stream q, k and v
 // linears of a joint block: each alone leaves CUs idle in its last round).
-constexpr int kMaxProblems = 6;
+constexpr int kMaxProblems = 8;
 struct TileProblems {
     TileProblem p[kMaxProblems];
     int n, total;
 };
 
-// VT: the launch may hold V^T-layout problems (an instance of its own, so
-// that the extra epilogue leaves the others' register allocation alone).
-template <int OP, int OUT_DT, bool GELU, bool VT = false>
+// HD: the launch may hold problems with attention-layout outputs
+// (TileProblem::hk; an instance of its own, so that the extra epilogues
+// leave the others' register allocation alone).
+template <int OP, int OUT_DT, bool GELU, bool HD = false>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr bool FP8 = OP == OP_F8;
     constexpr bool BF = OP == OP_BF16;
@@ -473,6 +480,146 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     }
     __syncthreads();
 
+    if constexpr (HD && OUT_DT == QIMG_FP32 && !BF && !GELU) {
+        if (pr.hk == HEADS_K || pr.hk == HEADS_Q) {
+            // K or Q heads (the tile is two whole heads), in steps of 64 rows
+            // (32 of each wave row wm): (A) every wave stores its dequantized
+            // fp32 values in the shared tile T [64][256]; (B) wave w takes
+            // tokens 8w .. 8w + 7 of the step, both heads: RMSNorm, RoPE and
+            // fp16 with the arithmetic of joint_heads_f16_kernel (lane l holds
+            // dims 2l, 2l + 1; the same wave sum and fused multiply-adds), K
+            // stored at once, Q kept in R [64][2][128]; (C) for Q, waves 0-3
+            // take one (32-token slice, head) each and quantize it as the
+            // second phase of heads_quant_q_wave_kernel (lane 8g + j holds
+            // dims 16j .. +16 of tokens g, g + 8, g + 16, g + 24). Rows past
+            // M count as zeros, as tokens past S do there.
+            constexpr int TP = BN + 4;      // T pitch (floats)
+            constexpr int RP = 2 * 64 + 4;  // R pitch (32-bit words of two fp16)
+            static_assert(64 * TP * 4 + 64 * RP * 4 <= SCALE_OFF, "heads staging overlaps the scales");
+            float* T = reinterpret_cast<float*>(lds);
+            uint32_t* R = reinterpret_cast<uint32_t*>(lds + 64 * TP * 4);
+            const int H = pr.hH, S = pr.hS, hoff = pr.hoff, hn = pr.hn, hb0 = pr.hb0;
+            const bool isq = pr.hk == HEADS_Q;
+            const float heps = pr.heps;
+            const float* __restrict__ pe = pr.hpe;
+            const uint32_t wp = reinterpret_cast<const uint32_t*>(pr.hnorm)[lane];
+            const float w0 = bf16_to_f32(static_cast<uint16_t>(wp & 0xffffu));
+            const float w1 = bf16_to_f32(static_cast<uint16_t>(wp >> 16));
+            const int hfirst = n0 >> 7;  // the tile's first head
+            const int row = lane & 31;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                // (A)
+                {
+                    const float sa = s_as[wm * WTM + i * 32 + row];
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            float v[4];
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) {
+                                const int nl = wn * WTN + j * 32 + 4 * half + 8 * g + c;
+                                {
+#pragma clang fp contract(off)
+                                    v[c] = static_cast<float>(acc[i][j][4 * g + c]) * sa * s_ws[nl];
+                                    v[c] = v[c] + s_bias[nl];
+                                }
+                            }
+                            *reinterpret_cast<v4f*>(T + (wm * 32 + row) * TP + wn * WTN + j * 32 + 8 * g + 4 * half) =
+                                (v4f){v[0], v[1], v[2], v[3]};
+                        }
+                }
+                __syncthreads();
+                // (B)
+                {
+                    v4f p[8];
+                    int tb[8], ts[8];
+                    bool ok[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const int tr = wave * 8 + k;
+                        const int r = m0 + (tr >> 5) * WTM + i * 32 + (tr & 31);
+                        ok[k] = r < M;
+                        const int q = ok[k] ? r / hn : 0;
+                        tb[k] = hb0 + q;
+                        ts[k] = hoff + (ok[k] ? r - q * hn : 0);
+                        p[k] = ok[k] ? reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(ts[k]) * 64 + lane]
+                                     : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const int tr = wave * 8 + k;
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            float2 y = *reinterpret_cast<const float2*>(T + tr * TP + hh * 128 + 2 * lane);
+                            const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
+                            const float rms = rsqrtf(ss / 128 + heps);
+                            y.x = y.x * rms * w0;
+                            y.y = y.y * rms * w1;
+                            const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
+                            const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
+                            const uint32_t packed =
+                                static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
+                            if (isq) {
+                                R[tr * RP + hh * 64 + lane] = ok[k] ? packed : 0u;
+                            } else if (ok[k]) {
+                                const int64_t bh = static_cast<int64_t>(tb[k]) * H + hfirst + hh;
+                                reinterpret_cast<uint32_t*>(out)[(bh * S + ts[k]) * 64 + lane] = packed;
+                            }
+                        }
+                    }
+                }
+                __syncthreads();  // T is free for the next step; R is complete
+                // (C)
+                if (isq && wave < 4) {
+                    const int blk = wave >> 1, hh = wave & 1;
+                    const int r0 = m0 + blk * WTM + i * 32;
+                    if (r0 < M) {
+                        const int q0 = r0 / hn;
+                        const int s0 = hoff + r0 - q0 * hn;  // a multiple of 32
+                        const int64_t bh = static_cast<int64_t>(hb0 + q0) * H + hfirst + hh;
+                        const int g = lane >> 3, jj = lane & 7;
+                        uint32_t raw[4][8];
+                        float amax = 0.0f;
+#pragma unroll
+                        for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+                            for (int c = 0; c < 8; ++c) {
+                                raw[ii][c] = R[(blk * 32 + g + 8 * ii) * RP + hh * 64 + 8 * jj + c];
+                                amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[ii][c] & 0xffffu))));
+                                amax = fmaxf(amax, fabsf(f16_to_f32(static_cast<uint16_t>(raw[ii][c] >> 16))));
+                            }
+#pragma unroll
+                        for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+                        const float a = fmaxf(1e-7f, amax);  // the reference starts its max at 1e-7
+                        const float scale = a / 127.0f + 1e-7f;
+                        const int nq = ((S + 127) / 128) * 32;
+                        const int slice = s0 >> 5;
+                        if (jj == 0) pr.hqs[bh * nq + (slice >> 2) * 32 + (slice & 3) * 8 + g] = scale;
+                        const float inv = 1.0f / scale;
+#pragma unroll
+                        for (int ii = 0; ii < 4; ++ii) {
+                            if (r0 + g + 8 * ii >= M) continue;
+                            u32x4 pk;
+#pragma unroll
+                            for (int wd = 0; wd < 4; ++wd) {
+                                const uint32_t a0 = raw[ii][2 * wd], a1 = raw[ii][2 * wd + 1];
+                                pk[wd] = i8x4_rne_sat(f16_to_f32(static_cast<uint16_t>(a0 & 0xffffu)) * inv,
+                                                      f16_to_f32(static_cast<uint16_t>(a0 >> 16)) * inv,
+                                                      f16_to_f32(static_cast<uint16_t>(a1 & 0xffffu)) * inv,
+                                                      f16_to_f32(static_cast<uint16_t>(a1 >> 16)) * inv);
+                            }
+                            *reinterpret_cast<u32x4*>(reinterpret_cast<int8_t*>(out) +
+                                                      (bh * S + s0 + g + 8 * ii) * 128 + 16 * jj) = pk;
+                        }
+                    }
+                }
+            }
+            return;
+        }
+    }
+
     // Epilogue. The MFMA was issued as D = W_frag x A_frag, so the 32x32
     // block is indexed [n][m]: lane holds m = lane%32 and n rows
     // 8*(r/4) + 4*(lane/32) + r%4. Each lane therefore owns one output row
@@ -483,7 +630,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // edge tiles still store whole 4-column groups with one vector store
     // when the row is in range (rows past M are skipped below)
     const bool vec_n = (N & 3) == 0;
-    const bool vt = VT && OUT_DT == QIMG_FP32 && !BF && pr.vt_heads > 0;
+    const bool vt = HD && OUT_DT == QIMG_FP32 && !BF && pr.hk == HEADS_V;
     if (interior && (vt || ((OUT_DT == QIMG_FP32 || !has_gate) && !accumulate))) {  // (no gate with bf16 outputs)
         float wsv[TN][16], bv[TN][16];
 #pragma unroll
@@ -504,7 +651,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             constexpr int PH = WTN + 4;  // staging pitch in fp16 elements (136 bytes)
             uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * (32 * PH * 2));
             uint16_t* vo = reinterpret_cast<uint16_t*>(out);
-            const int vh = pr.vt_heads, vS = pr.vt_S, voff = pr.vt_off, vn = pr.vt_n;
+            const int vh = pr.hH, vS = pr.hS, voff = pr.hoff, vn = pr.hn, vb0 = pr.hb0;
             const int row = lane & 31;
             const int col = n0 + wn * WTN + lane;
 #pragma unroll
@@ -536,7 +683,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 const int b0 = r0 / vn;
                 const int s0 = voff + r0 - b0 * vn;
                 if ((r0 + 31) / vn == b0 && (s0 & 31) == 0) {
-                    uint16_t* dst = vo + vt_index(r0, col, vh, vS, voff, vn);
+                    uint16_t* dst = vo + vt_index(r0, col, vh, vS, voff, vn, vb0);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         u32x4 wv;
@@ -549,7 +696,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                         *reinterpret_cast<u32x4*>(dst + 8 * q) = wv;
                     }
                 } else {
-                    for (int t = 0; t < 32; ++t) vo[vt_index(r0 + t, col, vh, vS, voff, vn)] = stg[t * PH + lane];
+                    for (int t = 0; t < 32; ++t) vo[vt_index(r0 + t, col, vh, vS, voff, vn, vb0)] = stg[t * PH + lane];
                 }
                 asm volatile("" ::: "memory");  // the next block's writes go after these reads
             }
@@ -648,7 +795,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int m = m0 + wm * WTM + i * 32 + (lane & 31);
-            vrow[i] = m < M ? vt_index(m, (n0 + wn * WTN) & ~127, pr.vt_heads, pr.vt_S, pr.vt_off, pr.vt_n) : 0;
+            vrow[i] = m < M ? vt_index(m, (n0 + wn * WTN) & ~127, pr.hH, pr.hS, pr.hoff, pr.hn, pr.hb0) : 0;
         }
     }
 #pragma unroll
@@ -800,9 +947,9 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
 
 template <int OP, int OUT_DT, bool GELU>
 hipError_t launch_tiled(const TileProblems& P, hipStream_t stream) {
-    bool vt = false;
-    for (int i = 0; i < P.n; ++i) vt = vt || P.p[i].vt_heads > 0;
-    if (vt) {
+    bool hd = false;
+    for (int i = 0; i < P.n; ++i) hd = hd || P.p[i].hk > 0;
+    if (hd) {
         if constexpr (OUT_DT == QIMG_FP32 && !GELU && OP != OP_BF16)
             hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, true>), dim3(P.total), dim3(NTHR), 0, stream, P);
         else
@@ -1012,15 +1159,24 @@ hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_
         if (a.M <= 0 || a.N <= 0 || (a.K % BK) != 0) return hipErrorNotSupported;
         if (a.gate && out_dtype != QIMG_FP32) return hipErrorInvalidValue;
         TileProblem t = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate);
-        if (a.vt != nullptr) {
-            const VtLayout& v = *a.vt;
-            if (out_dtype != QIMG_FP32 || a.gate || v.heads <= 0 || a.N != 128 * v.heads || v.n <= 0 ||
-                a.M % v.n != 0 || v.off < 0 || v.off + v.n > v.S)
+        if (a.heads != nullptr) {
+            const HeadsOut& h = *a.heads;
+            const bool qk = h.kind == HEADS_K || h.kind == HEADS_Q;
+            if (out_dtype != QIMG_FP32 || gelu || a.gate || h.kind < HEADS_V || h.kind > HEADS_Q || h.heads <= 0 ||
+                a.N != 128 * h.heads || h.n <= 0 || a.M % h.n != 0 || h.off < 0 || h.off + h.n > h.S || h.b0 < 0 ||
+                (qk && (h.norm == nullptr || h.pe == nullptr || a.N % BN != 0)) ||
+                (h.kind == HEADS_Q && (h.q_scale == nullptr || h.off % 32 != 0 || (a.M != h.n && h.n % 32 != 0))))
                 return hipErrorInvalidValue;
-            t.vt_heads = v.heads;
-            t.vt_S = v.S;
-            t.vt_off = v.off;
-            t.vt_n = v.n;
+            t.hk = h.kind;
+            t.hH = h.heads;
+            t.hS = h.S;
+            t.hoff = h.off;
+            t.hn = h.n;
+            t.hb0 = h.b0;
+            t.hnorm = h.norm;
+            t.hpe = h.pe;
+            t.hqs = h.q_scale;
+            t.heps = h.eps;
         }
         P.p[P.n++] = t;
         P.total += t.tiles;

@@ -224,64 +224,108 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                                    : gemm_pair(Mi, *il[i], w.img_qkv[i], nullptr, nullptr, Mt, *tl[i], w.txt_qkv[i],
                                                nullptr, nullptr, 0);
         };
-        // K first: its RMSNorm + concat + transpose + RoPE -> fp16
-        // (transformer.cu:617-666), then its mean (sageattention_sm80.cu:
-        // 759-773) on the side stream beside the q and v linears (their 204
-        // tiles at 4096 + 256 tokens leave CUs idle) and the Q / V preparation.
         SideStream* side = nullptr;
         QIMG_TRY(side_stream(&side));
         SageScratch ss;
         sage_scratch_layout(HEADS * batch, S, HEAD_DIM, w.sage, &ss);
-        // All six linears in one launch when both streams' three share their
-        // input quantization and every linear has the same mode: 612 tiles in
-        // 2.4 rounds at 4096 + 256 tokens instead of three launches of 204
-        // (then the K mean runs beside the Q and V preparation instead).
-        bool merged = false;
-        // the V linears write the attention's V^T tiles from their epilogue
-        const VtLayout vt_img{HEADS, S, n_txt, n_img}, vt_txt{HEADS, S, 0, n_txt};
+        // When both streams' three linears share their input quantization and
+        // every linear has the same mode, the linears write the attention's
+        // operands from their epilogues: K as RMSNorm + RoPE fp16, Q also
+        // quantized to the Sage int8 (when its 32-token slices lie inside one
+        // linear: n_txt a multiple of 32, the image rows split per sequence
+        // unless n_img is one too), V in the V^T tile layout. K's two linears
+        // go first so that its mean runs on the side stream beside the Q and V
+        // linears (one launch of four to six problems).
+        bool merged = false, q_fused = false;
+        const int nsplit = (batch > 1 && n_img % 32 != 0) ? batch : 1;
+        const bool q_ok = n_txt % 32 == 0 && nsplit <= 4;
+        HeadsOut hq_img[4], hv_img[4], hq_txt{}, hk_img{}, hk_txt{}, hv_txt{};
         if (share_i && share_t && Mi > 0 && Mt > 0) {
-            LinearArgs six[6];
             bool same_mode = true;
-            for (int i = 0; i < 3; ++i) {
+            for (int i = 0; i < 3; ++i)
                 same_mode = same_mode && il[i]->mode == il[0]->mode && tl[i]->mode == il[0]->mode;
-                six[2 * i] = LinearArgs{w.act_q, w.act_scales, Mi, il[i]->K, il[i]->w, il[i]->scales, il[i]->N,
-                                        il[i]->bias, w.img_qkv[i], nullptr, nullptr};
-                six[2 * i + 1] = LinearArgs{w.act_q_txt, w.act_scales_txt, Mt, tl[i]->K, tl[i]->w, tl[i]->scales,
-                                            tl[i]->N, tl[i]->bias, w.txt_qkv[i], nullptr, nullptr};
-            }
-            six[4].out = ss.v_t;
-            six[4].vt = &vt_img;
-            six[5].out = ss.v_t;
-            six[5].vt = &vt_txt;
             if (same_mode) {
-                const hipError_t r = launch_linear_multi(six, 6, il[0]->mode, QIMG_FP32, 0, s);
-                if (r != hipSuccess && r != hipErrorNotSupported) {
+                auto args = [&](int i, bool img, int rows, int row0, void* out, const HeadsOut* h) {
+                    const qimg_qlinear& l = img ? *il[i] : *tl[i];
+                    const uint8_t* aq = static_cast<const uint8_t*>(img ? w.act_q : w.act_q_txt);
+                    const float* as = img ? w.act_scales : w.act_scales_txt;
+                    LinearArgs a{aq + static_cast<int64_t>(row0) * l.K, as + row0, rows, l.K, l.w, l.scales, l.N,
+                                 l.bias, out, nullptr, nullptr};
+                    a.heads = h;
+                    return a;
+                };
+                hk_img = HeadsOut{HEADS_K, HEADS, S, n_txt, n_img, 0, b.norm_k, pe, nullptr, EPS};
+                hk_txt = HeadsOut{HEADS_K, HEADS, S, 0, n_txt, 0, b.norm_added_k, pe, nullptr, EPS};
+                const LinearArgs ks[2] = {args(1, true, Mi, 0, w.k16, &hk_img), args(1, false, Mt, 0, w.k16, &hk_txt)};
+                hipError_t r = launch_linear_multi(ks, 2, il[0]->mode, QIMG_FP32, 0, s);
+                if (r == hipSuccess) {
+                    merged = true;
+                    QIMG_TRY(hipEventRecord(side->fork, s));
+                    QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+                    QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
+                    QIMG_TRY(hipEventRecord(side->join, side->stream));
+                    LinearArgs qv[8];
+                    int n = 0;
+                    if (q_ok) {
+                        for (int q = 0; q < nsplit; ++q) {
+                            hq_img[q] = HeadsOut{HEADS_Q, HEADS, S, n_txt, n_img, q * (batch / nsplit), b.norm_q, pe,
+                                                 ss.q_scale, EPS};
+                            qv[n++] = args(0, true, Mi / nsplit, q * (Mi / nsplit), ss.q_i8, &hq_img[q]);
+                        }
+                        hq_txt = HeadsOut{HEADS_Q, HEADS, S, 0, n_txt, 0, b.norm_added_q, pe, ss.q_scale, EPS};
+                        qv[n++] = args(0, false, Mt, 0, ss.q_i8, &hq_txt);
+                    } else {
+                        qv[n++] = args(0, true, Mi, 0, w.img_qkv[0], nullptr);
+                        qv[n++] = args(0, false, Mt, 0, w.txt_qkv[0], nullptr);
+                    }
+                    // (V rows split per sequence as Q's: a 32-row block then
+                    // fills half of one key tile's rows, stored whole)
+                    const int vsplit = (n_txt % 32 == 0 && nsplit <= 2) ? nsplit : 1;
+                    for (int q = 0; q < vsplit; ++q) {
+                        hv_img[q] = HeadsOut{HEADS_V, HEADS, S, n_txt, n_img, q * (batch / vsplit), nullptr, nullptr,
+                                             nullptr, EPS};
+                        qv[n++] = args(2, true, Mi / vsplit, q * (Mi / vsplit), ss.v_t, &hv_img[q]);
+                    }
+                    hv_txt = HeadsOut{HEADS_V, HEADS, S, 0, n_txt, 0, nullptr, nullptr, nullptr, EPS};
+                    qv[n++] = args(2, false, Mt, 0, ss.v_t, &hv_txt);
+                    r = launch_linear_multi(qv, n, il[0]->mode, QIMG_FP32, 0, s);
+                    if (r != hipSuccess) {
+                        e = r;  // the K linears ran: no fallback from here
+                        goto done;
+                    }
+                    q_fused = q_ok;
+                } else if (r != hipErrorNotSupported) {
                     e = r;
                     goto done;
                 }
-                merged = r == hipSuccess;
             }
         }
-        if (!merged) QIMG_TRY(qkv_gemm(1));
-        QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.k16, n_txt,
-                                        n_img, batch, HEADS, EPS, s));
-        QIMG_TRY(hipEventRecord(side->fork, s));
-        QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
-        QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
-        QIMG_TRY(hipEventRecord(side->join, side->stream));
         if (!merged) {
+            // K first: its RMSNorm + concat + transpose + RoPE -> fp16
+            // (transformer.cu:617-666), then its mean (sageattention_sm80.cu:
+            // 759-773) on the side stream beside the q and v linears and the
+            // Q / V preparation.
+            QIMG_TRY(qkv_gemm(1));
+            QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.k16, n_txt,
+                                            n_img, batch, HEADS, EPS, s));
+            QIMG_TRY(hipEventRecord(side->fork, s));
+            QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+            QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
+            QIMG_TRY(hipEventRecord(side->join, side->stream));
             QIMG_TRY(qkv_gemm(0));
             QIMG_TRY(qkv_gemm(2));
         }
         // Q: RMSNorm + RoPE + fp16 and the Sage int8 quantization in one pass
         QIMG_TRY(mark(QIMG_PROF_QK_NORM));
-        QIMG_TRY(launch_heads_quant_q(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, ss.q_i8, ss.q_scale,
-                                      n_txt, n_img, batch, HEADS, EPS, s));
+        if (!q_fused)
+            QIMG_TRY(launch_heads_quant_q(w.txt_qkv[0], w.img_qkv[0], b.norm_added_q, b.norm_q, pe, ss.q_i8,
+                                          ss.q_scale, n_txt, n_img, batch, HEADS, EPS, s));
         QIMG_TRY(mark(QIMG_PROF_CONCAT_TRANSPOSE));
-        // V: fp16 straight into the attention's Vt tile layout (done by the
-        // merged linears' epilogue, which leaves the tail keys' zeros to set)
+        // V: fp16 straight into the attention's Vt tile layout (by the linears'
+        // epilogue when merged, which leaves the tail keys' zeros, and the
+        // scales of slices without tokens when Q is fused, to set)
         if (merged)
-            QIMG_TRY(launch_vt_zero_tail(ss.v_t, HEADS * batch, S, s));
+            QIMG_TRY(launch_sage_tail_fill(ss.v_t, q_fused ? ss.q_scale : nullptr, HEADS * batch, S, s));
         else
             QIMG_TRY(launch_heads_v_relayout(w.txt_qkv[2], w.img_qkv[2], ss.v_t, n_txt, n_img, batch, HEADS, s));
         QIMG_TRY(mark(QIMG_PROF_ROPE));

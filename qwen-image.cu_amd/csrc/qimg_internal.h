@@ -44,14 +44,27 @@ hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t s
 
 // gemm_w8a8.hip
 // One linear of launch_linear_pair.
-// The attention's V^T tile layout as the output of a linear: row r of the
-// [M, N] product is token off + r % n of sequence r / n (n rows per
-// sequence, S tokens per sequence in all), column c is dim c % 128 of head
-// c / 128 (N = 128 heads); the fp16 value goes to [seq * heads + head]
-// [ceil(S/64)][128][64] where the attention kernel reads it. Positions of
-// keys past S are not written.
-struct VtLayout {
-    int heads, S, off, n;
+// A linear whose output goes straight into the attention's operand layouts.
+// Row r of its [M, N] product is token off + r % n of sequence b0 + r / n
+// (S tokens per sequence), column c is dim c % 128 of head c / 128
+// (N = 128 * heads):
+//   HEADS_V: fp16 in the V^T tile layout [seq * heads + head][ceil(S/64)]
+//     [128][64] (positions of keys past S are not written);
+//   HEADS_K: RMSNorm with the bf16 [128] weight `norm` and eps, RoPE with
+//     `pe` [S][64][4], fp16 [seq * heads + head][S][128], as
+//     launch_joint_heads_f16 computes it;
+//   HEADS_Q: the same, then the Sage int8 quantization of
+//     launch_heads_quant_q: int8 [seq * heads + head][S][128] and `q_scale`
+//     for the 32-token slices that hold tokens. Each slice must lie inside
+//     the linear: off a multiple of 32, and n too unless M = n.
+// fp32-out launch_linear_multi only, without GELU.
+constexpr int HEADS_V = 1, HEADS_K = 2, HEADS_Q = 3;
+struct HeadsOut {
+    int kind, heads, S, off, n, b0;
+    const uint16_t* norm;
+    const float* pe;
+    float* q_scale;
+    float eps;
 };
 
 struct LinearArgs {
@@ -68,9 +81,9 @@ struct LinearArgs {
     // tmp [M, N] and the gate-add kernel
     const float* gate;
     float* tmp;
-    // non-null (launch_linear_multi, fp32 launches): this linear's output
-    // goes to `out` in the V^T tile layout instead
-    const VtLayout* vt = nullptr;
+    // non-null (launch_linear_multi): this linear's output goes to `out`
+    // in an attention operand layout instead
+    const HeadsOut* heads = nullptr;
 };
 hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
                               hipStream_t stream);
@@ -180,9 +193,11 @@ hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t*
                                int causal, hipStream_t stream);
 // The joint block's V (fp32 text and image linear outputs, H heads of 128)
 // -> fp16 in the Vt layout of launch_sage_attn_vt.
-// Zeros at the Vt positions of the keys past S in each last key tile
-// (for a Vt written by a linear's V^T epilogue).
-hipError_t launch_vt_zero_tail(uint16_t* v_t, int BH, int S, hipStream_t stream);
+// What the attention's operand passes write and linears writing those
+// operands (HeadsOut) do not: zeros at the Vt positions of the keys past S
+// in each last key tile, and (q_scale non-null) the Q scales of the 32-token
+// slices without tokens in the last 128-token block.
+hipError_t launch_sage_tail_fill(uint16_t* v_t, float* q_scale, int BH, int S, hipStream_t stream);
 hipError_t launch_heads_v_relayout(const float* txt, const float* img, uint16_t* v_t, int n_txt, int n_img,
                                    int batch, int H, hipStream_t stream);
 // The joint block's Q (fp32 text and image linear outputs) -> RMSNorm +

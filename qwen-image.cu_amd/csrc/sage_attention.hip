@@ -432,15 +432,29 @@ __global__ __launch_bounds__(256) void v_relayout_kernel(const uint16_t* __restr
 // Zeros at the positions of keys S .. 64 ceil(S/64) - 1 of the last key
 // tile of every (sequence, head) of Vt [BH][ceil(S/64)][D][64], which the
 // relayout kernels write and a linear writing Vt directly does not (the
-// attention reads whole tiles and gives those keys zero weight). Grid BH,
-// one thread per dim.
+// attention reads whole tiles and gives those keys zero weight); with
+// q_scale, also the scales heads_quant_q_wave_kernel writes for the 32-token
+// slices of the last 128-token block that hold no token (its group maximum
+// of zeros). Grid BH, one thread per dim.
 template <int D>
-__global__ __launch_bounds__(D) void vt_zero_tail_kernel(uint16_t* __restrict__ vt, int S) {
+__global__ __launch_bounds__(D) void sage_tail_fill_kernel(uint16_t* __restrict__ vt, float* __restrict__ q_scale,
+                                                           int S) {
     const int nt = div_up(S, KTILE);
     const int rem = S - (nt - 1) * KTILE;
-    uint16_t* row = vt + ((static_cast<int64_t>(blockIdx.x) * nt + nt - 1) * D + threadIdx.x) * KTILE;
-    for (int p = 0; p < KTILE; ++p)
-        if (vt_key_of_pos(p) >= rem) row[p] = 0;
+    if (rem < KTILE) {
+        uint16_t* row = vt + ((static_cast<int64_t>(blockIdx.x) * nt + nt - 1) * D + threadIdx.x) * KTILE;
+        for (int p = 0; p < KTILE; ++p)
+            if (vt_key_of_pos(p) >= rem) row[p] = 0;
+    }
+    const int nslice = div_up(S, QBLK) * 4;
+    const int first_empty = div_up(S, 32);
+    const int idx = first_empty * 8 + static_cast<int>(threadIdx.x);  // (slice, group g) pairs
+    if (q_scale != nullptr && idx < nslice * 8) {
+        const int slice = idx >> 3, g = idx & 7;
+        const float a = fmaxf(1e-7f, 0.0f);
+        const int nq = div_up(S, QBLK) * 32;
+        q_scale[static_cast<int64_t>(blockIdx.x) * nq + (slice >> 2) * 32 + (slice & 3) * 8 + g] = a / 127.0f + 1e-7f;
+    }
 }
 
 // The V of the joint block straight from the text and image linears' fp32
@@ -1074,9 +1088,11 @@ hipError_t launch_heads_quant_q(const float* txt, const float* img, const uint16
     return hipGetLastError();
 }
 
-hipError_t launch_vt_zero_tail(uint16_t* v_t, int BH, int S, hipStream_t stream) {
-    if (S % KTILE == 0 || BH == 0) return hipSuccess;
-    hipLaunchKernelGGL(vt_zero_tail_kernel<128>, dim3(BH), dim3(128), 0, stream, v_t, S);
+hipError_t launch_sage_tail_fill(uint16_t* v_t, float* q_scale, int BH, int S, hipStream_t stream) {
+    const bool v_tail = S % KTILE != 0;
+    const bool q_tail = q_scale != nullptr && div_up(S, 32) < div_up(S, QBLK) * 4;
+    if (BH == 0 || S == 0 || (!v_tail && !q_tail)) return hipSuccess;
+    hipLaunchKernelGGL(sage_tail_fill_kernel<128>, dim3(BH), dim3(128), 0, stream, v_t, q_tail ? q_scale : nullptr, S);
     return hipGetLastError();
 }
 
