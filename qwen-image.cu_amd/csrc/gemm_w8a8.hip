@@ -509,6 +509,22 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             const int row = lane & 31;
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
+                // this step's tokens and their RoPE rows (the loads in flight
+                // during (A))
+                v4f p[8];
+                int tb[8], ts[8];
+                bool ok[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int tr = wave * 8 + k;
+                    const int r = m0 + (tr >> 5) * WTM + i * 32 + (tr & 31);
+                    ok[k] = r < M;
+                    const int q = ok[k] ? r / hn : 0;
+                    tb[k] = hb0 + q;
+                    ts[k] = hoff + (ok[k] ? r - q * hn : 0);
+                    p[k] = ok[k] ? reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(ts[k]) * 64 + lane]
+                                 : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+                }
                 // (A)
                 {
                     const float sa = s_as[wm * WTM + i * 32 + row];
@@ -517,13 +533,15 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
 #pragma unroll
                         for (int g = 0; g < 4; ++g) {
                             float v[4];
+                            const int nl = wn * WTN + j * 32 + 4 * half + 8 * g;
+                            const v4f wv = *reinterpret_cast<const v4f*>(s_ws + nl);
+                            const v4f bb = *reinterpret_cast<const v4f*>(s_bias + nl);
 #pragma unroll
                             for (int c = 0; c < 4; ++c) {
-                                const int nl = wn * WTN + j * 32 + 4 * half + 8 * g + c;
                                 {
 #pragma clang fp contract(off)
-                                    v[c] = static_cast<float>(acc[i][j][4 * g + c]) * sa * s_ws[nl];
-                                    v[c] = v[c] + s_bias[nl];
+                                    v[c] = static_cast<float>(acc[i][j][4 * g + c]) * sa * wv[c];
+                                    v[c] = v[c] + bb[c];
                                 }
                             }
                             *reinterpret_cast<v4f*>(T + (wm * 32 + row) * TP + wn * WTN + j * 32 + 8 * g + 4 * half) =
@@ -533,20 +551,6 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 __syncthreads();
                 // (B)
                 {
-                    v4f p[8];
-                    int tb[8], ts[8];
-                    bool ok[8];
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const int tr = wave * 8 + k;
-                        const int r = m0 + (tr >> 5) * WTM + i * 32 + (tr & 31);
-                        ok[k] = r < M;
-                        const int q = ok[k] ? r / hn : 0;
-                        tb[k] = hb0 + q;
-                        ts[k] = hoff + (ok[k] ? r - q * hn : 0);
-                        p[k] = ok[k] ? reinterpret_cast<const v4f*>(pe)[static_cast<int64_t>(ts[k]) * 64 + lane]
-                                     : (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-                    }
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
                         const int tr = wave * 8 + k;
