@@ -551,25 +551,32 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 __syncthreads();
                 // (B)
                 {
+                    // all 16 (token, head) rows computed in one branch-free
+                    // block (their latencies overlap), then stored
+                    uint32_t pk[16];
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const int tr = wave * 8 + k;
+                    for (int u = 0; u < 16; ++u) {
+                        const int k = u >> 1, hh = u & 1;
+                        float2 y = *reinterpret_cast<const float2*>(T + (wave * 8 + k) * TP + hh * 128 + 2 * lane);
+                        const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
+                        const float rms = rsqrtf(ss / 128 + heps);
+                        y.x = y.x * rms * w0;
+                        y.y = y.y * rms * w1;
+                        const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
+                        const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
+                        pk[u] = static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
+                    }
+                    if (isq) {
 #pragma unroll
-                        for (int hh = 0; hh < 2; ++hh) {
-                            float2 y = *reinterpret_cast<const float2*>(T + tr * TP + hh * 128 + 2 * lane);
-                            const float ss = wave_sum_dpp(__builtin_fmaf(y.x, y.x, y.y * y.y));
-                            const float rms = rsqrtf(ss / 128 + heps);
-                            y.x = y.x * rms * w0;
-                            y.y = y.y * rms * w1;
-                            const float o0 = __builtin_fmaf(y.x, p[k].x, y.y * p[k].y);
-                            const float o1 = __builtin_fmaf(y.x, p[k].z, y.y * p[k].w);
-                            const uint32_t packed =
-                                static_cast<uint32_t>(f32_to_f16(o0)) | (static_cast<uint32_t>(f32_to_f16(o1)) << 16);
-                            if (isq) {
-                                R[tr * RP + hh * 64 + lane] = ok[k] ? packed : 0u;
-                            } else if (ok[k]) {
-                                const int64_t bh = static_cast<int64_t>(tb[k]) * H + hfirst + hh;
-                                reinterpret_cast<uint32_t*>(out)[(bh * S + ts[k]) * 64 + lane] = packed;
+                        for (int u = 0; u < 16; ++u)
+                            R[(wave * 8 + (u >> 1)) * RP + (u & 1) * 64 + lane] = ok[u >> 1] ? pk[u] : 0u;
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 16; ++u) {
+                            const int k = u >> 1;
+                            if (ok[k]) {
+                                const int64_t bh = static_cast<int64_t>(tb[k]) * H + hfirst + (u & 1);
+                                reinterpret_cast<uint32_t*>(out)[(bh * S + ts[k]) * 64 + lane] = pk[u];
                             }
                         }
                     }
