@@ -435,7 +435,7 @@ struct LnLoader : RowsLoader<float> {
         return t;
     }
     template <int NB>
-    __device__ __forceinline__ void finish_row(int lane, float (&v)[NB][16]) const {
+    __device__ __forceinline__ void finish_row(int /*row*/, int lane, float (&v)[NB][16]) const {
 #pragma clang fp contract(off)
         static_assert(NB <= LN_MAXV && LN_THR == 256, "ln_modulate_row's thread layout");
         float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -475,10 +475,48 @@ struct LnLoader : RowsLoader<float> {
     }
 };
 
-template <typename Loader, RowOut OUT, int NB>
-__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, void* out,
-                                                                   float* __restrict__ scales, int M, int K,
-                                                                   float norm) {
+// Where row r's quantized values and scale go: a row-major [M, K] output ...
+struct RowDest {
+    void* out;
+    float* scales;
+    __device__ __forceinline__ uint8_t* row_out(int r, int K) const {
+        return reinterpret_cast<uint8_t*>(out) + static_cast<int64_t>(r) * K;
+    }
+    __device__ __forceinline__ float* scale(int r) const { return scales + r; }
+};
+
+// ... or two of them, rows [0, Ma) to the first and the rest to the second
+// (with PairLoader: the image and text rows of a joint block in one launch,
+// so that the few text rows' latency hides behind the image rows).
+struct PairDest {
+    RowDest a, b;
+    int Ma;
+    __device__ __forceinline__ uint8_t* row_out(int r, int K) const {
+        return r < Ma ? a.row_out(r, K) : b.row_out(r - Ma, K);
+    }
+    __device__ __forceinline__ float* scale(int r) const { return r < Ma ? a.scale(r) : b.scale(r - Ma); }
+};
+template <typename L>
+struct PairLoader {
+    static constexpr bool kWholeRow = L::kWholeRow;
+    typedef typename L::Raw Raw;
+    L a, b;
+    int Ma;
+    // (one copy of the segment's code, on the selected operands)
+    __device__ __forceinline__ void fetch(int row, int c, Raw& r) const {
+        const L& l = row < Ma ? a : b;
+        l.fetch(row < Ma ? row : row - Ma, c, r);
+    }
+    __device__ __forceinline__ static void unpack(const Raw& r, float* v) { L::unpack(r, v); }
+    template <int NB>
+    __device__ __forceinline__ void finish_row(int row, int lane, float (&v)[NB][16]) const {
+        const L& l = row < Ma ? a : b;
+        l.template finish_row<NB>(row < Ma ? row : row - Ma, lane, v);
+    }
+};
+
+template <typename Loader, RowOut OUT, int NB, typename Dest>
+__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, Dest dst, int M, int K, float norm) {
     constexpr int HBS = 1024;
     constexpr int PADDED = HBS + HBS / 16;
     __shared__ float lds_all[4 * PADDED];
@@ -494,7 +532,7 @@ __global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, vo
     float v[NB][16];
 #pragma unroll
     for (int b = 0; b < NB; ++b) Loader::unpack(raw[b], v[b]);
-    if constexpr (Loader::kWholeRow) ld.template finish_row<NB>(lane, v);
+    if constexpr (Loader::kWholeRow) ld.template finish_row<NB>(row, lane, v);
     float amax = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -530,9 +568,9 @@ __global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, vo
     }
     amax = wave_max_dpp(amax);
     constexpr float QMAX = (OUT == RowOut::Int8) ? 127.0f : 448.0f;
-    if (lane == 0) scales[row] = amax / QMAX;
+    if (lane == 0) *dst.scale(row) = amax / QMAX;
     const float inv = (amax > 0.0f) ? QMAX / amax : 0.0f;
-    uint8_t* o = reinterpret_cast<uint8_t*>(out) + static_cast<int64_t>(row) * K + lane;
+    uint8_t* o = dst.row_out(row, K) + lane;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -715,29 +753,33 @@ static int ilog2(int v) {
 size_t rows_lds_bytes(int K) { return sizeof(float) * (static_cast<size_t>(K) + K / 16 + 1 + 8); }
 
 // Rows of 1-4 Hadamard blocks of 1024 (K / 1024 of them), one wave per row.
-template <RowOut OUT, typename Loader>
-static hipError_t launch_wave_rows(const Loader& ld, void* out, float* scales, int M, int K, float norm,
-                                   hipStream_t stream) {
+template <RowOut OUT, typename Loader, typename Dest>
+static hipError_t launch_wave_rows(const Loader& ld, const Dest& dst, int M, int K, float norm, hipStream_t stream) {
     const int blocks = (M + 3) / 4;
     switch (K / 1024) {
         case 1:
-            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 1>), dim3(blocks), dim3(256), 0, stream, ld,
-                               out, scales, M, K, norm);
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 1, Dest>), dim3(blocks), dim3(256), 0, stream,
+                               ld, dst, M, K, norm);
             break;
         case 2:
-            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 2>), dim3(blocks), dim3(256), 0, stream, ld,
-                               out, scales, M, K, norm);
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 2, Dest>), dim3(blocks), dim3(256), 0, stream,
+                               ld, dst, M, K, norm);
             break;
         case 3:
-            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 3>), dim3(blocks), dim3(256), 0, stream, ld,
-                               out, scales, M, K, norm);
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 3, Dest>), dim3(blocks), dim3(256), 0, stream,
+                               ld, dst, M, K, norm);
             break;
         default:
-            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 4>), dim3(blocks), dim3(256), 0, stream, ld,
-                               out, scales, M, K, norm);
+            hipLaunchKernelGGL((fwht_quant_wave_rows_kernel<Loader, OUT, 4, Dest>), dim3(blocks), dim3(256), 0, stream,
+                               ld, dst, M, K, norm);
             break;
     }
     return hipGetLastError();
+}
+template <RowOut OUT, typename Loader>
+static hipError_t launch_wave_rows(const Loader& ld, void* out, float* scales, int M, int K, float norm,
+                                   hipStream_t stream) {
+    return launch_wave_rows<OUT>(ld, RowDest{out, scales}, M, K, norm, stream);
 }
 
 template <typename InT, RowOut OUT>
@@ -841,6 +883,38 @@ hipError_t launch_heads_fwht_quant(const uint16_t* attn, int batch, int H, int S
         hipLaunchKernelGGL(heads_fwht_quant_kernel<RowOut::Int8>, dim3(M), dim3(threads), lds, stream, attn, S, H, s0,
                            n, q_out, scales, ilog2(hbs), norm);
     return hipGetLastError();
+}
+
+hipError_t launch_ln_fwht_quant_pair(const float* xa, const float* shift_a, const float* scale_a, int Ma, void* qa,
+                                     float* sa, const float* xb, const float* shift_b, const float* scale_b, int Mb,
+                                     void* qb, float* sb, int K, int hbs, int mode, float eps, hipStream_t stream) {
+    if (!(hbs == 1024 && K % 1024 == 0 && K <= LN_MAX_DIM && Ma > 0 && Mb > 0 && Ma + Mb >= 1024)) {
+        const hipError_t e = launch_ln_fwht_quant(xa, shift_a, scale_a, Ma, K, hbs, mode, eps, qa, sa, stream);
+        return e != hipSuccess ? e : launch_ln_fwht_quant(xb, shift_b, scale_b, Mb, K, hbs, mode, eps, qb, sb, stream);
+    }
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(1024.0));
+    const PairLoader<LnLoader> ld{LnLoader{{xa, K}, shift_a, scale_a, eps}, LnLoader{{xb, K}, shift_b, scale_b, eps},
+                                  Ma};
+    const PairDest dst{RowDest{qa, sa}, RowDest{qb, sb}, Ma};
+    return mode == QIMG_QM_FP8_HADAMARD ? launch_wave_rows<RowOut::Fp8>(ld, dst, Ma + Mb, K, norm, stream)
+                                        : launch_wave_rows<RowOut::Int8>(ld, dst, Ma + Mb, K, norm, stream);
+}
+
+hipError_t launch_heads_fwht_quant_pair(const uint16_t* attn, int batch, int H, int S, int n_txt, int n_img, int hbs,
+                                        int mode, void* q_img, float* s_img, void* q_txt, float* s_txt,
+                                        hipStream_t stream) {
+    const int K = H * 128;
+    const int Ma = batch * n_img, Mb = batch * n_txt;
+    if (!(hbs == 1024 && K % 1024 == 0 && K / 1024 <= 4 && Ma > 0 && Mb > 0 && n_txt + n_img == S)) {
+        const hipError_t e =
+            launch_heads_fwht_quant(attn, batch, H, S, n_txt, n_img, hbs, mode, q_img, s_img, stream);
+        return e != hipSuccess ? e : launch_heads_fwht_quant(attn, batch, H, S, 0, n_txt, hbs, mode, q_txt, s_txt, stream);
+    }
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(1024.0));
+    const PairLoader<HeadsLoader> ld{HeadsLoader{attn, S, H, n_txt, n_img}, HeadsLoader{attn, S, H, 0, n_txt}, Ma};
+    const PairDest dst{RowDest{q_img, s_img}, RowDest{q_txt, s_txt}, Ma};
+    return mode == QIMG_QM_FP8_HADAMARD ? launch_wave_rows<RowOut::Fp8>(ld, dst, Ma + Mb, K, norm, stream)
+                                        : launch_wave_rows<RowOut::Int8>(ld, dst, Ma + Mb, K, norm, stream);
 }
 
 hipError_t launch_fwht_inplace(float* data, int M, int K, int hbs, hipStream_t stream) {

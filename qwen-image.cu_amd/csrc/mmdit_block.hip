@@ -204,16 +204,24 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         const bool share_i = same_quant(*il[0], *il[1]) && same_quant(*il[0], *il[2]);
         const bool share_t = same_quant(*tl[0], *tl[1]) && same_quant(*tl[0], *tl[2]);
         QIMG_TRY(mark(QIMG_PROF_ATTN_NORM));
-        if (share_i)
-            QIMG_TRY(launch_ln_fwht_quant(img, im + 0 * DIM, im + 1 * DIM, Mi, DIM, il[0]->hbs, il[0]->mode, EPS,
-                                          w.act_q, w.act_scales, s));
-        else
-            QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, Mi, DIM, EPS, s));
-        if (share_t)
-            QIMG_TRY(launch_ln_fwht_quant(txt, tm + 0 * DIM, tm + 1 * DIM, Mt, DIM, tl[0]->hbs, tl[0]->mode, EPS,
-                                          w.act_q_txt, w.act_scales_txt, s));
-        else
-            QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
+        // (both streams' rows in one launch when their quantizations agree:
+        // the few text rows' latency then hides behind the image rows)
+        if (share_i && share_t && same_quant(*il[0], *tl[0])) {
+            QIMG_TRY(launch_ln_fwht_quant_pair(img, im + 0 * DIM, im + 1 * DIM, Mi, w.act_q, w.act_scales, txt,
+                                               tm + 0 * DIM, tm + 1 * DIM, Mt, w.act_q_txt, w.act_scales_txt, DIM,
+                                               il[0]->hbs, il[0]->mode, EPS, s));
+        } else {
+            if (share_i)
+                QIMG_TRY(launch_ln_fwht_quant(img, im + 0 * DIM, im + 1 * DIM, Mi, DIM, il[0]->hbs, il[0]->mode, EPS,
+                                              w.act_q, w.act_scales, s));
+            else
+                QIMG_TRY(launch_layernorm_modulate(img, im + 0 * DIM, im + 1 * DIM, w.img_norm, Mi, DIM, EPS, s));
+            if (share_t)
+                QIMG_TRY(launch_ln_fwht_quant(txt, tm + 0 * DIM, tm + 1 * DIM, Mt, DIM, tl[0]->hbs, tl[0]->mode,
+                                              EPS, w.act_q_txt, w.act_scales_txt, s));
+            else
+                QIMG_TRY(launch_layernorm_modulate(txt, tm + 0 * DIM, tm + 1 * DIM, w.txt_norm, Mt, DIM, EPS, s));
+        }
 
         QIMG_TRY(mark(QIMG_PROF_QKV_GEMM));
         auto qkv_gemm = [&](int i) -> hipError_t {
@@ -350,19 +358,25 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             QIMG_TRY(launch_split_heads(w.attn16, w.txt_qkv[0], w.img_qkv[0], n_txt, n_img, batch, HEADS, s));
         }
         QIMG_TRY(mark(QIMG_PROF_OUT_GEMM));
-        if (Mi) {
-            if (heads_i)
-                QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, n_txt, n_img, b.to_out.hbs, b.to_out.mode,
-                                                 w.act_q, w.act_scales, s));
-            else
-                QIMG_TRY(quant(w.img_qkv[0], Mi, b.to_out));
-        }
-        if (Mt) {
-            if (heads_t)
-                QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, 0, n_txt, b.to_add_out.hbs,
-                                                 b.to_add_out.mode, w.act_q_txt, w.act_scales_txt, s));
-            else
-                QIMG_TRY(quant_txt(w.txt_qkv[0], Mt, b.to_add_out, s));
+        if (heads_i && heads_t && same_quant(b.to_out, b.to_add_out)) {
+            QIMG_TRY(launch_heads_fwht_quant_pair(w.attn16, batch, HEADS, S, n_txt, n_img, b.to_out.hbs,
+                                                  b.to_out.mode, w.act_q, w.act_scales, w.act_q_txt,
+                                                  w.act_scales_txt, s));
+        } else {
+            if (Mi) {
+                if (heads_i)
+                    QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, n_txt, n_img, b.to_out.hbs,
+                                                     b.to_out.mode, w.act_q, w.act_scales, s));
+                else
+                    QIMG_TRY(quant(w.img_qkv[0], Mi, b.to_out));
+            }
+            if (Mt) {
+                if (heads_t)
+                    QIMG_TRY(launch_heads_fwht_quant(w.attn16, batch, HEADS, S, 0, n_txt, b.to_add_out.hbs,
+                                                     b.to_add_out.mode, w.act_q_txt, w.act_scales_txt, s));
+                else
+                    QIMG_TRY(quant_txt(w.txt_qkv[0], Mt, b.to_add_out, s));
+            }
         }
         QIMG_TRY(gemm_pair(Mi, b.to_out, img, im + 2 * DIM, w.img_qkv[1], Mt, b.to_add_out, txt, tm + 2 * DIM,
                            w.txt_qkv[1], 0));
@@ -371,10 +385,16 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // LayerNorm + modulate (transformer.cu:754-764) straight into the
         // fc1 input quantization
         QIMG_TRY(mark(QIMG_PROF_MLP_NORM));
-        QIMG_TRY(launch_ln_fwht_quant(img, im + 3 * DIM, im + 4 * DIM, Mi, DIM, b.img_mlp_fc1.hbs, b.img_mlp_fc1.mode,
-                                      EPS, w.act_q, w.act_scales, s));
-        QIMG_TRY(launch_ln_fwht_quant(txt, tm + 3 * DIM, tm + 4 * DIM, Mt, DIM, b.txt_mlp_fc1.hbs, b.txt_mlp_fc1.mode,
-                                      EPS, w.act_q_txt, w.act_scales_txt, s));
+        if (same_quant(b.img_mlp_fc1, b.txt_mlp_fc1)) {
+            QIMG_TRY(launch_ln_fwht_quant_pair(img, im + 3 * DIM, im + 4 * DIM, Mi, w.act_q, w.act_scales, txt,
+                                               tm + 3 * DIM, tm + 4 * DIM, Mt, w.act_q_txt, w.act_scales_txt, DIM,
+                                               b.img_mlp_fc1.hbs, b.img_mlp_fc1.mode, EPS, s));
+        } else {
+            QIMG_TRY(launch_ln_fwht_quant(img, im + 3 * DIM, im + 4 * DIM, Mi, DIM, b.img_mlp_fc1.hbs,
+                                          b.img_mlp_fc1.mode, EPS, w.act_q, w.act_scales, s));
+            QIMG_TRY(launch_ln_fwht_quant(txt, tm + 3 * DIM, tm + 4 * DIM, Mt, DIM, b.txt_mlp_fc1.hbs,
+                                          b.txt_mlp_fc1.mode, EPS, w.act_q_txt, w.act_scales_txt, s));
+        }
 
         // GELU MLP (transformer.cu:780-808): fc1 of each stream on its own
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));

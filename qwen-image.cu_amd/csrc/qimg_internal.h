@@ -35,6 +35,18 @@ hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, 
 // FWHT + int8/e4m3 quantization of launch_fwht_quant (same values).
 hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float* scale, int M, int K, int hbs,
                                 int mode, float eps, void* q_out, float* scales, hipStream_t stream);
+// launch_ln_fwht_quant on the rows of two matrices with the same K, hbs
+// and mode (a joint block's image and text streams) in one launch where
+// the wave-per-row kernel takes them; the same values as two calls.
+hipError_t launch_ln_fwht_quant_pair(const float* xa, const float* shift_a, const float* scale_a, int Ma, void* qa,
+                                     float* sa, const float* xb, const float* shift_b, const float* scale_b, int Mb,
+                                     void* qb, float* sb, int K, int hbs, int mode, float eps, hipStream_t stream);
+// launch_heads_fwht_quant of the image rows (s0 = n_txt) and the text rows
+// (s0 = 0) of the joint sequences in one launch where the wave-per-row
+// kernel takes them; the same values as the two calls.
+hipError_t launch_heads_fwht_quant_pair(const uint16_t* attn, int batch, int H, int S, int n_txt, int n_img, int hbs,
+                                        int mode, void* q_img, float* s_img, void* q_txt, float* s_txt,
+                                        hipStream_t stream);
 // Rows s0 .. s0+n of each of `batch` sequences of the fp16 attention
 // output [batch][H][S][128] (K = H * 128, hbs >= 16) quantized as
 // launch_fwht_quant quantizes their fp32 split copy.
