@@ -674,10 +674,11 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     __builtin_amdgcn_s_barrier();
 
     // S^T = K Q^T of the tile in ring slot `slot`: blocks of keys
-    // 32*kb + (8*(r/4) + 4*half + r%4), query l32.
-    auto qk = [&](int slot, v16i (&acc)[2]) {
+    // 32*kb + (8*(r/4) + 4*half + r%4), query l32. The K fragments are read
+    // (qk_load) at the start of the softmax, well before the MFMAs that use
+    // them (qk_mma) at its end.
+    auto qk_load = [&](int slot, v4i (&kf)[2 * C::KSTEPS]) {
         const uint8_t* kb_lds = lds + slot * C::STAGE;
-        v4i kf[2 * C::KSTEPS];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const int row = kb * 32 + l32;
@@ -687,7 +688,8 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
                 kf[kb * C::KSTEPS + s] = *reinterpret_cast<const v4i*>(kb_lds + row * D + chunk * 16);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto qk_mma = [&](const v4i (&kf)[2 * C::KSTEPS], v16i (&acc)[2]) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -710,7 +712,11 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     // both groups compute what a single sequence of steps computes. Tiles
     // kt-1 (V, for waves 4-7), kt and kt+1 are resident during step kt.
     v16i sacc[2];
-    qk(0, sacc);
+    {
+        v4i kf[2 * C::KSTEPS];
+        qk_load(0, kf);
+        qk_mma(kf, sacc);
+    }
     const bool lag = wave >= AWAVES / 2;  // waves 4-7 run PV one step late
     v8h p[4];
     typedef float f2 __attribute__((ext_vector_type(2)));
@@ -723,6 +729,11 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
     float4 ks_cur = *reinterpret_cast<const float4*>(ksh);
     auto softmax = [&](int kt, auto masked_c) {
         constexpr bool MASKED = decltype(masked_c)::value;
+        // the next tile's K fragments (past the last tile the slot holds a
+        // re-fetched valid tile whose scores are not used)
+        v4i kf[2 * C::KSTEPS];
+        qk_load((kt + 1) % ANSLOT, kf);
+        __builtin_amdgcn_sched_barrier(0);
         const float4 ks4 = ks_cur;
         const float ks_lo = half ? ks4.z : ks4.x;
         const float ks_hi = half ? ks4.w : ks4.y;
@@ -794,9 +805,7 @@ __global__ __launch_bounds__(AQ * 2, 1) void sage_attn_kernel(
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        // the next tile's scores (past the last tile the slot holds a
-        // re-fetched valid tile whose scores are not used)
-        qk((kt + 1) % ANSLOT, sacc);
+        qk_mma(kf, sacc);  // the next tile's scores
     };
 
     auto pv = [&](int kt) {
