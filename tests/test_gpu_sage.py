@@ -97,6 +97,38 @@ def test_sage_output_dtypes(qimg, dt):
     assert torch.equal(o.float(), o32.to(dt).float())
 
 
+def test_sage_attention_graph_replays(qimg):
+    """The entry point's launches (K mean, Q/K quantization, V relayout,
+    attention) captured into a HIP graph replay to the eager result, with the
+    output and scratch cleared and eager work between replays."""
+    q, k, v = _inputs(4, 777, 128, 11)
+    qd, kd, vd = _dev(q), _dev(k), _dev(v)
+    scratch = torch.empty(qimg.sage_scratch_bytes(4, 777, 128), dtype=torch.uint8, device=DEV)
+    ref = qimg.attention_forward_sage_fp16io(qd, kd, vd, 0.0883883, scratch=scratch)
+    out = torch.empty_like(ref)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream
+        qimg.attention_forward_sage_fp16io(qd, kd, vd, 0.0883883, out=out, scratch=scratch)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qimg.attention_forward_sage_fp16io(qd, kd, vd, 0.0883883, out=out, scratch=scratch)
+    for rep in range(3):
+        out.zero_()
+        scratch.zero_()
+        junk = torch.randn(1 << 20, device=DEV).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), rep
+        del junk
+    del graph
+
+
 @pytest.mark.slow
 def test_sage_joint_attention_full_size_sampled(qimg, oracle):
     """Config: 24 heads, S = 4352 (256 txt + 4096 img), D = 128, sampled rows."""
