@@ -64,6 +64,9 @@ def _attn64(q, k, v, scale, causal):
 @pytest.mark.parametrize("BH,S,D,causal", [
     (2, 300, 128, False), (2, 64, 128, False), (1, 1, 128, False), (2, 200, 64, False),
     (2, 333, 128, True), (1, 130, 64, True), (2, 1000, 128, False),
+    # key-tile (64) and query-block (256) boundaries
+    (1, 63, 128, False), (1, 65, 128, True), (1, 256, 128, True), (1, 257, 64, False), (1, 513, 128, True),
+    (1, 512, 64, True),
 ])
 def test_sage_attention_vs_oracle(qimg, oracle, BH, S, D, causal):
     q, k, v = _inputs(BH, S, D, S * D + causal)
