@@ -271,6 +271,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                     QIMG_TRY(hipEventRecord(side->fork, s));
                     QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
                     QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
+                    QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM,
+                                                 side->stream));
                     QIMG_TRY(hipEventRecord(side->join, side->stream));
                     LinearArgs qv[8];
                     int n = 0;
@@ -319,6 +321,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             QIMG_TRY(hipEventRecord(side->fork, s));
             QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
             QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
+            QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM,
+                                         side->stream));
             QIMG_TRY(hipEventRecord(side->join, side->stream));
             QIMG_TRY(qkv_gemm(0));
             QIMG_TRY(qkv_gemm(2));
@@ -341,7 +345,6 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)
         QIMG_TRY(mark(QIMG_PROF_ATTENTION));
         QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
-        QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM, s));
         QIMG_TRY(launch_sage_attn_vt(ss.q_i8, ss.k_i8, ss.v_t, ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, s));
 
