@@ -17,8 +17,8 @@
 //    in the GEMM epilogue (one fused multiply-add, as the gate-add kernel);
 //  - the image- and text-stream linears of q, k, v, out-proj and fc2 share
 //    a launch when the text tiles fit the image GEMM's last tile round;
-//  - the K mean runs on a second stream, beside the Q and V preparation
-//    and the Q quantization (fork and join by events, which a graph
+//  - the K mean and the K quantization run on a second stream, beside
+//    the Q and V preparation and the Q quantization (fork and join by events, which a graph
 //    capture of the calling stream records as dependencies);
 //  - buffers whose producer has been consumed are reused (q/k/v of each
 //    stream hold the attention output, the projection and the MLP output);
@@ -242,8 +242,8 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // quantized to the Sage int8 (when its 32-token slices lie inside one
         // linear: n_txt a multiple of 32, the image rows split per sequence
         // unless n_img is one too), V in the V^T tile layout. K's two linears
-        // go first so that its mean runs on the side stream beside the Q and V
-        // linears (one launch of four to six problems).
+        // go first so that its mean and quantization run on the side stream
+        // beside the Q and V linears (one launch of four to six problems).
         bool merged = false, q_fused = false;
         const int nsplit = (batch > 1 && n_img % 32 != 0) ? batch : 1;
         const bool q_ok = n_txt % 32 == 0 && nsplit <= 4;
@@ -312,9 +312,9 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         }
         if (!merged) {
             // K first: its RMSNorm + concat + transpose + RoPE -> fp16
-            // (transformer.cu:617-666), then its mean (sageattention_sm80.cu:
-            // 759-773) on the side stream beside the q and v linears and the
-            // Q / V preparation.
+            // (transformer.cu:617-666), then its mean and quantization
+            // (sageattention_sm80.cu:759-773, 826-886) on the side stream beside
+            // the q and v linears and the Q / V preparation.
             QIMG_TRY(qkv_gemm(1));
             QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.k16, n_txt,
                                             n_img, batch, HEADS, EPS, s));
