@@ -87,6 +87,8 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
     };
     BlockScratch w{};
     w.t_silu = reinterpret_cast<float*>(take(4 * DIM));
+    w.mod_q = take(DIM);
+    w.mod_scale = reinterpret_cast<float*>(take(4));
     w.img_mods = reinterpret_cast<float*>(take(4 * 6 * DIM));
     w.txt_mods = reinterpret_cast<float*>(take(4 * 6 * DIM));
     w.img_norm = reinterpret_cast<float*>(take(4 * ri * DIM));
@@ -113,7 +115,8 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
 }
 
 hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
-                           int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s) {
+                           int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s,
+                           bool t_ready) {
     const int S = n_img + n_txt;
     // row counts of the img / txt streams over all sequences
     const int Mi = batch * n_img;
@@ -168,23 +171,29 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
 
         // modulation: silu(t_emb) -> img_mod / txt_mod (transformer.cu:506-515)
         QIMG_TRY(mark(QIMG_PROF_MODULATION));
-        QIMG_TRY(launch_silu(t_emb, w.t_silu, DIM, s));
-        QIMG_TRY(quant(w.t_silu, 1, b.img_mod));
+        // silu(t_emb) and its quantization are the same for every block of a
+        // call: computed by the first block (and again where img_mod's
+        // quantization changes), then kept in their own buffers
+        if (!t_ready) {
+            QIMG_TRY(launch_silu(t_emb, w.t_silu, DIM, s));
+            QIMG_TRY(launch_fwht_quant(w.t_silu, QIMG_FP32, 1, b.img_mod.K, b.img_mod.hbs, b.img_mod.mode, w.mod_q,
+                                       w.mod_scale, s));
+        }
         // both modulation linears in one GEMV launch where they share the
         // activation quantization (int8, the reference's weights)
         bool mods_done = false;
         if (same_quant(b.img_mod, b.txt_mod) && b.img_mod.mode == QIMG_QM_INT8_HADAMARD) {
-            const LinearArgs mi{w.act_q, w.act_scales, 1, b.img_mod.K, b.img_mod.w, b.img_mod.scales, b.img_mod.N,
+            const LinearArgs mi{w.mod_q, w.mod_scale, 1, b.img_mod.K, b.img_mod.w, b.img_mod.scales, b.img_mod.N,
                                 b.img_mod.bias, w.img_mods, nullptr, nullptr};
-            const LinearArgs mt{w.act_q, w.act_scales, 1, b.txt_mod.K, b.txt_mod.w, b.txt_mod.scales, b.txt_mod.N,
+            const LinearArgs mt{w.mod_q, w.mod_scale, 1, b.txt_mod.K, b.txt_mod.w, b.txt_mod.scales, b.txt_mod.N,
                                 b.txt_mod.bias, w.txt_mods, nullptr, nullptr};
-            mods_done = launch_gemv_pair(w.act_q, w.act_scales, 1, b.img_mod.K, mi, mt, QIMG_FP32, s, &e);
+            mods_done = launch_gemv_pair(w.mod_q, w.mod_scale, 1, b.img_mod.K, mi, mt, QIMG_FP32, s, &e);
             if (mods_done && e != hipSuccess) goto done;
         }
         if (!mods_done) {
-            QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.img_mod, w.img_mods, 0, s));
+            QIMG_TRY(gemm(w.mod_q, w.mod_scale, 1, b.img_mod, w.img_mods, 0, s));
             if (same_quant(b.img_mod, b.txt_mod)) {
-                QIMG_TRY(gemm(w.act_q, w.act_scales, 1, b.txt_mod, w.txt_mods, 0, s));
+                QIMG_TRY(gemm(w.mod_q, w.mod_scale, 1, b.txt_mod, w.txt_mods, 0, s));
             } else {
                 QIMG_TRY(linear(w.t_silu, 1, b.txt_mod, w.txt_mods, 0));
             }

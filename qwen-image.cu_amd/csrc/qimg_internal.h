@@ -234,6 +234,8 @@ hipError_t launch_gate_add(const float* x, const float* gate, const float* y, fl
 // mmdit_block.hip
 struct BlockScratch {
     float* t_silu;
+    uint8_t* mod_q;    // quantized silu(t_emb), the modulation linears' input,
+    float* mod_scale;  // kept across the blocks of one call
     float* img_mods;
     float* txt_mods;
     float* img_norm;
@@ -256,7 +258,11 @@ struct BlockScratch {
 int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, BlockScratch* out);
 // prof_ms != nullptr: the stream is synchronised at the end and each
 // category's time is ADDED to prof_ms[c].
+// t_ready: silu(t_emb) and its quantization for b.img_mod are already in
+// w.t_silu / w.mod_q (left by the previous block of the same call, whose
+// img_mod has the same K, Hadamard block and mode).
 hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
-                           int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s);
+                           int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s,
+                           bool t_ready = false);
 
 }  // namespace qimg
