@@ -318,6 +318,139 @@ def _time(torch, fn, iters=10):
     return _time_cycle(torch, [fn], iters=iters)
 
 
+def _c3_inputs(q, torch, dev, seed=3):
+    """The C3 attention operands as the joint block makes them: fp32 N(0,1)
+    Q, K, V rows of the 256 text and 4096 image tokens ([tokens, 24 x 128],
+    drawn from torch.Generator('cpu').manual_seed(seed) in the order q_txt,
+    q_img, k_txt, k_img, v_txt, v_img), per-head RMSNorm (eps 1e-6, weight 1)
+    and RoPE (qwen_image_pe(128, 128, 2, 256)) on Q and K, text first, fp16
+    [24, 4352, 128] (joint_heads_f16: cuda_kernels.cu:1656-1687, 1935-1962,
+    transformer.cu:106-130, 617-674)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    n_txt, n_img = 256, 4096
+    rows = [torch.randn(n, 3072, generator=g).to(dev) for n in (n_txt, n_img) * 3]
+    ones = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    pe = torch.from_numpy(q.qwen_image_pe(128, 128, 2, n_txt)).to(dev)
+    q16 = q.joint_heads_f16(rows[0], rows[1], ones, ones, pe)
+    k16 = q.joint_heads_f16(rows[2], rows[3], ones, ones, pe)
+    v16 = q.joint_heads_f16(rows[4], rows[5])
+    torch.cuda.synchronize()
+    return q16, k16, v16
+
+
+PROBE_KINDS = {  # qimg_probe_mfma kind: (name, ops per instruction, spec peak in TOP/s, cycles per instruction)
+    0: ("v_mfma_i32_32x32x32_i8", 65536, PEAK_INT8_TOPS, 32),
+    1: ("v_mfma_i32_16x16x64_i8", 32768, PEAK_INT8_TOPS, 16),
+    2: ("v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3)", 131072, 5033.0, 64),
+    3: ("v_mfma_f32_32x32x16_f16", 32768, PEAK_FP16_TFLOPS, 32),
+    4: ("v_mfma_f32_32x32x16_bf16", 32768, PEAK_FP16_TFLOPS, 32),
+}
+
+
+def _mfma_ceiling(torch, dev, launches=12, timed=3):
+    """The matrix cores' sustained rate on this GPU (lib/libqimg_probe.so,
+    csrc/mfma_probe.hip): a register-only loop of one MFMA form on every SIMD
+    (one or two waves per SIMD), `launches` back-to-back launches of ~10-20
+    ms, the median of the last `timed` taken (the clock ramps under load). The
+    shader clock comes from the waves' own s_memtime / s_memrealtime (100
+    MHz) counters. frac_of_spec = rate / the spec peak (2.4 GHz);
+    clock_ghz x 1024 SIMDs x ops per cycle is what that clock allows."""
+    import ctypes
+    import numpy as np
+    lib = ctypes.CDLL(os.path.join(ROOT, "qwen-image.cu_amd", "lib", "libqimg_probe.so"))
+    lib.qimg_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for kind, (name, ops, peak, cyc) in PROBE_KINDS.items():
+        per_iter = lib.qimg_probe_mfma_per_iter(kind)
+        iters = max(1, int(2.0e7 // (per_iter * cyc)))  # ~10 ms per wave at 2 GHz
+        for wps in (1, 2):
+            waves = cus * wps * 4
+            clocks = torch.zeros(4 * waves, dtype=torch.int64, device=dev)
+            sink = torch.zeros(cus * wps * 256, dtype=torch.int32, device=dev)
+            ts = []
+            for i in range(launches):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                st = lib.qimg_probe_mfma(kind, wps, cus, iters, ctypes.c_void_p(clocks.data_ptr()),
+                                         ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+                e1.record(stream)
+                if st != 0:
+                    raise RuntimeError(f"qimg_probe_mfma({kind}, {wps}) failed: {st}")
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            c = clocks.cpu().numpy().reshape(-1, 4).astype(np.float64)
+            ghz = float(np.median((c[:, 1] - c[:, 0]) / np.maximum(c[:, 3] - c[:, 2], 1) * 0.1))
+            ms = float(np.median(ts[-timed:]))
+            total = float(ops) * per_iter * iters * waves
+            tops = total / ms / 1e9
+            res[f"{name} wps{wps}"] = {"tops": round(tops, 1), "frac_of_spec": round(tops / peak, 4),
+                                       "clock_ghz": round(ghz, 3),
+                                       "frac_at_clock": round(tops * 1e12 / (ops / cyc * 1024 * ghz * 1e9), 4),
+                                       "ms": round(ms, 3)}
+            del clocks, sink
+    return res
+
+
+def _vendor_gemms(torch, dev, iters=20):
+    """hipBLASLt (through torch._int_mm and torch._scaled_mm) on this box at
+    the quantized linears' shapes, as a vendor-library reference point: int8
+    x int8 -> int32 [M, N] (no dequant epilogue) and e4m3 x e4m3 -> bf16
+    with unit scales; each the median of `iters` eager calls between
+    events. Operands are A [M, K] row-major times W [N, K] row-major (W^T
+    passed as a column-major [K, N] view), as this library's GEMMs take them."""
+    g = torch.Generator(device=dev).manual_seed(21)
+    res = {}
+    shapes = {"C1 4096x3072x3072": (4096, 3072, 3072), "fc1 4352x12288x3072": (4352, 12288, 3072),
+              "fc2 4352x3072x12288": (4352, 3072, 12288), "C5 fc1 13778x12288x3072": (13778, 12288, 3072),
+              "C5 fc2 13778x3072x12288": (13778, 3072, 12288)}
+    f8 = getattr(torch, "float8_e4m3fn", None)
+    for tag, (M, N, K) in shapes.items():
+        a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+        w = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        ops = 2.0 * M * N * K
+        entry = {}
+
+        def timed(fn):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(iters):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                ts.append((e0, e1))
+            torch.cuda.synchronize()
+            return sorted(e0.elapsed_time(e1) for e0, e1 in ts)[iters // 2]
+
+        try:
+            ms = timed(lambda: torch._int_mm(a, w.t()))
+            entry["int8_ms"] = round(ms, 4)
+            entry["int8_tops"] = round(ops / ms / 1e9, 1)
+            entry["int8_frac_of_spec"] = round(ops / ms / 1e9 / PEAK_INT8_TOPS, 4)
+        except Exception as ex:  # noqa: BLE001 - reported, not fatal
+            entry["int8_error"] = str(ex)[:200]
+        if f8 is not None:
+            try:
+                af = (torch.randn(M, K, generator=g, device=dev) * 0.5).to(f8)
+                wf = (torch.randn(N, K, generator=g, device=dev) * 0.5).to(f8)
+                one = torch.ones((), device=dev)
+                ms = timed(lambda: torch._scaled_mm(af, wf.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
+                entry["e4m3_ms"] = round(ms, 4)
+                entry["e4m3_tflops"] = round(ops / ms / 1e9, 1)
+                entry["e4m3_frac_of_spec"] = round(ops / ms / 1e9 / 5033.0, 4)
+                del af, wf
+            except Exception as ex:  # noqa: BLE001
+                entry["e4m3_error"] = str(ex)[:200]
+        res[tag] = entry
+        del a, w
+    return res
+
+
 def _extra(q, torch, dev):
     out = {}
     g = torch.Generator(device="cpu").manual_seed(0)
@@ -338,24 +471,42 @@ def _extra(q, torch, dev):
     out["linear_c1_gemm_only_tflops"] = round(ops / ms_gemm / 1e9, 1)
     ms_q = _time(torch, lambda: q.quantize_activation_hadamard(x, 1024))
     out["act_quant_c1_gbs"] = round((M * K * 3 + 4 * M) / ms_q / 1e6, 1)
-    # C3: SageAttention, 24 heads, S = 4352, D = 128
-    BH, S, Dh = 24, 4352, 128
-    qh = torch.randn(BH, S, Dh, generator=g).to(torch.float16).to(dev)
-    kh = torch.randn(BH, S, Dh, generator=g).to(torch.float16).to(dev)
-    vh = torch.randn(BH, S, Dh, generator=g).to(torch.float16).to(dev)
-    ao = torch.empty(BH, S, Dh, dtype=torch.float32, device=dev)
+    # C3: SageAttention, 24 heads, S = 4352 (256 text + 4096 image tokens),
+    # D = 128, on its configured inputs: Q, K, V fp32 N(0,1) as the text and
+    # image streams' [tokens, 24 x 128] rows; Q and K get the per-head RMSNorm
+    # (eps 1e-6, weight 1) and the Qwen-Image RoPE of a 64 x 64 latent grid
+    # (qwen_image_pe(128, 128, 2, 256), text tokens first), all three are
+    # concatenated text first and transposed to fp16 [24, 4352, 128] by
+    # joint_heads_f16 (the block's pre-attention pass). Output: fp16 [24,
+    # 4352, 128] (head-major, what the block's out-projection quantization
+    # reads) and bf16 in the same layout; the config's bf16 [1, 4352, 24,
+    # 128] is the same values with heads and tokens swapped.
+    q16, k16, v16 = _c3_inputs(q, torch, dev)
+    BH, S, Dh = q16.shape
+    ao = torch.empty(BH, S, Dh, dtype=torch.float16, device=dev)
+    ab = torch.empty(BH, S, Dh, dtype=torch.bfloat16, device=dev)
     sscr = torch.empty(q.sage_scratch_bytes(BH, S, Dh), dtype=torch.uint8, device=dev)
     sc = 1.0 / math.sqrt(128.0)
-    ms_att = _time(torch, lambda: q.attention_forward_sage_fp16io(qh, kh, vh, sc, out=ao, scratch=sscr))
-    qi, qs = q.sage_quant_q(qh)
-    km = q.sage_k_mean(kh)
-    ki, ks = q.sage_quant_k(kh, km)
-    ms_core = _time(torch, lambda: q.sage_attn_quantized(qi, ki, vh, qs, ks, sc, scratch=sscr))
+    ms_att = _time(torch, lambda: q.attention_forward_sage_fp16io(q16, k16, v16, sc, out=ao, scratch=sscr),
+                   iters=21)
+    ms_att_bf = _time(torch, lambda: q.attention_forward_sage_fp16io(q16, k16, v16, sc, out=ab, scratch=sscr),
+                      iters=21)
+    qi, qs = q.sage_quant_q(q16)
+    km = q.sage_k_mean(k16)
+    ki, ks = q.sage_quant_k(k16, km)
+    ms_core = _time(torch, lambda: q.sage_attn_quantized(qi, ki, v16, qs, ks, sc, scratch=sscr), iters=21)
     flops = 4.0 * BH * S * S * Dh
+    out["sage_c3_inputs"] = ("Q,K,V fp32 N(0,1) [4352, 24x128] (256 txt + 4096 img); RMSNorm (eps 1e-6, w 1) + "
+                             "RoPE(qwen_image_pe(128,128,2,256)) on Q,K; fp16 [24,4352,128] via joint_heads_f16")
+    out["sage_c3_output"] = "fp16 [24,4352,128] head-major (sage_c3_ms); bf16 same layout (sage_c3_bf16out_ms)"
     out["sage_c3_ms"] = round(ms_att, 4)
+    out["sage_c3_bf16out_ms"] = round(ms_att_bf, 4)
     out["sage_c3_tflops"] = round(flops / ms_att / 1e9, 1)
+    out["sage_c3_attn_kernel_ms"] = round(ms_core, 4)
     out["sage_c3_attn_kernel_tflops"] = round(flops / ms_core / 1e9, 1)
     out["sage_c3_frac_of_mixed_peak"] = round(flops / ms_att / 1e9 / 3355.0, 4)
+    out["sage_c3_attn_kernel_frac_of_mixed_peak"] = round(flops / ms_core / 1e9 / 3355.0, 4)
+    del q16, k16, v16, ao, ab, sscr, qi, ki, km
     # Small M: modulation (M = 1, and 2 rows for a CFG pair; 18432 x 3072)
     # and text-stream linears (M = 256). HBM bytes = int8 weights + scales +
     # bias + activations + fp32 outputs, each once. Each call uses the next
@@ -399,16 +550,19 @@ def _extra(q, torch, dev):
         del qws, qw0
     out.update(_block_c4(q, torch, dev, g))
     out.update(_step_c5(q, torch, dev))
+    out["mfma_ceiling"] = _mfma_ceiling(torch, dev)
+    out["hipblaslt_reference"] = _vendor_gemms(torch, dev)
     return out
 
 
-def _step_c5(q, torch, dev, n_blocks=60, steps=3):
+def _step_c5(q, torch, dev, n_blocks=60, steps=20):
     """One denoising step's transformer blocks at 1328x1328: 60 MMDiT joint
     blocks over 6889 image + 512 text tokens with e4m3 weights (FWHT front
     end, N(0, 0.02) weights, N(0, 0.01) biases, RMSNorm weights 1), for the
     two classifier-free-guidance branches (main.cu:761-773), run as two
     sequential forwards and as one forward of batch 2. The weights (20.4 GB)
-    are drawn on the GPU; every block has its own."""
+    are drawn on the GPU; every block has its own. Each figure is the median
+    of `steps` steps, each between its own pair of events."""
     n_img, n_txt, D, F = 83 * 83, 512, 3072, 12288
     gen = torch.Generator(device=dev).manual_seed(5)
     shapes = {"img_mod": (6 * D, D), "txt_mod": (6 * D, D)}
@@ -450,17 +604,19 @@ def _step_c5(q, torch, dev, n_blocks=60, steps=3):
     def run_bat():
         q.mmdit_blocks_forward(table, bat_img, bat_txt, t_emb, pe, scratch=sc2)
 
-    res = {}
+    res, spread = {}, {}
     for tag, fn in (("seq", run_seq), ("batched", run_bat)):
         fn()  # warm-up step
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for e0, e1 in ev:
+            e0.record()
             fn()
-        e1.record()
-        e1.synchronize()
-        res[tag] = e0.elapsed_time(e1) / steps
+            e1.record()
+        torch.cuda.synchronize()
+        ts = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+        res[tag] = ts[len(ts) // 2]
+        spread[tag] = (ts[0], ts[-1])
     prof = q.mmdit_blocks_forward(table, bat_img, bat_txt, t_emb, pe, scratch=sc2, profile=True)
     finite = all(bool(torch.isfinite(x).all().item()) for x in (bat_img, bat_txt, seq[0][0], seq[1][1]))
     S = n_img + n_txt
@@ -472,6 +628,8 @@ def _step_c5(q, torch, dev, n_blocks=60, steps=3):
     step_ops = 2 * n_blocks * (lin + att)
     del table, blocks
     return {"step_c5_seq_ms": round(res["seq"], 2), "step_c5_batched_ms": round(res["batched"], 2),
+            "step_c5_timing": f"median of {steps} steps each (min-max: seq {spread['seq'][0]:.2f}-"
+                              f"{spread['seq'][1]:.2f}, batched {spread['batched'][0]:.2f}-{spread['batched'][1]:.2f} ms)",
             "step_c5_top": round(step_ops / 1e12, 2),
             "step_c5_seq_tflops": round(step_ops / res["seq"] / 1e9, 1),
             "step_c5_batched_tflops": round(step_ops / res["batched"] / 1e9, 1),
@@ -485,9 +643,10 @@ def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
     weights and N(0, 0.01) biases, RMSNorm weights 1, the Qwen-Image RoPE
     table for a 64x64 latent grid, SageAttention. `copies` weight sets
     (340 MB each) alternate so weights stream from HBM as in a 60-block
-    forward. ms/block from a HIP graph of `blocks` consecutive blocks; the
-    13-category split from events around each category (no synchronisation
-    between categories), averaged over `profiled` eager blocks."""
+    forward. ms/block: the median over 21 replays of a HIP graph of `blocks`
+    consecutive blocks; the 13-category split from events around each
+    category (no synchronisation between categories), averaged over
+    `profiled` eager blocks."""
     n_img, n_txt, D, MLPD = 4096, 256, 3072, 12288
     shapes = {"img_mod": (6 * D, D), "txt_mod": (6 * D, D)}
     for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
@@ -518,7 +677,7 @@ def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
         return lambda: q.mmdit_block_forward(W, B, norms, img, txt, t_emb, pe, scratch=scratch)
 
     fns = [block(i) for i in range(blocks)]
-    ms_graph = _time_cycle(torch, fns, iters=5, min_calls=blocks, ramp_s=0.5)
+    ms_graph = _time_cycle(torch, fns, iters=21, min_calls=blocks, ramp_s=0.5)
     img.copy_(img0)
     txt.copy_(txt0)
     torch.cuda.synchronize()
@@ -609,34 +768,34 @@ def _cpu_model():
 
 
 def _cpu_baseline_sage(np, torch, q, dev, min_seconds=10.0, heads_per_run=2):
-    """The C3 attention (24 heads, S = 4352, D = 128, sm_scale 1/sqrt(128))
-    through the oracle's SageAttention (K mean, per-thread Q/K int8 quant,
-    integer QK^T, online softmax, fp16 PV) on the host cores, `heads_per_run`
-    heads at a time over successive heads until `min_seconds` of CPU work;
-    each sample's heads are also run on the GPU and compared."""
+    """The C3 attention (24 heads, S = 4352, D = 128, sm_scale 1/sqrt(128), on
+    the configured inputs of _c3_inputs: RMSNorm + RoPE on Q and K) through
+    the oracle's SageAttention (K mean, per-thread Q/K int8 quant, integer
+    QK^T, online softmax, fp16 PV) on the host cores, `heads_per_run` heads at
+    a time over successive heads until `min_seconds` of CPU work; the first
+    sample's heads are also compared with the GPU's output."""
     from oracle import oracle as o
-    BH, S, D = 24, 4352, 128
-    g = torch.Generator(device="cpu").manual_seed(3)
-    qh = torch.randn(BH, S, D, generator=g).to(torch.float16)
-    kh = torch.randn(BH, S, D, generator=g).to(torch.float16)
-    vh = torch.randn(BH, S, D, generator=g).to(torch.float16)
+    q16, k16, v16 = _c3_inputs(q, torch, dev)
+    BH, S, D = q16.shape
+    qh, kh, vh = (t.cpu().numpy() for t in (q16, k16, v16))
     sc = 1.0 / math.sqrt(128.0)
-    heads, worst = 0, 0.0
+    heads = 0
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < min_seconds and heads < BH:
         h0, h1 = heads, min(BH, heads + heads_per_run)
-        ref = o.sage_attention_fp16io(qh[h0:h1].numpy(), kh[h0:h1].numpy(), vh[h0:h1].numpy(), sc)
+        ref = o.sage_attention_fp16io(qh[h0:h1], kh[h0:h1], vh[h0:h1], sc)
+        if h0 == 0:
+            ref0 = ref.astype(np.float32)
         heads = h1
     dt = time.perf_counter() - t0
     # GPU parity on the first sample's heads
-    got = q.attention_forward_sage_fp16io(qh[:heads_per_run].to(dev), kh[:heads_per_run].to(dev),
-                                          vh[:heads_per_run].to(dev), sc, out_dtype=torch.float16)
-    ref0 = o.sage_attention_fp16io(qh[:heads_per_run].numpy(), kh[:heads_per_run].numpy(),
-                                   vh[:heads_per_run].numpy(), sc).astype(np.float32)
+    got = q.attention_forward_sage_fp16io(q16[:heads_per_run].contiguous(), k16[:heads_per_run].contiguous(),
+                                          v16[:heads_per_run].contiguous(), sc, out_dtype=torch.float16)
     worst = float(np.max(np.abs(got.float().cpu().numpy() - ref0)) / np.max(np.abs(ref0)))
     flops = 4.0 * heads * S * S * D
     return {"value": round(flops / dt / 1e9, 2), "unit": "GFLOP/s", "cores": o.get_threads(), "kind": "port",
-            "sample": f"{heads} of the 24 heads (S={S}, D={D}) through the C oracle's SageAttention in {dt:.1f} s",
+            "sample": f"{heads} of the 24 heads (S={S}, D={D}, RMSNorm+RoPE inputs) through the C oracle's "
+                      f"SageAttention in {dt:.1f} s",
             "gpu_max_rel_vs_oracle": worst}
 
 

@@ -390,7 +390,13 @@ int qimg_w4a4_gemm(const uint8_t* act_packed, const uint8_t* wgt_packed, const f
  * unswizzled nunchaku form), otherwise W4A16 over qweight [N, K/2] (NF4 or
  * offset-8 codes, nf4_grid) and scales4 fp32 [N, K/group_size]. svd_up bf16
  * [N, rank] and svd_down bf16 [K, rank] are the low-rank factors; smooth fp32
- * [K] is optional; had_block_size > 1 rotates x before the W4A16 residual. */
+ * [K] is optional; had_block_size > 1 rotates x before the W4A16 residual.
+ * w4a16_nunchaku != 0 (with w4a4_qweight NULL) is the reference's W4A16
+ * fallback for nunchaku weights (cuda_kernels.cu:4443-4470, taken there under
+ * FORCE_W4A16 or without the MMA copy): qweight holds the unswizzled two's
+ * complement nibbles, scales4 the fp32 [K/group_size, N] scales, nf4_grid and
+ * had_block_size are ignored, and the residual's input is bf16(x / smooth)
+ * with no rotation. */
 typedef struct qimg_int4_weight {
     int N, K, rank, group_size;
     int nf4_grid, had_block_size;
@@ -401,6 +407,7 @@ typedef struct qimg_int4_weight {
     const uint16_t* svd_up;
     const uint16_t* svd_down;
     const float* smooth;
+    int w4a16_nunchaku;
 } qimg_int4_weight;
 
 /* int4_scratch_bytes (cuda_kernels.cuh:475-487), or more where this

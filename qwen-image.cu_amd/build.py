@@ -3,6 +3,9 @@
     lib/libqimg_hot.so   the kernels + C ABI (include/qimg_hot.h), from csrc/
     lib/libqimg_host.so  the reference-signature C++ layer (host/kernels.h)
                          over the C ABI
+    lib/libqimg_probe.so the matrix-core rate probe bench.py reports the
+                         kernels against (csrc/mfma_probe.hip; no product
+                         code links it)
     tests/cpp/_build/test_host_api
                          the C++ layer's parity test program (links the CPU
                          oracle, so it is built only after oracle/ is)
@@ -28,6 +31,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib")
 HOT_SO = os.path.join(LIB, "libqimg_hot.so")
 HOST_SO = os.path.join(LIB, "libqimg_host.so")
+PROBE_SO = os.path.join(LIB, "libqimg_probe.so")
 TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host_api.cpp")
 TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host_api")
 ORACLE_DIR = os.path.join(ROOT, "oracle")
@@ -45,6 +49,7 @@ HIP_FLAGS = [
 SOURCES = ["hadamard_quant.hip", "gemm_w8a8.hip", "gemm_small_m.hip", "gemm_bf16.hip", "sage_attention.hip", "block_ops.hip",
            "mmdit_block.hip", "capi.hip", "linear_noalloc.hip", "int4.hip", "capi_int4.hip"]
 HOST_SOURCES = ["kernels.cpp", "checkpoint.cpp"]
+PROBE_SOURCE = "mfma_probe.hip"
 
 
 def _run(cmd):
@@ -74,13 +79,16 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
             o = os.path.join(OBJ, "host_" + os.path.splitext(s)[0] + ".o")
             futs.append(ex.submit(_compile, os.path.join(HOST, s), o, ("-x", "hip", "-I", HOST)))
             host_objs.append(o)
+        probe_obj = os.path.join(OBJ, "mfma_probe.o")
+        futs.append(ex.submit(_compile, os.path.join(CSRC, PROBE_SOURCE), probe_obj))
         for f in futs:
             f.result()
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", HOT_SO, *hot_objs])
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", HOST_SO, *host_objs,
           "-L", LIB, "-lqimg_hot", "-Wl,-rpath,$ORIGIN"])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", PROBE_SO, probe_obj])
     if verbose:
-        print(f"built {HOT_SO} and {HOST_SO}")
+        print(f"built {HOT_SO}, {HOST_SO} and {PROBE_SO}")
     return HOT_SO
 
 

@@ -159,7 +159,10 @@ int qimg_linear_int4(const float* x, int M, const qimg_int4_weight* w, const uin
     const bool w4a4 = w->w4a4_qweight != nullptr;
     if (w4a4 && gs != 64 && gs != 128)
         return api_fail(QIMG_ERR_UNSUPPORTED, "%s: W4A4 group_size %d not supported (64 or 128)", fn, gs);
-    const int hbs = w4a4 ? 1 : (w->had_block_size > 1 ? w->had_block_size : 1);
+    // nunchaku weights through the W4A16 residual: signed nibbles, scales
+    // [K/gs, N], no rotation (cuda_kernels.cu:4443-4470)
+    const bool nk16 = !w4a4 && w->w4a16_nunchaku != 0;
+    const int hbs = (w4a4 || nk16) ? 1 : (w->had_block_size > 1 ? w->had_block_size : 1);
     QIMG_REQUIRE((hbs & (hbs - 1)) == 0 && K % hbs == 0, "%s: had_block_size %d must be a power of two dividing K", fn,
                  w->had_block_size);
     if (K > 32768) return api_fail(QIMG_ERR_UNSUPPORTED, "%s: K=%d exceeds the row limit 32768", fn, K);
@@ -202,7 +205,8 @@ int qimg_linear_int4(const float* x, int M, const qimg_int4_weight* w, const uin
                                    w->w4a4_wscales, out, M, N, K, gs, r > 0, bias_bf16, gelu != 0, s);
     } else {
         uint16_t* deq = reinterpret_cast<uint16_t*>(base + L.a);
-        e = qimg::launch_dequant_int4_bf16(w->qweight, w->scales4, deq, N, K, gs, w->nf4_grid != 0, 0, 0, s);
+        e = nk16 ? qimg::launch_dequant_int4_bf16(w->qweight, w->scales4, deq, N, K, gs, 0, 1, 1, s)
+                 : qimg::launch_dequant_int4_bf16(w->qweight, w->scales4, deq, N, K, gs, w->nf4_grid != 0, 0, 0, s);
         if (e == hipSuccess)
             e = qimg::launch_linear_bf16(reinterpret_cast<const uint16_t*>(base + L.xr), QIMG_BF16, M, K, deq, N,
                                          bias_bf16, out, gelu != 0, s, r > 0);

@@ -763,7 +763,7 @@ int small_m_variant(int M, int N, int K) {
     if (M <= GV_MAXM) return 3;
     if (M <= 32) return 1;
     const int64_t big_tiles = static_cast<int64_t>((M + 255) / 256) * ((N + 255) / 256);
-    return big_tiles < 128 ? 2 : 0;
+    return big_tiles < kSmallMTileLimit ? 2 : 0;
 }
 
 hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int M, int K, const void* w_q,

@@ -1152,19 +1152,22 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
                                         : dispatch_tiled<false>(P, out_dtype, gelu, stream);
 }
 
-// Up to six linears of one mode, output type and epilogue in one launch of
-// the large tiles (the joint block's q, k and v of both streams: at 4096 +
-// 256 tokens each pair is 204 tiles on 256 CUs, together 612 tiles in 2.4
-// rounds instead of three launches of one round each; 4352 x 9216 x 3072
+// Up to kMaxProblems linears of one mode, output type and epilogue in one
+// launch of the large tiles (the joint block's q, k and v of both streams: at
+// 4096 + 256 tokens each pair is 204 tiles on 256 CUs, together 612 tiles in
+// 2.4 rounds instead of three launches of one round each; 4352 x 9216 x 3072
 // measured 131 us against 3 x 48 us). Returns hipErrorNotSupported, having
-// launched nothing, when the kernel choice is not automatic or a linear does
-// not fit the large tiles; the caller then runs them one by one. Each output
-// element is computed exactly as in a launch of its own.
-hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_dtype, int gelu,
-                               hipStream_t stream) {
+// launched nothing, when the kernel choice is not automatic, a linear does
+// not fit the large tiles or the whole launch has fewer tiles than a single
+// linear needs to be given the large tiles (small_m_variant's threshold); the
+// caller then runs them one by one. Each output element is computed exactly
+// as in a launch of its own.
+static_assert(kMaxLinearMulti == kMaxProblems, "the multi-linear limit is the launch's problem table");
+
+static hipError_t build_linear_multi(const LinearArgs* list, int n, int out_dtype, int gelu, TileProblems& P) {
     if (n < 1 || n > kMaxProblems || g_linear_kernel.load(std::memory_order_relaxed) != QIMG_LINEAR_AUTO)
         return hipErrorNotSupported;
-    TileProblems P{};
+    P = TileProblems{};
     for (int i = 0; i < n; ++i) {
         const LinearArgs& a = list[i];
         if (a.M <= 0 || a.N <= 0 || (a.K % BK) != 0) return hipErrorNotSupported;
@@ -1192,8 +1195,23 @@ hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_
         P.p[P.n++] = t;
         P.total += t.tiles;
     }
-    // the first linear must be one the large tiles serve on its own
-    if (small_m_variant(list[0].M, list[0].N, list[0].K) != 0) return hipErrorNotSupported;
+    // as many tiles as a lone linear needs to be given the large tiles
+    // (a problem of one sequence's rows may be smaller: C5's per-sequence Q
+    // slices of 2025 rows at batch 2 are 96 tiles each)
+    if (P.total < kSmallMTileLimit) return hipErrorNotSupported;
+    return hipSuccess;
+}
+
+hipError_t check_linear_multi(const LinearArgs* list, int n, int out_dtype, int gelu) {
+    TileProblems P;
+    return build_linear_multi(list, n, out_dtype, gelu, P);
+}
+
+hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_dtype, int gelu,
+                               hipStream_t stream) {
+    TileProblems P;
+    const hipError_t r = build_linear_multi(list, n, out_dtype, gelu, P);
+    if (r != hipSuccess) return r;
     return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
                                         : dispatch_tiled<false>(P, out_dtype, gelu, stream);
 }

@@ -129,6 +129,22 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         e = (x);                 \
         if (e != hipSuccess) goto done; \
     } while (0)
+    // Work forked to the side stream is joined back before any return, an
+    // error exit included: a graph capture then holds no unjoined fork, and
+    // in eager use no side-stream work outlives the call.
+    SideStream* forked = nullptr;
+    auto fork = [&](SideStream* f) -> hipError_t {
+        hipError_t r = hipEventRecord(f->fork, s);
+        if (r == hipSuccess) r = hipStreamWaitEvent(f->stream, f->fork, 0);
+        if (r == hipSuccess) forked = f;
+        return r;
+    };
+    // (the caller has recorded f->join on the side stream after its work)
+    auto join = [&](SideStream* f) -> hipError_t {
+        const hipError_t r = hipStreamWaitEvent(s, f->join, 0);
+        if (r == hipSuccess) forked = nullptr;
+        return r;
+    };
     if (prof) {
         for (auto& x : ev) QIMG_TRY(hipEventCreate(&x));
     }
@@ -252,7 +268,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // linear: n_txt a multiple of 32, the image rows split per sequence
         // unless n_img is one too), V in the V^T tile layout. K's two linears
         // go first so that its mean and quantization run on the side stream
-        // beside the Q and V linears (one launch of four to six problems).
+        // beside the Q and V linears (one launch of three to seven problems).
         bool merged = false, q_fused = false;
         const int nsplit = (batch > 1 && n_img % 32 != 0) ? batch : 1;
         const bool q_ok = n_txt % 32 == 0 && nsplit <= 4;
@@ -274,44 +290,46 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                 hk_img = HeadsOut{HEADS_K, HEADS, S, n_txt, n_img, 0, b.norm_k, pe, nullptr, EPS};
                 hk_txt = HeadsOut{HEADS_K, HEADS, S, 0, n_txt, 0, b.norm_added_k, pe, nullptr, EPS};
                 const LinearArgs ks[2] = {args(1, true, Mi, 0, w.k16, &hk_img), args(1, false, Mt, 0, w.k16, &hk_txt)};
-                hipError_t r = launch_linear_multi(ks, 2, il[0]->mode, QIMG_FP32, 0, s);
+                // the Q and V linears: nsplit image Q problems (at most 4),
+                // the text Q, up to 2 image V problems and the text V
+                static_assert(4 + 1 + 2 + 1 <= kMaxLinearMulti, "the Q/V launch holds at most eight linears");
+                LinearArgs qv[kMaxLinearMulti];
+                int n = 0;
+                if (q_ok) {
+                    for (int q = 0; q < nsplit; ++q) {
+                        hq_img[q] = HeadsOut{HEADS_Q, HEADS, S, n_txt, n_img, q * (batch / nsplit), b.norm_q, pe,
+                                             ss.q_scale, EPS};
+                        qv[n++] = args(0, true, Mi / nsplit, q * (Mi / nsplit), ss.q_i8, &hq_img[q]);
+                    }
+                    hq_txt = HeadsOut{HEADS_Q, HEADS, S, 0, n_txt, 0, b.norm_added_q, pe, ss.q_scale, EPS};
+                    qv[n++] = args(0, false, Mt, 0, ss.q_i8, &hq_txt);
+                } else {
+                    qv[n++] = args(0, true, Mi, 0, w.img_qkv[0], nullptr);
+                    qv[n++] = args(0, false, Mt, 0, w.txt_qkv[0], nullptr);
+                }
+                // (V rows split per sequence as Q's: a 32-row block then
+                // fills half of one key tile's rows, stored whole)
+                const int vsplit = (n_txt % 32 == 0 && nsplit <= 2) ? nsplit : 1;
+                for (int q = 0; q < vsplit; ++q) {
+                    hv_img[q] = HeadsOut{HEADS_V, HEADS, S, n_txt, n_img, q * (batch / vsplit), nullptr, nullptr,
+                                         nullptr, EPS};
+                    qv[n++] = args(2, true, Mi / vsplit, q * (Mi / vsplit), ss.v_t, &hv_img[q]);
+                }
+                hv_txt = HeadsOut{HEADS_V, HEADS, S, 0, n_txt, 0, nullptr, nullptr, nullptr, EPS};
+                qv[n++] = args(2, false, Mt, 0, ss.v_t, &hv_txt);
+                // Both launches are validated before the first is issued, so
+                // a refusal falls back to the unmerged path with nothing run.
+                hipError_t r = check_linear_multi(ks, 2, QIMG_FP32, 0);
+                if (r == hipSuccess) r = check_linear_multi(qv, n, QIMG_FP32, 0);
                 if (r == hipSuccess) {
+                    QIMG_TRY(launch_linear_multi(ks, 2, il[0]->mode, QIMG_FP32, 0, s));
                     merged = true;
-                    QIMG_TRY(hipEventRecord(side->fork, s));
-                    QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+                    QIMG_TRY(fork(side));
                     QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
                     QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM,
                                                  side->stream));
                     QIMG_TRY(hipEventRecord(side->join, side->stream));
-                    LinearArgs qv[8];
-                    int n = 0;
-                    if (q_ok) {
-                        for (int q = 0; q < nsplit; ++q) {
-                            hq_img[q] = HeadsOut{HEADS_Q, HEADS, S, n_txt, n_img, q * (batch / nsplit), b.norm_q, pe,
-                                                 ss.q_scale, EPS};
-                            qv[n++] = args(0, true, Mi / nsplit, q * (Mi / nsplit), ss.q_i8, &hq_img[q]);
-                        }
-                        hq_txt = HeadsOut{HEADS_Q, HEADS, S, 0, n_txt, 0, b.norm_added_q, pe, ss.q_scale, EPS};
-                        qv[n++] = args(0, false, Mt, 0, ss.q_i8, &hq_txt);
-                    } else {
-                        qv[n++] = args(0, true, Mi, 0, w.img_qkv[0], nullptr);
-                        qv[n++] = args(0, false, Mt, 0, w.txt_qkv[0], nullptr);
-                    }
-                    // (V rows split per sequence as Q's: a 32-row block then
-                    // fills half of one key tile's rows, stored whole)
-                    const int vsplit = (n_txt % 32 == 0 && nsplit <= 2) ? nsplit : 1;
-                    for (int q = 0; q < vsplit; ++q) {
-                        hv_img[q] = HeadsOut{HEADS_V, HEADS, S, n_txt, n_img, q * (batch / vsplit), nullptr, nullptr,
-                                             nullptr, EPS};
-                        qv[n++] = args(2, true, Mi / vsplit, q * (Mi / vsplit), ss.v_t, &hv_img[q]);
-                    }
-                    hv_txt = HeadsOut{HEADS_V, HEADS, S, 0, n_txt, 0, nullptr, nullptr, nullptr, EPS};
-                    qv[n++] = args(2, false, Mt, 0, ss.v_t, &hv_txt);
-                    r = launch_linear_multi(qv, n, il[0]->mode, QIMG_FP32, 0, s);
-                    if (r != hipSuccess) {
-                        e = r;  // the K linears ran: no fallback from here
-                        goto done;
-                    }
+                    QIMG_TRY(launch_linear_multi(qv, n, il[0]->mode, QIMG_FP32, 0, s));
                     q_fused = q_ok;
                 } else if (r != hipErrorNotSupported) {
                     e = r;
@@ -327,8 +345,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             QIMG_TRY(qkv_gemm(1));
             QIMG_TRY(launch_joint_heads_f16(w.txt_qkv[1], w.img_qkv[1], b.norm_added_k, b.norm_k, pe, w.k16, n_txt,
                                             n_img, batch, HEADS, EPS, s));
-            QIMG_TRY(hipEventRecord(side->fork, s));
-            QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+            QIMG_TRY(fork(side));
             QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
             QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM,
                                          side->stream));
@@ -353,7 +370,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
 
         // SageAttention, sm_scale = 1/sqrt(128) (transformer.cu:676-684)
         QIMG_TRY(mark(QIMG_PROF_ATTENTION));
-        QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
+        QIMG_TRY(join(side));
         QIMG_TRY(launch_sage_attn_vt(ss.q_i8, ss.k_i8, ss.v_t, ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, s));
 
@@ -418,8 +435,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         if (Mt) {
             hipStream_t st = s;
             if (Mi) {
-                QIMG_TRY(hipEventRecord(side->fork, s));
-                QIMG_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+                QIMG_TRY(fork(side));
                 st = side->stream;
             }
             QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1, st));
@@ -427,7 +443,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
             if (Mi) QIMG_TRY(hipEventRecord(side->join, side->stream));
         }
         if (Mi) QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
-        if (Mt && Mi) QIMG_TRY(hipStreamWaitEvent(s, side->join, 0));
+        if (Mt && Mi) QIMG_TRY(join(side));
         // both fc2 in one launch, with the gate2 residual (transformer.cu:
         // 812-818) in their epilogue
         QIMG_TRY(gemm_pair(Mi, b.img_mlp_fc2, img, im + 5 * DIM, w.img_qkv[2], Mt, b.txt_mlp_fc2, txt, tm + 5 * DIM,
@@ -446,6 +462,11 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
     }
 done:
 #undef QIMG_TRY
+    if (forked != nullptr) {
+        // error exit between a fork and its join: join whatever the side
+        // stream has queued (the first error is the one returned)
+        if (hipEventRecord(forked->join, forked->stream) == hipSuccess) (void)hipStreamWaitEvent(s, forked->join, 0);
+    }
     if (prof)
         for (auto& x : ev)
             if (x) (void)hipEventDestroy(x);

@@ -99,9 +99,14 @@ struct LinearArgs {
 };
 hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode, int out_dtype, int gelu,
                               hipStream_t stream);
-// Up to six linears (same mode, output type and epilogue) in one launch of
-// the large tiles; hipErrorNotSupported (nothing launched) when they do not
-// all fit it or the kernel choice is forced.
+// Up to kMaxLinearMulti linears (same mode, output type and epilogue) in one
+// launch of the large tiles; hipErrorNotSupported (nothing launched) when
+// they do not all fit it, the launch is too small for the large tiles or the
+// kernel choice is forced. check_linear_multi answers the same question
+// without launching, so a caller can validate several launches before it
+// starts the first.
+constexpr int kMaxLinearMulti = 8;
+hipError_t check_linear_multi(const LinearArgs* list, int n, int out_dtype, int gelu);
 hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_dtype, int gelu,
                                hipStream_t stream);
 hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales, int M, int K,
@@ -163,8 +168,9 @@ int set_linear_kernel(int which);
 int get_linear_kernel();
 
 // gemm_small_m.hip: 0 = use the large-tile kernel, 1 = 32x32 tiles
-// (M <= 32), 2 = 64x64 tiles (few large tiles), 3 = vector-ALU GEMV (int8,
-// M <= 4; e4m3 falls back to 1)
+// (M <= 32), 2 = 64x64 tiles (fewer than kSmallMTileLimit large tiles),
+// 3 = vector-ALU GEMV (int8, M <= 4; e4m3 falls back to 1)
+constexpr int kSmallMTileLimit = 128;
 int small_m_variant(int M, int N, int K);
 // Two int8 linears of one M <= 4 activation (act_q, act_scales, K) as one
 // GEMV launch into a.out and b.out (a.act_q / b.act_q are not read). Returns

@@ -5,6 +5,7 @@
 #include "kernels.h"
 
 #include <cstdarg>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -402,12 +403,21 @@ void linear_forward_int4(const Tensor& x, const QuantizedWeight& weight, const T
     w.svd_up = static_cast<const uint16_t*>(weight.svd_up.data);
     w.svd_down = static_cast<const uint16_t*>(weight.svd_down.data);
     w.smooth = static_cast<const float*>(weight.smooth.data);
-    const Tensor& w4 = weight.qweight_mma.data ? weight.qweight_mma : weight.qweight_rowmajor;
-    if (weight.nunchaku_swizzle && w4.data) {
+    // The reference takes W4A4 only for nunchaku weights with the MMA copy
+    // and without FORCE_W4A16 (cuda_kernels.cu:4362); other nunchaku weights
+    // go through its W4A16 fallback on the row-major nibbles (:4443-4470).
+    const bool use_w4a4 = weight.nunchaku_swizzle && weight.qweight_mma.data && !getenv("FORCE_W4A16");
+    if (use_w4a4) {
         REQUIRE(weight.wscales_rowmajor.dtype == DType::FP32 && weight.wscales_rowmajor.data, fn,
                 "W4A4 needs wscales_rowmajor FP32 [num_groups, N]");
-        w.w4a4_qweight = static_cast<const uint8_t*>(w4.data);
+        w.w4a4_qweight = static_cast<const uint8_t*>(weight.qweight_mma.data);
         w.w4a4_wscales = static_cast<const float*>(weight.wscales_rowmajor.data);
+    } else if (weight.nunchaku_swizzle && weight.qweight_rowmajor.data) {
+        REQUIRE(weight.wscales_rowmajor.dtype == DType::FP32 && weight.wscales_rowmajor.data, fn,
+                "W4A16 (nunchaku) needs wscales_rowmajor FP32 [num_groups, N]");
+        w.qweight = static_cast<const uint8_t*>(weight.qweight_rowmajor.data);
+        w.scales4 = static_cast<const float*>(weight.wscales_rowmajor.data);
+        w.w4a16_nunchaku = 1;
     } else {
         REQUIRE(weight.qweight.data && weight.scales4.dtype == DType::FP32, fn,
                 "W4A16 needs qweight [N, K/2] and scales4 FP32 [N, K/group_size]");

@@ -422,28 +422,33 @@ def w4a4_gemm(act_packed: torch.Tensor, wgt_packed: torch.Tensor, act_scales: to
 class _Int4Weight(ctypes.Structure):
     _fields_ = [("N", _I), ("K", _I), ("rank", _I), ("group_size", _I), ("nf4_grid", _I), ("had_block_size", _I),
                 ("qweight", _P), ("scales4", _P), ("w4a4_qweight", _P), ("w4a4_wscales", _P), ("svd_up", _P),
-                ("svd_down", _P), ("smooth", _P)]
+                ("svd_down", _P), ("smooth", _P), ("w4a16_nunchaku", _I)]
 
 
 class Int4Weight:
     """The INT4_SVD fields of QuantizedWeight (cuda_kernels.cuh:194-213).
     W4A4 when w4a4_qweight (two's complement [N, K/2]) and w4a4_wscales
-    ([K/gs, N]) are given, else W4A16 over qweight / scales4 ([N, K/gs])."""
+    ([K/gs, N]) are given, else W4A16 over qweight / scales4 ([N, K/gs]).
+    w4a16_nunchaku: the reference's W4A16 fallback for nunchaku weights
+    (cuda_kernels.cu:4443-4470): qweight holds two's complement nibbles,
+    scales4 is [K/gs, N], and x is not rotated."""
 
     def __init__(self, N, K, group_size, svd_up=None, svd_down=None, qweight=None, scales4=None, nf4_grid=True,
-                 had_block_size=1, w4a4_qweight=None, w4a4_wscales=None, smooth=None):
+                 had_block_size=1, w4a4_qweight=None, w4a4_wscales=None, smooth=None, w4a16_nunchaku=False):
         self.N, self.K, self.group_size = N, K, group_size
         self.svd_up, self.svd_down = svd_up, svd_down
         self.rank = 0 if svd_up is None else int(svd_up.shape[1])
         self.qweight, self.scales4, self.nf4_grid, self.had_block_size = qweight, scales4, nf4_grid, had_block_size
         self.w4a4_qweight, self.w4a4_wscales, self.smooth = w4a4_qweight, w4a4_wscales, smooth
+        self.w4a16_nunchaku = w4a16_nunchaku
 
     def struct(self) -> _Int4Weight:
         def p(t):
             return None if t is None else t.data_ptr()
         return _Int4Weight(self.N, self.K, self.rank, self.group_size, int(bool(self.nf4_grid)),
                            int(self.had_block_size), p(self.qweight), p(self.scales4), p(self.w4a4_qweight),
-                           p(self.w4a4_wscales), p(self.svd_up), p(self.svd_down), p(self.smooth))
+                           p(self.w4a4_wscales), p(self.svd_up), p(self.svd_down), p(self.smooth),
+                           int(bool(self.w4a16_nunchaku)))
 
 
 def int4_scratch_bytes(M: int, K: int, N: int, svd_rank: int) -> int:

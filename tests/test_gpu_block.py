@@ -340,7 +340,8 @@ def _gpu_block(qimg, seed, mode=0):
     return gpu_block(qimg, seed, mode)
 
 
-@pytest.mark.parametrize("n_img,n_txt,batch", [(4096, 256, 1), (1024, 512, 2), (4356, 512, 1)])
+@pytest.mark.parametrize("n_img,n_txt,batch", [(4096, 256, 1), (1024, 512, 2), (4356, 512, 1), (2025, 256, 2),
+                                              (1681, 256, 3)])
 def test_mmdit_block_same_for_every_kernel_choice(qimg, n_img, n_txt, batch):
     """At full block sizes the dispatcher pairs the image- and text-stream
     linears in one launch, splits tail tile rows off to the small-tile kernel
@@ -348,7 +349,11 @@ def test_mmdit_block_same_for_every_kernel_choice(qimg, n_img, n_txt, batch):
     kernel everywhere must give the same bits (int8 accumulation is exact).
     At 4356 + 512 tokens the image fc1 splits its tail rows off while the
     text fc1 (two tile rows) runs on the side stream beside the image
-    fc2-input quantization."""
+    fc2-input quantization. At 2025 + 256 tokens in a batch of 2 (and 1681
+    + 256 in a batch of 3) the image Q linears are split per sequence into
+    problems smaller than the large tiles take alone (96 and 84 tiles): the
+    merged q/k/v launches are sized as a whole and checked before the first
+    is issued."""
     W, B, nr = _gpu_block(qimg, 3)
     table = qimg.BlockTable([(W, B, nr)])
     g = torch.Generator(device=DEV).manual_seed(4)

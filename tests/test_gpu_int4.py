@@ -259,6 +259,53 @@ def test_linear_int4(qimg, oracle, M, N, K, r, gs, w4a4, smooth, nf4, hbs, gelu)
     assert rel <= 2e-2 and cos >= 0.999, (rel, cos)
 
 
+@pytest.mark.parametrize("M,N,K,r,gs,smooth,gelu", [
+    (256, 3072, 3072, 32, 64, True, False),   # the W4A4 case's nunchaku weights through W4A16
+    (40, 256, 512, 16, 128, False, True),
+])
+def test_linear_int4_nunchaku_w4a16(qimg, oracle, M, N, K, r, gs, smooth, gelu):
+    """The reference's W4A16 fallback for nunchaku weights
+    (cuda_kernels.cu:4443-4470): the row-major two's complement nibbles and
+    [K/gs, N] scales dequantized to bf16 (signed, scales_gn), times bf16 of
+    the smoothed x with no rotation, onto the low-rank product, then the
+    bias and GELU."""
+    rng = np.random.default_rng(7 * M + N + K + r + gs + smooth)
+    c = _int4_case(oracle, rng, M, N, K, r, gs, True, smooth)
+    dev = lambda a: None if a is None else _f32(a)
+    bdev = lambda a: None if a is None else _bf16_bits_dev(a)
+    w = qimg.Int4Weight(N, K, gs, svd_up=bdev(c["up"]), svd_down=bdev(c["down"]), qweight=_u8(c["wp"]),
+                        scales4=_f32(c["ws"]), had_block_size=1024, nf4_grid=True, smooth=dev(c["sm"]),
+                        w4a16_nunchaku=True)
+    out = qimg.linear_forward_int4(_f32(c["x"]), w, bias=_bf16_bits_dev(c["bias"]), apply_gelu=gelu)
+    torch.cuda.synchronize()
+    rows = _rows(M, rng, 16)
+    got = out.cpu().numpy()[rows].astype(np.float64)
+    assert np.isfinite(got).all()
+    # the oracle's W4A16 composite with the nunchaku dequantization
+    x = c["x"][rows]
+    v = (x / c["sm"] if c["sm"] is not None else x).astype(np.float32)
+    xs = oracle.bf16_bits_to_f32(oracle.bf16_bits_from_f32(v)).reshape(v.shape).astype(np.float64)
+    lora = np.zeros((len(rows), N))
+    if r:
+        down = oracle.bf16_bits_to_f32(c["down"]).reshape(K, r).astype(np.float64)
+        up = oracle.bf16_bits_to_f32(c["up"]).reshape(N, r).astype(np.float64)
+        lr = (xs @ down).astype(np.float32)
+        lr16 = oracle.bf16_bits_to_f32(oracle.bf16_bits_from_f32(lr)).reshape(lr.shape).astype(np.float64)
+        lora = (lr16 @ up.T).astype(np.float32)
+    deq = oracle.dequant_int4_bf16(c["wp"], c["ws"], K, gs, nf4=False, scales_gn=True, signed_int4=True)
+    wd = oracle.bf16_bits_to_f32(deq).reshape(N, K).astype(np.float64)
+    want = lora.astype(np.float64) + xs @ wd.T + oracle.bf16_bits_to_f32(c["bias"]).astype(np.float64)
+    if gelu:
+        want = oracle.gelu_tanh64(want)
+    assert np.max(np.abs(got - want)) <= 1e-3 * np.max(np.abs(want)) + 1e-6, np.max(np.abs(got - want))
+    # and not the W4A4 result on the same weights (activations kept in bf16)
+    w4 = qimg.Int4Weight(N, K, gs, svd_up=bdev(c["up"]), svd_down=bdev(c["down"]), w4a4_qweight=_u8(c["wp"]),
+                         w4a4_wscales=_f32(c["ws"]), smooth=dev(c["sm"]))
+    out4 = qimg.linear_forward_int4(_f32(c["x"]), w4, bias=_bf16_bits_dev(c["bias"]), apply_gelu=gelu)
+    torch.cuda.synchronize()
+    assert not torch.equal(out, out4)
+
+
 def test_linear_int4_rejects_bad_arguments(qimg):
     x = torch.zeros(4, 128, device=DEV)
     w = qimg.Int4Weight(64, 128, 64)  # neither residual form

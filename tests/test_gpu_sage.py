@@ -148,3 +148,66 @@ def test_sage_joint_attention_full_size_sampled(qimg, oracle):
         ref = oracle.sage_attn(qi, ki, v, qs, ks, scale, rows=(r0, r0 + 128))[:, r0:r0 + 128].astype(np.float32)
         g = got[:, r0:r0 + 128]
         assert np.max(np.abs(g - ref)) <= 2e-3 * np.max(np.abs(ref)) + 2e-3
+
+
+@pytest.mark.slow
+def test_sage_joint_attention_c3_inputs(qimg, oracle):
+    """C3 on its configured inputs: Q, K, V fp32 N(0,1) rows of the 256 text
+    and 4096 image tokens ([tokens, 24 x 128]); per-head RMSNorm (eps 1e-6,
+    weight 1) and the Qwen-Image RoPE (qwen_image_pe(128, 128, 2, 256), text
+    first) on Q and K; concatenated text first and transposed to fp16 [24,
+    4352, 128] (cuda_kernels.cu:1656-1687, 1935-1962; transformer.cu:106-130,
+    617-674). The operands are made by the oracle's restatement on the CPU,
+    and the GPU's joint_heads_f16 is checked against them at its own bar; the
+    attention is then compared with the oracle on 128-query windows of every
+    head (text rows, the first image rows, a middle window and the ragged
+    tail) and with float64 attention at the stated tolerance."""
+    from oracle import block as blk
+    n_txt, n_img, H, D = 256, 4096, 24, 128
+    S = n_txt + n_img
+    rng = np.random.default_rng(31)
+    rows = [rng.standard_normal((n, H * D)).astype(np.float32) for n in (n_txt, n_img) * 3]
+    ones = oracle.bf16_bits_from_f32(np.ones(D, np.float32))
+    pe = qimg.qwen_image_pe(128, 128, 2, n_txt)
+    q = blk.rope_f16(blk.concat_transpose(blk.rms_norm_heads(rows[0], ones), blk.rms_norm_heads(rows[1], ones)), pe)
+    k = blk.rope_f16(blk.concat_transpose(blk.rms_norm_heads(rows[2], ones), blk.rms_norm_heads(rows[3], ones)), pe)
+    v = blk.concat_transpose(rows[4], rows[5]).astype(np.float16)
+    # the library's pre-attention pass on the same rows, at its own bar
+    ones_d = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    qg = qimg.joint_heads_f16(_dev(rows[0]), _dev(rows[1]), ones_d, ones_d, _dev(pe))
+    torch.cuda.synchronize()
+    r = q.astype(np.float64)
+    assert np.all(np.abs(qg.cpu().numpy().astype(np.float64) - r) <= 2.0 ** -10 * np.abs(r) + 2.0 ** -14 * np.abs(r).max())
+    scale = 1.0 / math.sqrt(128.0)
+    out = qimg.attention_forward_sage_fp16io(_dev(q), _dev(k), _dev(v), scale, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    mean = oracle.sage_k_mean(k)
+    qi, qs = oracle.sage_quant_q(q)
+    ki, ks = oracle.sage_quant_k(k, mean)
+    qd, kd, vd = (_dev(a) for a in (q, k, v))
+    qi_g, qs_g = qimg.sage_quant_q(qd)
+    mean_g = qimg.sage_k_mean(kd)
+    ki_g, ks_g = qimg.sage_quant_k(kd, mean_g)
+    torch.cuda.synchronize()
+    # int8 Q/K values and scales bit-exact on these inputs too
+    np.testing.assert_array_equal(mean_g.cpu().numpy(), mean)
+    np.testing.assert_array_equal(qi_g.cpu().numpy(), qi)
+    np.testing.assert_array_equal(qs_g.cpu().numpy(), qs)
+    np.testing.assert_array_equal(ki_g.cpu().numpy(), ki)
+    np.testing.assert_array_equal(ks_g.cpu().numpy(), ks)
+    for r0 in (0, 256, 2112, S - 128):
+        ref = oracle.sage_attn(qi, ki, v, qs, ks, scale, rows=(r0, r0 + 128))[:, r0:r0 + 128].astype(np.float32)
+        # bf16 output: one bf16 rounding (2^-9 relative) on top of the fp16 bar
+        ref_b = torch.from_numpy(ref).to(torch.bfloat16).float().numpy()
+        g = got[:, r0:r0 + 128]
+        assert np.max(np.abs(g - ref_b)) <= 2e-3 * np.max(np.abs(ref)) + 2e-3 + 2.0 ** -8 * np.max(np.abs(ref)), r0
+    # float64 attention on the unquantized fp16 operands, one window of every head
+    r0 = 2112
+    s64 = np.matmul(q[:, r0:r0 + 128].astype(np.float64), k.astype(np.float64).transpose(0, 2, 1)) * scale
+    s64 -= s64.max(-1, keepdims=True)
+    p64 = np.exp(s64)
+    exact = np.matmul(p64 / p64.sum(-1, keepdims=True), v.astype(np.float64))
+    rel, cos = _metrics(got[:, r0:r0 + 128], exact)
+    assert rel <= 2e-2 and cos >= 0.999, (rel, cos)

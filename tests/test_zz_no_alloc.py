@@ -1,8 +1,9 @@
 """qimg_linear_noalloc (the allocation-free quantized linear) through the C
 ABI, against qimg_linear (the caller-scratch entry point that runs the same
 kernels) on identical inputs: two calls in a row, the second smaller, each
-equal bit for bit; no device memory taken by the calls; sizes beyond the
-static scratch rejected before any launch."""
+equal bit for bit; the call captured in a graph in global capture mode
+(which any allocation during the capture fails) and replayed between eager
+calls; sizes beyond the static scratch rejected before any launch."""
 import ctypes
 
 import pytest
@@ -47,15 +48,24 @@ def test_linear_noalloc_matches_linear(qimg):
         assert _noalloc(qimg, x, qw, bias, out, gelu=qw.mode == qimg.FP8_HADAMARD) == 0, qimg.lib().qimg_last_error()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), (x.shape, qw.mode)
-    # repeated calls take no device memory (the array was mapped with the
-    # library's code object)
+    # The call is captured into a graph in global capture mode, where an
+    # allocation (hipMalloc, hipFree) by this process during the capture
+    # fails it: so the call allocates nothing, whatever other processes on
+    # the GPU do. Each replay, with eager work on the same buffers between
+    # the replays, gives the eager result again.
     x, qw, bias, ref, out = small
-    free0 = torch.cuda.mem_get_info()[0]
-    for _ in range(3):
-        assert _noalloc(qimg, x, qw, bias, out, gelu=True) == 0
-    torch.cuda.synchronize()
-    assert torch.cuda.mem_get_info()[0] == free0
-    assert torch.equal(out, ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="global"):
+        st = _noalloc(qimg, x, qw, bias, out, gelu=True)
+    assert st == 0, qimg.lib().qimg_last_error()
+    for i in range(3):
+        out.fill_(float("nan"))
+        big[4].fill_(0.0)
+        assert _noalloc(qimg, *big[:3], big[4], gelu=False) == 0  # eager use of the same static array
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        assert torch.equal(big[4], big[3]), i
 
 
 def test_linear_noalloc_rejects_oversize(qimg):
