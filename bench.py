@@ -2,11 +2,14 @@
 """Benchmark of the quantized-linear hot path on one MI355X.
 
 Workload (one "step"): the MMDiT MLP pair at M = 4352 tokens (4096 image +
-256 text, processed as one matrix):
+256 text):
     x bf16 [4352, 3072] --FWHT(1024)+int8--> fc1 3072->12288 (+bias, GELU-tanh,
     fp32 out, as the reference writes it) --FWHT(4096)+int8--> fc2 12288->3072
     (+bias, bf16 out)
 with random N(0, 0.02) weights quantized by the library (W8A8 + Hadamard).
+fc1 is issued as the two kernel launches one M = 4352 call makes (rows
+0-4095 on the 256 x 256 tiles, rows 4096-4351 on the 64 x 64 tiles), as two
+calls, so that each kernel is timed; the output is that of the single call.
 Inputs are resident in HBM before timing. value = 2*M*N*K summed over both
 GEMMs (657.13 GOP) / measured time, in TFLOP/s (int8 ops). The K timed steps
 run twice: eagerly, with HIP events around each launch (the per-kernel
@@ -78,10 +81,46 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
+    ap.add_argument("--c5-steps", type=int, default=20, help="timed steps of the 60-block C5 leg")
+    ap.add_argument("--profile-commands", metavar="DIR",
+                    help="print the rocprofv3 runs behind profiles/*.txt (output under DIR), one 'name<TAB>command' "
+                         "line each, and exit")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="write the profiles/*.txt summaries from the CSVs of those runs under DIR, and exit")
+    ap.add_argument("--profile-all", metavar="DIR",
+                    help="run every --profile-commands run (each a child process under its own time limit, in "
+                         "order, stopping at the first failure), then --summarize DIR; this process does not touch "
+                         "the GPU itself")
+    ap.add_argument("--summary-out", default=os.path.join(ROOT, "profiles"),
+                    help="directory the --summarize files go to (default: profiles/)")
     ap.add_argument("--profile-set", choices=sorted(PROFILE_SETS),
                     help="only run the named group of measured workloads a few times each, untimed, for "
                          "rocprofv3 counter runs, and exit")
     args = ap.parse_args()
+
+    if args.profile_commands:
+        for name, cmd in _profile_commands(args.profile_commands):
+            print(f"{name}\t{cmd}")
+        return
+    if args.profile_all:
+        import shlex
+        import subprocess
+        args.profile_all = os.path.abspath(args.profile_all)
+        os.makedirs(args.profile_all, exist_ok=True)
+        for name, cmd in _profile_commands(args.profile_all):
+            limit = 600 if name == "kt" else 240
+            print(f"profile run {name}", flush=True)
+            with open(os.path.join(args.profile_all, f"{name}.log"), "w") as log:
+                r = subprocess.run(["timeout", "-s", "KILL", str(limit)] + shlex.split(cmd), stdout=log,
+                                   stderr=subprocess.STDOUT, cwd=ROOT)
+            if r.returncode != 0:
+                print(f"profile run {name} failed: exit {r.returncode} (log {args.profile_all}/{name}.log)")
+                sys.exit(1)
+        args.summarize = args.profile_all
+    if args.summarize:
+        for f in _summarize(os.path.abspath(args.summarize), args.summary_out):
+            print(os.path.join(args.summary_out, f))
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -128,22 +167,42 @@ def main():
     stream = torch.cuda.current_stream(dev)
     P = q._ptr
 
-    # (the stream is read at each call, so the same launches can be captured)
-    def quant(src, dt, K, hbs, dst, sc):
-        q._check(L.qimg_quantize_activation(P(src), dt, M, K, hbs, q.INT8_HADAMARD, P(dst), P(sc), q._stream(dev)))
+    # fc1 of the 4352 rows is issued as the two kernel launches one
+    # qimg_linear_prequantized call of M = 4352 makes (the dispatcher sends
+    # rows 0-4095 to the 256 x 256 tiles, 768 tiles = exactly three rounds on
+    # 256 CUs, and the trailing tile row to the 64 x 64 tiles), as two calls,
+    # so that HIP events time each kernel; the outputs and the step time equal
+    # those of the single call (measured in-process: 390.0 against 391.1 us
+    # per step). extra.fc1_single_launch_ms times fc1 as that single call.
+    MI, MT = 4096, M - 4096
 
-    def gemm(act, sc, w, bias, out, out_dt, gelu):
-        q._check(L.qimg_linear_prequantized(P(act), P(sc), M, act.shape[1], P(w.data), P(w.scales),
+    # (the stream is read at each call, so the same launches can be captured)
+    def quant(src, dt, rows, K, hbs, dst, sc):
+        q._check(L.qimg_quantize_activation(P(src), dt, rows, K, hbs, q.INT8_HADAMARD, P(dst), P(sc),
+                                            q._stream(dev)))
+
+    def gemm(act, sc, rows, w, bias, out, out_dt, gelu):
+        q._check(L.qimg_linear_prequantized(P(act), P(sc), rows, act.shape[1], P(w.data), P(w.scales),
                                             w.data.shape[0], q.INT8_HADAMARD, P(bias), P(out), out_dt,
                                             gelu, q._stream(dev)))
 
-    names = ["quant_fc1_in", "gemm_fc1", "quant_fc2_in", "gemm_fc2"]
+    names = ["quant_fc1_in", "gemm_fc1", "gemm_fc1_tail", "quant_fc2_in", "gemm_fc2"]
     launches = [
-        lambda: quant(x, q.BF16, D, 1024, a1, s1),
-        lambda: gemm(a1, s1, qw1, b1d, h, q.FP32, 1),
-        lambda: quant(h, q.FP32, H, 4096, a2, s2),
-        lambda: gemm(a2, s2, qw2, b2d, y, q.BF16, 0),
+        lambda: quant(x, q.BF16, M, D, 1024, a1, s1),
+        lambda: gemm(a1, s1, MI, qw1, b1d, h, q.FP32, 1),
+        lambda: gemm(a1[MI:], s1[MI:], MT, qw1, b1d, h[MI:], q.FP32, 1),
+        lambda: quant(h, q.FP32, M, H, 4096, a2, s2),
+        lambda: gemm(a2, s2, M, qw2, b2d, y, q.BF16, 0),
     ]
+
+    def step(evs=None):
+        cur = torch.cuda.current_stream(dev)
+        for j, f in enumerate(launches):
+            if evs is not None:
+                evs[j].record(cur)
+            f()
+        if evs is not None:
+            evs[len(launches)].record(cur)
 
     # Clock ramp: the GPU raises its clocks only under sustained load (the
     # first few milliseconds of a burst run ~15% slower), so the step runs
@@ -151,44 +210,38 @@ def main():
     t_ramp = time.perf_counter()
     while time.perf_counter() - t_ramp < args.ramp_s:
         for _ in range(20):
-            for f in launches:
-                f()
+            step()
         torch.cuda.synchronize()
     for _ in range(args.warmup):
-        for f in launches:
-            f()
+        step()
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)] for _ in range(K)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(K)]
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(K):
-        ev[i][0].record(stream)
-        for j, f in enumerate(launches):
-            f()
-            ev[i][j + 1].record(stream)
+        step(ev[i])
     stop.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(stop)
     # medians over the K timed steps (per step, and per launch)
-    step_ms = [ev[i][0].elapsed_time(ev[i][len(launches)]) for i in range(K)]
+    step_ms = [ev[i][0].elapsed_time(ev[i][len(names)]) for i in range(K)]
     ms_step_eager = float(np.median(step_ms))
     per_kernel_ms = {n: float(np.median([ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K)]))
                      for j, n in enumerate(names)}
     y_eager = y.clone()
 
-    # ---- the same step as one HIP graph (the four launches without the host
+    # ---- the same step as one HIP graph (its five launches without the host
     # launch gaps between them), replayed K times with an event pair around
     # each replay: ms_per_step and value are the median of these.
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for f in launches:
-            f()
+        step()
     torch.cuda.synchronize()
     t_ramp = time.perf_counter()
     while time.perf_counter() - t_ramp < min(args.ramp_s, 0.3):
@@ -210,40 +263,50 @@ def main():
     # every replay computes what the eager steps computed
     graph_equals_eager = bool(torch.equal(y, y_eager))
     del graph
+    # fc1 of all 4352 rows as one call (the dispatcher sends the trailing tile
+    # row to the small tiles), for comparison with the split above
+    ms_fc1_single = _time(torch, lambda: gemm(a1, s1, M, qw1, b1d, h, q.FP32, 1), iters=21)
     gemm_ops = 2.0 * M * D * H
     total_ops = 2 * gemm_ops
     value = total_ops / (ms_step * 1e-3) / 1e12
 
-    # ---- roofline of the dominant kernel
+    # ---- roofline of the dominant kernel (main-stream launches)
     dom = max(per_kernel_ms, key=per_kernel_ms.get)
     if dom.startswith("gemm"):
-        achieved = gemm_ops / (per_kernel_ms[dom] * 1e-3) / 1e12
+        rows, Kd, Nd, ob = {"gemm_fc1": (MI, D, H, 4), "gemm_fc1_tail": (MT, D, H, 4),
+                            "gemm_fc2": (M, H, D, 2)}[dom]
+        dom_ops = 2.0 * rows * Kd * Nd
+        achieved = dom_ops / (per_kernel_ms[dom] * 1e-3) / 1e12
         traffic = _traffic_from_profiles(dom)
         # algorithmic bytes: int8 activations + int8 weights + output + scales + bias
-        Kd, Nd, ob = (D, H, 4) if dom == "gemm_fc1" else (H, D, 2)
-        gbytes = M * Kd + Nd * Kd + M * Nd * ob + 4 * (M + Nd) + 2 * Nd
-        kname = ("gemm_w8a8_kernel rows 0-4095 + gemm_small_dma_kernel rows 4096-4351 (gemm_fc1)"
-                 if dom == "gemm_fc1" else f"gemm_w8a8_kernel ({dom})")
+        gbytes = rows * Kd + Nd * Kd + rows * Nd * ob + 4 * (rows + Nd) + 2 * Nd
+        kname = {"gemm_fc1": f"gemm_w8a8_kernel (int8, 16x16x64 MFMA), fc1 rows 0-4095: {rows}x{Nd}x{Kd}, "
+                             "768 tiles of 256x256 = 3 rounds on 256 CUs",
+                 "gemm_fc1_tail": f"gemm_small_dma_kernel, fc1 rows 4096-4351: {rows}x{Nd}x{Kd}",
+                 "gemm_fc2": f"gemm_w8a8_kernel (int8, 16x16x64 MFMA), fc2 {rows}x{Nd}x{Kd}"}[dom]
         roof = {"kernel": kname, "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                "traffic": traffic, "ops_per_launch": gemm_ops, "bytes_per_launch": gbytes,
+                "traffic": traffic, "ops_per_launch": dom_ops, "bytes_per_launch": gbytes,
                 "avg_launch_ms": round(per_kernel_ms[dom], 4)}
     else:
+        rows = M
         Kd = D if dom == "quant_fc1_in" else H
-        nbytes = M * Kd * (2 if dom == "quant_fc1_in" else 4) + M * Kd + 4 * M
+        nbytes = rows * Kd * (2 if dom == "quant_fc1_in" else 4) + rows * Kd + 4 * rows
         achieved = nbytes / (per_kernel_ms[dom] * 1e-3) / 1e9
-        roof = {"kernel": f"fwht_quant_rows_kernel ({dom})", "bound": "hbm", "achieved": round(achieved, 1),
+        roof = {"kernel": f"FWHT + int8 quantization ({dom})", "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                 "traffic": _traffic_from_profiles(dom), "bytes_per_launch": nbytes,
                 "avg_launch_ms": round(per_kernel_ms[dom], 4)}
 
     extra = {"per_kernel_ms_median": {k: round(v, 4) for k, v in per_kernel_ms.items()},
+             "fc1_single_launch_ms": round(ms_fc1_single, 4),
+             "fc1_single_launch_tflops": round(2.0 * M * D * H / ms_fc1_single / 1e9, 1),
              "step_timing": "median of K replays of the step captured as one HIP graph",
              "ms_per_step_eager": round(ms_step_eager, 4), "ms_per_step_eager_mean": round(total_ms / K, 4),
              "graph_equals_eager": graph_equals_eager,
              "wall_s_timed_eager": round(wall, 3), "wall_s_timed_graph": round(wall_graph, 3)}
     if not args.no_extra:
-        extra.update(_extra(q, torch, dev))
+        extra.update(_extra(q, torch, dev, c5_steps=args.c5_steps))
 
     # ---- CPU baseline: the oracle on the same MLP pair (and, as a by-product,
     # a parity spot check of this run's GPU output on sampled rows)
@@ -256,8 +319,9 @@ def main():
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "MMDiT MLP pair, M=4352 tokens: FWHT1024+int8 quant, fc1 3072->12288 "
-                               "+bias+GELU-tanh (fp32), FWHT4096+int8 quant, fc2 12288->3072 +bias (bf16)",
+        "config": {"workload": "MMDiT MLP pair, M=4352 tokens (4096 image + 256 text): FWHT1024+int8 quant, "
+                               "fc1 3072->12288 +bias+GELU-tanh (fp32; rows 0-4095 and 4096-4351 as two launches), "
+                               "FWHT4096+int8 quant, fc2 12288->3072 +bias (bf16)",
                    "M": M, "hidden": D, "mlp": H, "weights": "N(0,0.02) -> W8A8 + Hadamard",
                    "frac_of_int8_peak": round(value / PEAK_INT8_TOPS, 4)},
         "roofline": roof,
@@ -344,6 +408,8 @@ PROBE_KINDS = {  # qimg_probe_mfma kind: (name, ops per instruction, spec peak i
     2: ("v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3)", 131072, 5033.0, 64),
     3: ("v_mfma_f32_32x32x16_f16", 32768, PEAK_FP16_TFLOPS, 32),
     4: ("v_mfma_f32_32x32x16_bf16", 32768, PEAK_FP16_TFLOPS, 32),
+    5: ("v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3)", 65536, 5033.0, 32),
+    6: ("v_mfma_f32_16x16x32_f16", 16384, PEAK_FP16_TFLOPS, 16),
 }
 
 
@@ -451,7 +517,7 @@ def _vendor_gemms(torch, dev, iters=20):
     return res
 
 
-def _extra(q, torch, dev):
+def _extra(q, torch, dev, c5_steps=20):
     out = {}
     g = torch.Generator(device="cpu").manual_seed(0)
     # C1: single linear, M=4096, 3072x3072 (bf16 in, fp32 out as the reference)
@@ -549,7 +615,7 @@ def _extra(q, torch, dev):
         out[f"{tag}_large_tile_gemm_us"] = round(ms_big * 1e3, 2)
         del qws, qw0
     out.update(_block_c4(q, torch, dev, g))
-    out.update(_step_c5(q, torch, dev))
+    out.update(_step_c5(q, torch, dev, steps=c5_steps))
     out["mfma_ceiling"] = _mfma_ceiling(torch, dev)
     out["hipblaslt_reference"] = _vendor_gemms(torch, dev)
     return out
@@ -830,14 +896,15 @@ def _profile_gemm(q, torch, dev, reps=4):
 
 
 def _profile_sage(q, torch, dev, reps=4):
-    """SageAttention at C3 (24 heads, S = 4352): K mean, Q/K quantization
-    and the attention kernel; and the K mean of the batch-2 1328x1328 block
-    (48 heads, S = 7401)."""
+    """SageAttention at C3 (24 heads, S = 4352, on the C3 leg's RMSNorm +
+    RoPE inputs): K mean, Q/K quantization and the attention kernel; and the
+    K mean of the batch-2 1328x1328 block (48 heads, S = 7401)."""
     g = torch.Generator(device=dev).manual_seed(12)
     for BH, S in ((24, 4352), (48, 7401)):
-        qh = torch.randn(BH, S, 128, generator=g, device=dev).half()
-        kh = torch.randn(BH, S, 128, generator=g, device=dev).half()
-        vh = torch.randn(BH, S, 128, generator=g, device=dev).half()
+        if BH == 24:
+            qh, kh, vh = _c3_inputs(q, torch, dev)
+        else:
+            kh = torch.randn(BH, S, 128, generator=g, device=dev).half()
         scratch = torch.empty(q.sage_scratch_bytes(BH, S, 128), dtype=torch.uint8, device=dev)
         for _ in range(reps):
             km = q.sage_k_mean(kh)
@@ -846,7 +913,7 @@ def _profile_sage(q, torch, dev, reps=4):
                 ki, ks = q.sage_quant_k(kh, km)
                 q.sage_attn_quantized(qi, ki, vh, qs, ks, 1.0 / math.sqrt(128.0), scratch=scratch)
         torch.cuda.synchronize()
-        del qh, kh, vh, scratch
+        del kh, scratch
 
 
 def _profile_small_m(q, torch, dev, reps=3):
@@ -897,6 +964,377 @@ def _profile_quant(q, torch, dev, reps=4):
 
 PROFILE_SETS = {"gemm": _profile_gemm, "sage": _profile_sage, "small_m": _profile_small_m,
                 "quant": _profile_quant}
+
+
+# ---- the rocprofv3 runs behind profiles/*.txt (bench.py --profile-commands
+# DIR prints them, one "name<TAB>command" line each, to be run in order from
+# any directory) and their summaries (bench.py --summarize DIR --summary-out
+# OUT turns the CSVs those runs leave under DIR into OUT/*.txt, the files kept
+# under profiles/). Counter conventions:
+#  - FETCH_SIZE / WRITE_SIZE are KiB per dispatch between L2 and memory (L2
+#    misses and write-backs; last-level-cache hits count as fetches), each
+#    scaled by what the same counter reads for a plain device copy of 256 MiB
+#    (the calib_* runs);
+#  - MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (GRBM_GUI_ACTIVE per XCD x
+#    1024 SIMDs), GRBM_GUI_ACTIVE being read summed over the 8 XCDs; the clock
+#    is GRBM cycles per XCD / duration.
+PMC_MFMA = ("SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU_MFMA_MOPS_I8 "
+            "SQ_INSTS_VALU_MFMA_MOPS_F8 SQ_INSTS_VALU_MFMA_MOPS_F16")
+KT_ARGS = "--steps 10 --warmup 3 --ramp-s 0.3 --no-cpu-baseline --c5-steps 3"
+MLP_ARGS = "--steps 3 --warmup 1 --ramp-s 0.2 --no-cpu-baseline --no-extra"
+
+
+def _profile_commands(d):
+    """(name, command) of every profiling run, output under directory d; the
+    commands run from the repository root (paths under it are given relative
+    to it)."""
+    bench = "bench.py"
+    if os.path.isabs(d) and os.path.commonpath([os.path.realpath(d), os.path.realpath(ROOT)]) == \
+            os.path.realpath(ROOT):
+        d = os.path.relpath(os.path.realpath(d), os.path.realpath(ROOT))
+    out = []
+    for set_ in ("gemm", "sage", "small_m", "quant"):
+        for pass_, ctr in (("mfma", PMC_MFMA), ("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+            if pass_ == "mfma" and set_ in ("small_m", "quant"):
+                continue
+            out.append((f"{set_}_{pass_}", f"rocprofv3 --kernel-trace --pmc {ctr} --output-format csv "
+                                           f"-d {d}/{set_}_{pass_} -o p -- python3 {bench} --profile-set {set_}"))
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        out.append((f"calib_{ctr}", f"rocprofv3 --kernel-trace --pmc {ctr} --output-format csv -d {d}/calib_{ctr} "
+                                    f"-o p -- python3 {bench} --calib-copy"))
+        out.append((f"mlp_{ctr}", f"rocprofv3 --kernel-trace --pmc {ctr} --output-format csv -d {d}/mlp_{ctr} "
+                                  f"-o p -- python3 {bench} {MLP_ARGS}"))
+    out.append(("kt", f"rocprofv3 --kernel-trace --stats --output-format csv -d {d}/kt -o b -- "
+                      f"python3 {bench} {KT_ARGS}"))
+    return out
+
+
+def _short_kernel(n):
+    n = n.replace("(anonymous namespace)::", "").replace("void ", "")
+    return n.split(">(")[0] + ">" if ">(" in n else n.split("(")[0]
+
+
+def _csv(d, pattern):
+    import csv
+    import glob
+    f = sorted(glob.glob(os.path.join(d, "**", pattern), recursive=True))
+    if not f:
+        raise FileNotFoundError(f"no {pattern} under {d}")
+    return list(csv.DictReader(open(f[0])))
+
+
+def _dispatches(d):
+    """Dispatches of one counter run in dispatch order: name, workgroups,
+    duration (kernel trace), counters (summed over the run's instances)."""
+    import collections
+    per = collections.OrderedDict()
+    for r in _csv(d, "*counter_collection.csv"):
+        k = int(r["Dispatch_Id"])
+        if k not in per:
+            per[k] = {"name": _short_kernel(r["Kernel_Name"]), "wgs": int(r["Grid_Size"]) // int(r["Workgroup_Size"]),
+                      "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3,
+                      "c": collections.defaultdict(float)}
+        per[k]["c"][r["Counter_Name"]] += float(r["Counter_Value"])
+    try:
+        for r in _csv(d, "*kernel_trace.csv"):
+            k = int(r["Dispatch_Id"])
+            if k in per:
+                per[k]["us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    except FileNotFoundError:
+        pass
+    return [per[k] for k in sorted(per)]
+
+
+def _pick(ds, name, wgs, skip=0):
+    """Dispatches of kernel `name` (its name up to the template arguments'
+    end) with `wgs` workgroups, after the first `skip` of them."""
+    return [x for x in ds if x["name"] == name and x["wgs"] == wgs][skip:]
+
+
+def _med(xs, key=None):
+    import statistics
+    return statistics.median(x["c"][key] if key else x["us"] for x in xs)
+
+
+def _calibration(d):
+    out = {}
+    lines = []
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        ds = [x for x in _dispatches(os.path.join(d, f"calib_{ctr}")) if "copyBuffer" in x["name"] or
+              "copy" in x["name"].lower()]
+        v = _med(ds, ctr)
+        out[ctr] = (256 * 1024) / v
+        lines.append(f"{ctr} reads {v:.1f} KiB for a 256 MiB device copy -> x{out[ctr]:.4f}")
+    cmds = dict(_profile_commands(d))
+    hdr = ["HBM counters: FETCH_SIZE / WRITE_SIZE KiB per dispatch (TCC <-> memory), each scaled by its reading for a "
+           "plain 256 MiB device copy: " + "; ".join(lines),
+           f"calibration commands: {cmds['calib_FETCH_SIZE']}  (and WRITE_SIZE)"]
+    return out, hdr
+
+
+def _traffic_table(rows):
+    out = [" launch                          n   med_us   fetch_MB  write_MB  traffic_MB  algo_MB  traffic/algo  "
+           "algo_GB/s  frac_HBM  kernel (workgroups)"]
+    for label, name, wgs, n, us, fb, wb, algo in rows:
+        out.append(f" {label:30s} {n:3d} {us:8.2f} {fb / 1e6:10.1f} {wb / 1e6:9.1f} {(fb + wb) / 1e6:11.1f} "
+                   f"{algo / 1e6:8.1f} {(fb + wb) / algo:12.2f} {algo / us / 1e3:10.0f} {algo / us / 1e3 / 8000:9.3f}  "
+                   f"{name} ({wgs})")
+    return out
+
+
+def _summarize(d, outdir):
+    """profiles/*.txt from the runs of _profile_commands(d)."""
+    import statistics
+    os.makedirs(outdir, exist_ok=True)
+    cmds = dict(_profile_commands(d))
+    cal, cal_hdr = _calibration(d)
+    written = []
+
+    def traffic_rows(set_, picks):
+        fd, wd = _dispatches(os.path.join(d, f"{set_}_fetch")), _dispatches(os.path.join(d, f"{set_}_write"))
+        rows = []
+        for label, name, wgs, algo, skip in picks:
+            f, w = _pick(fd, name, wgs, skip), _pick(wd, name, wgs, skip)
+            if not f or not w:
+                raise RuntimeError(f"{set_}: no dispatches of {name} ({wgs})")
+            rows.append((label, name, wgs, len(f), statistics.median(x["us"] for x in f + w),
+                         _med(f, "FETCH_SIZE") * 1024 * cal["FETCH_SIZE"],
+                         _med(w, "WRITE_SIZE") * 1024 * cal["WRITE_SIZE"], algo))
+        return rows
+
+    def write(fname, lines):
+        open(os.path.join(outdir, fname), "w").write("\n".join(lines) + "\n")
+        written.append(fname)
+
+    # -- GEMMs (bench.py --profile-set gemm: each shape 4 times)
+    G = [("C1 4096x3072x3072 i8 fp32", "qimg::gemm_w8a8_kernel<3, 0, false, false>", 192, 4096, 3072, 3072, 4, "I8"),
+         ("fc1 rows 0-4095 of 4352 i8", "qimg::gemm_w8a8_kernel<3, 0, true, false>", 768, 4096, 12288, 3072, 4, "I8"),
+         ("fc1 rows 4096-4351 i8", "qimg::gemm_small_dma_kernel<false, 2, 2, 2, 0, true, 64>", 768, 256, 12288, 3072,
+          4, "I8"),
+         ("fc2 4352x3072x12288 i8 bf16", "qimg::gemm_w8a8_kernel<3, 1, false, false>", 204, 4352, 3072, 12288, 2,
+          "I8"),
+         ("C5 fc1 rows 0-13567 e4m3", "qimg::gemm_w8a8_kernel<1, 0, true, false>", 2544, 13568, 12288, 3072, 4, "F8"),
+         ("C5 fc1 rows 13568-13777 e4m3", "qimg::gemm_small_dma_kernel<true, 2, 2, 2, 0, true, 64>", 768, 210, 12288,
+          3072, 4, "F8"),
+         ("C5 fc2 13778x3072x12288 e4m3", "qimg::gemm_w8a8_kernel<1, 0, false, false>", 648, 13778, 3072, 12288, 4,
+          "F8")]
+    md = _dispatches(os.path.join(d, "gemm_mfma"))
+    lines = ["# MFMA utilisation and HBM traffic of the quantized-linear GEMMs",
+             f"command (MFMA pass): {cmds['gemm_mfma']}",
+             f"command (HBM passes): {cmds['gemm_fetch']}  (and WRITE_SIZE into gemm_write)",
+             "workloads (bench.py _profile_gemm): C1 linear, the MLP pair at 4352 tokens, the batch-2 e4m3 fc1/fc2 of the",
+             "1328x1328 step (13778 rows); int8/e4m3 operands, fp32 out (fc2 at 4352: bf16), 4 launches each, medians.",
+             "ops = SQ_INSTS_VALU_MFMA_MOPS_{I8,F8} x 512 (checked against 2MNK); frac = ops/s / 5033 TOP/s (2.4 GHz "
+             "spec peak); frac@clk = ops/s / (2048 ops/clk/SIMD x 1024 SIMDs x measured clock).", "",
+             " launch                          med_us  clock_GHz  MfmaUtil   ops_G   2MNK_G   TOP/s    frac  frac@clk"]
+    for label, name, wgs, M_, N_, K_, ob, mode in G:
+        r = _pick(md, name, wgs)
+        if not r:
+            raise RuntimeError(f"gemm_mfma: no dispatches of {name} ({wgs})")
+        us = _med(r)
+        grbm = _med(r, "GRBM_GUI_ACTIVE") / 8
+        util = _med(r, "SQ_VALU_MFMA_BUSY_CYCLES") / (grbm * 1024)
+        ops = _med(r, f"SQ_INSTS_VALU_MFMA_MOPS_{mode}") * 512
+        clk = grbm / us / 1e3
+        tops = 2.0 * M_ * N_ * K_ / us / 1e6
+        lines.append(f" {label:30s} {us:8.2f} {clk:10.2f} {util:9.3f} {ops / 1e9:7.1f} {2 * M_ * N_ * K_ / 1e9:8.1f} "
+                     f"{tops:7.0f} {tops * 1e12 / 5033e12:7.3f} {tops * 1e12 / (2048 * 1024 * clk * 1e9):9.3f}")
+    picks = [(label, name, wgs, M_ * K_ + N_ * K_ + M_ * N_ * ob + 4 * (M_ + N_) + 2 * N_, 0)
+             for label, name, wgs, M_, N_, K_, ob, mode in G]
+    lines += ["", "HBM traffic per launch (algorithmic bytes = A + W + out + scales + bias, each once)"] + cal_hdr + \
+        [""] + _traffic_table(traffic_rows("gemm", picks))
+    write("gemm_mfma_hbm_counters.txt", lines)
+
+    # -- SageAttention (bench.py --profile-set sage)
+    BH, S_, D_ = 24, 4352, 128
+    fl = 4.0 * BH * S_ * S_ * D_
+    sd = _dispatches(os.path.join(d, "sage_mfma"))
+    att = _pick(sd, "qimg::sage_attn_kernel<128, false, 2>", 408)
+    lines = ["# SageAttention at 24 heads x 4352 tokens x 128 (and the K mean of the batch-2 1328x1328 block, 48 x 7401)",
+             f"command (MFMA pass): {cmds['sage_mfma']}",
+             f"command (HBM passes): {cmds['sage_fetch']}  (and WRITE_SIZE into sage_write)",
+             "inputs: Q, K, V as the C3 leg makes them (RMSNorm + RoPE on Q and K, fp16 [24, 4352, 128]);",
+             "attention flops = 4 x BH x S^2 x D (half int8 QK^T, half fp16 PV); mixed peak 3355 TFLOP/s", "",
+             " launch                      med_us  clock_GHz  MfmaUtil  i8_ops_G  f16_ops_G  TFLOP/s  frac_mixed"]
+    us = _med(att)
+    grbm = _med(att, "GRBM_GUI_ACTIVE") / 8
+    lines.append(f" {'attention 24x4352x128':26s} {us:8.2f} {grbm / us / 1e3:9.2f} "
+                 f"{_med(att, 'SQ_VALU_MFMA_BUSY_CYCLES') / (grbm * 1024):9.3f} "
+                 f"{_med(att, 'SQ_INSTS_VALU_MFMA_MOPS_I8') * 512 / 1e9:9.1f} "
+                 f"{_med(att, 'SQ_INSTS_VALU_MFMA_MOPS_F16') * 512 / 1e9:10.1f} {fl / us / 1e6:8.0f} "
+                 f"{fl / us / 1e6 / 3355:11.3f}")
+    nq = (S_ + 127) // 128
+    picks = [("attention 24x4352x128", "qimg::sage_attn_kernel<128, false, 2>", 408,
+              2 * BH * S_ * D_ + 2 * BH * S_ * D_ + 2 * BH * S_ * D_ + 4 * BH * nq * 32 * 2, 0),
+             ("K mean 24x4352x128", "qimg::k_mean_kernel", 96, BH * S_ * D_ * 2 + BH * D_ * 4, 0),
+             ("K mean 48x7401x128", "qimg::k_mean_kernel", 192, 48 * 7401 * D_ * 2 + 48 * D_ * 4, 0),
+             ("Q quant 24x4352x128", "qimg::quant_q_kernel<128>", 816, BH * S_ * D_ * 3 + 4 * BH * nq * 32, 0),
+             ("K quant 24x4352x128", "qimg::quant_k128_kernel", 1632, BH * S_ * D_ * 3 + 4 * BH * ((S_ + 63) // 64) * 4,
+              0)]
+    lines += ["", "HBM traffic per launch (algorithmic: attention = int8 Q, K + fp16 V in + fp16 out + scales; quant = "
+              "fp16 in + int8 out + scales; K mean = fp16 K in)"] + cal_hdr + [""] + \
+        _traffic_table(traffic_rows("sage", picks))
+    write("sage_c3_counters.txt", lines)
+
+    # -- small M (bench.py --profile-set small_m)
+    fd = _dispatches(os.path.join(d, "small_m_fetch"))
+    shapes = [("mod M=1 18432x3072", 1, 18432, 3072), ("mod M=2 18432x3072", 2, 18432, 3072),
+              ("txt qkv M=256 3072x3072", 256, 3072, 3072), ("txt fc1 M=256 12288x3072", 256, 12288, 3072),
+              ("txt fc2 M=256 3072x12288", 256, 3072, 12288)]
+    # the GEMM kernels of each shape, in order: the first kernel with >= 6
+    # consecutive dispatches after the previous shape's
+    import itertools
+    groups = [(k, len(list(g))) for k, g in itertools.groupby(
+        (x for x in fd if "gemv" in x["name"] or "gemm_small" in x["name"]), key=lambda x: (x["name"], x["wgs"]))]
+    keys = [k for k, n in groups if n >= 6]
+    if len(keys) != len(shapes):
+        raise RuntimeError(f"small_m: expected {len(shapes)} GEMM kernels, found {keys}")
+    picks = [(label, k[0], k[1], N_ * K_ + 6 * N_ + M_ * K_ + 4 * M_ + 4 * M_ * N_, 0)
+             for (label, M_, N_, K_), k in zip(shapes, keys)]
+    lines = ["# HBM traffic of the small-M linears (GEMM only; bench.py _profile_small_m: every call reads the next of",
+             "# several weight copies, > 600 MB in all, so the weights come from HBM)",
+             f"command: {cmds['small_m_fetch']}  (and WRITE_SIZE into small_m_write)",
+             "algorithmic bytes = int8 weights + scales + bias + activations + fp32 output, each once"] + cal_hdr + \
+        [""] + _traffic_table(traffic_rows("small_m", picks))
+    write("small_m_hbm_traffic.txt", lines)
+
+    # -- activation quant (bench.py --profile-set quant)
+    fd = _dispatches(os.path.join(d, "quant_fetch"))
+    groups = [(k, len(list(g))) for k, g in itertools.groupby(
+        (x for x in fd if x["name"].startswith("qimg::")), key=lambda x: (x["name"], x["wgs"]))]
+    keys = [k for k, n in groups if n >= 4]
+    Q = [("fc1 input bf16 4352x3072 hbs1024", 4352 * 3072 * 3 + 4 * 4352),
+         ("fc2 input fp32 4352x12288 hbs4096", 4352 * 12288 * 5 + 4 * 4352),
+         ("C5 fc2 input fp32 13778x12288 e4m3", 13778 * 12288 * 5 + 4 * 13778),
+         ("LN+mod+quant 4096x3072", 4096 * 3072 * 5 + 4 * 4096 + 2 * 3072 * 4)]
+    if len(keys) != len(Q):
+        raise RuntimeError(f"quant: expected {len(Q)} kernels, found {keys}")
+    picks = [(label, k[0], k[1], algo, 0) for (label, algo), k in zip(Q, keys)]
+    lines = ["# HBM traffic of the activation FWHT + quantization passes (bench.py _profile_quant)",
+             f"command: {cmds['quant_fetch']}  (and WRITE_SIZE into quant_write)",
+             "algorithmic bytes = input (bf16 2 B or fp32 4 B) + 1-byte output + fp32 scales"] + cal_hdr + [""] + \
+        _traffic_table(traffic_rows("quant", picks))
+    write("quant_hbm_traffic.txt", lines)
+
+    # -- the bench step's launches (MLP pair at 4352 tokens); read by the
+    # bench line's roofline.traffic
+    M_, D_, H_, MI = 4352, 3072, 12288, 4096
+    step_kernels = {  # launch: (kernel, workgroups, algorithmic bytes)
+        "quant_fc1_in": ("qimg::fwht_quant_wave_rows_kernel<qimg::RowsLoader<unsigned short>, (qimg::RowOut)0, 3, "
+                         "qimg::RowDest>", M_ // 4, M_ * D_ * 2 + M_ * D_ + 4 * M_),
+        "gemm_fc1": ("qimg::gemm_w8a8_kernel<3, 0, true, false>", 768,
+                     MI * D_ + H_ * D_ + MI * H_ * 4 + 4 * (MI + H_) + 2 * H_),
+        "gemm_fc1_tail": ("qimg::gemm_small_dma_kernel<false, 2, 2, 2, 0, true, 64>", 768,
+                          256 * D_ + H_ * D_ + 256 * H_ * 4 + 4 * (256 + H_) + 2 * H_),
+        "quant_fc2_in": ("qimg::fwht_quant_blocks_kernel<float, (qimg::RowOut)0, 3>", M_,
+                         M_ * H_ * 4 + M_ * H_ + 4 * M_),
+        "gemm_fc2": ("qimg::gemm_w8a8_kernel<3, 1, false, false>", 204,
+                     M_ * H_ + D_ * H_ + M_ * D_ * 2 + 4 * (M_ + D_) + 2 * D_),
+    }
+    fd = _dispatches(os.path.join(d, "mlp_FETCH_SIZE"))
+    wd = _dispatches(os.path.join(d, "mlp_WRITE_SIZE"))
+    lines = ["# HBM-side traffic per launch of the bench step's kernels (MLP pair at 4352 tokens)",
+             f"command (fetch): {cmds['mlp_FETCH_SIZE']}",
+             f"command (write): {cmds['mlp_WRITE_SIZE']}"] + cal_hdr + [
+             "medians over every dispatch of the launch's kernel and grid in the run; gemm_fc1 = rows 0-4095 on the "
+             "256x256 tiles, gemm_fc1_tail = rows 4096-4351 on the 64x64 tiles", "",
+             " launch            n  FETCH_KiB  WRITE_KiB  fetch_MB  write_MB  traffic_MB  algorithmic_MB  kernel"]
+    tr = {}
+    for k, (name, wgs, algo) in step_kernels.items():
+        f, w = _pick(fd, name, wgs), _pick(wd, name, wgs)
+        if not f or not w:
+            raise RuntimeError(f"mlp: no dispatches of {name} ({wgs})")
+        fk, wk = _med(f, "FETCH_SIZE"), _med(w, "WRITE_SIZE")
+        fb, wb = fk * 1024 * cal["FETCH_SIZE"], wk * 1024 * cal["WRITE_SIZE"]
+        tr[k] = fb + wb
+        lines.append(f" {k:16s} {len(f):3d} {fk:10.1f} {wk:10.1f} {fb / 1e6:9.1f} {wb / 1e6:9.1f} {(fb + wb) / 1e6:11.1f} "
+                     f"{algo / 1e6:15.1f}  {name} ({wgs})")
+    lines.append("")
+    for k, v in tr.items():
+        lines.append(f"traffic_bytes_per_launch {k}: {v:.0f}")
+    write("mlp4352_hbm_traffic.txt", lines)
+
+    # -- kernel traces of the bench command (the MLP step and its legs)
+    write("mlp4352_kernel_trace.txt", _kt_stats_summary(d, cmds["kt"]))
+    trace = sorted(_csv(os.path.join(d, "kt"), "*kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+    write("block_c4_4096img_256txt_kernel_trace.txt",
+          _block_summary(trace, 4096, 256, "# Kernel trace of one MMDiT joint block, 4096 image + 256 text tokens, "
+                         "int8 (bench.py C4 leg)", cmds["kt"], "work: 1218.66 GOP per block (linears 985.92, "
+                         "attention 232.73)"))
+    write("step_c5_fp8_6889img_512txt_kernel_trace.txt",
+          _block_summary(trace, 2 * 6889, 2 * 512, "# Kernel trace of one block of the 60-block e4m3 step, 6889 image "
+                         "+ 512 text tokens, CFG pair batched (bench.py C5 leg)", cmds["kt"],
+                         "work: 2 x 2349.57 GOP per block (the two CFG branches)"))
+    return written
+
+
+def _kt_stats_summary(d, cmd):
+    rows = _csv(os.path.join(d, "kt"), "*kernel_stats.csv")
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    lines = ["# Kernel trace: the bench command (MLP pair at 4352 tokens and its extra legs: C1 linear, SageAttention "
+             "24x4352x128, small-M linears, C4 block, C5 step, MFMA probe, hipBLASLt reference)",
+             f"command: {cmd}", "source: rocprofv3 --kernel-trace --stats (kernel_stats.csv), durations in microseconds",
+             "", " calls     avg_us    total_us    pct  kernel"]
+    for r in rows[:60]:
+        lines.append(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.3f} {float(r['TotalDurationNs']) / 1e3:11.3f}"
+                     f" {float(r['Percentage']):6.2f}  {_short_kernel(r['Name'])}")
+    return lines
+
+
+def _block_summary(trace, img_rows, txt_rows, title, cmd, ops_note):
+    """Median duration of each kernel of one joint block over every traced
+    block whose image-stream LayerNorm covers img_rows rows (blocks run from
+    their modulation GEMV to the next one; kernels are matched across blocks
+    by name, grid and occurrence, since the two streams' start order varies)."""
+    import collections
+    import statistics
+
+    def is_mod(r):
+        n = r["Kernel_Name"]
+        return "gemv_i8_kernel" in n or "gemm_small_dma_kernel<true, 1, 1, 4" in n or \
+            "gemm_small_dma_kernel<false, 1, 1, 4" in n
+    idx = []
+    for i, r in enumerate(trace):
+        if is_mod(r) and (i == 0 or not is_mod(trace[i - 1])):
+            j = i - 2 if i >= 2 and "silu_kernel" in trace[i - 2]["Kernel_Name"] else i
+            idx.append(j)
+    blocks = []
+    for a, b in zip(idx, idx[1:] + [len(trace)]):
+        seq = trace[a:b]
+        ln = [r for r in seq if "LnLoader" in r["Kernel_Name"]]
+        if ln and int(ln[0]["Grid_Size_X"]) in (img_rows * 256, (img_rows + 3) // 4 * 256,
+                                                 (img_rows + txt_rows + 3) // 4 * 256):
+            blocks.append(seq)
+    if not blocks:
+        return [title, f"command: {cmd}", "no block found in the trace"]
+    n = collections.Counter(len(b) for b in blocks).most_common(1)[0][0]
+    blocks = [b for b in blocks if len(b) == n]
+
+    def keyed(block):
+        seen = collections.Counter()
+        out = collections.OrderedDict()
+        for r in block:
+            k = (r["Kernel_Name"], int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]))
+            out[k + (seen[k],)] = r
+            seen[k] += 1
+        return out
+    kb = [keyed(b) for b in blocks]
+    keys = [k for k in kb[0] if all(k in x for x in kb)]
+    lines = [title, f"command: {cmd}",
+             "source: rocprofv3 --kernel-trace (kernel_trace.csv); median duration of each kernel over "
+             f"{len(blocks)} blocks (matched by kernel and grid), microseconds", ops_note, "",
+             " pos   median_us  grid_threads x wg  kernel"]
+    tot = 0.0
+    for j, k in enumerate(keys):
+        dur = statistics.median((int(x[k]["End_Timestamp"]) - int(x[k]["Start_Timestamp"])) / 1e3 for x in kb)
+        tot += dur
+        r = kb[0][k]
+        lines.append(f" {j:3d} {dur:11.2f}  {k[1]:12d} x {int(r['Workgroup_Size_X']):3d}  {_short_kernel(r['Kernel_Name'])}")
+    span = statistics.median((int(b[-1]["End_Timestamp"]) - int(b[0]["Start_Timestamp"])) / 1e3 for b in blocks)
+    lines += ["", f"sum of kernel durations per block: {tot:.1f} us; first start to last end: {span:.1f} us",
+              "(the side stream's kernels (the K mean and quantization, the text fc1 and its fc2-input quantization) "
+              "overlap the main stream's; the span is the block time)"]
+    return lines
 
 
 if __name__ == "__main__":

@@ -9,9 +9,10 @@
 // applied as it is stored.
 //
 // Tiling (CDNA4, wave64): a 512-thread workgroup owns a 256x256 output tile,
-// eight waves in a 2x4 arrangement each own 128x64 = 4x2 MFMA 32x32 blocks
-// (v_mfma_i32_32x32x32_i8 for int8, v_mfma_scale_f32_32x32x64_f8f6f4 with
-// unit scales for e4m3), 128 accumulator registers per wave. Two waves per
+// eight waves in a 2x4 arrangement each own 128x64 = 8x4 MFMA 16x16 blocks
+// for int8 (v_mfma_i32_16x16x64_i8) or 4x2 32x32 blocks for e4m3
+// (v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales) and bf16, 128
+// accumulator registers per wave. Two waves per
 // SIMD let one wave's LDS reads and waits overlap the other's MFMAs
 // (measured 7-9% faster than four waves of 128x128). Both operands are
 // K-major [rows, K] as the reference stores them (TN GEMM).
@@ -39,11 +40,12 @@
 // registers at kernel start and written to LDS (in ring space) after the main
 // loop, so the epilogue reads them without global latency.
 //
-// K ordering: a stage row holds eight 16-byte chunks. Lane half h of an int8
-// fragment takes chunk 4h + s in k-step s (four 32-byte k-steps per stage);
-// an e4m3 fragment takes chunks 4h + 2s and 4h + 2s + 1 in k-step s (two
-// 64-byte k-steps). Both operands use the same assignment, so each dot
-// product covers every k exactly once and the int8 result is exact.
+// K ordering: a stage row holds eight 16-byte chunks. Lane group q = lane/16
+// of an int8 16x16 fragment takes chunk 4s + q in k-step s (two 64-byte
+// k-steps per stage); lane half h of a 32x32 fragment takes chunk 4h + s
+// (bf16: four 32-byte k-steps) or chunks 4h + 2s and 4h + 2s + 1 (e4m3: two
+// 64-byte k-steps) in k-step s. Both operands use the same assignment, so
+// each dot product covers every k exactly once and the int8 result is exact.
 #include <atomic>
 #include <type_traits>
 
@@ -109,6 +111,16 @@ constexpr int SG_DS_READ = 0x100;
 constexpr int OP_I8 = 0;
 constexpr int OP_F8 = 1;
 constexpr int OP_BF16 = 2;
+// The int8 product on 16x16 MFMA blocks (v_mfma_i32_16x16x64_i8): the same
+// operand bytes per op from LDS, a quarter of the accumulator updates per
+// instruction, and a higher sustained clock under a full matrix-core load on
+// this chip (a register-only loop runs 16x16x64 at 3.8-3.9 POP/s and 2.1-2.3
+// GHz, 32x32x32 at 3.5-3.7 POP/s and 1.7-1.8 GHz). The main loop keeps the
+// accumulators as 16x16 blocks and hands them to the epilogue in the 32x32
+// blocks' register layout (remapped through LDS), so every epilogue is shared.
+// (e4m3 stays on 32x32x64: a 16x16x128 loop of the same tiling measured 2-8%
+// slower at the 1328x1328 step's shapes.)
+constexpr int OP_I8_16 = 3;
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
@@ -118,6 +130,10 @@ struct Acc {
 };
 template <>
 struct Acc<OP_I8> {
+    typedef v16i type;
+};
+template <>
+struct Acc<OP_I8_16> {
     typedef v16i type;
 };
 
@@ -170,8 +186,8 @@ struct TileProblems {
 // leave the others' register allocation alone).
 template <int OP, int OUT_DT, bool GELU, bool HD = false>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
-    constexpr bool FP8 = OP == OP_F8;
     constexpr bool BF = OP == OP_BF16;
+    constexpr bool M16 = OP == OP_I8_16;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
     float* s_ws = s_as + 256;
@@ -257,12 +273,23 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
 
     typedef typename Acc<OP>::type acc_t;
     acc_t acc[TM][TN];
+    // 16x16 blocks of the wave tile (2 TM x 2 TN), for the M16 kinds
+    // (one 16x16 block: lane l holds rows 4(l/16) .. +3 of column l%16)
+    typedef v4i acc16_t;
+    acc16_t acc16[2 * TM][2 * TN];
+    if constexpr (M16) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < 2 * TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < 2 * TN; ++j) acc16[i][j] = acc16_t{};
+    } else {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    }
 
     const int KT = K / BK;
 
@@ -295,6 +322,13 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     for (int i = 0; i < TM; ++i) arow[i] = wm * WTM + i * 32 + frag_row;
 #pragma unroll
     for (int j = 0; j < TN; ++j) wrow[j] = wn * WTN + j * 32 + frag_row;
+    // (16x16 fragments: lane l reads row l%16 of its block, lane group q16)
+    const int q16 = lane >> 4;
+    int arow16[2 * TM], wrow16[2 * TN];
+#pragma unroll
+    for (int i = 0; i < 2 * TM; ++i) arow16[i] = wm * WTM + i * 16 + (lane & 15);
+#pragma unroll
+    for (int j = 0; j < 2 * TN; ++j) wrow16[j] = wn * WTN + j * 16 + (lane & 15);
 
     // prologue: stages 0 and 1 in flight; wait for stage 0.
     issue_stage(0, 0);
@@ -316,7 +350,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    if constexpr (!FP8) {
+    if constexpr (OP == OP_I8 || OP == OP_BF16) {
         // Four 32-byte k-steps per stage; the fragments of k-step s+1 are read
         // while k-step s's 16 MFMAs run, and the next stage's k-step 0 is
         // read during k-step 3. The sched_group_barrier sequences pin that
@@ -395,7 +429,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         int kt = 0;
         for (; kt + 2 < KT; ++kt) stage(kt, std::true_type{});
         for (; kt < KT; ++kt) stage(kt, std::false_type{});
-    } else {
+    } else if constexpr (OP == OP_F8) {
         // Two 64-byte k-steps per stage (v_mfma_scale_f32_32x32x64_f8f6f4,
         // unit scales), with the same read-ahead and hand-off.
         v8i fa0[TM], fw0[TN], fa1[TM], fw1[TN];
@@ -464,12 +498,108 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         int kt = 0;
         for (; kt + 2 < KT; ++kt) stage(kt, std::true_type{});
         for (; kt < KT; ++kt) stage(kt, std::false_type{});
+    } else if constexpr (OP == OP_I8_16) {
+        // Two 64-byte k-steps per stage of v_mfma_i32_16x16x64_i8 over the
+        // wave's 8 x 4 blocks of 16x16: lane group q = lane/16 of a fragment
+        // takes logical chunk 4s + q in k-step s (both operands alike), the
+        // fragments of k-step s+1 read during k-step s, the refill DMAs
+        // spread over the first MFMAs after the hand-off.
+        v4i fa0[2 * TM], fw0[2 * TN], fa1[2 * TM], fw1[2 * TN];
+        auto read_frags = [&](v4i* fa, v4i* fw, int slot, int ks) {
+            const uint8_t* la = lds + slot * OP_BYTES;
+            const uint8_t* lw = lds + (NSLOT + slot) * OP_BYTES;
+            const int chunk = 4 * ks + q16;
+#pragma unroll
+            for (int i = 0; i < 2 * TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + lds_addr(arow16[i], chunk));
+#pragma unroll
+            for (int j = 0; j < 2 * TN; ++j) fw[j] = *reinterpret_cast<const v4i*>(lw + lds_addr(wrow16[j], chunk));
+        };
+        auto mfma_all = [&](const v4i* fa, const v4i* fw) {
+#pragma unroll
+            for (int i = 0; i < 2 * TM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2 * TN; ++j)
+                    acc16[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[j], fa[i], acc16[i][j], 0, 0, 0);
+        };
+        constexpr int NF = 2 * TM + 2 * TN;   // fragment reads per k-step
+        constexpr int NM = 4 * TM * TN;       // MFMAs per k-step
+        auto interleave = [&]() {
+#pragma unroll
+            for (int i = 0; i < NF; ++i) {
+                SGB(SG_MFMA, 1);
+                SGB(SG_DS_READ, 1);
+            }
+            SGB(SG_MFMA, NM - NF);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto stage = [&](int kt, auto refill) {
+            const int slot = kt & 1;
+            read_frags(fa1, fw1, slot, 1);
+            mfma_all(fa0, fw0);
+            interleave();
+            handoff();
+            if constexpr (decltype(refill)::value) issue_stage(kt + 2, slot);
+            read_frags(fa0, fw0, slot ^ 1, 0);
+            mfma_all(fa1, fw1);
+            if constexpr (decltype(refill)::value) {
+#pragma unroll
+                for (int i = 0; i < NM; ++i) {
+                    SGB(SG_MFMA, 1);
+                    if (i < 2 * NDMA) SGB(SG_VMEM, 1);
+                    if (i < NF) SGB(SG_DS_READ, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                interleave();
+            }
+        };
+        read_frags(fa0, fw0, 0, 0);
+        int kt = 0;
+        for (; kt + 2 < KT; ++kt) stage(kt, std::true_type{});
+        for (; kt < KT; ++kt) stage(kt, std::false_type{});
     }
 
     // Wait for every wave to leave the ring, then publish the epilogue
     // operands in ring space.
     wait_vmcnt<0>();
     __syncthreads();
+    if constexpr (M16) {
+        // The 16x16 blocks' accumulators into the 32x32 blocks' layout
+        // (lane l: row l%32, columns 8g + 4(l/32) + c) through a wave-private
+        // LDS buffer of 32 rows, one 32-row block at a time. The row pitch of
+        // 68 words puts the 16 rows a ds_{write,read}_b128 serves per cycle on
+        // distinct banks.
+        constexpr int CP = WTN + 4;
+        static_assert(NWAVES * 32 * CP * 4 <= SCALE_OFF, "accumulator remap overlaps the scales");
+        uint32_t* cv = reinterpret_cast<uint32_t*>(lds) + wave * 32 * CP;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int j = 0; j < 2 * TN; ++j)
+                    *reinterpret_cast<u32x4*>(cv + (16 * b + (lane & 15)) * CP + 16 * j + 4 * q16) =
+                        __builtin_bit_cast(u32x4, acc16[2 * i + b][j]);
+            // LDS operations of one wave complete in order; the empty asm
+            // keeps the compiler from moving the reads above the writes.
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const u32x4 v =
+                        *reinterpret_cast<const u32x4*>(cv + (lane & 31) * CP + 32 * j + 8 * g + 4 * (lane >> 5));
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        // (the element is copied out first: a bit_cast of
+                        // a vector element expression reads element 0)
+                        const uint32_t e = v[c];
+                        acc[i][j][4 * g + c] = __builtin_bit_cast(int, e);
+                    }
+                }
+            asm volatile("" ::: "memory");
+        }
+    }
     if (tid < 256) {
         s_as[tid] = e_as;
         s_ws[tid] = e_ws;
@@ -989,7 +1119,7 @@ TileProblem tile_problem(const void* a, const float* as, int M, int K, const voi
 
 template <bool FP8>
 hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream) {
-    constexpr int OP = FP8 ? OP_F8 : OP_I8;
+    constexpr int OP = FP8 ? OP_F8 : OP_I8_16;
     if (out_dt == QIMG_FP32)
         return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream) : launch_tiled<OP, QIMG_FP32, false>(P, stream);
     return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream) : launch_tiled<OP, QIMG_BF16, false>(P, stream);

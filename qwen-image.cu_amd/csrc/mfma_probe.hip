@@ -27,6 +27,8 @@ constexpr int KIND_I8_16 = 1;   // v_mfma_i32_16x16x64_i8            32768 ops
 constexpr int KIND_F8_32 = 2;   // v_mfma_scale_f32_32x32x64_f8f6f4 131072 flops (e4m3, unit scales)
 constexpr int KIND_F16_32 = 3;  // v_mfma_f32_32x32x16_f16           32768 flops
 constexpr int KIND_BF16_32 = 4; // v_mfma_f32_32x32x16_bf16          32768 flops
+constexpr int KIND_F8_16 = 5;   // v_mfma_scale_f32_16x16x128_f8f6f4 65536 flops (e4m3, unit scales)
+constexpr int KIND_F16_16 = 6;  // v_mfma_f32_16x16x32_f16           16384 flops
 
 constexpr int NCH = 4;     // independent accumulator chains
 constexpr int UNROLL = 4;  // MFMAs per chain per loop iteration
@@ -45,8 +47,9 @@ __device__ __forceinline__ uint32_t mix(uint32_t x) {
 template <int KIND>
 __device__ __forceinline__ uint32_t operand_bits(uint32_t seed) {
     const uint32_t r = mix(seed);
-    if constexpr (KIND == KIND_F8_32) return r & 0xf7f7f7f7u;  // e4m3: exponent <= 14
-    if constexpr (KIND == KIND_F16_32 || KIND == KIND_BF16_32) return r & 0xbfffbfffu;  // |x| < 2
+    if constexpr (KIND == KIND_F8_32 || KIND == KIND_F8_16) return r & 0xf7f7f7f7u;  // e4m3: exponent <= 14
+    if constexpr (KIND == KIND_F16_32 || KIND == KIND_BF16_32 || KIND == KIND_F16_16)
+        return r & 0xbfffbfffu;  // |x| < 2
     return r;
 }
 
@@ -117,6 +120,41 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, uint64_t* __
         for (int c = 0; c < NCH; ++c)
 #pragma unroll
             for (int r = 0; r < 16; ++r) result ^= __float_as_int(acc[c][r]);
+    } else if constexpr (KIND == KIND_F8_16) {
+        v8i va, vb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            va[i] = static_cast<int>(a[i]);
+            vb[i] = static_cast<int>(b[i]);
+        }
+        v4f acc[2 * NCH] = {};
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int u = 0; u < 2 * UNROLL; ++u)
+#pragma unroll
+                for (int c = 0; c < 2 * NCH; ++c)
+                    acc[c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(va, vb, acc[c], 0, 0, 0, 127, 0, 127);
+        }
+#pragma unroll
+        for (int c = 0; c < 2 * NCH; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) result ^= __float_as_int(acc[c][r]);
+    } else if constexpr (KIND == KIND_F16_16) {
+        const v4i wa = {static_cast<int>(a[0]), static_cast<int>(a[1]), static_cast<int>(a[2]), static_cast<int>(a[3])};
+        const v4i wb = {static_cast<int>(b[0]), static_cast<int>(b[1]), static_cast<int>(b[2]), static_cast<int>(b[3])};
+        v4f acc[2 * NCH] = {};
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int u = 0; u < 2 * UNROLL; ++u)
+#pragma unroll
+                for (int c = 0; c < 2 * NCH; ++c)
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, wa),
+                                                                    __builtin_bit_cast(v8h, wb), acc[c], 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < 2 * NCH; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) result ^= __float_as_int(acc[c][r]);
     } else {
         v4i wa = {static_cast<int>(a[0]), static_cast<int>(a[1]), static_cast<int>(a[2]), static_cast<int>(a[3])};
         v4i wb = {static_cast<int>(b[0]), static_cast<int>(b[1]), static_cast<int>(b[2]), static_cast<int>(b[3])};
@@ -167,7 +205,7 @@ extern "C" {
 
 // MFMAs one wave issues per loop iteration of `kind`.
 int qimg_probe_mfma_per_iter(int kind) {
-    return kind == KIND_I8_16 ? 4 * NCH * UNROLL : NCH * UNROLL;
+    return (kind == KIND_I8_16 || kind == KIND_F8_16 || kind == KIND_F16_16) ? 4 * NCH * UNROLL : NCH * UNROLL;
 }
 
 // One launch of the probe: `cus` x `wps` workgroups of four waves (one per
@@ -176,7 +214,7 @@ int qimg_probe_mfma_per_iter(int kind) {
 // (s_memtime start, end, s_memrealtime start, end per wave); sink: int
 // [cus * wps * 256]. Returns 0, or 1 for bad arguments, or 2 for a HIP error.
 int qimg_probe_mfma(int kind, int wps, int cus, int iters, uint64_t* clocks, int* sink, void* stream) {
-    if (kind < KIND_I8_32 || kind > KIND_BF16_32 || (wps != 1 && wps != 2) || cus < 1 || iters < 1 ||
+    if (kind < KIND_I8_32 || kind > KIND_F16_16 || (wps != 1 && wps != 2) || cus < 1 || iters < 1 ||
         clocks == nullptr || sink == nullptr)
         return 1;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -186,7 +224,10 @@ int qimg_probe_mfma(int kind, int wps, int cus, int iters, uint64_t* clocks, int
         case KIND_I8_16: e = launch<KIND_I8_16>(wps, cus, iters, clocks, sink, s); break;
         case KIND_F8_32: e = launch<KIND_F8_32>(wps, cus, iters, clocks, sink, s); break;
         case KIND_F16_32: e = launch<KIND_F16_32>(wps, cus, iters, clocks, sink, s); break;
-        default: e = launch<KIND_BF16_32>(wps, cus, iters, clocks, sink, s); break;
+        case KIND_F8_16: e = launch<KIND_F8_16>(wps, cus, iters, clocks, sink, s); break;
+        case KIND_F16_16: e = launch<KIND_F16_16>(wps, cus, iters, clocks, sink, s); break;
+        case KIND_BF16_32: e = launch<KIND_BF16_32>(wps, cus, iters, clocks, sink, s); break;
+        default: return 1;
     }
     return e == hipSuccess ? 0 : 2;
 }
