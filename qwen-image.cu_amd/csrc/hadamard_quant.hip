@@ -253,7 +253,10 @@ __global__ __launch_bounds__(256) void fwht_quant_rows_kernel(
 // row's absmax is known; the quantized bytes are stored from there (each
 // store instruction writes 64 consecutive bytes per wave). Each value sees
 // the same butterfly stages in the same order as in fwht_quant_rows_kernel.
-template <typename InT, RowOut OUT, int NB>
+// GELU_IN: each loaded value v is first replaced by gelu_tanh_fast(v), the
+// GELU of the linear epilogue (the fc1 -> fc2 hop with the GELU applied by
+// the consumer: the same function of the same fp32 value, so the same bits).
+template <typename InT, RowOut OUT, int NB, bool GELU_IN = false>
 __global__ __launch_bounds__(256) void fwht_quant_blocks_kernel(const InT* x, void* out, float* __restrict__ scales,
                                                                 int M, int K, float norm) {
     constexpr int HBS = 4096;
@@ -267,6 +270,12 @@ __global__ __launch_bounds__(256) void fwht_quant_blocks_kernel(const InT* x, vo
     float v[NB][16];
 #pragma unroll
     for (int b = 0; b < NB; ++b) load16<InT>(xin + b * HBS + 16 * tid, v[b]);
+    if constexpr (GELU_IN) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[b][i] = gelu_tanh_fast(v[b][i]);
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -830,6 +839,29 @@ hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, 
     const float* xf = static_cast<const float*>(x);
     return fp8 ? launch_rows<float, RowOut::Fp8>(xf, q_out, scales, M, K, hbs, stream)
                : launch_rows<float, RowOut::Int8>(xf, q_out, scales, M, K, hbs, stream);
+}
+
+bool fwht_quant_gelu_supported(int K, int hbs) {
+    const int nb = K / 4096;
+    return hbs == 4096 && nb >= 2 && nb <= 4 && nb * 4096 == K;
+}
+
+hipError_t launch_fwht_quant_gelu(const float* x, int M, int K, int hbs, int mode, void* q_out, float* scales,
+                                  hipStream_t stream) {
+    if (!fwht_quant_gelu_supported(K, hbs)) return hipErrorNotSupported;
+    if (M == 0) return hipSuccess;
+    const float norm = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(hbs)));
+    const size_t lds = sizeof(float) * (4096 + 4096 / 16 + 1 + 8);
+    const int nb = K / 4096;
+    const bool fp8 = mode == QIMG_QM_FP8_HADAMARD;
+    auto kern = fp8 ? (nb == 2   ? fwht_quant_blocks_kernel<float, RowOut::Fp8, 2, true>
+                       : nb == 3 ? fwht_quant_blocks_kernel<float, RowOut::Fp8, 3, true>
+                                 : fwht_quant_blocks_kernel<float, RowOut::Fp8, 4, true>)
+                    : (nb == 2   ? fwht_quant_blocks_kernel<float, RowOut::Int8, 2, true>
+                       : nb == 3 ? fwht_quant_blocks_kernel<float, RowOut::Int8, 3, true>
+                                 : fwht_quant_blocks_kernel<float, RowOut::Int8, 4, true>);
+    hipLaunchKernelGGL(kern, dim3(M), dim3(256), lds, stream, x, q_out, scales, M, K, norm);
+    return hipGetLastError();
 }
 
 hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float* scale, int M, int K, int hbs,

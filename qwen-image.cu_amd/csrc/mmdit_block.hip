@@ -425,24 +425,42 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                                           b.txt_mlp_fc1.mode, EPS, w.act_q_txt, w.act_scales_txt, s));
         }
 
-        // GELU MLP (transformer.cu:780-808): fc1 of each stream on its own
+        // GELU MLP (transformer.cu:780-808): fc1 of each stream on its own.
+        // With e4m3 weights fc1 is run without its GELU and the fc2-input
+        // quantization applies it to the values it loads (the same function
+        // of the same fp32 values: the same quantized bytes; C5 step
+        // measured faster, the int8 block equal).
+        const bool gelu_i = b.img_mlp_fc1.mode == QIMG_QM_FP8_HADAMARD &&
+                            fwht_quant_gelu_supported(b.img_mlp_fc2.K, b.img_mlp_fc2.hbs);
+        const bool gelu_t = b.txt_mlp_fc1.mode == QIMG_QM_FP8_HADAMARD &&
+                            fwht_quant_gelu_supported(b.txt_mlp_fc2.K, b.txt_mlp_fc2.hbs);
         QIMG_TRY(mark(QIMG_PROF_MLP_GEMM));
         // The text stream's fc1 and fc2-input quantization run on the side
         // stream beside the image fc2-input quantization, which is HBM-bound
         // and leaves the matrix cores idle (they start once the image fc1,
         // which fills every CU, is done).
-        if (Mi) QIMG_TRY(gemm(w.act_q, w.act_scales, Mi, b.img_mlp_fc1, w.img_mlp, 1, s));
+        if (Mi) QIMG_TRY(gemm(w.act_q, w.act_scales, Mi, b.img_mlp_fc1, w.img_mlp, gelu_i ? 0 : 1, s));
         if (Mt) {
             hipStream_t st = s;
             if (Mi) {
                 QIMG_TRY(fork(side));
                 st = side->stream;
             }
-            QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, 1, st));
-            QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2, st));
+            QIMG_TRY(gemm(w.act_q_txt, w.act_scales_txt, Mt, b.txt_mlp_fc1, w.txt_mlp, gelu_t ? 0 : 1, st));
+            if (gelu_t)
+                QIMG_TRY(launch_fwht_quant_gelu(w.txt_mlp, Mt, b.txt_mlp_fc2.K, b.txt_mlp_fc2.hbs, b.txt_mlp_fc2.mode,
+                                                w.act_q_txt, w.act_scales_txt, st));
+            else
+                QIMG_TRY(quant_txt(w.txt_mlp, Mt, b.txt_mlp_fc2, st));
             if (Mi) QIMG_TRY(hipEventRecord(side->join, side->stream));
         }
-        if (Mi) QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
+        if (Mi) {
+            if (gelu_i)
+                QIMG_TRY(launch_fwht_quant_gelu(w.img_mlp, Mi, b.img_mlp_fc2.K, b.img_mlp_fc2.hbs, b.img_mlp_fc2.mode,
+                                                w.act_q, w.act_scales, s));
+            else
+                QIMG_TRY(quant(w.img_mlp, Mi, b.img_mlp_fc2));
+        }
         if (Mt && Mi) QIMG_TRY(join(side));
         // both fc2 in one launch, with the gate2 residual (transformer.cu:
         // 812-818) in their epilogue

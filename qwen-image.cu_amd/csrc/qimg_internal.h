@@ -31,6 +31,12 @@ int run_linear(const char* fn, const void* x, int x_dtype, int M, int K, const v
 size_t rows_lds_bytes(int K);
 hipError_t launch_fwht_quant(const void* x, int x_dtype, int M, int K, int hbs, int mode,
                              void* q_out, float* scales, hipStream_t stream);
+// launch_fwht_quant of gelu_tanh_fast(x) for fp32 rows of 2-4 Hadamard blocks
+// of 4096 (the fc2 input, with fc1 run without its GELU: the same values as
+// the GELU in fc1's epilogue); hipErrorNotSupported for other shapes.
+bool fwht_quant_gelu_supported(int K, int hbs);
+hipError_t launch_fwht_quant_gelu(const float* x, int M, int K, int hbs, int mode, void* q_out, float* scales,
+                                  hipStream_t stream);
 // LayerNorm + modulate of fp32 rows [M, K] (K <= 4096) straight into the
 // FWHT + int8/e4m3 quantization of launch_fwht_quant (same values).
 hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float* scale, int M, int K, int hbs,
