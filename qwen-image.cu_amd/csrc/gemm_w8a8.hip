@@ -117,7 +117,9 @@ constexpr int OP_BF16 = 2;
 // this chip (a register-only loop runs 16x16x64 at 3.8-3.9 POP/s and 2.1-2.3
 // GHz, 32x32x32 at 3.5-3.7 POP/s and 1.7-1.8 GHz). The main loop keeps the
 // accumulators as 16x16 blocks and hands them to the epilogue in the 32x32
-// blocks' register layout (remapped through LDS), so every epilogue is shared.
+// blocks' register layout (remapped through LDS) only where an attention
+// layout is written; plain launches dequantize and stage the 16x16 blocks
+// directly.
 // (e4m3 stays on 32x32x64: a 16x16x128 loop of the same tiling measured 2-8%
 // slower at the 1328x1328 step's shapes.)
 constexpr int OP_I8_16 = 3;
@@ -563,41 +565,48 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // operands in ring space.
     wait_vmcnt<0>();
     __syncthreads();
-    if constexpr (M16) {
-        // The 16x16 blocks' accumulators into the 32x32 blocks' layout
-        // (lane l: row l%32, columns 8g + 4(l/32) + c) through a wave-private
-        // LDS buffer of 32 rows, one 32-row block at a time. The row pitch of
-        // 68 words puts the 16 rows a ds_{write,read}_b128 serves per cycle on
-        // distinct banks.
-        constexpr int CP = WTN + 4;
-        static_assert(NWAVES * 32 * CP * 4 <= SCALE_OFF, "accumulator remap overlaps the scales");
-        uint32_t* cv = reinterpret_cast<uint32_t*>(lds) + wave * 32 * CP;
+    // Interior tiles (the common case) take paths with no per-element
+    // bounds checks.
+    const bool interior = (m0 + BM <= M) && (n0 + BN <= N) && ((N & 3) == 0);
+    // (plain int8 launches are stored straight from the 16x16 blocks, below;
+    // the attention-layout epilogues take the 32x32 layout)
+    if constexpr (M16 && HD) {
+        {
+            // The 16x16 blocks' accumulators into the 32x32 blocks' layout
+            // (lane l: row l%32, columns 8g + 4(l/32) + c) through a
+            // wave-private LDS buffer of 32 rows, one 32-row block at a time.
+            // The row pitch of 68 words puts the 16 rows a
+            // ds_{write,read}_b128 serves per cycle on distinct banks.
+            constexpr int CP = WTN + 4;
+            static_assert(NWAVES * 32 * CP * 4 <= SCALE_OFF, "accumulator remap overlaps the scales");
+            uint32_t* cv = reinterpret_cast<uint32_t*>(lds) + wave * 32 * CP;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+            for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+                for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int j = 0; j < 2 * TN; ++j)
-                    *reinterpret_cast<u32x4*>(cv + (16 * b + (lane & 15)) * CP + 16 * j + 4 * q16) =
-                        __builtin_bit_cast(u32x4, acc16[2 * i + b][j]);
-            // LDS operations of one wave complete in order; the empty asm
-            // keeps the compiler from moving the reads above the writes.
-            asm volatile("" ::: "memory");
+                    for (int j = 0; j < 2 * TN; ++j)
+                        *reinterpret_cast<u32x4*>(cv + (16 * b + (lane & 15)) * CP + 16 * j + 4 * q16) =
+                            __builtin_bit_cast(u32x4, acc16[2 * i + b][j]);
+                // LDS operations of one wave complete in order; the empty asm
+                // keeps the compiler from moving the reads above the writes.
+                asm volatile("" ::: "memory");
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const u32x4 v =
-                        *reinterpret_cast<const u32x4*>(cv + (lane & 31) * CP + 32 * j + 8 * g + 4 * (lane >> 5));
+                    for (int g = 0; g < 4; ++g) {
+                        const u32x4 v = *reinterpret_cast<const u32x4*>(cv + (lane & 31) * CP + 32 * j + 8 * g +
+                                                                        4 * (lane >> 5));
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        // (the element is copied out first: a bit_cast of
-                        // a vector element expression reads element 0)
-                        const uint32_t e = v[c];
-                        acc[i][j][4 * g + c] = __builtin_bit_cast(int, e);
+                        for (int c = 0; c < 4; ++c) {
+                            // (the element is copied out first: a bit_cast of
+                            // a vector element expression reads element 0)
+                            const uint32_t e = v[c];
+                            acc[i][j][4 * g + c] = __builtin_bit_cast(int, e);
+                        }
                     }
-                }
-            asm volatile("" ::: "memory");
+                asm volatile("" ::: "memory");
+            }
         }
     }
     if (tid < 256) {
@@ -609,6 +618,127 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         s_gate[tid] = e_gate;
     }
     __syncthreads();
+
+    if constexpr (M16 && !HD) {
+        // Plain int8 launches: each lane holds 4 consecutive columns of one
+        // row per 16x16 block (columns 16j + 4(l/16) .. +3 of row
+        // 16i + l%16: D = W x A is indexed [n][m]). They are dequantized with
+        // the arithmetic of the 32x32-layout paths below and written to the
+        // wave's staging rows (32 at a time, padded by 16 bytes), which are
+        // stored 16 bytes a lane, 1 KB per instruction; rows past M and
+        // columns past N are skipped there. (Stored directly, 16 rows x 64
+        // bytes per instruction, the fp32 GEMM measured 10-15% slower.)
+        constexpr int ESZ = (OUT_DT == QIMG_FP32) ? 4 : 2;
+        constexpr int ROWB = WTN * ESZ;
+        constexpr int PITCH = ROWB + 16;
+        constexpr int CPR = ROWB / 16;  // 16-byte chunks per staged row
+        constexpr int EPC = 16 / ESZ;   // elements per chunk
+        constexpr int NIT = 32 * CPR / 64;
+        uint8_t* stage = lds + wave * (32 * PITCH);
+        const bool gated = OUT_DT == QIMG_FP32 && has_gate;
+        const bool vec = (N % EPC) == 0;
+        const bool fast = interior && vec;  // (bf16 chunks need N % 8 == 0)
+        v4f wv[2 * TN], bv[2 * TN];
+#pragma unroll
+        for (int j = 0; j < 2 * TN; ++j) {
+            const int nl = wn * WTN + 16 * j + 4 * q16;
+            wv[j] = *reinterpret_cast<const v4f*>(s_ws + nl);
+            bv[j] = *reinterpret_cast<const v4f*>(s_bias + nl);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int rb = m0 + wm * WTM + i * 32;  // first row of the block
+            const int cb = n0 + wn * WTN;           // first column of the wave
+            uint8_t* obase = reinterpret_cast<uint8_t*>(out) + (static_cast<int64_t>(rb) * N + cb) * ESZ;
+            v4f res[NIT];
+            if (gated) {
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const int idx = it * 64 + lane;
+                    const int r = idx / CPR, c = cb + (idx % CPR) * EPC;
+                    const float* o = reinterpret_cast<const float*>(obase + static_cast<int64_t>(r) * N * ESZ) +
+                                     (idx % CPR) * EPC;
+                    if (fast || (rb + r < M && vec && c + EPC <= N)) {
+                        res[it] = *reinterpret_cast<const v4f*>(o);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) res[it][e] = (rb + r < M && c + e < N) ? o[e] : 0.0f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int rl = 16 * b + (lane & 15);
+                const float sa = s_as[wm * WTM + i * 32 + rl];
+#pragma unroll
+                for (int j = 0; j < 2 * TN; ++j) {
+                    float v[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int e = acc16[2 * i + b][j][c];
+                        float t;
+                        {
+#pragma clang fp contract(off)
+                            t = static_cast<float>(e) * sa * wv[j][c];
+                            t = t + bv[j][c];
+                        }
+                        if (GELU) t = gelu_tanh_fast(t);
+                        v[c] = t;
+                    }
+                    uint8_t* dst = stage + rl * PITCH + (16 * j + 4 * q16) * ESZ;
+                    if constexpr (OUT_DT == QIMG_FP32)
+                        *reinterpret_cast<v4f*>(dst) = (v4f){v[0], v[1], v[2], v[3]};
+                    else
+                        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                }
+            }
+            // LDS operations of one wave complete in order; the empty asm
+            // keeps the compiler from moving the reads above the writes.
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int idx = it * 64 + lane;
+                const int r = idx / CPR;
+                const int c16 = idx % CPR;
+                const int c = cb + c16 * EPC;
+                v4i val = *reinterpret_cast<const v4i*>(stage + r * PITCH + c16 * 16);
+                if (gated) {
+                    // gate_add_fp32f (cuda_kernels.cu:2181-2189): out + gate[n] * value
+                    const v4f t = __builtin_bit_cast(v4f, val);
+                    const v4f gv = *reinterpret_cast<const v4f*>(s_gate + wn * WTN + c16 * 4);
+                    const v4f rv = res[it];
+                    val = __builtin_bit_cast(v4i, (v4f){__builtin_fmaf(gv[0], t[0], rv[0]),
+                                                        __builtin_fmaf(gv[1], t[1], rv[1]),
+                                                        __builtin_fmaf(gv[2], t[2], rv[2]),
+                                                        __builtin_fmaf(gv[3], t[3], rv[3])});
+                }
+                uint8_t* o = obase + static_cast<int64_t>(r) * N * ESZ + c16 * 16;
+                if (fast || (rb + r < M && vec && c + EPC <= N)) {
+                    *reinterpret_cast<v4i*>(o) = val;
+                } else if (ESZ == 2 && (N & 3) == 0) {
+                    // bf16 with N % 8 == 4: 8-byte halves (a chunk starts at
+                    // a multiple of 8 columns, so each half is wholly in or
+                    // out)
+                    const u32x4 u = __builtin_bit_cast(u32x4, val);
+                    if (rb + r < M && c + 4 <= N) *reinterpret_cast<uint2*>(o) = make_uint2(u[0], u[1]);
+                    if (rb + r < M && c + 8 <= N) *reinterpret_cast<uint2*>(o + 8) = make_uint2(u[2], u[3]);
+                } else if (rb + r < M) {
+                    const u32x4 u = __builtin_bit_cast(u32x4, val);
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) {
+                        if (c + e >= N) break;
+                        const uint32_t word = u[(e * ESZ) / 4];
+                        if constexpr (ESZ == 4)
+                            reinterpret_cast<uint32_t*>(o)[e] = word;
+                        else
+                            reinterpret_cast<uint16_t*>(o)[e] = static_cast<uint16_t>(word >> (16 * (e & 1)));
+                    }
+                }
+            }
+            asm volatile("" ::: "memory");
+        }
+        return;
+    }
 
     if constexpr (HD && OUT_DT == QIMG_FP32 && !BF && !GELU) {
         if (pr.hk == HEADS_K || pr.hk == HEADS_Q) {
@@ -765,9 +895,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // block is indexed [n][m]: lane holds m = lane%32 and n rows
     // 8*(r/4) + 4*(lane/32) + r%4. Each lane therefore owns one output row
     // per block and 16 columns in four runs of 4 consecutive n, stored as
-    // one 16-byte (fp32) or 8-byte (bf16) write per run. Interior tiles
-    // (the common case) take a path with no per-element bounds checks.
-    const bool interior = (m0 + BM <= M) && (n0 + BN <= N) && ((N & 3) == 0);
+    // one 16-byte (fp32) or 8-byte (bf16) write per run.
     // edge tiles still store whole 4-column groups with one vector store
     // when the row is in range (rows past M are skipped below)
     const bool vec_n = (N & 3) == 0;

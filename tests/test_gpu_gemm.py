@@ -201,6 +201,34 @@ def test_dequantize_and_bias_matches_oracle_and_fused(qimg, oracle):
                                rtol=2e-6, atol=2e-6)
 
 
+@pytest.mark.parametrize("M,N,K", [(4100, 3076, 1024), (600, 518, 512), (777, 1000, 256), (513, 264, 3072)])
+def test_large_tile_epilogue_edges(qimg, oracle, M, N, K):
+    """The 256x256-tile kernel's int8 epilogue on ragged tiles: rows past M,
+    N % 4 = 2 (element stores), N % 8 = 4 (bf16 half-chunk stores), N % 8 = 0.
+    fp32 out bit-exact against the oracle's dequant of the int32 product, bf16
+    out its RNE rounding, GELU identical to the stand-alone epilogue kernel."""
+    rng = np.random.default_rng(M + 5 * N + K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    s = (rng.random(M) * 1e-3 + 1e-5).astype(np.float32)
+    ws = (rng.random(N) * 1e-3 + 1e-5).astype(np.float32)
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    c = oracle.gemm_s8s8s32(a, w)
+    ref = oracle.dequant_epilogue(c, s, ws, b_bits)
+    qw = _qw(qimg, w, ws, 1)
+    ad, sd, bd = _dev(a), _dev(s), _bf16_dev(b_bits)
+    with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
+        o32 = qimg.linear_forward_prequantized(ad, sd, qw, bd)
+        o16 = qimg.linear_forward_prequantized(ad, sd, qw, bd, out_dtype=torch.bfloat16)
+        og = qimg.linear_forward_prequantized(ad, sd, qw, bd, apply_gelu=True)
+    sep_g = qimg.dequantize_and_bias(_dev(c), sd, _dev(ws), bd, apply_gelu=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o32.cpu().numpy(), ref)
+    np.testing.assert_array_equal(o16.float().cpu().numpy(),
+                                  oracle.bf16_bits_to_f32(oracle.bf16_bits_from_f32(ref)).reshape(M, N))
+    assert torch.equal(og, sep_g)
+
+
 @pytest.mark.parametrize("M,N,K", [(3328, 2560, 128), (3328, 2560, 320), (4352, 3072, 1024)])
 def test_int8_gemm_partial_round_shapes_exact(qimg, oracle, M, N, K):
     """Tile counts that do not fill whole rounds of the 256 CUs (130 and 204
