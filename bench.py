@@ -1226,7 +1226,7 @@ def _summarize(d, outdir):
                      MI * D_ + H_ * D_ + MI * H_ * 4 + 4 * (MI + H_) + 2 * H_),
         "gemm_fc1_tail": ("qimg::gemm_small_dma_kernel<false, 2, 2, 2, 0, true, 64>", 768,
                           256 * D_ + H_ * D_ + 256 * H_ * 4 + 4 * (256 + H_) + 2 * H_),
-        "quant_fc2_in": ("qimg::fwht_quant_blocks_kernel<float, (qimg::RowOut)0, 3>", M_,
+        "quant_fc2_in": ("qimg::fwht_quant_blocks_kernel<float, (qimg::RowOut)0, 3, false>", M_,
                          M_ * H_ * 4 + M_ * H_ + 4 * M_),
         "gemm_fc2": ("qimg::gemm_w8a8_kernel<3, 1, false, false>", 204,
                      M_ * H_ + D_ * H_ + M_ * D_ * 2 + 4 * (M_ + D_) + 2 * D_),
