@@ -173,7 +173,8 @@ def main():
     # 256 CUs, and the trailing tile row to the 64 x 64 tiles), as two calls,
     # so that HIP events time each kernel; the outputs and the step time equal
     # those of the single call (measured in-process: 390.0 against 391.1 us
-    # per step). extra.fc1_single_launch_ms times fc1 as that single call.
+    # per step). extra.fc1_single_call_ms times fc1 as that single call (its
+    # two kernels back to back, without the events between them).
     MI, MT = 4096, M - 4096
 
     # (the stream is read at each call, so the same launches can be captured)
@@ -299,8 +300,8 @@ def main():
                 "avg_launch_ms": round(per_kernel_ms[dom], 4)}
 
     extra = {"per_kernel_ms_median": {k: round(v, 4) for k, v in per_kernel_ms.items()},
-             "fc1_single_launch_ms": round(ms_fc1_single, 4),
-             "fc1_single_launch_tflops": round(2.0 * M * D * H / ms_fc1_single / 1e9, 1),
+             "fc1_single_call_ms": round(ms_fc1_single, 4),
+             "fc1_single_call_tflops": round(2.0 * M * D * H / ms_fc1_single / 1e9, 1),
              "step_timing": "median of K replays of the step captured as one HIP graph",
              "ms_per_step_eager": round(ms_step_eager, 4), "ms_per_step_eager_mean": round(total_ms / K, 4),
              "graph_equals_eager": graph_equals_eager,
