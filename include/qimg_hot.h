@@ -111,17 +111,21 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * multiple of 64. No counterpart in the reference (cuBLAS picks its own
  * algorithm); it exists for tests and tuning, which compare the kernels on
  * one shape. AUTO (the default) takes the vector-ALU GEMV for int8 with
- * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 128 tiles of
- * 256x256 would cover the output, and 256x256 tiles otherwise. GEMV with
- * e4m3 or M > 4 runs the 32x32 tiles. Process-wide; returns QIMG_OK, or
- * QIMG_ERR_INVALID_ARG for an unknown value. All choices give identical int8
- * results. */
+ * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
+ * 256x256 would cover the output, and 256x256 tiles otherwise; int8 takes
+ * 256x192 tiles instead when they need fewer rounds of tiles on the device's
+ * CUs (counting a round of them as 3/4 of a 256x256 round; 4096 x 3072 is one
+ * full round of them). LARGE_NARROW forces the 256x192 tiles (int8; e4m3
+ * runs 256x256). GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide;
+ * returns QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices
+ * give identical int8 results. */
 enum {
     QIMG_LINEAR_AUTO = 0,
     QIMG_LINEAR_LARGE_TILE = 1,
     QIMG_LINEAR_SMALL_32 = 2,
     QIMG_LINEAR_SMALL_64 = 3,
-    QIMG_LINEAR_GEMV = 4
+    QIMG_LINEAR_GEMV = 4,
+    QIMG_LINEAR_LARGE_NARROW = 5
 };
 int qimg_set_linear_kernel(int which);
 int qimg_get_linear_kernel(void);

@@ -15,7 +15,9 @@
 // accumulator registers per wave. Two waves per
 // SIMD let one wave's LDS reads and waits overlap the other's MFMAs
 // (measured 7-9% faster than four waves of 128x128). Both operands are
-// K-major [rows, K] as the reference stores them (TN GEMM).
+// K-major [rows, K] as the reference stores them (TN GEMM). Plain int8
+// launches can also run 256x192 tiles (waves of 128x48), chosen where they
+// take fewer rounds of the CUs (4096 x 3072: 256 tiles, one full round).
 //
 // K advances 128 bytes per stage through a two-slot LDS ring (2 x 64 KB):
 // while one stage is consumed the next is in flight. Stages are filled by
@@ -186,10 +188,25 @@ struct TileProblems {
 // HD: the launch may hold problems with attention-layout outputs
 // (TileProblem::hk; an instance of its own, so that the extra epilogues
 // leave the others' register allocation alone).
-template <int OP, int OUT_DT, bool GELU, bool HD = false>
+// TW: the tile's width, 256 or 192 (NARROW_BN). The 256x192 tiles serve
+// plain int8 launches whose 256x256 tiles would leave CUs idle: 4096 x 3072
+// is 192 tiles of 256x256 on 256 CUs, a quarter of the chip idle for the
+// whole launch, but 256 tiles of 256x192, one round with every CU busy.
+// Each wave then owns 128 x 48 = 8 x 3 blocks of 16x16, and a stage's W
+// share is 192 rows (3 DMA instructions per wave).
+constexpr int NARROW_BN = 192;
+template <int OP, int OUT_DT, bool GELU, bool HD = false, int TW = BN>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr bool BF = OP == OP_BF16;
     constexpr bool M16 = OP == OP_I8_16;
+    static_assert(TW == BN || (TW == NARROW_BN && M16 && !HD),
+                  "the narrow tile serves the plain int8 epilogue on 16x16 blocks");
+    // (these hide the file-scope 256-wide values inside the kernel)
+    constexpr int BN = TW;                       // tile width
+    constexpr int WTN = BN / WAVES_N;            // wave tile width (64 or 48)
+    constexpr int TN = WTN / 32;                 // 32x32 blocks across a wave (256 wide only)
+    constexpr int TN16 = WTN / 16;               // 16x16 blocks across a wave
+    constexpr int NDMA_W = BN / (NWAVES * DMA_ROWS);  // W DMA instructions per wave per stage
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
     float* s_ws = s_as + 256;
@@ -260,17 +277,19 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // DMA_ROWS*(NWAVES*i + w) .. +DMA_ROWS of the A tile (and the same rows
     // of the W tile); lane -> row +lane/8, physical chunk lane%8.
     const uint8_t* a_src[NDMA];
-    const uint8_t* w_src[NDMA];
+    const uint8_t* w_src[NDMA_W];
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
         const int r = DMA_ROWS * (NWAVES * i + wave) + (lane >> 3);
         const int c = (lane & 7) ^ swz8(r);
         int gm = m0 + r;
         gm = gm < M ? gm : M - 1;  // clamp: rows past M are computed, never stored
-        int gn = n0 + r;
-        gn = gn < N ? gn : N - 1;
         a_src[i] = A + static_cast<int64_t>(gm) * K + c * 16;
-        w_src[i] = W + static_cast<int64_t>(gn) * K + c * 16;
+        if (i < NDMA_W) {
+            int gn = n0 + r;
+            gn = gn < N ? gn : N - 1;
+            w_src[i] = W + static_cast<int64_t>(gn) * K + c * 16;
+        }
     }
 
     typedef typename Acc<OP>::type acc_t;
@@ -278,12 +297,12 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     // 16x16 blocks of the wave tile (2 TM x 2 TN), for the M16 kinds
     // (one 16x16 block: lane l holds rows 4(l/16) .. +3 of column l%16)
     typedef v4i acc16_t;
-    acc16_t acc16[2 * TM][2 * TN];
+    acc16_t acc16[2 * TM][TN16];
     if constexpr (M16) {
 #pragma unroll
         for (int i = 0; i < 2 * TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2 * TN; ++j) acc16[i][j] = acc16_t{};
+            for (int j = 0; j < TN16; ++j) acc16[i][j] = acc16_t{};
     } else {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -310,7 +329,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                                              (lds_ptr_t)(abase + rowblk * BK), 16, 0, kDmaPolicy);
         }
 #pragma unroll
-        for (int i = 0; i < NDMA; ++i) {
+        for (int i = 0; i < NDMA_W; ++i) {
             const int rowblk = DMA_ROWS * (NWAVES * i + wave);
             __builtin_amdgcn_global_load_lds((gbl_ptr_t)(w_src[i] + koff),
                                              (lds_ptr_t)(wbase + rowblk * BK), 16, 0, kDmaPolicy);
@@ -326,16 +345,16 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     for (int j = 0; j < TN; ++j) wrow[j] = wn * WTN + j * 32 + frag_row;
     // (16x16 fragments: lane l reads row l%16 of its block, lane group q16)
     const int q16 = lane >> 4;
-    int arow16[2 * TM], wrow16[2 * TN];
+    int arow16[2 * TM], wrow16[TN16];
 #pragma unroll
     for (int i = 0; i < 2 * TM; ++i) arow16[i] = wm * WTM + i * 16 + (lane & 15);
 #pragma unroll
-    for (int j = 0; j < 2 * TN; ++j) wrow16[j] = wn * WTN + j * 16 + (lane & 15);
+    for (int j = 0; j < TN16; ++j) wrow16[j] = wn * WTN + j * 16 + (lane & 15);
 
     // prologue: stages 0 and 1 in flight; wait for stage 0.
     issue_stage(0, 0);
     issue_stage(1, 1);
-    wait_vmcnt<2 * NDMA>();
+    wait_vmcnt<NDMA + NDMA_W>();
     __builtin_amdgcn_s_barrier();
 
     // Hand-off before a stage's last k-step, right after that k-step's
@@ -506,7 +525,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         // takes logical chunk 4s + q in k-step s (both operands alike), the
         // fragments of k-step s+1 read during k-step s, the refill DMAs
         // spread over the first MFMAs after the hand-off.
-        v4i fa0[2 * TM], fw0[2 * TN], fa1[2 * TM], fw1[2 * TN];
+        v4i fa0[2 * TM], fw0[TN16], fa1[2 * TM], fw1[TN16];
         auto read_frags = [&](v4i* fa, v4i* fw, int slot, int ks) {
             const uint8_t* la = lds + slot * OP_BYTES;
             const uint8_t* lw = lds + (NSLOT + slot) * OP_BYTES;
@@ -514,17 +533,17 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
 #pragma unroll
             for (int i = 0; i < 2 * TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + lds_addr(arow16[i], chunk));
 #pragma unroll
-            for (int j = 0; j < 2 * TN; ++j) fw[j] = *reinterpret_cast<const v4i*>(lw + lds_addr(wrow16[j], chunk));
+            for (int j = 0; j < TN16; ++j) fw[j] = *reinterpret_cast<const v4i*>(lw + lds_addr(wrow16[j], chunk));
         };
         auto mfma_all = [&](const v4i* fa, const v4i* fw) {
 #pragma unroll
             for (int i = 0; i < 2 * TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2 * TN; ++j)
+                for (int j = 0; j < TN16; ++j)
                     acc16[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[j], fa[i], acc16[i][j], 0, 0, 0);
         };
-        constexpr int NF = 2 * TM + 2 * TN;   // fragment reads per k-step
-        constexpr int NM = 4 * TM * TN;       // MFMAs per k-step
+        constexpr int NF = 2 * TM + TN16;     // fragment reads per k-step
+        constexpr int NM = 2 * TM * TN16;     // MFMAs per k-step
         auto interleave = [&]() {
 #pragma unroll
             for (int i = 0; i < NF; ++i) {
@@ -547,7 +566,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
 #pragma unroll
                 for (int i = 0; i < NM; ++i) {
                     SGB(SG_MFMA, 1);
-                    if (i < 2 * NDMA) SGB(SG_VMEM, 1);
+                    if (i < NDMA + NDMA_W) SGB(SG_VMEM, 1);
                     if (i < NF) SGB(SG_DS_READ, 1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -601,9 +620,9 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         const bool gated = OUT_DT == QIMG_FP32 && has_gate;
         const bool vec = (N % EPC) == 0;
         const bool fast = interior && vec;  // (bf16 chunks need N % 8 == 0)
-        v4f wv[2 * TN], bv[2 * TN];
+        v4f wv[TN16], bv[TN16];
 #pragma unroll
-        for (int j = 0; j < 2 * TN; ++j) {
+        for (int j = 0; j < TN16; ++j) {
             const int nl = wn * WTN + 16 * j + 4 * q16;
             wv[j] = *reinterpret_cast<const v4f*>(s_ws + nl);
             bv[j] = *reinterpret_cast<const v4f*>(s_bias + nl);
@@ -634,7 +653,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 const int rl = 16 * b + (lane & 15);
                 const float sa = s_as[wm * WTM + i * 32 + rl];
 #pragma unroll
-                for (int j = 0; j < 2 * TN; ++j) {
+                for (int j = 0; j < TN16; ++j) {
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
@@ -758,7 +777,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                         const int rl = 16 * b + (lane & 15);
                         const float sa = s_as[wm * WTM + i * 32 + rl];
 #pragma unroll
-                        for (int j = 0; j < 2 * TN; ++j) {
+                        for (int j = 0; j < TN16; ++j) {
                             const int nl = wn * WTN + 16 * j + 4 * q16;
                             const v4f wv = *reinterpret_cast<const v4f*>(s_ws + nl);
                             const v4f bb = *reinterpret_cast<const v4f*>(s_bias + nl);
@@ -896,9 +915,9 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         const int vh = pr.hH, vS = pr.hS, voff = pr.hoff, vn = pr.hn, vb0 = pr.hb0;
         const int col = n0 + wn * WTN + lane;
         const bool cols_in = n0 + wn * WTN < N;
-        v4f wv[2 * TN], bv[2 * TN];
+        v4f wv[TN16], bv[TN16];
 #pragma unroll
-        for (int j = 0; j < 2 * TN; ++j) {
+        for (int j = 0; j < TN16; ++j) {
             const int nl = wn * WTN + 16 * j + 4 * q16;
             wv[j] = *reinterpret_cast<const v4f*>(s_ws + nl);
             bv[j] = *reinterpret_cast<const v4f*>(s_bias + nl);
@@ -910,7 +929,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 const int rl = 16 * b + (lane & 15);
                 const float sa = s_as[wm * WTM + i * 32 + rl];
 #pragma unroll
-                for (int j = 0; j < 2 * TN; ++j) {
+                for (int j = 0; j < TN16; ++j) {
                     uint16_t hv[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
@@ -1282,11 +1301,21 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
     }
 }
 
+// narrow: the 256x192 tiles (plain int8 launches only; P's tile counts
+// must have been computed for that width)
 template <int OP, int OUT_DT, bool GELU>
-hipError_t launch_tiled(const TileProblems& P, hipStream_t stream) {
+hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, bool narrow = false) {
     bool hd = false;
     for (int i = 0; i < P.n; ++i) hd = hd || P.p[i].hk > 0;
-    if (hd) {
+    if (narrow) {
+        if constexpr (OP == OP_I8_16) {
+            if (hd) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, NARROW_BN>), dim3(P.total), dim3(NTHR), 0,
+                               stream, P);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else if (hd) {
         if constexpr (OUT_DT == QIMG_FP32 && !GELU && OP != OP_BF16)
             hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, true>), dim3(P.total), dim3(NTHR), 0, stream, P);
         else
@@ -1307,18 +1336,21 @@ TileProblems problems(const TileProblem& p0, const TileProblem& p1) {
     return P;
 }
 
+// bn: the tile width the problem will be launched with (BN or NARROW_BN)
 TileProblem tile_problem(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
-                         const uint16_t* bias, void* out, const float* gate) {
+                         const uint16_t* bias, void* out, const float* gate, int bn = BN) {
     return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, gate, M, N, K,
-            ((M + BM - 1) / BM) * ((N + BN - 1) / BN), 0};
+            ((M + BM - 1) / BM) * ((N + bn - 1) / bn), 0};
 }
 
 template <bool FP8>
-hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream) {
+hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, bool narrow = false) {
     constexpr int OP = FP8 ? OP_F8 : OP_I8_16;
     if (out_dt == QIMG_FP32)
-        return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream) : launch_tiled<OP, QIMG_FP32, false>(P, stream);
-    return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream) : launch_tiled<OP, QIMG_BF16, false>(P, stream);
+        return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream, narrow)
+                    : launch_tiled<OP, QIMG_FP32, false>(P, stream, narrow);
+    return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream, narrow)
+                : launch_tiled<OP, QIMG_BF16, false>(P, stream, narrow);
 }
 
 }  // namespace
@@ -1352,7 +1384,48 @@ static int device_cu_count() {
     return n;
 }
 
+// The large-tile plan of an automatic choice (K % 128 == 0, not a small-M
+// case): rows [0, m_big) on the large tiles, the rest on the 64x64 kernel,
+// and whether int8 takes the 256x192 tiles.
+//  - One 256x256 tile per CU at a time. When the last round would be mostly
+//    idle, the trailing tile rows (at most two) go to the 64x64 kernel, which
+//    spreads them over every CU (M = 4352 = 4096 + 256 rows, N = 12288: 816
+//    tiles = 3 rounds + 48 tiles; the 48 become 192 small tiles).
+//  - int8 takes the 256x192 tiles when their rounds, each 3/4 of a 256x256
+//    round's work, add up to less (4096 x 3072: one full round of them
+//    against one round with a quarter of the CUs idle; 4096 x 12288: 4
+//    rounds against 3, kept on 256x256).
+struct LargePlan {
+    int m_big;
+    bool narrow;
+};
+static LargePlan large_plan(int M, int N, int K, bool fp8) {
+    LargePlan plan{M, false};
+    const int cus = device_cu_count();
+    if (cus <= 0) return plan;
+    const int tiles_n = (N + BN - 1) / BN;
+    const int tiles_m = (M + BM - 1) / BM;
+    const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
+    const int64_t rounds = (total + cus - 1) / cus;
+    const int64_t tail = total - (rounds - 1) * cus;
+    if (rounds > 1 && tail * 2 < cus) {
+        for (int r = 1; r <= 2 && r < tiles_m; ++r) {
+            if (static_cast<int64_t>(tiles_m - r) * tiles_n <= (rounds - 1) * cus) {
+                plan.m_big = (tiles_m - r) * BM;
+                break;
+            }
+        }
+    }
+    if (plan.m_big < M && !small_m_fits(M - plan.m_big, N, K)) plan.m_big = M;
+    if (!fp8 && plan.m_big == M) {
+        const int64_t t_narrow = static_cast<int64_t>(tiles_m) * ((N + NARROW_BN - 1) / NARROW_BN);
+        plan.narrow = 3 * ((t_narrow + cus - 1) / cus) < 4 * rounds;
+    }
+    return plan;
+}
+
 int set_linear_kernel(int which) { return g_linear_kernel.exchange(which); }
+
 int get_linear_kernel() { return g_linear_kernel.load(); }
 
 hipError_t launch_dequant_bias(const int32_t* acc, const float* as, const float* ws, const uint16_t* bias,
@@ -1395,33 +1468,16 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
         return e != hipSuccess || !gate ? e : gate_rest(0);
     }
     if ((K % BK) == 0) {
-        // Tile rounds: one 256x256 tile per CU at a time. When the last
-        // round would be mostly idle, the trailing tile rows (at most two)
-        // go to the 64x64 kernel instead, which spreads them over every CU
-        // (e.g. M = 4352 = 4096 + 256 rows, N = 12288: 816 tiles = 3 rounds
-        // + 48 tiles; the 48 become 192 small tiles).
-        int m_big = M;
-        if (choice == QIMG_LINEAR_AUTO) {
-            const int cus = device_cu_count();
-            const int tiles_n = (N + BN - 1) / BN;
-            const int tiles_m = (M + BM - 1) / BM;
-            const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
-            const int64_t rounds = (total + cus - 1) / cus;
-            const int64_t tail = total - (rounds - 1) * cus;
-            if (cus > 0 && rounds > 1 && tail * 2 < cus) {
-                for (int r = 1; r <= 2 && r < tiles_m; ++r) {
-                    if (static_cast<int64_t>(tiles_m - r) * tiles_n <= (rounds - 1) * cus) {
-                        m_big = (tiles_m - r) * BM;
-                        break;
-                    }
-                }
-            }
-            if (m_big < M && !small_m_fits(M - m_big, N, K)) m_big = M;
-        }
-        const TileProblems P =
-            problems(tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate), TileProblem{});
+        // (large_plan: the tail-row split and the tile width)
+        LargePlan plan{M, !fp8 && choice == QIMG_LINEAR_LARGE_NARROW};
+        if (choice == QIMG_LINEAR_AUTO) plan = large_plan(M, N, K, fp8);
+        const int m_big = plan.m_big;
+        const bool narrow = plan.narrow;
+        const TileProblems P = problems(
+            tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate, narrow ? NARROW_BN : BN),
+            TileProblem{});
         hipError_t e = fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
-                           : dispatch_tiled<false>(P, out_dtype, gelu, stream);
+                           : dispatch_tiled<false>(P, out_dtype, gelu, stream, narrow);
         if (e != hipSuccess || m_big == M) return e;
         const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
         void* rest = gate ? static_cast<void*>(tmp + static_cast<int64_t>(m_big) * N)

@@ -176,7 +176,9 @@ int get_linear_kernel();
 // gemm_small_m.hip: 0 = use the large-tile kernel, 1 = 32x32 tiles
 // (M <= 32), 2 = 64x64 tiles (fewer than kSmallMTileLimit large tiles),
 // 3 = vector-ALU GEMV (int8, M <= 4; e4m3 falls back to 1)
-constexpr int kSmallMTileLimit = 128;
+// (64: at 48 tiles of 256x256 or fewer the 64x64 tiles measured faster, at
+// 72 or more the large tiles, for int8 and e4m3, K = 3072 and 12288)
+constexpr int kSmallMTileLimit = 64;
 int small_m_variant(int M, int N, int K);
 // Two int8 linears of one M <= 4 activation (act_q, act_scales, K) as one
 // GEMV launch into a.out and b.out (a.act_q / b.act_q are not read). Returns

@@ -58,13 +58,18 @@ def cu_count():
     return torch.cuda.get_device_properties(0).multi_processor_count
 
 
+# the dispatcher's small-M threshold (kSmallMTileLimit): linears with fewer
+# 256x256 tiles than this run on the 64x64 tiles
+SMALL_M_TILE_LIMIT = 64
+
+
 def pair_in_one_launch(Ma, Na, Mb, Nb, cus):
     """Whether the dispatcher runs two linears (image and text stream) in one
-    launch of the 256x256-tile kernel: the first needs at least 128 tiles
-    (below that the small-tile kernel takes it), the second's tiles must fit
-    the first's last round, and the first must not be a case for the
-    tail-row split (a last round less than half full)."""
-    if min(Ma, Na, Mb, Nb) <= 0 or Ma <= 32 or large_tiles(Ma, Na) < 128:
+    launch of the 256x256-tile kernel: the first needs at least
+    SMALL_M_TILE_LIMIT tiles (below that the small-tile kernel takes it), the
+    second's tiles must fit the first's last round, and the first must not be
+    a case for the tail-row split (a last round less than half full)."""
+    if min(Ma, Na, Mb, Nb) <= 0 or Ma <= 32 or large_tiles(Ma, Na) < SMALL_M_TILE_LIMIT:
         return False
     ta, tb = large_tiles(Ma, Na), large_tiles(Mb, Nb)
     rounds = (ta + cus - 1) // cus

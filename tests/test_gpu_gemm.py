@@ -37,7 +37,7 @@ def _qw(qimg, q, s, hbs, mode=0):
     return qimg.QuantizedWeight(_dev(q), _dev(s), hbs, mode)
 
 
-KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4}
+KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4, "narrow": 5}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
@@ -202,11 +202,14 @@ def test_dequantize_and_bias_matches_oracle_and_fused(qimg, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(4100, 3076, 1024), (600, 518, 512), (777, 1000, 256), (513, 264, 3072)])
-def test_large_tile_epilogue_edges(qimg, oracle, M, N, K):
-    """The 256x256-tile kernel's int8 epilogue on ragged tiles: rows past M,
-    N % 4 = 2 (element stores), N % 8 = 4 (bf16 half-chunk stores), N % 8 = 0.
-    fp32 out bit-exact against the oracle's dequant of the int32 product, bf16
-    out its RNE rounding, GELU identical to the stand-alone epilogue kernel."""
+@pytest.mark.parametrize("kernel", ["large", "narrow"])
+def test_large_tile_epilogue_edges(qimg, oracle, M, N, K, kernel):
+    """The 256x256- and 256x192-tile kernels' int8 epilogue on ragged tiles:
+    rows past M, N % 4 = 2 (element stores), N % 8 = 4 (bf16 half-chunk
+    stores), N % 8 = 0, and (192 wide) last tiles of 4, 40, 72 and 134
+    columns. fp32 out bit-exact against the oracle's dequant of the int32
+    product, bf16 out its RNE rounding, GELU identical to the stand-alone
+    epilogue kernel."""
     rng = np.random.default_rng(M + 5 * N + K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
     w = rng.integers(-128, 128, (N, K), dtype=np.int8)
@@ -217,7 +220,7 @@ def test_large_tile_epilogue_edges(qimg, oracle, M, N, K):
     ref = oracle.dequant_epilogue(c, s, ws, b_bits)
     qw = _qw(qimg, w, ws, 1)
     ad, sd, bd = _dev(a), _dev(s), _bf16_dev(b_bits)
-    with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
+    with qimg.linear_kernel(KERNELS[kernel]):
         o32 = qimg.linear_forward_prequantized(ad, sd, qw, bd)
         o16 = qimg.linear_forward_prequantized(ad, sd, qw, bd, out_dtype=torch.bfloat16)
         og = qimg.linear_forward_prequantized(ad, sd, qw, bd, apply_gelu=True)
