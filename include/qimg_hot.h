@@ -112,20 +112,22 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * algorithm); it exists for tests and tuning, which compare the kernels on
  * one shape. AUTO (the default) takes the vector-ALU GEMV for int8 with
  * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
- * 256x256 would cover the output, and 256x256 tiles otherwise; int8 takes
- * 256x192 tiles instead when they need fewer rounds of tiles on the device's
- * CUs (counting a round of them as 3/4 of a 256x256 round; 4096 x 3072 is one
- * full round of them). LARGE_NARROW forces the 256x192 tiles (int8; e4m3
- * runs 256x256). GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide;
- * returns QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices
- * give identical int8 results. */
+ * 256x256 would cover the output, and 256-row tiles otherwise: int8 takes
+ * the width of 256, 224 or 192 columns whose rounds of tiles on the device's
+ * CUs, each weighted by the width, add up to least (4096 x 3072: one full
+ * round of 256x192; 4352 x 3072: one round of 256x224), e4m3 256.
+ * LARGE_192 and LARGE_224 force those widths (int8; e4m3 runs 256x256).
+ * GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide; returns
+ * QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices give
+ * identical int8 results. */
 enum {
     QIMG_LINEAR_AUTO = 0,
     QIMG_LINEAR_LARGE_TILE = 1,
     QIMG_LINEAR_SMALL_32 = 2,
     QIMG_LINEAR_SMALL_64 = 3,
     QIMG_LINEAR_GEMV = 4,
-    QIMG_LINEAR_LARGE_NARROW = 5
+    QIMG_LINEAR_LARGE_192 = 5,
+    QIMG_LINEAR_LARGE_224 = 6
 };
 int qimg_set_linear_kernel(int which);
 int qimg_get_linear_kernel(void);

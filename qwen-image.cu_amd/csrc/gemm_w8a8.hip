@@ -16,8 +16,9 @@
 // SIMD let one wave's LDS reads and waits overlap the other's MFMAs
 // (measured 7-9% faster than four waves of 128x128). Both operands are
 // K-major [rows, K] as the reference stores them (TN GEMM). Plain int8
-// launches can also run 256x192 tiles (waves of 128x48), chosen where they
-// take fewer rounds of the CUs (4096 x 3072: 256 tiles, one full round).
+// launches can also run 256x224 (waves 4 x 2 of 64x112) or 256x192 (waves of
+// 128x48) tiles, chosen where they take fewer rounds of the CUs (4352 x
+// 3072: 238 tiles of 256x224 in one round; 4096 x 3072: 256 of 256x192).
 //
 // K advances 128 bytes per stage through a two-slot LDS ring (2 x 64 KB):
 // while one stage is consumed the next is in flight. Stages are filled by
@@ -83,6 +84,7 @@ constexpr int SCALE_OFF = LDS_BYTES - 4 * 256 * 4;  // as, ws, bias, gate
 static_assert(NWAVES * 32 * (BN / WAVES_N * 4 + 16) <= SCALE_OFF, "output staging overlaps the scales");
 static_assert(2 * NDMA == TM * TN, "the int8 loop issues one refill DMA per MFMA of a k-step");
 constexpr int GROUP_M = 4;  // tile rows per group in the tile order
+constexpr int div_up_c(int a, int b) { return (a + b - 1) / b; }
 // Cache policy of the operand DMA: sc0 (measured ~10% faster than the
 // default policy at the MMDiT shapes; the non-temporal policy is slower).
 constexpr int kDmaPolicy = 1;
@@ -188,25 +190,36 @@ struct TileProblems {
 // HD: the launch may hold problems with attention-layout outputs
 // (TileProblem::hk; an instance of its own, so that the extra epilogues
 // leave the others' register allocation alone).
-// TW: the tile's width, 256 or 192 (NARROW_BN). The 256x192 tiles serve
-// plain int8 launches whose 256x256 tiles would leave CUs idle: 4096 x 3072
-// is 192 tiles of 256x256 on 256 CUs, a quarter of the chip idle for the
-// whole launch, but 256 tiles of 256x192, one round with every CU busy.
-// Each wave then owns 128 x 48 = 8 x 3 blocks of 16x16, and a stage's W
-// share is 192 rows (3 DMA instructions per wave).
+// TW: the tile's width, 256, 224 (MID_BN) or 192 (NARROW_BN). The narrower
+// tiles serve plain int8 launches whose 256x256 tiles would leave CUs idle:
+// 4096 x 3072 is 192 tiles of 256x256 on 256 CUs, a quarter of the chip
+// idle for the whole launch, but 256 tiles of 256x192, one round with every
+// CU busy; 4352 x 3072 is 204 tiles of 256x256 but 238 of 256x224.
+//  - 256x192: waves of 128 x 48 = 8 x 3 blocks of 16x16; a stage's W share
+//    is 192 rows, 3 DMA instructions per wave.
+//  - 256x224: 224 columns are not four waves of whole 16x16 blocks, so the
+//    waves are arranged 4 x 2, each 64 x 112 = 4 x 7 blocks; the W DMA still
+//    fills 256 rows (4 instructions per wave, the last 32 rows unread), so
+//    every wave runs the same instruction stream.
 constexpr int NARROW_BN = 192;
+constexpr int MID_BN = 224;
 template <int OP, int OUT_DT, bool GELU, bool HD = false, int TW = BN>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr bool BF = OP == OP_BF16;
     constexpr bool M16 = OP == OP_I8_16;
-    static_assert(TW == BN || (TW == NARROW_BN && M16 && !HD),
-                  "the narrow tile serves the plain int8 epilogue on 16x16 blocks");
+    static_assert(TW == BN || ((TW == NARROW_BN || TW == MID_BN) && M16 && !HD),
+                  "the narrower tiles serve the plain int8 epilogue on 16x16 blocks");
     // (these hide the file-scope 256-wide values inside the kernel)
-    constexpr int BN = TW;                       // tile width
-    constexpr int WTN = BN / WAVES_N;            // wave tile width (64 or 48)
-    constexpr int TN = WTN / 32;                 // 32x32 blocks across a wave (256 wide only)
-    constexpr int TN16 = WTN / 16;               // 16x16 blocks across a wave
-    constexpr int NDMA_W = BN / (NWAVES * DMA_ROWS);  // W DMA instructions per wave per stage
+    constexpr int WVN = TW == MID_BN ? 2 : WAVES_N;  // waves across N
+    constexpr int BN = TW;                           // tile width
+    constexpr int WTM = BM / (NWAVES / WVN);         // wave tile: 128 or 64 rows
+    constexpr int TM = WTM / 32;                     // 32-row blocks of a wave
+    constexpr int WTN = BN / WVN;                    // wave tile width (64, 112 or 48)
+    constexpr int TN = WTN / 32;                     // 32x32 blocks across a wave (256 wide only)
+    constexpr int TN16 = WTN / 16;                   // 16x16 blocks across a wave
+    constexpr int NDMA_W = div_up_c(BN, NWAVES * DMA_ROWS);  // W DMA instructions per wave per stage
+    static_assert(WTN % 16 == 0 && NDMA_W * NWAVES * DMA_ROWS * BK <= OP_BYTES, "wave tile or W slot");
+    static_assert(NWAVES * 32 * (WTN * 4 + 16) <= SCALE_OFF, "output staging overlaps the scales");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
     float* s_ws = s_as + 256;
@@ -250,8 +263,8 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WAVES_N;
-    const int wn = wave % WAVES_N;
+    const int wm = wave / WVN;
+    const int wn = wave % WVN;
     const bool has_bias = bias != nullptr;
     const bool has_gate = gate != nullptr;
 
@@ -620,12 +633,19 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         const bool gated = OUT_DT == QIMG_FP32 && has_gate;
         const bool vec = (N % EPC) == 0;
         const bool fast = interior && vec;  // (bf16 chunks need N % 8 == 0)
-        v4f wv[TN16], bv[TN16];
+        // The weight scales and bias of the lane's columns stay in registers
+        // for up to 4 blocks across; wider waves (7 blocks: 112 registers
+        // with the residual prefetch beside 112 accumulators) read them from
+        // LDS at each use instead.
+        constexpr bool WREG = TN16 <= 4;
+        v4f wv[WREG ? TN16 : 1], bv[WREG ? TN16 : 1];
+        if constexpr (WREG) {
 #pragma unroll
-        for (int j = 0; j < TN16; ++j) {
-            const int nl = wn * WTN + 16 * j + 4 * q16;
-            wv[j] = *reinterpret_cast<const v4f*>(s_ws + nl);
-            bv[j] = *reinterpret_cast<const v4f*>(s_bias + nl);
+            for (int j = 0; j < TN16; ++j) {
+                const int nl = wn * WTN + 16 * j + 4 * q16;
+                wv[j] = *reinterpret_cast<const v4f*>(s_ws + nl);
+                bv[j] = *reinterpret_cast<const v4f*>(s_bias + nl);
+            }
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -654,6 +674,9 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 const float sa = s_as[wm * WTM + i * 32 + rl];
 #pragma unroll
                 for (int j = 0; j < TN16; ++j) {
+                    const int nl = wn * WTN + 16 * j + 4 * q16;
+                    const v4f wj = WREG ? wv[j] : *reinterpret_cast<const v4f*>(s_ws + nl);
+                    const v4f bj = WREG ? bv[j] : *reinterpret_cast<const v4f*>(s_bias + nl);
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
@@ -661,8 +684,8 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                         float t;
                         {
 #pragma clang fp contract(off)
-                            t = static_cast<float>(e) * sa * wv[j][c];
-                            t = t + bv[j][c];
+                            t = static_cast<float>(e) * sa * wj[c];
+                            t = t + bj[c];
                         }
                         if (GELU) t = gelu_tanh_fast(t);
                         v[c] = t;
@@ -1301,17 +1324,23 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
     }
 }
 
-// narrow: the 256x192 tiles (plain int8 launches only; P's tile counts
-// must have been computed for that width)
+// tw: the tile width, BN, MID_BN or NARROW_BN (the last two for plain int8
+// launches only; P's tile counts must have been computed for that width)
 template <int OP, int OUT_DT, bool GELU>
-hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, bool narrow = false) {
+hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, int tw = BN) {
     bool hd = false;
     for (int i = 0; i < P.n; ++i) hd = hd || P.p[i].hk > 0;
-    if (narrow) {
+    if (tw != BN) {
         if constexpr (OP == OP_I8_16) {
             if (hd) return hipErrorInvalidValue;
-            hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, NARROW_BN>), dim3(P.total), dim3(NTHR), 0,
-                               stream, P);
+            if (tw == NARROW_BN)
+                hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, NARROW_BN>), dim3(P.total), dim3(NTHR),
+                                   0, stream, P);
+            else if (tw == MID_BN)
+                hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, MID_BN>), dim3(P.total), dim3(NTHR), 0,
+                                   stream, P);
+            else
+                return hipErrorInvalidValue;
         } else {
             return hipErrorInvalidValue;
         }
@@ -1336,7 +1365,7 @@ TileProblems problems(const TileProblem& p0, const TileProblem& p1) {
     return P;
 }
 
-// bn: the tile width the problem will be launched with (BN or NARROW_BN)
+// bn: the tile width the problem will be launched with (BN, MID_BN or NARROW_BN)
 TileProblem tile_problem(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
                          const uint16_t* bias, void* out, const float* gate, int bn = BN) {
     return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, gate, M, N, K,
@@ -1344,13 +1373,13 @@ TileProblem tile_problem(const void* a, const float* as, int M, int K, const voi
 }
 
 template <bool FP8>
-hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, bool narrow = false) {
+hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, int tw = BN) {
     constexpr int OP = FP8 ? OP_F8 : OP_I8_16;
     if (out_dt == QIMG_FP32)
-        return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream, narrow)
-                    : launch_tiled<OP, QIMG_FP32, false>(P, stream, narrow);
-    return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream, narrow)
-                : launch_tiled<OP, QIMG_BF16, false>(P, stream, narrow);
+        return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream, tw)
+                    : launch_tiled<OP, QIMG_FP32, false>(P, stream, tw);
+    return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream, tw)
+                : launch_tiled<OP, QIMG_BF16, false>(P, stream, tw);
 }
 
 }  // namespace
@@ -1384,23 +1413,51 @@ static int device_cu_count() {
     return n;
 }
 
+// Tiles of width w that cover M x N (256 rows each).
+static int64_t tiles_of(int M, int N, int w) {
+    return static_cast<int64_t>((M + BM - 1) / BM) * ((N + w - 1) / w);
+}
+
+// The cost of running `tiles` tiles of width w, in 256x256-tile-widths of
+// the slowest CU: its rounds of the CUs, each weighted by the tile's share
+// of a 256x256 tile's work.
+static int64_t tile_cost(int64_t tiles, int w, int cus) { return (tiles + cus - 1) / cus * w; }
+
+// The int8 tile width with the least tile_cost for `tiles_w(w)` tiles (the
+// widest of equals).
+template <class F>
+static int best_width(F tiles_w, int cus) {
+    int tw = BN;
+    int64_t best = tile_cost(tiles_w(BN), BN, cus);
+    for (const int w : {MID_BN, NARROW_BN}) {
+        const int64_t c = tile_cost(tiles_w(w), w, cus);
+        if (c < best) {
+            best = c;
+            tw = w;
+        }
+    }
+    return tw;
+}
+
 // The large-tile plan of an automatic choice (K % 128 == 0, not a small-M
 // case): rows [0, m_big) on the large tiles, the rest on the 64x64 kernel,
-// and whether int8 takes the 256x192 tiles.
-//  - One 256x256 tile per CU at a time. When the last round would be mostly
-//    idle, the trailing tile rows (at most two) go to the 64x64 kernel, which
-//    spreads them over every CU (M = 4352 = 4096 + 256 rows, N = 12288: 816
-//    tiles = 3 rounds + 48 tiles; the 48 become 192 small tiles).
-//  - int8 takes the 256x192 tiles when their rounds, each 3/4 of a 256x256
-//    round's work, add up to less (4096 x 3072: one full round of them
-//    against one round with a quarter of the CUs idle; 4096 x 12288: 4
-//    rounds against 3, kept on 256x256).
+// and the tile width.
+//  - One tile per CU at a time. When the last round of 256x256 tiles would
+//    be mostly idle, the trailing tile rows (at most two) go to the 64x64
+//    kernel, which spreads them over every CU (M = 4352 = 4096 + 256 rows,
+//    N = 12288: 816 tiles = 3 rounds + 48 tiles; the 48 become 192 small
+//    tiles).
+//  - Otherwise int8 takes the width whose rounds, each weighted by the
+//    tile's width, add up to least (best_width): 4096 x 3072 runs 256 tiles
+//    of 256x192 in one round (192 tiles of 256x256 leave a quarter of the
+//    CUs idle), 4352 x 3072 238 tiles of 256x224 (204 of 256x256, 272 of
+//    256x192), 4096 x 12288 stays on 256x256 (3 rounds; 4 of 256x192).
 struct LargePlan {
     int m_big;
-    bool narrow;
+    int tw;
 };
 static LargePlan large_plan(int M, int N, int K, bool fp8) {
-    LargePlan plan{M, false};
+    LargePlan plan{M, BN};
     const int cus = device_cu_count();
     if (cus <= 0) return plan;
     const int tiles_n = (N + BN - 1) / BN;
@@ -1417,10 +1474,7 @@ static LargePlan large_plan(int M, int N, int K, bool fp8) {
         }
     }
     if (plan.m_big < M && !small_m_fits(M - plan.m_big, N, K)) plan.m_big = M;
-    if (!fp8 && plan.m_big == M) {
-        const int64_t t_narrow = static_cast<int64_t>(tiles_m) * ((N + NARROW_BN - 1) / NARROW_BN);
-        plan.narrow = 3 * ((t_narrow + cus - 1) / cus) < 4 * rounds;
-    }
+    if (!fp8 && plan.m_big == M) plan.tw = best_width([&](int w) { return tiles_of(M, N, w); }, cus);
     return plan;
 }
 
@@ -1469,15 +1523,16 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
     }
     if ((K % BK) == 0) {
         // (large_plan: the tail-row split and the tile width)
-        LargePlan plan{M, !fp8 && choice == QIMG_LINEAR_LARGE_NARROW};
+        LargePlan plan{M, fp8                                  ? BN
+                          : choice == QIMG_LINEAR_LARGE_192 ? NARROW_BN
+                          : choice == QIMG_LINEAR_LARGE_224 ? MID_BN
+                                                            : BN};
         if (choice == QIMG_LINEAR_AUTO) plan = large_plan(M, N, K, fp8);
         const int m_big = plan.m_big;
-        const bool narrow = plan.narrow;
         const TileProblems P = problems(
-            tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate, narrow ? NARROW_BN : BN),
-            TileProblem{});
+            tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate, plan.tw), TileProblem{});
         hipError_t e = fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
-                           : dispatch_tiled<false>(P, out_dtype, gelu, stream, narrow);
+                           : dispatch_tiled<false>(P, out_dtype, gelu, stream, plan.tw);
         if (e != hipSuccess || m_big == M) return e;
         const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
         void* rest = gate ? static_cast<void*>(tmp + static_cast<int64_t>(m_big) * N)
@@ -1513,25 +1568,32 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
     bool pair = a.M > 0 && a.N > 0 && b.M > 0 && b.N > 0 &&
                 g_linear_kernel.load(std::memory_order_relaxed) == QIMG_LINEAR_AUTO && (a.K % BK) == 0 &&
                 (b.K % BK) == 0 && small_m_variant(a.M, a.N, a.K) == 0;
+    int tw = BN;
     if (pair) {
         const int cus = device_cu_count();
-        const int64_t ta = static_cast<int64_t>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-        const int64_t tb = static_cast<int64_t>((b.M + BM - 1) / BM) * ((b.N + BN - 1) / BN);
+        const int64_t ta = tiles_of(a.M, a.N, BN);
+        const int64_t tb = tiles_of(b.M, b.N, BN);
         const int64_t rounds = cus > 0 ? (ta + cus - 1) / cus : 0;
         const int64_t tail = ta - (rounds - 1) * cus;
         // no extra round, and not a case for the tail-row split of a lone launch
         pair = cus > 0 && ta + tb <= rounds * cus && !(rounds > 1 && tail * 2 < cus);
+        // int8: the tile width for both (4096 + 256 rows of N = 3072: 238
+        // tiles of 256x224 in one round, against 204 of 256x256)
+        if (pair && mode != QIMG_QM_FP8_HADAMARD)
+            tw = best_width([&](int w) { return tiles_of(a.M, a.N, w) + tiles_of(b.M, b.N, w); }, cus);
     }
     if (!pair) {
         hipError_t e = a.M > 0 ? single(a) : hipSuccess;
         return e != hipSuccess || b.M == 0 ? e : single(b);
     }
     if ((a.gate || b.gate) && out_dtype != QIMG_FP32) return hipErrorInvalidValue;
-    const TileProblem p0 = tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate);
-    const TileProblem p1 = tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out, b.gate);
+    const TileProblem p0 =
+        tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate, tw);
+    const TileProblem p1 =
+        tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out, b.gate, tw);
     const TileProblems P = problems(p0, p1);
     return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
-                                        : dispatch_tiled<false>(P, out_dtype, gelu, stream);
+                                        : dispatch_tiled<false>(P, out_dtype, gelu, stream, tw);
 }
 
 // Up to kMaxProblems linears of one mode, output type and epilogue in one

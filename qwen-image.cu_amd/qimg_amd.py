@@ -21,7 +21,8 @@ LIB_PATH = os.path.join(_HERE, "lib", "libqimg_hot.so")
 QIMG_OK, QIMG_ERR_INVALID_ARG, QIMG_ERR_UNSUPPORTED, QIMG_ERR_SCRATCH, QIMG_ERR_HIP = range(5)
 FP32, BF16, FP16, INT8, INT32, FP8_E4M3 = range(6)
 INT8_HADAMARD, FP8_HADAMARD = 0, 1
-LINEAR_AUTO, LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64, LINEAR_GEMV, LINEAR_LARGE_NARROW = range(6)
+(LINEAR_AUTO, LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64, LINEAR_GEMV, LINEAR_LARGE_192,
+ LINEAR_LARGE_224) = range(7)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -288,7 +289,7 @@ def linear_forward_prequantized(act_q: torch.Tensor, act_scales: torch.Tensor, w
 def set_linear_kernel(which: int) -> int:
     """Select the quantized-linear kernel process-wide (LINEAR_AUTO,
     LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64, LINEAR_GEMV,
-    LINEAR_LARGE_NARROW); returns the previous choice. Every choice gives the
+    LINEAR_LARGE_192, LINEAR_LARGE_224); returns the previous choice. Every choice gives the
     same int8 results."""
     prev = int(_lib.qimg_get_linear_kernel())
     _check(_lib.qimg_set_linear_kernel(int(which)))

@@ -37,7 +37,7 @@ def _qw(qimg, q, s, hbs, mode=0):
     return qimg.QuantizedWeight(_dev(q), _dev(s), hbs, mode)
 
 
-KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4, "narrow": 5}
+KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4, "w192": 5, "w224": 6}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
@@ -202,12 +202,12 @@ def test_dequantize_and_bias_matches_oracle_and_fused(qimg, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(4100, 3076, 1024), (600, 518, 512), (777, 1000, 256), (513, 264, 3072)])
-@pytest.mark.parametrize("kernel", ["large", "narrow"])
+@pytest.mark.parametrize("kernel", ["large", "w192", "w224"])
 def test_large_tile_epilogue_edges(qimg, oracle, M, N, K, kernel):
-    """The 256x256- and 256x192-tile kernels' int8 epilogue on ragged tiles:
-    rows past M, N % 4 = 2 (element stores), N % 8 = 4 (bf16 half-chunk
-    stores), N % 8 = 0, and (192 wide) last tiles of 4, 40, 72 and 134
-    columns. fp32 out bit-exact against the oracle's dequant of the int32
+    """The 256-row tiles' int8 epilogue (256, 224 and 192 columns) on ragged
+    tiles: rows past M, N % 4 = 2 (element stores), N % 8 = 4 (bf16
+    half-chunk stores), N % 8 = 0, and last tiles of 4, 40, 72 and 134
+    columns (192 wide) or 164, 70, 104 and 40 (224 wide). fp32 out bit-exact against the oracle's dequant of the int32
     product, bf16 out its RNE rounding, GELU identical to the stand-alone
     epilogue kernel."""
     rng = np.random.default_rng(M + 5 * N + K)
