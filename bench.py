@@ -1113,7 +1113,7 @@ def _summarize(d, outdir):
          ("fc1 rows 0-4095 of 4352 i8", "qimg::gemm_w8a8_kernel<3, 0, true, false, 256>", 768, 4096, 12288, 3072, 4, "I8"),
          ("fc1 rows 4096-4351 i8", "qimg::gemm_small_dma_kernel<false, 2, 2, 2, 0, true, 64>", 768, 256, 12288, 3072,
           4, "I8"),
-         ("fc2 4352x3072x12288 i8 bf16", "qimg::gemm_w8a8_kernel<3, 1, false, false, 256>", 204, 4352, 3072, 12288, 2,
+         ("fc2 4352x3072x12288 i8 bf16", "qimg::gemm_w8a8_kernel<3, 1, false, false, 224>", 238, 4352, 3072, 12288, 2,
           "I8"),
          ("C5 fc1 rows 0-13567 e4m3", "qimg::gemm_w8a8_kernel<1, 0, true, false, 256>", 2544, 13568, 12288, 3072, 4, "F8"),
          ("C5 fc1 rows 13568-13777 e4m3", "qimg::gemm_small_dma_kernel<true, 2, 2, 2, 0, true, 64>", 768, 210, 12288,
@@ -1230,7 +1230,7 @@ def _summarize(d, outdir):
                           256 * D_ + H_ * D_ + 256 * H_ * 4 + 4 * (256 + H_) + 2 * H_),
         "quant_fc2_in": ("qimg::fwht_quant_blocks_kernel<float, (qimg::RowOut)0, 3, false>", M_,
                          M_ * H_ * 4 + M_ * H_ + 4 * M_),
-        "gemm_fc2": ("qimg::gemm_w8a8_kernel<3, 1, false, false, 256>", 204,
+        "gemm_fc2": ("qimg::gemm_w8a8_kernel<3, 1, false, false, 224>", 238,
                      M_ * H_ + D_ * H_ + M_ * D_ * 2 + 4 * (M_ + D_) + 2 * D_),
     }
     fd = _dispatches(os.path.join(d, "mlp_FETCH_SIZE"))
