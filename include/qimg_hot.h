@@ -113,10 +113,11 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * one shape. AUTO (the default) takes the vector-ALU GEMV for int8 with
  * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
  * 256x256 would cover the output, and 256-row tiles otherwise: int8 takes
- * the width of 256, 224 or 192 columns whose rounds of tiles on the device's
- * CUs, each weighted by the width, add up to least (4096 x 3072: one full
- * round of 256x192; 4352 x 3072: one round of 256x224), e4m3 256.
- * LARGE_192 and LARGE_224 force those widths (int8; e4m3 runs 256x256).
+ * the width of 256, 224 or 192 columns (e4m3: 256 or 192) whose rounds of
+ * tiles on the device's CUs, each weighted by the width, add up to least
+ * (4096 x 3072: one full round of 256x192; int8 4352 x 3072: one round of
+ * 256x224). LARGE_192 and LARGE_224 force those widths (e4m3 runs 224 as
+ * 256).
  * GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide; returns
  * QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices give
  * identical int8 results. */

@@ -201,16 +201,17 @@ struct TileProblems {
 //    waves are arranged 4 x 2, each 64 x 112 = 4 x 7 blocks; the W DMA still
 //    fills 256 rows (4 instructions per wave, the last 32 rows unread), so
 //    every wave runs the same instruction stream.
+//  - e4m3 256x192 (32x32 blocks): waves 4 x 2 of 64 x 96 = 2 x 3 blocks.
 constexpr int NARROW_BN = 192;
 constexpr int MID_BN = 224;
 template <int OP, int OUT_DT, bool GELU, bool HD = false, int TW = BN>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr bool BF = OP == OP_BF16;
     constexpr bool M16 = OP == OP_I8_16;
-    static_assert(TW == BN || ((TW == NARROW_BN || TW == MID_BN) && M16 && !HD),
-                  "the narrower tiles serve the plain int8 epilogue on 16x16 blocks");
+    static_assert(TW == BN || (!HD && (((TW == NARROW_BN || TW == MID_BN) && M16) || (TW == NARROW_BN && OP == OP_F8))),
+                  "the narrower tiles serve the plain int8 (16x16 blocks) and e4m3 epilogues");
     // (these hide the file-scope 256-wide values inside the kernel)
-    constexpr int WVN = TW == MID_BN ? 2 : WAVES_N;  // waves across N
+    constexpr int WVN = (TW == MID_BN || (TW == NARROW_BN && !M16)) ? 2 : WAVES_N;  // waves across N
     constexpr int BN = TW;                           // tile width
     constexpr int WTM = BM / (NWAVES / WVN);         // wave tile: 128 or 64 rows
     constexpr int TM = WTM / 32;                     // 32-row blocks of a wave
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr int TN = WTN / 32;                     // 32x32 blocks across a wave (256 wide only)
     constexpr int TN16 = WTN / 16;                   // 16x16 blocks across a wave
     constexpr int NDMA_W = div_up_c(BN, NWAVES * DMA_ROWS);  // W DMA instructions per wave per stage
-    static_assert(WTN % 16 == 0 && NDMA_W * NWAVES * DMA_ROWS * BK <= OP_BYTES, "wave tile or W slot");
+    static_assert(WTN % (M16 ? 16 : 32) == 0 && NDMA_W * NWAVES * DMA_ROWS * BK <= OP_BYTES, "wave tile or W slot");
     static_assert(NWAVES * 32 * (WTN * 4 + 16) <= SCALE_OFF, "output staging overlaps the scales");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     float* s_as = reinterpret_cast<float*>(lds + SCALE_OFF);
@@ -249,6 +250,10 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
 
     const int tiles_n = (N + BN - 1) / BN;
     const int tiles_m = (M + BM - 1) / BM;
+    // A problem whose tile count was computed for another width than this
+    // kernel's would index tiles past its output (and divide by a group
+    // height of zero below): its workgroups do nothing instead.
+    if (pr.tiles != tiles_m * tiles_n) return;
     // Grouped tile order: groups of GROUP_M tile rows, column-major inside a
     // group, so the 32 tiles an XCD runs at once form a 4 x 8 block that
     // shares 4 activation slices and 8 weight slices in that XCD's L2.
@@ -511,18 +516,22 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             read_frags(fa0, fw0, slot ^ 1, 0);
             mfma_all(fa1, fw1);
             // the refill DMAs spread over the first MFMAs (measured 2-5%
-            // faster than issuing them all before the first MFMA)
+            // faster than issuing them all before the first MFMA): each
+            // MFMA of the k-step is followed by its share of the stage's
+            // DMAs and, while they last, one fragment's two reads
             if constexpr (decltype(refill)::value) {
+                constexpr int NM = TM * TN, NV = NDMA + NDMA_W;
+                constexpr int VQ = NV / NM, VR = NV % NM;  // DMAs per MFMA, and the first VR MFMAs' extra one
 #pragma unroll
-                for (int i = 0; i < TM + TN; ++i) {
+                for (int i = 0; i < NM; ++i) {
                     SGB(SG_MFMA, 1);
-                    SGB(SG_VMEM, 1);
-                    SGB(SG_DS_READ, 2);
+                    if (i < VR) {
+                        SGB(SG_VMEM, VQ + 1);
+                    } else if constexpr (VQ > 0) {
+                        SGB(SG_VMEM, VQ);
+                    }
+                    if (i < TM + TN) SGB(SG_DS_READ, 2);
                 }
-                SGB(SG_MFMA, 1);
-                SGB(SG_VMEM, 1);
-                SGB(SG_MFMA, 1);
-                SGB(SG_VMEM, 1);
                 __builtin_amdgcn_sched_barrier(0);
             } else {
                 interleave();
@@ -1010,16 +1019,23 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
         const bool vec_n = (N & 3) == 0;
         const bool vt = HD && OUT_DT == QIMG_FP32 && !BF && pr.hk == HEADS_V;
         if (interior && (vt || ((OUT_DT == QIMG_FP32 || !has_gate) && !accumulate))) {  // (no gate with bf16 outputs)
-            float wsv[TN][16], bv[TN][16];
+            // The lane's weight scales and bias stay in registers for up to
+            // two blocks across; wider waves (3 blocks: 96 registers beside
+            // 96 accumulators and the residual prefetch) read each run of 4
+            // from LDS at its use instead.
+            constexpr bool WREG = TN <= 2;
+            float wsv[WREG ? TN : 1][16], bv[WREG ? TN : 1][16];
+            if constexpr (WREG) {
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int nl = wn * WTN + j * 32 + 4 * half + 8 * (q >> 2) + (q & 3);
-                    wsv[j][q] = s_ws[nl];
-                    bv[j][q] = s_bias[nl];
-                }
-            if (vt) {
+                    for (int q = 0; q < 16; ++q) {
+                        const int nl = wn * WTN + j * 32 + 4 * half + 8 * (q >> 2) + (q & 3);
+                        wsv[j][q] = s_ws[nl];
+                        bv[j][q] = s_bias[nl];
+                    }
+            }
+            if constexpr (HD) if (vt) {  // (HD instances are 256 wide: WREG)
                 // V^T output: each wave stages a 32-row block as fp16 [row][column]
                 // in a private LDS buffer, then lane l reads column l (one head dim)
                 // down the 32 rows. When the rows are 32 consecutive keys of one
@@ -1118,18 +1134,23 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
                 for (int j = 0; j < TN; ++j) {
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
+                        const int nl = wn * WTN + j * 32 + 4 * half + 8 * g;
+                        const v4f wg = WREG ? (v4f){wsv[j][4 * g], wsv[j][4 * g + 1], wsv[j][4 * g + 2], wsv[j][4 * g + 3]}
+                                            : *reinterpret_cast<const v4f*>(s_ws + nl);
+                        const v4f bg = WREG ? (v4f){bv[j][4 * g], bv[j][4 * g + 1], bv[j][4 * g + 2], bv[j][4 * g + 3]}
+                                            : *reinterpret_cast<const v4f*>(s_bias + nl);
                         float v[4];
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
                             float t;
                             if constexpr (BF) {
-                                t = acc[i][j][4 * g + c] + bv[j][4 * g + c];
+                                t = acc[i][j][4 * g + c] + bg[c];
                                 if (GELU) t = gelu_tanh(t);
                             } else {
                                 {
 #pragma clang fp contract(off)
-                                    t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wsv[j][4 * g + c];
-                                    t = t + bv[j][4 * g + c];
+                                    t = static_cast<float>(acc[i][j][4 * g + c]) * sa * wg[c];
+                                    t = t + bg[c];
                                 }
                                 if (GELU) t = gelu_tanh_fast(t);
                             }
@@ -1329,21 +1350,32 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
 template <int OP, int OUT_DT, bool GELU>
 hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, int tw = BN) {
     bool hd = false;
-    for (int i = 0; i < P.n; ++i) hd = hd || P.p[i].hk > 0;
+    int64_t total = 0;
+    for (int i = 0; i < P.n; ++i) {
+        const TileProblem& p = P.p[i];
+        hd = hd || p.hk > 0;
+        // every problem's tiles counted for the width launched
+        if (tw <= 0 || p.tiles != ((p.M + BM - 1) / BM) * ((p.N + tw - 1) / tw)) return hipErrorInvalidValue;
+        total += p.tiles;
+    }
+    if (total != P.total) return hipErrorInvalidValue;
     if (tw != BN) {
-        if constexpr (OP == OP_I8_16) {
-            if (hd) return hipErrorInvalidValue;
-            if (tw == NARROW_BN)
+        if (hd) return hipErrorInvalidValue;
+        if constexpr (OP == OP_I8_16 || OP == OP_F8) {
+            if (tw == NARROW_BN) {
                 hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, NARROW_BN>), dim3(P.total), dim3(NTHR),
                                    0, stream, P);
-            else if (tw == MID_BN)
+                return hipGetLastError();
+            }
+        }
+        if constexpr (OP == OP_I8_16) {
+            if (tw == MID_BN) {
                 hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, MID_BN>), dim3(P.total), dim3(NTHR), 0,
                                    stream, P);
-            else
-                return hipErrorInvalidValue;
-        } else {
-            return hipErrorInvalidValue;
+                return hipGetLastError();
+            }
         }
+        return hipErrorInvalidValue;
     } else if (hd) {
         if constexpr (OUT_DT == QIMG_FP32 && !GELU && OP != OP_BF16)
             hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, true>), dim3(P.total), dim3(NTHR), 0, stream, P);
@@ -1372,8 +1404,9 @@ TileProblem tile_problem(const void* a, const float* as, int M, int K, const voi
             ((M + BM - 1) / BM) * ((N + bn - 1) / bn), 0};
 }
 
+// tw must be the width P's tile counts were computed for (tile_problem's bn).
 template <bool FP8>
-hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, int tw = BN) {
+hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, int tw) {
     constexpr int OP = FP8 ? OP_F8 : OP_I8_16;
     if (out_dt == QIMG_FP32)
         return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream, tw)
@@ -1423,13 +1456,15 @@ static int64_t tiles_of(int M, int N, int w) {
 // of a 256x256 tile's work.
 static int64_t tile_cost(int64_t tiles, int w, int cus) { return (tiles + cus - 1) / cus * w; }
 
-// The int8 tile width with the least tile_cost for `tiles_w(w)` tiles (the
-// widest of equals).
+// The tile width with the least tile_cost for `tiles_w(w)` tiles (the
+// widest of equals): 256, 224 or 192 for int8, 256 or 192 for e4m3 (whose
+// 32x32 blocks do not divide a 224-wide tile's waves).
 template <class F>
-static int best_width(F tiles_w, int cus) {
+static int best_width(F tiles_w, int cus, bool fp8) {
     int tw = BN;
     int64_t best = tile_cost(tiles_w(BN), BN, cus);
     for (const int w : {MID_BN, NARROW_BN}) {
+        if (fp8 && w == MID_BN) continue;
         const int64_t c = tile_cost(tiles_w(w), w, cus);
         if (c < best) {
             best = c;
@@ -1447,11 +1482,12 @@ static int best_width(F tiles_w, int cus) {
 //    kernel, which spreads them over every CU (M = 4352 = 4096 + 256 rows,
 //    N = 12288: 816 tiles = 3 rounds + 48 tiles; the 48 become 192 small
 //    tiles).
-//  - Otherwise int8 takes the width whose rounds, each weighted by the
-//    tile's width, add up to least (best_width): 4096 x 3072 runs 256 tiles
-//    of 256x192 in one round (192 tiles of 256x256 leave a quarter of the
-//    CUs idle), 4352 x 3072 238 tiles of 256x224 (204 of 256x256, 272 of
-//    256x192), 4096 x 12288 stays on 256x256 (3 rounds; 4 of 256x192).
+//  - Otherwise the width whose rounds, each weighted by the tile's width,
+//    add up to least (best_width): 4096 x 3072 runs 256 tiles of 256x192 in
+//    one round (192 tiles of 256x256 leave a quarter of the CUs idle),
+//    int8 4352 x 3072 238 tiles of 256x224 (204 of 256x256, 272 of
+//    256x192), 4096 x 12288 stays on 256x256 (3 rounds; 4 of 256x192),
+//    6889 x 3072 432 tiles of 256x192 (two rounds, as 324 of 256x256).
 struct LargePlan {
     int m_big;
     int tw;
@@ -1474,7 +1510,7 @@ static LargePlan large_plan(int M, int N, int K, bool fp8) {
         }
     }
     if (plan.m_big < M && !small_m_fits(M - plan.m_big, N, K)) plan.m_big = M;
-    if (!fp8 && plan.m_big == M) plan.tw = best_width([&](int w) { return tiles_of(M, N, w); }, cus);
+    if (plan.m_big == M) plan.tw = best_width([&](int w) { return tiles_of(M, N, w); }, cus, fp8);
     return plan;
 }
 
@@ -1523,15 +1559,14 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
     }
     if ((K % BK) == 0) {
         // (large_plan: the tail-row split and the tile width)
-        LargePlan plan{M, fp8                                  ? BN
-                          : choice == QIMG_LINEAR_LARGE_192 ? NARROW_BN
-                          : choice == QIMG_LINEAR_LARGE_224 ? MID_BN
-                                                            : BN};
+        LargePlan plan{M, choice == QIMG_LINEAR_LARGE_192           ? NARROW_BN
+                          : choice == QIMG_LINEAR_LARGE_224 && !fp8 ? MID_BN
+                                                                    : BN};
         if (choice == QIMG_LINEAR_AUTO) plan = large_plan(M, N, K, fp8);
         const int m_big = plan.m_big;
         const TileProblems P = problems(
             tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate, plan.tw), TileProblem{});
-        hipError_t e = fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
+        hipError_t e = fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream, plan.tw)
                            : dispatch_tiled<false>(P, out_dtype, gelu, stream, plan.tw);
         if (e != hipSuccess || m_big == M) return e;
         const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
@@ -1577,10 +1612,11 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
         const int64_t tail = ta - (rounds - 1) * cus;
         // no extra round, and not a case for the tail-row split of a lone launch
         pair = cus > 0 && ta + tb <= rounds * cus && !(rounds > 1 && tail * 2 < cus);
-        // int8: the tile width for both (4096 + 256 rows of N = 3072: 238
+        // the tile width for both (int8 4096 + 256 rows of N = 3072: 238
         // tiles of 256x224 in one round, against 204 of 256x256)
-        if (pair && mode != QIMG_QM_FP8_HADAMARD)
-            tw = best_width([&](int w) { return tiles_of(a.M, a.N, w) + tiles_of(b.M, b.N, w); }, cus);
+        if (pair)
+            tw = best_width([&](int w) { return tiles_of(a.M, a.N, w) + tiles_of(b.M, b.N, w); }, cus,
+                            mode == QIMG_QM_FP8_HADAMARD);
     }
     if (!pair) {
         hipError_t e = a.M > 0 ? single(a) : hipSuccess;
@@ -1592,7 +1628,7 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
     const TileProblem p1 =
         tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out, b.gate, tw);
     const TileProblems P = problems(p0, p1);
-    return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
+    return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream, tw)
                                         : dispatch_tiled<false>(P, out_dtype, gelu, stream, tw);
 }
 
@@ -1656,8 +1692,8 @@ hipError_t launch_linear_multi(const LinearArgs* list, int n, int mode, int out_
     TileProblems P;
     const hipError_t r = build_linear_multi(list, n, out_dtype, gelu, P);
     if (r != hipSuccess) return r;
-    return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream)
-                                        : dispatch_tiled<false>(P, out_dtype, gelu, stream);
+    return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream, BN)
+                                        : dispatch_tiled<false>(P, out_dtype, gelu, stream, BN);
 }
 
 }  // namespace qimg

@@ -133,6 +133,36 @@ def test_fp8_linear(qimg, oracle, M, N, K):
     assert rel <= 5e-2 and cos >= 0.999, (rel, cos)
 
 
+@pytest.mark.parametrize("M,N,K", [(600, 518, 512), (777, 1000, 256), (1100, 3076, 1024), (6889, 3072, 1024)])
+def test_fp8_tile_widths(qimg, oracle, M, N, K):
+    """e4m3 on 256x256 and 256x192 tiles (waves 4 x 2 of 64x96): each
+    output's k-sum runs through the same MFMA sequence, so the two widths
+    agree bit for bit (fp32 and bf16 out, GELU), on ragged tiles too (last
+    tiles of 134, 40, 4 and 0 columns), and both are within the fp32
+    accumulation-order bound of the oracle's float64 sum."""
+    rng = np.random.default_rng(M + 7 * N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b_bits = oracle.bf16_bits_from_f32((rng.standard_normal(N) * 0.01).astype(np.float32))
+    wq, ws, hbs = oracle.quantize_weight_fp8(w_bits)
+    xq, xs = oracle.quantize_activation_fp8(x, hbs)
+    qw = _qw(qimg, wq, ws, hbs, mode=qimg.FP8_HADAMARD)
+    xd, bd = _dev(x), _bf16_dev(b_bits)
+    outs = {}
+    for kernel in ("large", "w192"):
+        with qimg.linear_kernel(KERNELS[kernel]):
+            outs[kernel] = (qimg.linear_forward_quantized(xd, qw, bd),
+                            qimg.linear_forward_quantized(xd, qw, bd, out_dtype=torch.bfloat16),
+                            qimg.linear_forward_quantized(xd, qw, bd, apply_gelu=True))
+    torch.cuda.synchronize()
+    for a, b in zip(outs["large"], outs["w192"]):
+        assert torch.equal(a, b)
+    rows = (0, min(M, 300))
+    ref = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, rows=rows)[rows[0]:rows[1]]
+    got = outs["w192"][0].cpu().numpy()[rows[0]:rows[1]]
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.abs(ref).max() * np.sqrt(K / 64)
+
+
 @pytest.mark.slow
 def test_mlp_pair_full_size_sampled(qimg, oracle):
     """MMDiT MLP at M=4352: fc1 (3072->12288, GELU) -> FWHT(4096)+quant -> fc2,
