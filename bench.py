@@ -536,6 +536,16 @@ def _extra(q, torch, dev, c5_steps=20):
     out["linear_c1_ms"] = round(ms_lin, 4)
     out["linear_c1_tflops"] = round(ops / ms_lin / 1e9, 1)
     out["linear_c1_gemm_only_tflops"] = round(ops / ms_gemm / 1e9, 1)
+    # the same linear with bf16 out (the config's output type; fp32 above is
+    # the reference's linear_forward_quantized output)
+    o16 = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ms_lin16 = _time(torch, lambda: q.linear_forward_quantized(x, qw, b, out=o16, scratch=scratch))
+    ms_gemm16 = _time(torch, lambda: q.linear_forward_prequantized(aq, asc, qw, b, out=o16))
+    out["linear_c1_bf16out_ms"] = round(ms_lin16, 4)
+    out["linear_c1_bf16out_tflops"] = round(ops / ms_lin16 / 1e9, 1)
+    out["linear_c1_bf16out_gemm_only_tflops"] = round(ops / ms_gemm16 / 1e9, 1)
+    out["linear_c1_gemm_only_frac"] = round(ops / ms_gemm / 1e9 / 5033.0, 4)
+    out["linear_c1_bf16out_gemm_only_frac"] = round(ops / ms_gemm16 / 1e9 / 5033.0, 4)
     ms_q = _time(torch, lambda: q.quantize_activation_hadamard(x, 1024))
     out["act_quant_c1_gbs"] = round((M * K * 3 + 4 * M) / ms_q / 1e6, 1)
     # C3: SageAttention, 24 heads, S = 4352 (256 text + 4096 image tokens),
