@@ -201,15 +201,17 @@ struct TileProblems {
 //    waves are arranged 4 x 2, each 64 x 112 = 4 x 7 blocks; the W DMA still
 //    fills 256 rows (4 instructions per wave, the last 32 rows unread), so
 //    every wave runs the same instruction stream.
-//  - e4m3 256x192 (32x32 blocks): waves 4 x 2 of 64 x 96 = 2 x 3 blocks.
+//  - e4m3 and bf16 256x192 (32x32 blocks): waves 4 x 2 of 64 x 96 = 2 x 3
+//    blocks.
 constexpr int NARROW_BN = 192;
 constexpr int MID_BN = 224;
 template <int OP, int OUT_DT, bool GELU, bool HD = false, int TW = BN>
 __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
     constexpr bool BF = OP == OP_BF16;
     constexpr bool M16 = OP == OP_I8_16;
-    static_assert(TW == BN || (!HD && (((TW == NARROW_BN || TW == MID_BN) && M16) || (TW == NARROW_BN && OP == OP_F8))),
-                  "the narrower tiles serve the plain int8 (16x16 blocks) and e4m3 epilogues");
+    static_assert(TW == BN || (!HD && (((TW == NARROW_BN || TW == MID_BN) && M16) ||
+                                       (TW == NARROW_BN && (OP == OP_F8 || OP == OP_BF16)))),
+                  "the narrower tiles serve the plain int8 (16x16 blocks), e4m3 and bf16 epilogues");
     // (these hide the file-scope 256-wide values inside the kernel)
     constexpr int WVN = (TW == MID_BN || (TW == NARROW_BN && !M16)) ? 2 : WAVES_N;  // waves across N
     constexpr int BN = TW;                           // tile width
@@ -453,10 +455,16 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
             read_frags(fa0, fw0, slot ^ 1, 0);
             mfma_all(fa1, fw1);
             if constexpr (decltype(refill)::value) {
+                constexpr int NM = TM * TN, NV = NDMA + NDMA_W;
+                constexpr int VQ = NV / NM, VR = NV % NM;  // DMAs per MFMA, and the first VR MFMAs' extra one
 #pragma unroll
-                for (int i = 0; i < TM * TN; ++i) {
+                for (int i = 0; i < NM; ++i) {
                     SGB(SG_MFMA, 1);
-                    SGB(SG_VMEM, 2 * NDMA / (TM * TN));
+                    if (i < VR) {
+                        SGB(SG_VMEM, VQ + 1);
+                    } else if constexpr (VQ > 0) {
+                        SGB(SG_VMEM, VQ);
+                    }
                     if (i < TM + TN) SGB(SG_DS_READ, 1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -1361,7 +1369,7 @@ hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, int tw = BN) 
     if (total != P.total) return hipErrorInvalidValue;
     if (tw != BN) {
         if (hd) return hipErrorInvalidValue;
-        if constexpr (OP == OP_I8_16 || OP == OP_F8) {
+        if constexpr (OP == OP_I8_16 || OP == OP_F8 || OP == OP_BF16) {
             if (tw == NARROW_BN) {
                 hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, NARROW_BN>), dim3(P.total), dim3(NTHR),
                                    0, stream, P);
@@ -1417,19 +1425,6 @@ hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream
 
 }  // namespace
 
-// bf16 x [M, K] times w [N, K]^T into fp32 out with the large tiles (K %
-// 64 == 0), as linear_forward_bf16_bf16in computes it: out (+)= product,
-// then + bias, then GELU.
-hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias,
-                                  float* out, int gelu, int accumulate, hipStream_t stream) {
-    if (M == 0 || N == 0) return hipSuccess;
-    if ((K * 2) % BK != 0) return hipErrorInvalidValue;
-    TileProblem p0 = tile_problem(x, nullptr, M, K * 2, w, nullptr, N, bias, out, nullptr);
-    p0.accumulate = accumulate;
-    const TileProblems P = problems(p0, TileProblem{});
-    return gelu ? launch_tiled<OP_BF16, QIMG_FP32, true>(P, stream) : launch_tiled<OP_BF16, QIMG_FP32, false>(P, stream);
-}
-
 static std::atomic<int> g_linear_kernel{QIMG_LINEAR_AUTO};
 
 // Compute units of the current device (queried once per device).
@@ -1457,14 +1452,14 @@ static int64_t tiles_of(int M, int N, int w) {
 static int64_t tile_cost(int64_t tiles, int w, int cus) { return (tiles + cus - 1) / cus * w; }
 
 // The tile width with the least tile_cost for `tiles_w(w)` tiles (the
-// widest of equals): 256, 224 or 192 for int8, 256 or 192 for e4m3 (whose
-// 32x32 blocks do not divide a 224-wide tile's waves).
+// widest of equals): 256, 224 or 192 for int8, 256 or 192 for the kernels on
+// 32x32 blocks (e4m3, bf16), which do not divide a 224-wide tile's waves.
 template <class F>
-static int best_width(F tiles_w, int cus, bool fp8) {
+static int best_width(F tiles_w, int cus, bool blocks32) {
     int tw = BN;
     int64_t best = tile_cost(tiles_w(BN), BN, cus);
     for (const int w : {MID_BN, NARROW_BN}) {
-        if (fp8 && w == MID_BN) continue;
+        if (blocks32 && w == MID_BN) continue;
         const int64_t c = tile_cost(tiles_w(w), w, cus);
         if (c < best) {
             best = c;
@@ -1512,6 +1507,22 @@ static LargePlan large_plan(int M, int N, int K, bool fp8) {
     if (plan.m_big < M && !small_m_fits(M - plan.m_big, N, K)) plan.m_big = M;
     if (plan.m_big == M) plan.tw = best_width([&](int w) { return tiles_of(M, N, w); }, cus, fp8);
     return plan;
+}
+
+// bf16 x [M, K] times w [N, K]^T into fp32 out with the large tiles (K %
+// 64 == 0), as linear_forward_bf16_bf16in computes it: out (+)= product,
+// then + bias, then GELU. The tile width (256 or 192) by best_width.
+hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias,
+                                  float* out, int gelu, int accumulate, hipStream_t stream) {
+    if (M == 0 || N == 0) return hipSuccess;
+    if ((K * 2) % BK != 0) return hipErrorInvalidValue;
+    const int cus = device_cu_count();
+    const int tw = cus > 0 ? best_width([&](int w_) { return tiles_of(M, N, w_); }, cus, true) : BN;
+    TileProblem p0 = tile_problem(x, nullptr, M, K * 2, w, nullptr, N, bias, out, nullptr, tw);
+    p0.accumulate = accumulate;
+    const TileProblems P = problems(p0, TileProblem{});
+    return gelu ? launch_tiled<OP_BF16, QIMG_FP32, true>(P, stream, tw)
+                : launch_tiled<OP_BF16, QIMG_FP32, false>(P, stream, tw);
 }
 
 int set_linear_kernel(int which) { return g_linear_kernel.exchange(which); }
