@@ -117,7 +117,8 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * tiles on the device's CUs, each weighted by the width, add up to least
  * (4096 x 3072: one full round of 256x192; int8 4352 x 3072: one round of
  * 256x224). LARGE_192 and LARGE_224 force those widths (e4m3 runs 224 as
- * 256).
+ * 256); qimg_linear_bf16's large-tile path follows LARGE_TILE and LARGE_192
+ * too.
  * GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide; returns
  * QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices give
  * identical int8 results. */

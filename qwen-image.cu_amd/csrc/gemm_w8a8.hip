@@ -1511,13 +1511,18 @@ static LargePlan large_plan(int M, int N, int K, bool fp8) {
 
 // bf16 x [M, K] times w [N, K]^T into fp32 out with the large tiles (K %
 // 64 == 0), as linear_forward_bf16_bf16in computes it: out (+)= product,
-// then + bias, then GELU. The tile width (256 or 192) by best_width.
+// then + bias, then GELU. The tile width (256 or 192) by best_width, or as
+// QIMG_LINEAR_LARGE_TILE / QIMG_LINEAR_LARGE_192 force it.
 hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias,
                                   float* out, int gelu, int accumulate, hipStream_t stream) {
     if (M == 0 || N == 0) return hipSuccess;
     if ((K * 2) % BK != 0) return hipErrorInvalidValue;
+    const int choice = g_linear_kernel.load(std::memory_order_relaxed);
     const int cus = device_cu_count();
-    const int tw = cus > 0 ? best_width([&](int w_) { return tiles_of(M, N, w_); }, cus, true) : BN;
+    const int tw = choice == QIMG_LINEAR_LARGE_TILE ? BN
+                   : choice == QIMG_LINEAR_LARGE_192 ? NARROW_BN
+                   : cus > 0 ? best_width([&](int w_) { return tiles_of(M, N, w_); }, cus, true)
+                             : BN;
     TileProblem p0 = tile_problem(x, nullptr, M, K * 2, w, nullptr, N, bias, out, nullptr, tw);
     p0.accumulate = accumulate;
     const TileProblems P = problems(p0, TileProblem{});

@@ -62,6 +62,32 @@ def test_linear_bf16_integer_operands_exact(qimg, oracle, M, N, K, x_fp32):
     np.testing.assert_array_equal(out.cpu().numpy()[idx], want.astype(np.float32))
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 3072), (4100, 3076, 1024)])
+def test_linear_bf16_large_tile_widths(qimg, oracle, M, N, K):
+    """bf16 x on the large tiles, 256 and 256x192 wide (waves 4 x 2 of
+    64x96): each output's k-sum runs through the same MFMA sequence, so the
+    widths agree bit for bit, with and without GELU, on ragged tiles too
+    (last tiles of 4 columns and 4 rows); and the values match the oracle's
+    integer-operand answer exactly."""
+    rng = np.random.default_rng(M + 2 * N + K)
+    xi = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    wi = rng.integers(-4, 5, (N, K)).astype(np.float32)
+    b = oracle.bf16_bits_from_f32(rng.integers(-8, 9, N).astype(np.float32))
+    x = torch.from_numpy(xi).to(DEV).to(torch.bfloat16)
+    w = torch.from_numpy(wi).to(DEV).to(torch.bfloat16)
+    bd = _bf16_dev(b)
+    outs = {}
+    for choice in (qimg.LINEAR_LARGE_TILE, qimg.LINEAR_LARGE_192):
+        with qimg.linear_kernel(choice):
+            outs[choice] = (qimg.linear_forward_bf16(x, w, bd), qimg.linear_forward_bf16(x, w, bd, apply_gelu=True))
+    torch.cuda.synchronize()
+    for a, c in zip(outs[qimg.LINEAR_LARGE_TILE], outs[qimg.LINEAR_LARGE_192]):
+        assert torch.equal(a, c)
+    idx = _rows(M, rng)
+    want = (xi[idx].astype(np.int64) @ wi.T.astype(np.int64)).astype(np.float64) + oracle.bf16_bits_to_f32(b)
+    np.testing.assert_array_equal(outs[qimg.LINEAR_LARGE_192][0].cpu().numpy()[idx], want.astype(np.float32))
+
+
 @pytest.mark.parametrize("M,K", [(300, 64), (17, 3584), (4, 96)])
 def test_linear_bf16_rounds_fp32_input_to_nearest_even(qimg, oracle, M, K):
     rng = np.random.default_rng(M + K)
