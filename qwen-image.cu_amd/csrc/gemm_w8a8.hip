@@ -15,10 +15,11 @@
 // accumulator registers per wave. Two waves per
 // SIMD let one wave's LDS reads and waits overlap the other's MFMAs
 // (measured 7-9% faster than four waves of 128x128). Both operands are
-// K-major [rows, K] as the reference stores them (TN GEMM). Plain int8
-// launches can also run 256x224 (waves 4 x 2 of 64x112) or 256x192 (waves of
-// 128x48) tiles, chosen where they take fewer rounds of the CUs (4352 x
-// 3072: 238 tiles of 256x224 in one round; 4096 x 3072: 256 of 256x192).
+// K-major [rows, K] as the reference stores them (TN GEMM). Plain launches
+// can also run narrower tiles, chosen where they take fewer rounds of the
+// CUs: int8 256x224 (waves 4 x 2 of 64x112) or 256x192 (waves of 128x48),
+// e4m3 and bf16 256x192 (waves 4 x 2 of 64x96); 4352 x 3072 is 238 tiles of
+// 256x224 in one round, 4096 x 3072 256 tiles of 256x192.
 //
 // K advances 128 bytes per stage through a two-slot LDS ring (2 x 64 KB):
 // while one stage is consumed the next is in flight. Stages are filled by
@@ -191,13 +192,13 @@ struct TileProblems {
 // (TileProblem::hk; an instance of its own, so that the extra epilogues
 // leave the others' register allocation alone).
 // TW: the tile's width, 256, 224 (MID_BN) or 192 (NARROW_BN). The narrower
-// tiles serve plain int8 launches whose 256x256 tiles would leave CUs idle:
+// tiles serve plain launches whose 256x256 tiles would leave CUs idle:
 // 4096 x 3072 is 192 tiles of 256x256 on 256 CUs, a quarter of the chip
 // idle for the whole launch, but 256 tiles of 256x192, one round with every
 // CU busy; 4352 x 3072 is 204 tiles of 256x256 but 238 of 256x224.
-//  - 256x192: waves of 128 x 48 = 8 x 3 blocks of 16x16; a stage's W share
-//    is 192 rows, 3 DMA instructions per wave.
-//  - 256x224: 224 columns are not four waves of whole 16x16 blocks, so the
+//  - int8 256x192: waves of 128 x 48 = 8 x 3 blocks of 16x16; a stage's W
+//    share is 192 rows, 3 DMA instructions per wave.
+//  - int8 256x224: 224 columns are not four waves of whole 16x16 blocks, so the
 //    waves are arranged 4 x 2, each 64 x 112 = 4 x 7 blocks; the W DMA still
 //    fills 256 rows (4 instructions per wave, the last 32 rows unread), so
 //    every wave runs the same instruction stream.
@@ -1353,8 +1354,9 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
     }
 }
 
-// tw: the tile width, BN, MID_BN or NARROW_BN (the last two for plain int8
-// launches only; P's tile counts must have been computed for that width)
+// tw: the tile width, BN, MID_BN (int8) or NARROW_BN (int8, e4m3, bf16);
+// narrower tiles take no attention-layout outputs. Every problem's tile
+// count is checked against the width before the launch.
 template <int OP, int OUT_DT, bool GELU>
 hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, int tw = BN) {
     bool hd = false;
