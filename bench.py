@@ -8,14 +8,15 @@ Workload (one "step"): the MMDiT MLP pair at M = 4352 tokens (4096 image +
     (+bias, bf16 out)
 with random N(0, 0.02) weights quantized by the library (W8A8 + Hadamard).
 fc1 is issued as the two kernel launches one M = 4352 call makes (rows
-0-4095 on the 256 x 256 tiles, rows 4096-4351 on the 64 x 64 tiles), as two
+0-4095 on the 256 x 256 tiles, rows 4096-4351 on the 128 x 128 tiles), as two
 calls, so that each kernel is timed; the output is that of the single call.
 Inputs are resident in HBM before timing. value = 2*M*N*K summed over both
 GEMMs (657.13 GOP) / measured time, in TFLOP/s (int8 ops). The K timed steps
 run twice: eagerly, with HIP events around each launch (the per-kernel
-times), then as K replays of the step captured in one HIP graph (the step
-time: the same launches without the host gaps between them; the output
-must equal the eager steps' bit for bit).
+times), then as K back-to-back replays of the step captured in one HIP graph
+between one event pair (the step time, span / K: the same launches without
+the host gaps between them; the output must equal the eager steps' bit for
+bit).
 
 Also printed in the same JSON line:
   roofline     the dominant kernel's achieved rate vs the int8 MFMA peak,
@@ -238,8 +239,11 @@ def main():
     y_eager = y.clone()
 
     # ---- the same step as one HIP graph (its five launches without the host
-    # launch gaps between them), replayed K times with an event pair around
-    # each replay: ms_per_step and value are the median of these.
+    # launch gaps between them), replayed K times back to back between one
+    # event pair: ms_per_step and value are that span / K (the throughput of
+    # consecutive steps). Bracketing each replay with its own event pair
+    # instead adds a gap per replay on some boxes (graph slower than eager);
+    # that median is reported beside it.
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
@@ -251,16 +255,25 @@ def main():
         torch.cuda.synchronize()
     for _ in range(args.warmup):
         graph.replay()
-    gev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    g0 = torch.cuda.Event(enable_timing=True)
+    g1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    g0.record(stream)
+    for i in range(K):
+        graph.replay()
+    g1.record(stream)
+    torch.cuda.synchronize()
+    wall_graph = time.perf_counter() - t0
+    ms_step = g0.elapsed_time(g1) / K
+    gev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
     for i in range(K):
         gev[i][0].record(stream)
         graph.replay()
         gev[i][1].record(stream)
     torch.cuda.synchronize()
-    wall_graph = time.perf_counter() - t0
-    ms_step = float(np.median([a.elapsed_time(b) for a, b in gev]))
+    ms_step_bracketed = float(np.median([a.elapsed_time(b) for a, b in gev]))
     # every replay computes what the eager steps computed
     graph_equals_eager = bool(torch.equal(y, y_eager))
     del graph
@@ -283,7 +296,8 @@ def main():
         gbytes = rows * Kd + Nd * Kd + rows * Nd * ob + 4 * (rows + Nd) + 2 * Nd
         kname = {"gemm_fc1": f"gemm_w8a8_kernel (int8, 16x16x64 MFMA), fc1 rows 0-4095: {rows}x{Nd}x{Kd}, "
                              "768 tiles of 256x256 = 3 rounds on 256 CUs",
-                 "gemm_fc1_tail": f"gemm_small_dma_kernel, fc1 rows 4096-4351: {rows}x{Nd}x{Kd}",
+                 "gemm_fc1_tail": f"gemm_w8a8_kernel (int8, 16x16x64 MFMA), fc1 rows 4096-4351: {rows}x{Nd}x{Kd}, "
+                                  "192 tiles of 128x128, two per CU",
                  "gemm_fc2": f"gemm_w8a8_kernel (int8, 16x16x64 MFMA), fc2 {rows}x{Nd}x{Kd}"}[dom]
         roof = {"kernel": kname, "bound": "mfma", "achieved": round(achieved, 1),
                 "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4),
@@ -302,7 +316,8 @@ def main():
     extra = {"per_kernel_ms_median": {k: round(v, 4) for k, v in per_kernel_ms.items()},
              "fc1_single_call_ms": round(ms_fc1_single, 4),
              "fc1_single_call_tflops": round(2.0 * M * D * H / ms_fc1_single / 1e9, 1),
-             "step_timing": "median of K replays of the step captured as one HIP graph",
+             "step_timing": "K back-to-back replays of the step captured as one HIP graph, span / K",
+             "ms_per_step_graph_bracketed_median": round(ms_step_bracketed, 4),
              "ms_per_step_eager": round(ms_step_eager, 4), "ms_per_step_eager_mean": round(total_ms / K, 4),
              "graph_equals_eager": graph_equals_eager,
              "wall_s_timed_eager": round(wall, 3), "wall_s_timed_graph": round(wall_graph, 3)}
@@ -1118,17 +1133,17 @@ def _summarize(d, outdir):
         written.append(fname)
 
     # -- GEMMs (bench.py --profile-set gemm: each shape 4 times)
-    G = [("C1 4096x3072x3072 i8 fp32", "qimg::gemm_w8a8_kernel<3, 0, false, false, 192>", 256, 4096, 3072, 3072, 4,
+    G = [("C1 4096x3072x3072 i8 fp32", "qimg::gemm_w8a8_kernel<3, 0, false, false, 192, 256>", 256, 4096, 3072, 3072, 4,
           "I8"),
-         ("fc1 rows 0-4095 of 4352 i8", "qimg::gemm_w8a8_kernel<3, 0, true, false, 256>", 768, 4096, 12288, 3072, 4, "I8"),
-         ("fc1 rows 4096-4351 i8", "qimg::gemm_small_dma_kernel<false, 2, 2, 2, 0, true, 64>", 768, 256, 12288, 3072,
-          4, "I8"),
-         ("fc2 4352x3072x12288 i8 bf16", "qimg::gemm_w8a8_kernel<3, 1, false, false, 224>", 238, 4352, 3072, 12288, 2,
+         ("fc1 rows 0-4095 of 4352 i8", "qimg::gemm_w8a8_kernel<3, 0, true, false, 256, 256>", 768, 4096, 12288, 3072, 4, "I8"),
+         ("fc1 rows 4096-4351 i8", "qimg::gemm_w8a8_kernel<3, 0, true, false, 128, 128>", 192, 256, 12288, 3072, 4,
           "I8"),
-         ("C5 fc1 rows 0-13567 e4m3", "qimg::gemm_w8a8_kernel<1, 0, true, false, 256>", 2544, 13568, 12288, 3072, 4, "F8"),
+         ("fc2 4352x3072x12288 i8 bf16", "qimg::gemm_w8a8_kernel<3, 1, false, false, 224, 256>", 238, 4352, 3072, 12288, 2,
+          "I8"),
+         ("C5 fc1 rows 0-13567 e4m3", "qimg::gemm_w8a8_kernel<1, 0, true, false, 256, 256>", 2544, 13568, 12288, 3072, 4, "F8"),
          ("C5 fc1 rows 13568-13777 e4m3", "qimg::gemm_small_dma_kernel<true, 2, 2, 2, 0, true, 64>", 768, 210, 12288,
           3072, 4, "F8"),
-         ("C5 fc2 13778x3072x12288 e4m3", "qimg::gemm_w8a8_kernel<1, 0, false, false, 256>", 648, 13778, 3072, 12288, 4,
+         ("C5 fc2 13778x3072x12288 e4m3", "qimg::gemm_w8a8_kernel<1, 0, false, false, 256, 256>", 648, 13778, 3072, 12288, 4,
           "F8")]
     md = _dispatches(os.path.join(d, "gemm_mfma"))
     lines = ["# MFMA utilisation and HBM traffic of the quantized-linear GEMMs",
@@ -1234,13 +1249,13 @@ def _summarize(d, outdir):
     step_kernels = {  # launch: (kernel, workgroups, algorithmic bytes)
         "quant_fc1_in": ("qimg::fwht_quant_wave_rows_kernel<qimg::RowsLoader<unsigned short>, (qimg::RowOut)0, 3, "
                          "qimg::RowDest>", M_ // 4, M_ * D_ * 2 + M_ * D_ + 4 * M_),
-        "gemm_fc1": ("qimg::gemm_w8a8_kernel<3, 0, true, false, 256>", 768,
+        "gemm_fc1": ("qimg::gemm_w8a8_kernel<3, 0, true, false, 256, 256>", 768,
                      MI * D_ + H_ * D_ + MI * H_ * 4 + 4 * (MI + H_) + 2 * H_),
-        "gemm_fc1_tail": ("qimg::gemm_small_dma_kernel<false, 2, 2, 2, 0, true, 64>", 768,
+        "gemm_fc1_tail": ("qimg::gemm_w8a8_kernel<3, 0, true, false, 128, 128>", 192,
                           256 * D_ + H_ * D_ + 256 * H_ * 4 + 4 * (256 + H_) + 2 * H_),
         "quant_fc2_in": ("qimg::fwht_quant_blocks_kernel<float, (qimg::RowOut)0, 3, false>", M_,
                          M_ * H_ * 4 + M_ * H_ + 4 * M_),
-        "gemm_fc2": ("qimg::gemm_w8a8_kernel<3, 1, false, false, 224>", 238,
+        "gemm_fc2": ("qimg::gemm_w8a8_kernel<3, 1, false, false, 224, 256>", 238,
                      M_ * H_ + D_ * H_ + M_ * D_ * 2 + 4 * (M_ + D_) + 2 * D_),
     }
     fd = _dispatches(os.path.join(d, "mlp_FETCH_SIZE"))
@@ -1249,7 +1264,7 @@ def _summarize(d, outdir):
              f"command (fetch): {cmds['mlp_FETCH_SIZE']}",
              f"command (write): {cmds['mlp_WRITE_SIZE']}"] + cal_hdr + [
              "medians over every dispatch of the launch's kernel and grid in the run; gemm_fc1 = rows 0-4095 on the "
-             "256x256 tiles, gemm_fc1_tail = rows 4096-4351 on the 64x64 tiles", "",
+             "256x256 tiles, gemm_fc1_tail = rows 4096-4351 on the 128x128 tiles", "",
              " launch            n  FETCH_KiB  WRITE_KiB  fetch_MB  write_MB  traffic_MB  algorithmic_MB  kernel"]
     tr = {}
     for k, (name, wgs, algo) in step_kernels.items():

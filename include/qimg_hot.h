@@ -112,13 +112,15 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * algorithm); it exists for tests and tuning, which compare the kernels on
  * one shape. AUTO (the default) takes the vector-ALU GEMV for int8 with
  * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
- * 256x256 would cover the output, and 256-row tiles otherwise: int8 takes
- * the width of 256, 224 or 192 columns (e4m3: 256 or 192) whose rounds of
- * tiles on the device's CUs, each weighted by the width, add up to least
+ * 256x256 would cover the output (int8: fewer than 32), and the large-tile
+ * kernel otherwise: 256 rows of 256, 224 or 192 columns, or int8 128x128
+ * tiles (two per CU), whichever's rounds of tiles on the device's CUs, each
+ * weighted by the tile's share of a 256x256 tile's time, add up to least
  * (4096 x 3072: one full round of 256x192; int8 4352 x 3072: one round of
- * 256x224). LARGE_192 and LARGE_224 force those widths (e4m3 runs 224 as
- * 256); qimg_linear_bf16's large-tile path follows LARGE_TILE and LARGE_192
- * too.
+ * 256x224; int8 2048 x 3072: one round of 128x128). e4m3 takes 256 or 192
+ * columns. LARGE_192, LARGE_224 and LARGE_128 force those tiles (e4m3 runs
+ * 224 and 128 as 256x256); qimg_linear_bf16's large-tile path follows
+ * LARGE_TILE and LARGE_192 too.
  * GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide; returns
  * QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices give
  * identical int8 results. */
@@ -129,7 +131,8 @@ enum {
     QIMG_LINEAR_SMALL_64 = 3,
     QIMG_LINEAR_GEMV = 4,
     QIMG_LINEAR_LARGE_192 = 5,
-    QIMG_LINEAR_LARGE_224 = 6
+    QIMG_LINEAR_LARGE_224 = 6,
+    QIMG_LINEAR_LARGE_128 = 7
 };
 int qimg_set_linear_kernel(int which);
 int qimg_get_linear_kernel(void);

@@ -224,7 +224,7 @@ int qimg_dequantize_bias(const int32_t* acc, const float* act_scales, const floa
 }
 
 int qimg_set_linear_kernel(int which) {
-    QIMG_REQUIRE(which >= QIMG_LINEAR_AUTO && which <= QIMG_LINEAR_LARGE_224,
+    QIMG_REQUIRE(which >= QIMG_LINEAR_AUTO && which <= QIMG_LINEAR_LARGE_128,
                  "qimg_set_linear_kernel: unknown kernel choice %d", which);
     qimg::set_linear_kernel(which);
     return QIMG_OK;

@@ -204,17 +204,31 @@ struct TileProblems {
 //    every wave runs the same instruction stream.
 //  - e4m3 and bf16 256x192 (32x32 blocks): waves 4 x 2 of 64 x 96 = 2 x 3
 //    blocks.
+// TH: the tile's height, 256 or 128 (SMALL_BM, with TW = 128: four waves
+// 2 x 2 of 64 x 64 and a 64 KB ring, two workgroups per CU; for problems
+// too small to fill the CUs with 256-row tiles).
 constexpr int NARROW_BN = 192;
 constexpr int MID_BN = 224;
-template <int OP, int OUT_DT, bool GELU, bool HD = false, int TW = BN>
-__global__ __launch_bounds__(NTHR, 1) void gemm_w8a8_kernel(TileProblems P) {
+constexpr int SMALL_BM = 128;
+template <int OP, int OUT_DT, bool GELU, bool HD = false, int TW = BN, int TH = BM>
+__global__ __launch_bounds__(TH == SMALL_BM ? 256 : NTHR, TH == SMALL_BM ? 2 : 1) void gemm_w8a8_kernel(
+    TileProblems P) {
     constexpr bool BF = OP == OP_BF16;
     constexpr bool M16 = OP == OP_I8_16;
     static_assert(TW == BN || (!HD && (((TW == NARROW_BN || TW == MID_BN) && M16) ||
-                                       (TW == NARROW_BN && (OP == OP_F8 || OP == OP_BF16)))),
+                                       (TW == NARROW_BN && (OP == OP_F8 || OP == OP_BF16)) ||
+                                       (TW == SMALL_BM && TH == SMALL_BM && M16))),
                   "the narrower tiles serve the plain int8 (16x16 blocks), e4m3 and bf16 epilogues");
-    // (these hide the file-scope 256-wide values inside the kernel)
-    constexpr int WVN = (TW == MID_BN || (TW == NARROW_BN && !M16)) ? 2 : WAVES_N;  // waves across N
+    static_assert(TH == BM || (TH == SMALL_BM && TW == SMALL_BM), "128-row tiles are 128 x 128");
+    // (these hide the file-scope 256 x 256 values inside the kernel)
+    constexpr bool SMALL = TH == SMALL_BM;
+    constexpr int BM = TH;                                   // tile height
+    constexpr int NWAVES = SMALL ? 4 : 8;                    // two waves per SIMD (over two workgroups if SMALL)
+    constexpr int NDMA = BM / (NWAVES * DMA_ROWS);           // A DMA instructions per wave per stage
+    constexpr int OP_BYTES = BM * BK;                        // one operand's slot
+    constexpr int LDS_BYTES = 2 * NSLOT * OP_BYTES;
+    constexpr int SCALE_OFF = LDS_BYTES - 4 * 256 * 4;       // as, ws, bias, gate
+    constexpr int WVN = (SMALL || TW == MID_BN || (TW == NARROW_BN && !M16)) ? 2 : WAVES_N;  // waves across N
     constexpr int BN = TW;                           // tile width
     constexpr int WTM = BM / (NWAVES / WVN);         // wave tile: 128 or 64 rows
     constexpr int TM = WTM / 32;                     // 32-row blocks of a wave
@@ -1358,17 +1372,27 @@ __global__ __launch_bounds__(256) void dequant_bias_kernel(const int32_t* __rest
 // narrower tiles take no attention-layout outputs. Every problem's tile
 // count is checked against the width before the launch.
 template <int OP, int OUT_DT, bool GELU>
-hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, int tw = BN) {
+hipError_t launch_tiled(const TileProblems& P, hipStream_t stream, int tw = BN, int th = BM) {
     bool hd = false;
     int64_t total = 0;
     for (int i = 0; i < P.n; ++i) {
         const TileProblem& p = P.p[i];
         hd = hd || p.hk > 0;
-        // every problem's tiles counted for the width launched
-        if (tw <= 0 || p.tiles != ((p.M + BM - 1) / BM) * ((p.N + tw - 1) / tw)) return hipErrorInvalidValue;
+        // every problem's tiles counted for the tile size launched
+        if (tw <= 0 || th <= 0 || p.tiles != ((p.M + th - 1) / th) * ((p.N + tw - 1) / tw))
+            return hipErrorInvalidValue;
         total += p.tiles;
     }
     if (total != P.total) return hipErrorInvalidValue;
+    if (th != BM) {
+        if constexpr (OP == OP_I8_16) {
+            if (hd || th != SMALL_BM || tw != SMALL_BM) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((gemm_w8a8_kernel<OP, OUT_DT, GELU, false, SMALL_BM, SMALL_BM>), dim3(P.total),
+                               dim3(256), 0, stream, P);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
     if (tw != BN) {
         if (hd) return hipErrorInvalidValue;
         if constexpr (OP == OP_I8_16 || OP == OP_F8 || OP == OP_BF16) {
@@ -1407,22 +1431,24 @@ TileProblems problems(const TileProblem& p0, const TileProblem& p1) {
     return P;
 }
 
-// bn: the tile width the problem will be launched with (BN, MID_BN or NARROW_BN)
+// bn, bm: the tile size the problem will be launched with (BN, MID_BN or
+// NARROW_BN wide; BM or SMALL_BM high)
 TileProblem tile_problem(const void* a, const float* as, int M, int K, const void* w, const float* ws, int N,
-                         const uint16_t* bias, void* out, const float* gate, int bn = BN) {
+                         const uint16_t* bias, void* out, const float* gate, int bn = BN, int bm = BM) {
     return {static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(w), as, ws, bias, out, gate, M, N, K,
-            ((M + BM - 1) / BM) * ((N + bn - 1) / bn), 0};
+            ((M + bm - 1) / bm) * ((N + bn - 1) / bn), 0};
 }
 
-// tw must be the width P's tile counts were computed for (tile_problem's bn).
+// tw, th must be the tile size P's tile counts were computed for
+// (tile_problem's bn, bm).
 template <bool FP8>
-hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, int tw) {
+hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream_t stream, int tw, int th = BM) {
     constexpr int OP = FP8 ? OP_F8 : OP_I8_16;
     if (out_dt == QIMG_FP32)
-        return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream, tw)
-                    : launch_tiled<OP, QIMG_FP32, false>(P, stream, tw);
-    return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream, tw)
-                : launch_tiled<OP, QIMG_BF16, false>(P, stream, tw);
+        return gelu ? launch_tiled<OP, QIMG_FP32, true>(P, stream, tw, th)
+                    : launch_tiled<OP, QIMG_FP32, false>(P, stream, tw, th);
+    return gelu ? launch_tiled<OP, QIMG_BF16, true>(P, stream, tw, th)
+                : launch_tiled<OP, QIMG_BF16, false>(P, stream, tw, th);
 }
 
 }  // namespace
@@ -1443,9 +1469,9 @@ static int device_cu_count() {
     return n;
 }
 
-// Tiles of width w that cover M x N (256 rows each).
-static int64_t tiles_of(int M, int N, int w) {
-    return static_cast<int64_t>((M + BM - 1) / BM) * ((N + w - 1) / w);
+// Tiles of w columns and h rows that cover M x N.
+static int64_t tiles_of(int M, int N, int w, int h = BM) {
+    return static_cast<int64_t>((M + h - 1) / h) * ((N + w - 1) / w);
 }
 
 // The cost of running `tiles` tiles of width w, in 256x256-tile-widths of
@@ -1453,22 +1479,29 @@ static int64_t tiles_of(int M, int N, int w) {
 // of a 256x256 tile's work.
 static int64_t tile_cost(int64_t tiles, int w, int cus) { return (tiles + cus - 1) / cus * w; }
 
-// The tile width with the least tile_cost for `tiles_w(w)` tiles (the
-// widest of equals): 256, 224 or 192 for int8, 256 or 192 for the kernels on
-// 32x32 blocks (e4m3, bf16), which do not divide a 224-wide tile's waves.
+// The tile with the least tile_cost for `tiles_wh(w, h)` tiles of w x h
+// (the largest of equals): 256 rows of 256, 224 or 192 columns, or int8
+// 128 x 128 (two workgroups per CU: 2 x cus tiles a round, each round half
+// a 256 x 256 round's time); the kernels on 32x32 blocks (e4m3, bf16) take
+// 256 or 192 columns (a 224-wide tile's waves do not divide into them).
+struct TileSize {
+    int tw, th;
+};
 template <class F>
-static int best_width(F tiles_w, int cus, bool blocks32) {
-    int tw = BN;
-    int64_t best = tile_cost(tiles_w(BN), BN, cus);
-    for (const int w : {MID_BN, NARROW_BN}) {
-        if (blocks32 && w == MID_BN) continue;
-        const int64_t c = tile_cost(tiles_w(w), w, cus);
-        if (c < best) {
-            best = c;
-            tw = w;
+static TileSize best_tile(F tiles_wh, int cus, bool blocks32) {
+    TileSize best{BN, BM};
+    int64_t c_best = tile_cost(tiles_wh(BN, BM), BN, cus);
+    const TileSize cand[3] = {{MID_BN, BM}, {NARROW_BN, BM}, {SMALL_BM, SMALL_BM}};
+    for (const TileSize& t : cand) {
+        if (blocks32 && t.tw != NARROW_BN) continue;
+        const int64_t c = t.th == SMALL_BM ? tile_cost(tiles_wh(t.tw, t.th), SMALL_BM, 2 * cus)
+                                           : tile_cost(tiles_wh(t.tw, t.th), t.tw, cus);
+        if (c < c_best) {
+            c_best = c;
+            best = t;
         }
     }
-    return tw;
+    return best;
 }
 
 // The large-tile plan of an automatic choice (K % 128 == 0, not a small-M
@@ -1479,15 +1512,18 @@ static int best_width(F tiles_w, int cus, bool blocks32) {
 //    kernel, which spreads them over every CU (M = 4352 = 4096 + 256 rows,
 //    N = 12288: 816 tiles = 3 rounds + 48 tiles; the 48 become 192 small
 //    tiles).
-//  - Otherwise the width whose rounds, each weighted by the tile's width,
-//    add up to least (best_width): 4096 x 3072 runs 256 tiles of 256x192 in
-//    one round (192 tiles of 256x256 leave a quarter of the CUs idle),
-//    int8 4352 x 3072 238 tiles of 256x224 (204 of 256x256, 272 of
-//    256x192), 4096 x 12288 stays on 256x256 (3 rounds; 4 of 256x192),
-//    6889 x 3072 432 tiles of 256x192 (two rounds, as 324 of 256x256).
+//  - Otherwise the tile whose rounds, each weighted by the tile's share of
+//    a 256x256 tile's time, add up to least (best_tile): 4096 x 3072 runs
+//    256 tiles of 256x192 in one round (192 tiles of 256x256 leave a quarter
+//    of the CUs idle), int8 4352 x 3072 238 tiles of 256x224 (204 of
+//    256x256, 272 of 256x192), 4096 x 12288 stays on 256x256 (3 rounds; 4
+//    of 256x192), 6889 x 3072 432 tiles of 256x192 (two rounds, as 324 of
+//    256x256), int8 2048 x 3072 384 tiles of 128x128 (one round of two per
+//    CU).
 struct LargePlan {
     int m_big;
     int tw;
+    int th = BM;
 };
 static LargePlan large_plan(int M, int N, int K, bool fp8) {
     LargePlan plan{M, BN};
@@ -1507,13 +1543,17 @@ static LargePlan large_plan(int M, int N, int K, bool fp8) {
         }
     }
     if (plan.m_big < M && !small_m_fits(M - plan.m_big, N, K)) plan.m_big = M;
-    if (plan.m_big == M) plan.tw = best_width([&](int w) { return tiles_of(M, N, w); }, cus, fp8);
+    if (plan.m_big == M) {
+        const TileSize t = best_tile([&](int w, int h) { return tiles_of(M, N, w, h); }, cus, fp8);
+        plan.tw = t.tw;
+        plan.th = t.th;
+    }
     return plan;
 }
 
 // bf16 x [M, K] times w [N, K]^T into fp32 out with the large tiles (K %
 // 64 == 0), as linear_forward_bf16_bf16in computes it: out (+)= product,
-// then + bias, then GELU. The tile width (256 or 192) by best_width, or as
+// then + bias, then GELU. The tile width (256 or 192) by best_tile, or as
 // QIMG_LINEAR_LARGE_TILE / QIMG_LINEAR_LARGE_192 force it.
 hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_t* w, int N, const uint16_t* bias,
                                   float* out, int gelu, int accumulate, hipStream_t stream) {
@@ -1523,7 +1563,7 @@ hipError_t launch_gemm_bf16_large(const uint16_t* x, int M, int K, const uint16_
     const int cus = device_cu_count();
     const int tw = choice == QIMG_LINEAR_LARGE_TILE ? BN
                    : choice == QIMG_LINEAR_LARGE_192 ? NARROW_BN
-                   : cus > 0 ? best_width([&](int w_) { return tiles_of(M, N, w_); }, cus, true)
+                   : cus > 0 ? best_tile([&](int w_, int h_) { return tiles_of(M, N, w_, h_); }, cus, true).tw
                              : BN;
     TileProblem p0 = tile_problem(x, nullptr, M, K * 2, w, nullptr, N, bias, out, nullptr, tw);
     p0.accumulate = accumulate;
@@ -1568,6 +1608,11 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
                 : choice == QIMG_LINEAR_SMALL_64 ? 2
                 : choice == QIMG_LINEAR_GEMV     ? 3
                                                  : 0;
+    // int8 with at least kMidTileMin tiles of 256x256 takes the large-tile
+    // plan, which includes 128x128 tiles (at 32-63 tiles they measured
+    // faster than the 64x64 ones: 1024 x 3072 x 3072 19.2 against 23.4 us)
+    if (choice == QIMG_LINEAR_AUTO && !fp8 && small == 2 && (K % BK) == 0 && tiles_of(M, N, BN) >= kMidTileMin)
+        small = 0;
     // the large tiles need K % 128 == 0; other multiples of 64 take 64x64 tiles
     if (small == 0 && (K % BK) != 0 && small_m_fits(M, N, K)) small = 2;
     if (small != 0) {
@@ -1579,15 +1624,30 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
         // (large_plan: the tail-row split and the tile width)
         LargePlan plan{M, choice == QIMG_LINEAR_LARGE_192           ? NARROW_BN
                           : choice == QIMG_LINEAR_LARGE_224 && !fp8 ? MID_BN
+                          : choice == QIMG_LINEAR_LARGE_128 && !fp8 ? SMALL_BM
                                                                     : BN};
+        if (choice == QIMG_LINEAR_LARGE_128 && !fp8) plan.th = SMALL_BM;
         if (choice == QIMG_LINEAR_AUTO) plan = large_plan(M, N, K, fp8);
         const int m_big = plan.m_big;
         const TileProblems P = problems(
-            tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate, plan.tw), TileProblem{});
-        hipError_t e = fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream, plan.tw)
-                           : dispatch_tiled<false>(P, out_dtype, gelu, stream, plan.tw);
+            tile_problem(act_q, act_scales, m_big, K, w_q, w_scales, N, bias, out, gate, plan.tw, plan.th),
+            TileProblem{});
+        hipError_t e = fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream, plan.tw, plan.th)
+                           : dispatch_tiled<false>(P, out_dtype, gelu, stream, plan.tw, plan.th);
         if (e != hipSuccess || m_big == M) return e;
         const int esz = out_dtype == QIMG_FP32 ? 4 : 2;
+        if (!fp8) {
+            // int8 tail rows on 128x128 tiles, with the gated epilogue when
+            // there is one (the fc1 tail at 4352 x 12288 x 3072: 192 tiles,
+            // 21.4 against 23.1 us on the 64x64 kernel)
+            const TileProblems Pt = problems(
+                tile_problem(static_cast<const uint8_t*>(act_q) + static_cast<int64_t>(m_big) * K, act_scales + m_big,
+                             M - m_big, K, w_q, w_scales, N, bias,
+                             static_cast<uint8_t*>(out) + static_cast<int64_t>(m_big) * N * esz, gate, SMALL_BM,
+                             SMALL_BM),
+                TileProblem{});
+            return dispatch_tiled<false>(Pt, out_dtype, gelu, stream, SMALL_BM, SMALL_BM);
+        }
         void* rest = gate ? static_cast<void*>(tmp + static_cast<int64_t>(m_big) * N)
                           : static_cast<void*>(static_cast<uint8_t*>(out) + static_cast<int64_t>(m_big) * N * esz);
         e = launch_linear_small_m(static_cast<const uint8_t*>(act_q) + static_cast<int64_t>(m_big) * K,
@@ -1618,10 +1678,15 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
         return launch_linear_prequantized(x.act_q, x.act_scales, x.M, x.K, x.w_q, x.w_scales, x.N, mode, x.bias,
                                           x.out, out_dtype, gelu, stream, x.gate, x.tmp);
     };
+    const bool fp8 = mode == QIMG_QM_FP8_HADAMARD;
+    // (int8 images of at least kMidTileMin tiles of 256x256 pair up too: on
+    // 128x128 tiles when those are best)
     bool pair = a.M > 0 && a.N > 0 && b.M > 0 && b.N > 0 &&
                 g_linear_kernel.load(std::memory_order_relaxed) == QIMG_LINEAR_AUTO && (a.K % BK) == 0 &&
-                (b.K % BK) == 0 && small_m_variant(a.M, a.N, a.K) == 0;
-    int tw = BN;
+                (b.K % BK) == 0 &&
+                (small_m_variant(a.M, a.N, a.K) == 0 ||
+                 (!fp8 && a.M > 32 && tiles_of(a.M, a.N, BN) >= kMidTileMin));
+    TileSize ts{BN, BM};
     if (pair) {
         const int cus = device_cu_count();
         const int64_t ta = tiles_of(a.M, a.N, BN);
@@ -1630,11 +1695,11 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
         const int64_t tail = ta - (rounds - 1) * cus;
         // no extra round, and not a case for the tail-row split of a lone launch
         pair = cus > 0 && ta + tb <= rounds * cus && !(rounds > 1 && tail * 2 < cus);
-        // the tile width for both (int8 4096 + 256 rows of N = 3072: 238
-        // tiles of 256x224 in one round, against 204 of 256x256)
+        // the tile for both (int8 4096 + 256 rows of N = 3072: 238 tiles of
+        // 256x224 in one round, against 204 of 256x256)
         if (pair)
-            tw = best_width([&](int w) { return tiles_of(a.M, a.N, w) + tiles_of(b.M, b.N, w); }, cus,
-                            mode == QIMG_QM_FP8_HADAMARD);
+            ts = best_tile([&](int w, int h) { return tiles_of(a.M, a.N, w, h) + tiles_of(b.M, b.N, w, h); }, cus,
+                           fp8);
     }
     if (!pair) {
         hipError_t e = a.M > 0 ? single(a) : hipSuccess;
@@ -1642,12 +1707,12 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
     }
     if ((a.gate || b.gate) && out_dtype != QIMG_FP32) return hipErrorInvalidValue;
     const TileProblem p0 =
-        tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate, tw);
+        tile_problem(a.act_q, a.act_scales, a.M, a.K, a.w_q, a.w_scales, a.N, a.bias, a.out, a.gate, ts.tw, ts.th);
     const TileProblem p1 =
-        tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out, b.gate, tw);
+        tile_problem(b.act_q, b.act_scales, b.M, b.K, b.w_q, b.w_scales, b.N, b.bias, b.out, b.gate, ts.tw, ts.th);
     const TileProblems P = problems(p0, p1);
-    return mode == QIMG_QM_FP8_HADAMARD ? dispatch_tiled<true>(P, out_dtype, gelu, stream, tw)
-                                        : dispatch_tiled<false>(P, out_dtype, gelu, stream, tw);
+    return fp8 ? dispatch_tiled<true>(P, out_dtype, gelu, stream, ts.tw, ts.th)
+               : dispatch_tiled<false>(P, out_dtype, gelu, stream, ts.tw, ts.th);
 }
 
 // Up to kMaxProblems linears of one mode, output type and epilogue in one

@@ -22,7 +22,7 @@ QIMG_OK, QIMG_ERR_INVALID_ARG, QIMG_ERR_UNSUPPORTED, QIMG_ERR_SCRATCH, QIMG_ERR_
 FP32, BF16, FP16, INT8, INT32, FP8_E4M3 = range(6)
 INT8_HADAMARD, FP8_HADAMARD = 0, 1
 (LINEAR_AUTO, LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64, LINEAR_GEMV, LINEAR_LARGE_192,
- LINEAR_LARGE_224) = range(7)
+ LINEAR_LARGE_224, LINEAR_LARGE_128) = range(8)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int

@@ -64,8 +64,8 @@ SMALL_M_TILE_LIMIT = 64
 
 
 def pair_in_one_launch(Ma, Na, Mb, Nb, cus):
-    """Whether the dispatcher runs two linears (image and text stream) in one
-    launch of the 256x256-tile kernel: the first needs at least
+    """Whether the dispatcher runs two e4m3 linears (image and text stream)
+    in one launch of the large-tile kernel: the first needs at least
     SMALL_M_TILE_LIMIT tiles (below that the small-tile kernel takes it), the
     second's tiles must fit the first's last round, and the first must not be
     a case for the tail-row split (a last round less than half full)."""

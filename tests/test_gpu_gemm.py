@@ -37,7 +37,7 @@ def _qw(qimg, q, s, hbs, mode=0):
     return qimg.QuantizedWeight(_dev(q), _dev(s), hbs, mode)
 
 
-KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4, "w192": 5, "w224": 6}
+KERNELS = {"auto": 0, "large": 1, "small32": 2, "small64": 3, "gemv": 4, "w192": 5, "w224": 6, "t128": 7}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
@@ -232,7 +232,7 @@ def test_dequantize_and_bias_matches_oracle_and_fused(qimg, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(4100, 3076, 1024), (600, 518, 512), (777, 1000, 256), (513, 264, 3072)])
-@pytest.mark.parametrize("kernel", ["large", "w192", "w224"])
+@pytest.mark.parametrize("kernel", ["large", "w192", "w224", "t128"])
 def test_large_tile_epilogue_edges(qimg, oracle, M, N, K, kernel):
     """The 256-row tiles' int8 epilogue (256, 224 and 192 columns) on ragged
     tiles: rows past M, N % 4 = 2 (element stores), N % 8 = 4 (bf16
