@@ -1212,7 +1212,8 @@ def _summarize(d, outdir):
     # consecutive dispatches after the previous shape's
     import itertools
     groups = [(k, len(list(g))) for k, g in itertools.groupby(
-        (x for x in fd if "gemv" in x["name"] or "gemm_small" in x["name"]), key=lambda x: (x["name"], x["wgs"]))]
+        (x for x in fd if "gemv" in x["name"] or "gemm_small" in x["name"] or "gemm_w8a8" in x["name"]),
+        key=lambda x: (x["name"], x["wgs"]))]
     keys = [k for k, n in groups if n >= 6]
     if len(keys) != len(shapes):
         raise RuntimeError(f"small_m: expected {len(shapes)} GEMM kernels, found {keys}")
