@@ -112,9 +112,10 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * algorithm); it exists for tests and tuning, which compare the kernels on
  * one shape. AUTO (the default) takes the vector-ALU GEMV for int8 with
  * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
- * 256x256 would cover the output (int8: fewer than 32), and the large-tile
- * kernel otherwise: 256 rows of 256, 224 or 192 columns, or int8 128x128
- * tiles (two per CU), whichever's rounds of tiles on the device's CUs, each
+ * 256x256 would cover the output (int8 of 128 rows or more: fewer than 32),
+ * and the large-tile kernel otherwise: 256 rows of 256, 224 or 192 columns,
+ * or int8 128x128 tiles (two per CU), whichever's rounds of tiles on the
+ * device's CUs, each
  * weighted by the tile's share of a 256x256 tile's time, add up to least
  * (4096 x 3072: one full round of 256x192; int8 4352 x 3072: one round of
  * 256x224; int8 2048 x 3072: one round of 128x128). e4m3 takes 256 or 192

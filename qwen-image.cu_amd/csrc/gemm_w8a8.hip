@@ -1608,10 +1608,12 @@ hipError_t launch_linear_prequantized(const void* act_q, const float* act_scales
                 : choice == QIMG_LINEAR_SMALL_64 ? 2
                 : choice == QIMG_LINEAR_GEMV     ? 3
                                                  : 0;
-    // int8 with at least kMidTileMin tiles of 256x256 takes the large-tile
-    // plan, which includes 128x128 tiles (at 32-63 tiles they measured
-    // faster than the 64x64 ones: 1024 x 3072 x 3072 19.2 against 23.4 us)
-    if (choice == QIMG_LINEAR_AUTO && !fp8 && small == 2 && (K % BK) == 0 && tiles_of(M, N, BN) >= kMidTileMin)
+    // int8 of at least 128 rows and kMidTileMin tiles of 256x256 takes the
+    // large-tile plan, which includes 128x128 tiles (at 32-63 tiles they
+    // measured faster than the 64x64 ones: 1024 x 3072 x 3072 19.2 against
+    // 23.4 us; below 128 rows most of such a tile would be empty)
+    if (choice == QIMG_LINEAR_AUTO && !fp8 && small == 2 && (K % BK) == 0 && M >= SMALL_BM &&
+        tiles_of(M, N, BN) >= kMidTileMin)
         small = 0;
     // the large tiles need K % 128 == 0; other multiples of 64 take 64x64 tiles
     if (small == 0 && (K % BK) != 0 && small_m_fits(M, N, K)) small = 2;
@@ -1685,7 +1687,7 @@ hipError_t launch_linear_pair(const LinearArgs& a, const LinearArgs& b, int mode
                 g_linear_kernel.load(std::memory_order_relaxed) == QIMG_LINEAR_AUTO && (a.K % BK) == 0 &&
                 (b.K % BK) == 0 &&
                 (small_m_variant(a.M, a.N, a.K) == 0 ||
-                 (!fp8 && a.M > 32 && tiles_of(a.M, a.N, BN) >= kMidTileMin));
+                 (!fp8 && a.M >= SMALL_BM && tiles_of(a.M, a.N, BN) >= kMidTileMin));
     TileSize ts{BN, BM};
     if (pair) {
         const int cus = device_cu_count();

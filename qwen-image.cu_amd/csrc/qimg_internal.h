@@ -179,8 +179,9 @@ int get_linear_kernel();
 // (64: at 48 tiles of 256x256 or fewer the 64x64 tiles measured faster, at
 // 72 or more the large tiles, for int8 and e4m3, K = 3072 and 12288)
 constexpr int kSmallMTileLimit = 64;
-// int8 linears of at least this many tiles of 256x256 leave the 64x64
-// tiles for the large-tile kernel's plan, whose 128x128 tiles serve them
+// int8 linears of at least 128 rows and this many tiles of 256x256 leave
+// the 64x64 tiles for the large-tile kernel's plan, whose 128x128 tiles
+// serve them
 // (1024 x 3072 x 3072: 19.2 against 23.4 us; 512 x 3072 x 3072, 24 tiles:
 // 16.4 against 15.2 us, kept on 64x64)
 constexpr int kMidTileMin = 32;

@@ -262,6 +262,31 @@ def test_large_tile_epilogue_edges(qimg, oracle, M, N, K, kernel):
     assert torch.equal(og, sep_g)
 
 
+@pytest.mark.parametrize("M", [33, 129, 257, 1000, 1024, 2049, 4095, 4352, 6889])
+@pytest.mark.parametrize("N", [1000, 3072, 12288])
+def test_int8_auto_dispatch_exact(qimg, M, N):
+    """The automatic choice over M and N around the dispatcher's
+    boundaries (the 64x64 small tiles, 128x128 tiles from 128 rows and 32
+    tiles of 256x256, 256-row tiles 192, 224 or 256 wide, the trailing tile
+    rows split off to 128x128 tiles): every row of a sample is the exact
+    int32 product, fp32 out, and bf16 out its rounding."""
+    K = 256
+    rng = np.random.default_rng(M * 7 + N)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    ones_m = np.ones(M, np.float32)
+    qw = _qw(qimg, w, np.ones(N, np.float32), 1)
+    ad, sd = _dev(a), _dev(ones_m)
+    o32 = qimg.linear_forward_prequantized(ad, sd, qw)
+    o16 = qimg.linear_forward_prequantized(ad, sd, qw, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    idx = np.unique(np.concatenate([[0, M - 1], np.arange(0, M, max(1, M // 16)), rng.integers(0, M, 24),
+                                    np.arange(max(0, M - 300), M, 37)]))
+    ref = (a[idx].astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    np.testing.assert_array_equal(o32.cpu().numpy()[idx], ref)
+    np.testing.assert_array_equal(o16.float().cpu().numpy()[idx], torch.from_numpy(ref).bfloat16().float().numpy())
+
+
 @pytest.mark.parametrize("M,N,K", [(3328, 2560, 128), (3328, 2560, 320), (4352, 3072, 1024)])
 def test_int8_gemm_partial_round_shapes_exact(qimg, oracle, M, N, K):
     """Tile counts that do not fill whole rounds of the 256 CUs (130 and 204
