@@ -12,11 +12,13 @@ fc1 is issued as the two kernel launches one M = 4352 call makes (rows
 calls, so that each kernel is timed; the output is that of the single call.
 Inputs are resident in HBM before timing. value = 2*M*N*K summed over both
 GEMMs (657.13 GOP) / measured time, in TFLOP/s (int8 ops). The K timed steps
-run twice: eagerly, with HIP events around each launch (the per-kernel
-times), then as K back-to-back replays of the step captured in one HIP graph
-between one event pair (the step time, span / K: the same launches without
-the host gaps between them; the output must equal the eager steps' bit for
-bit).
+run twice: eagerly on one stream, with HIP events around each launch (the
+per-kernel times), then as K back-to-back replays of the step captured in one
+HIP graph between one event pair (the step time, span / K). In the graph,
+rows 4096-4351 (their fc1 and fc2-input quantization) run on a second stream
+beside rows 0-4095's fc1 and quantization, and fc2 joins the two; the output
+must equal the eager steps' bit for bit. The one-stream step as a graph is
+reported beside it.
 
 Also printed in the same JSON line:
   roofline     the dominant kernel's achieved rate vs the int8 MFMA peak,
@@ -171,11 +173,12 @@ def main():
     # fc1 of the 4352 rows is issued as the two kernel launches one
     # qimg_linear_prequantized call of M = 4352 makes (the dispatcher sends
     # rows 0-4095 to the 256 x 256 tiles, 768 tiles = exactly three rounds on
-    # 256 CUs, and the trailing tile row to the 64 x 64 tiles), as two calls,
-    # so that HIP events time each kernel; the outputs and the step time equal
-    # those of the single call (measured in-process: 390.0 against 391.1 us
-    # per step). extra.fc1_single_call_ms times fc1 as that single call (its
-    # two kernels back to back, without the events between them).
+    # 256 CUs, and the trailing tile row to the 128 x 128 tiles), as two
+    # calls, so that HIP events time each kernel; the outputs and the
+    # one-stream step time equal those of the single call (measured
+    # in-process: 395.4 against 395.9 us per step). extra.fc1_single_call_ms
+    # times fc1 as that single call (its two kernels back to back, without
+    # the events between them).
     MI, MT = 4096, M - 4096
 
     # (the stream is read at each call, so the same launches can be captured)
@@ -205,6 +208,25 @@ def main():
             f()
         if evs is not None:
             evs[len(launches)].record(cur)
+
+    # The timed step: the same work, with rows 4096-4351 (fc1 on the 128 x 128
+    # tiles, then their fc2-input quantization) on a second stream from the
+    # fc1-input quantization on, so that they fill the CUs the main rows' fc1
+    # rounds leave free and overlap the main rows' fc2-input quantization
+    # (row-wise, so the quantized rows are the same bits); fc2 joins both.
+    side = torch.cuda.Stream(dev)
+
+    def step_two_streams():
+        cur = torch.cuda.current_stream(dev)
+        launches[0]()
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            launches[2]()
+            quant(h[MI:], q.FP32, MT, H, 4096, a2[MI:], s2[MI:])
+        launches[1]()
+        quant(h, q.FP32, MI, H, 4096, a2, s2)
+        cur.wait_stream(side)
+        launches[4]()
 
     # Clock ramp: the GPU raises its clocks only under sustained load (the
     # first few milliseconds of a burst run ~15% slower), so the step runs
@@ -238,34 +260,43 @@ def main():
                      for j, n in enumerate(names)}
     y_eager = y.clone()
 
-    # ---- the same step as one HIP graph (its five launches without the host
-    # launch gaps between them), replayed K times back to back between one
-    # event pair: ms_per_step and value are that span / K (the throughput of
-    # consecutive steps). Bracketing each replay with its own event pair
-    # instead adds a gap per replay on some boxes (graph slower than eager);
-    # that median is reported beside it.
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    torch.cuda.synchronize()
-    t_ramp = time.perf_counter()
-    while time.perf_counter() - t_ramp < min(args.ramp_s, 0.3):
-        for _ in range(20):
-            graph.replay()
+    # ---- the step on two streams captured as one HIP graph (without the host
+    # launch gaps), replayed K times back to back between one event pair:
+    # ms_per_step and value are that span / K (the throughput of consecutive
+    # steps). Bracketing each replay with its own event pair instead adds a
+    # gap per replay on some boxes (graph slower than eager); that median is
+    # reported beside it, and so is the one-stream step as a graph.
+    def graph_of(fn):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
         torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    g0 = torch.cuda.Event(enable_timing=True)
-    g1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    g0.record(stream)
-    for i in range(K):
-        graph.replay()
-    g1.record(stream)
-    torch.cuda.synchronize()
-    wall_graph = time.perf_counter() - t0
-    ms_step = g0.elapsed_time(g1) / K
+        return gr
+
+    def replay_span(gr):
+        t_ramp = time.perf_counter()
+        while time.perf_counter() - t_ramp < min(args.ramp_s, 0.3):
+            for _ in range(20):
+                gr.replay()
+            torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            gr.replay()
+        g0 = torch.cuda.Event(enable_timing=True)
+        g1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g0.record(stream)
+        for i in range(K):
+            gr.replay()
+        g1.record(stream)
+        torch.cuda.synchronize()
+        return g0.elapsed_time(g1) / K, time.perf_counter() - t0
+
+    graph = graph_of(step_two_streams)
+    y.zero_()
+    ms_step, wall_graph = replay_span(graph)
+    # every replay computes what the eager one-stream steps computed
+    graph_equals_eager = bool(torch.equal(y, y_eager))
     gev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     torch.cuda.synchronize()
     for i in range(K):
@@ -274,8 +305,11 @@ def main():
         gev[i][1].record(stream)
     torch.cuda.synchronize()
     ms_step_bracketed = float(np.median([a.elapsed_time(b) for a, b in gev]))
-    # every replay computes what the eager steps computed
-    graph_equals_eager = bool(torch.equal(y, y_eager))
+    del graph
+    graph = graph_of(step)
+    y.zero_()
+    ms_step_one_stream, _ = replay_span(graph)
+    graph_equals_eager = graph_equals_eager and bool(torch.equal(y, y_eager))
     del graph
     # fc1 of all 4352 rows as one call (the dispatcher sends the trailing tile
     # row to the small tiles), for comparison with the split above
@@ -316,8 +350,9 @@ def main():
     extra = {"per_kernel_ms_median": {k: round(v, 4) for k, v in per_kernel_ms.items()},
              "fc1_single_call_ms": round(ms_fc1_single, 4),
              "fc1_single_call_tflops": round(2.0 * M * D * H / ms_fc1_single / 1e9, 1),
-             "step_timing": "K back-to-back replays of the step captured as one HIP graph, span / K",
+             "step_timing": "K back-to-back replays of the two-stream step captured as one HIP graph, span / K",
              "ms_per_step_graph_bracketed_median": round(ms_step_bracketed, 4),
+             "ms_per_step_one_stream_graph": round(ms_step_one_stream, 4),
              "ms_per_step_eager": round(ms_step_eager, 4), "ms_per_step_eager_mean": round(total_ms / K, 4),
              "graph_equals_eager": graph_equals_eager,
              "wall_s_timed_eager": round(wall, 3), "wall_s_timed_graph": round(wall_graph, 3)}
@@ -337,7 +372,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "MMDiT MLP pair, M=4352 tokens (4096 image + 256 text): FWHT1024+int8 quant, "
                                "fc1 3072->12288 +bias+GELU-tanh (fp32; rows 0-4095 and 4096-4351 as two launches), "
-                               "FWHT4096+int8 quant, fc2 12288->3072 +bias (bf16)",
+                               "FWHT4096+int8 quant, fc2 12288->3072 +bias (bf16); rows 4096-4351's fc1 and "
+                               "fc2-input quant on a second stream",
                    "M": M, "hidden": D, "mlp": H, "weights": "N(0,0.02) -> W8A8 + Hadamard",
                    "frac_of_int8_peak": round(value / PEAK_INT8_TOPS, 4)},
         "roofline": roof,

@@ -289,8 +289,8 @@ def linear_forward_prequantized(act_q: torch.Tensor, act_scales: torch.Tensor, w
 def set_linear_kernel(which: int) -> int:
     """Select the quantized-linear kernel process-wide (LINEAR_AUTO,
     LINEAR_LARGE_TILE, LINEAR_SMALL_32, LINEAR_SMALL_64, LINEAR_GEMV,
-    LINEAR_LARGE_192, LINEAR_LARGE_224); returns the previous choice. Every choice gives the
-    same int8 results."""
+    LINEAR_LARGE_192, LINEAR_LARGE_224, LINEAR_LARGE_128); returns the previous choice. Every
+    choice gives the same int8 results."""
     prev = int(_lib.qimg_get_linear_kernel())
     _check(_lib.qimg_set_linear_kernel(int(which)))
     return prev
