@@ -215,6 +215,30 @@ def test_fwht_inplace_and_per_row(qimg, oracle):
     np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
 
 
+@pytest.mark.parametrize("K,hbs,in_bf16,fp8", [
+    (12288, 4096, False, False),  # the MLP's fc2 input
+    (12288, 4096, False, True),
+    (3072, 1024, True, False),    # the fc1 input
+])
+def test_activation_quant_row_split_identical(qimg, K, hbs, in_bf16, fp8):
+    """Quantization is row-wise: 4352 rows in one call equal rows 0-4095 and
+    4096-4351 in two calls (each call picks its kernel from its own row
+    count), as a caller that splits the image and text rows over two
+    streams relies on."""
+    M, MI = 4352, 4096
+    g = torch.Generator(device="cpu").manual_seed(K + fp8)
+    x = (torch.randn(M, K, generator=g) * torch.rand(M, 1, generator=g) * 10).to(DEV)
+    if in_bf16:
+        x = x.to(torch.bfloat16)
+    mode = qimg.FP8_HADAMARD if fp8 else qimg.INT8_HADAMARD
+    q_all, s_all = qimg.quantize_activation_hadamard(x, hbs, mode=mode)
+    q_a, s_a = qimg.quantize_activation_hadamard(x[:MI], hbs, mode=mode)
+    q_b, s_b = qimg.quantize_activation_hadamard(x[MI:], hbs, mode=mode)
+    torch.cuda.synchronize()
+    assert torch.equal(s_all, torch.cat([s_a, s_b]))
+    assert torch.equal(q_all.view(torch.uint8), torch.cat([q_a.view(torch.uint8), q_b.view(torch.uint8)]))
+
+
 def test_quant_repeatable_and_empty(qimg):
     x = torch.randn(64, 3072, device=DEV)
     a = qimg.quantize_activation_hadamard(x, 1024)
