@@ -139,7 +139,9 @@ def test_fp8_tile_widths(qimg, oracle, M, N, K):
     output's k-sum runs through the same MFMA sequence, so the two widths
     agree bit for bit (fp32 and bf16 out, GELU), on ragged tiles too (last
     tiles of 134, 40, 4 and 0 columns), and both are within the fp32
-    accumulation-order bound of the oracle's float64 sum."""
+    accumulation-order bound of the oracle's float64 sum: the fp32 output,
+    the bf16 output (plus its rounding) and the GELU output (plus the
+    GELU approximation's error)."""
     rng = np.random.default_rng(M + 7 * N + K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
@@ -160,7 +162,17 @@ def test_fp8_tile_widths(qimg, oracle, M, N, K):
     rows = (0, min(M, 300))
     ref = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, rows=rows)[rows[0]:rows[1]]
     got = outs["w192"][0].cpu().numpy()[rows[0]:rows[1]]
-    assert np.max(np.abs(got - ref)) <= 1e-5 * np.abs(ref).max() * np.sqrt(K / 64)
+    bound = 1e-5 * np.abs(ref).max() * np.sqrt(K / 64)
+    assert np.max(np.abs(got - ref)) <= bound
+    # bf16 out: the round-to-nearest of a value within that bound (half a
+    # bf16 ulp is at most 2^-8 relative)
+    got_h = outs["w192"][1].float().cpu().numpy()[rows[0]:rows[1]]
+    assert np.all(np.abs(got_h - ref) <= np.abs(ref) * 2.0 ** -8 + 1.01 * bound)
+    # GELU: the bound carried through GELU (slope below 1.13) plus the
+    # GELU approximation's own 2e-6
+    ref_g = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, gelu=True, rows=rows)[rows[0]:rows[1]]
+    got_g = outs["w192"][2].cpu().numpy()[rows[0]:rows[1]]
+    assert np.max(np.abs(got_g - ref_g)) <= 1.13 * bound + 2e-6 * np.abs(ref_g).max()
 
 
 @pytest.mark.slow
