@@ -382,12 +382,19 @@ def test_small_m_fp8(qimg, oracle, M, N, K):
     ref = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, rows=(0, M))
     qw = _qw(qimg, wq, ws, hbs, mode=qimg.FP8_HADAMARD)
     got = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits))
+    got_h = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits), out_dtype=torch.bfloat16)
+    got_g = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits), apply_gelu=True)
     with qimg.linear_kernel(qimg.LINEAR_LARGE_TILE):
         got_l = qimg.linear_forward_quantized(_dev(x), qw, _bf16_dev(b_bits))
     torch.cuda.synchronize()
     bound = 1e-5 * np.abs(ref).max() * np.sqrt(K / 64)
     assert np.max(np.abs(got.cpu().numpy() - ref)) <= bound
     assert np.max(np.abs(got_l.cpu().numpy() - ref)) <= bound
+    # bf16 out within the bound plus half a bf16 ulp; GELU within the bound
+    # through GELU's slope plus the approximation's error
+    assert np.all(np.abs(got_h.float().cpu().numpy() - ref) <= np.abs(ref) * 2.0 ** -8 + 1.01 * bound)
+    ref_g = oracle.gemm_fp8_epilogue(xq, wq, xs, ws, b_bits, gelu=True, rows=(0, M))
+    assert np.max(np.abs(got_g.cpu().numpy() - ref_g)) <= 1.13 * bound + 2e-6 * np.abs(ref_g).max()
 
 
 @pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4400, 12288, 1024), (4352, 12288, 256)])
