@@ -1505,13 +1505,13 @@ static TileSize best_tile(F tiles_wh, int cus, bool blocks32) {
 }
 
 // The large-tile plan of an automatic choice (K % 128 == 0, not a small-M
-// case): rows [0, m_big) on the large tiles, the rest on the 64x64 kernel,
-// and the tile width.
+// case): rows [0, m_big) on the large tiles, the rest on smaller ones (int8:
+// 128x128 tiles, e4m3: the 64x64 kernel), and the tile width.
 //  - One tile per CU at a time. When the last round of 256x256 tiles would
-//    be mostly idle, the trailing tile rows (at most two) go to the 64x64
-//    kernel, which spreads them over every CU (M = 4352 = 4096 + 256 rows,
-//    N = 12288: 816 tiles = 3 rounds + 48 tiles; the 48 become 192 small
-//    tiles).
+//    be mostly idle, the trailing tile rows (at most two) go to the smaller
+//    tiles, which spread them over every CU (M = 4352 = 4096 + 256 rows,
+//    N = 12288: 816 tiles = 3 rounds + 48 tiles; the 48 become 192 tiles of
+//    128x128, or 768 of 64x64).
 //  - Otherwise the tile whose rounds, each weighted by the tile's share of
 //    a 256x256 tile's time, add up to least (best_tile): 4096 x 3072 runs
 //    256 tiles of 256x192 in one round (192 tiles of 256x256 leave a quarter
