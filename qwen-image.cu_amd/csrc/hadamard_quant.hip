@@ -445,6 +445,15 @@ struct LnLoader : RowsLoader<float> {
     }
     template <int NB>
     __device__ __forceinline__ void finish_row(int /*row*/, int lane, float (&v)[NB][16]) const {
+        finish_row_get<NB>(lane, v, [&](int j, int e, v4f& sh, v4f& sc) {
+            sh = reinterpret_cast<const v4f*>(shift + j * 1024 + 16 * lane)[e];
+            sc = reinterpret_cast<const v4f*>(scale + j * 1024 + 16 * lane)[e];
+        });
+    }
+    // (get(j, e, sh, sc) gives float4 e of the lane's chunk j of shift and
+    // scale)
+    template <int NB, typename Get>
+    __device__ __forceinline__ void finish_row_get(int lane, float (&v)[NB][16], Get get) const {
 #pragma clang fp contract(off)
         static_assert(NB <= LN_MAXV && LN_THR == 256, "ln_modulate_row's thread layout");
         float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -469,12 +478,12 @@ struct LnLoader : RowsLoader<float> {
         const float inv_std = rsqrtf(total((q[0] + q[1]) + (q[2] + q[3])) / K + eps);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const v4f* sh = reinterpret_cast<const v4f*>(shift + j * 1024 + 16 * lane);
-            const v4f* sc = reinterpret_cast<const v4f*>(scale + j * 1024 + 16 * lane);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
+                v4f sh, sc;
+                get(j, e, sh, sc);
                 const v4f xv = (v4f){v[j][4 * e], v[j][4 * e + 1], v[j][4 * e + 2], v[j][4 * e + 3]};
-                const v4f o = (xv - mean) * inv_std * (1.0f + sc[e]) + sh[e];
+                const v4f o = (xv - mean) * inv_std * (1.0f + sc) + sh;
                 v[j][4 * e] = o.x;
                 v[j][4 * e + 1] = o.y;
                 v[j][4 * e + 2] = o.z;
@@ -524,24 +533,13 @@ struct PairLoader {
     }
 };
 
-template <typename Loader, RowOut OUT, int NB, typename Dest>
-__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, Dest dst, int M, int K, float norm) {
+// The transform, absmax and quantized store of one row held as lane l's
+// 16-value chunk l of each of the NB blocks (v), through the wave's LDS
+// buffer (lds, HBS + HBS / 16 floats).
+template <RowOut OUT, int NB, typename Dest>
+__device__ __forceinline__ void wave_row_fwht_quant_store(float (&v)[NB][16], float* lds, int lane, int row, int K,
+                                                          float norm, const Dest& dst) {
     constexpr int HBS = 1024;
-    constexpr int PADDED = HBS + HBS / 16;
-    __shared__ float lds_all[4 * PADDED];
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave;
-    if (row >= M) return;  // whole waves: no barrier below
-    float* lds = lds_all + wave * PADDED;
-
-    typename Loader::Raw raw[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) ld.fetch(row, b * (HBS / 16) + lane, raw[b]);
-    float v[NB][16];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) Loader::unpack(raw[b], v[b]);
-    if constexpr (Loader::kWholeRow) ld.template finish_row<NB>(row, lane, v);
     float amax = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -595,6 +593,122 @@ __global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, De
 #pragma unroll
             for (int c = 0; c < 4; ++c) o[b * HBS + 64 * c + 256 * i] = static_cast<uint8_t>(w >> (8 * c));
         }
+}
+
+template <typename Loader, RowOut OUT, int NB, typename Dest>
+__global__ __launch_bounds__(256) void fwht_quant_wave_rows_kernel(Loader ld, Dest dst, int M, int K, float norm) {
+    constexpr int HBS = 1024;
+    constexpr int PADDED = HBS + HBS / 16;
+    __shared__ float lds_all[4 * PADDED];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= M) return;  // whole waves: no barrier below
+    float* lds = lds_all + wave * PADDED;
+
+    typename Loader::Raw raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ld.fetch(row, b * (HBS / 16) + lane, raw[b]);
+    float v[NB][16];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) Loader::unpack(raw[b], v[b]);
+    if constexpr (Loader::kWholeRow) ld.template finish_row<NB>(row, lane, v);
+    wave_row_fwht_quant_store<OUT, NB>(v, lds, lane, row, K, norm, dst);
+}
+
+// LayerNorm + modulate + FWHT quant rows as above, eight rows (waves) per
+// workgroup sharing the modulation vectors: the workgroup stages the shift
+// and scale of its first row's stream in LDS once, instead of every wave
+// reading its 2 K floats from L2 (at 4352 rows those reads were twice the
+// activation bytes, and replacing them by constants made the kernel 22%
+// faster). A wave whose row belongs to the other stream (only in the
+// workgroup that straddles the two) reads them from global memory. Every
+// wave reaches the one barrier before a wave past M leaves.
+// (LDS chunk c of the staged vectors is stored at c ^ ((c >> 4) & 3): the
+// 16 lanes of a ds_read_b128 read chunks 4 l + e, which lands them on 16
+// different bank groups; the staging writes stay conflict-free too.)
+__device__ __forceinline__ int ln_vec_swz(int c) { return c ^ ((c >> 4) & 3); }
+
+template <RowOut OUT, int NB>
+__global__ __launch_bounds__(512) void ln_fwht_quant_rows8_kernel(PairLoader<LnLoader> ld, PairDest dst, int M,
+                                                                  float norm) {
+    constexpr int HBS = 1024;
+    constexpr int PADDED = HBS + HBS / 16;
+    constexpr int K = NB * HBS;
+    constexpr int NCH = 2 * K / 4;               // 16-byte chunks of shift, then scale
+    constexpr int PER = (NCH + 511) / 512;       // chunks staged by each thread
+    __shared__ float lds_all[8 * PADDED];
+    __shared__ __attribute__((aligned(16))) float lds_vec[2 * K];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row0 = blockIdx.x * 8;  // < M
+    const int row = row0 + wave;
+    const bool active = row < M;
+    const bool staged_a = row0 < ld.Ma;
+    const LnLoader& ls = staged_a ? ld.a : ld.b;
+
+    // the staged vectors' loads first, then the row's (a wave past M loads
+    // row M - 1 and drops it)
+    v4f stg[PER];
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int ci = threadIdx.x + 512 * t;
+        if (ci < NCH)
+            stg[t] = ci < K / 4 ? reinterpret_cast<const v4f*>(ls.shift)[ci]
+                                : reinterpret_cast<const v4f*>(ls.scale)[ci - K / 4];
+    }
+    const int rr = active ? row : M - 1;
+    typename LnLoader::Raw raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ld.fetch(rr, b * (HBS / 16) + lane, raw[b]);
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int ci = threadIdx.x + 512 * t;
+        if (ci < NCH) *reinterpret_cast<v4f*>(lds_vec + 4 * ln_vec_swz(ci)) = stg[t];
+    }
+    __syncthreads();
+    if (!active) return;
+
+    float v[NB][16];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) LnLoader::unpack(raw[b], v[b]);
+    const bool in_a = row < ld.Ma;
+    if (in_a == staged_a) {
+        const LnLoader& l = in_a ? ld.a : ld.b;
+        l.finish_row_get<NB>(lane, v, [&](int j, int e, v4f& sh, v4f& sc) {
+            const int c = 256 * j + 4 * lane + e;
+            sh = *reinterpret_cast<const v4f*>(lds_vec + 4 * ln_vec_swz(c));
+            sc = *reinterpret_cast<const v4f*>(lds_vec + 4 * ln_vec_swz(K / 4 + c));
+        });
+    } else {
+        ld.finish_row<NB>(row, lane, v);
+    }
+    wave_row_fwht_quant_store<OUT, NB>(v, lds_all + wave * PADDED, lane, row, K, norm, dst);
+}
+
+template <RowOut OUT>
+static hipError_t launch_ln_rows8(const PairLoader<LnLoader>& ld, const PairDest& dst, int M, int K, float norm,
+                                  hipStream_t stream) {
+    const int blocks = (M + 7) / 8;
+    switch (K / 1024) {
+        case 1:
+            hipLaunchKernelGGL((ln_fwht_quant_rows8_kernel<OUT, 1>), dim3(blocks), dim3(512), 0, stream, ld, dst, M,
+                               norm);
+            break;
+        case 2:
+            hipLaunchKernelGGL((ln_fwht_quant_rows8_kernel<OUT, 2>), dim3(blocks), dim3(512), 0, stream, ld, dst, M,
+                               norm);
+            break;
+        case 3:
+            hipLaunchKernelGGL((ln_fwht_quant_rows8_kernel<OUT, 3>), dim3(blocks), dim3(512), 0, stream, ld, dst, M,
+                               norm);
+            break;
+        default:
+            hipLaunchKernelGGL((ln_fwht_quant_rows8_kernel<OUT, 4>), dim3(blocks), dim3(512), 0, stream, ld, dst, M,
+                               norm);
+            break;
+    }
+    return hipGetLastError();
 }
 
 // The INT4 linear's input preparation (linear_forward_int4, cuda_kernels.cu:
@@ -877,10 +991,11 @@ hipError_t launch_ln_fwht_quant(const float* x, const float* shift, const float*
     // e4m3: 53.1 -> 45.4 us; with 256 or 300 rows one workgroup per row is
     // faster, 6.4 against 7.2 us)
     if (hbs == 1024 && K % 1024 == 0 && M >= 1024) {
-        const LnLoader ld{{x, K}, shift, scale, eps};
-        return mode == QIMG_QM_FP8_HADAMARD
-                   ? launch_wave_rows<RowOut::Fp8>(ld, q_out, scales, M, K, norm, stream)
-                   : launch_wave_rows<RowOut::Int8>(ld, q_out, scales, M, K, norm, stream);
+        const LnLoader l{{x, K}, shift, scale, eps};
+        const PairLoader<LnLoader> ld{l, l, M};
+        const PairDest dst{RowDest{q_out, scales}, RowDest{q_out, scales}, M};
+        return mode == QIMG_QM_FP8_HADAMARD ? launch_ln_rows8<RowOut::Fp8>(ld, dst, M, K, norm, stream)
+                                            : launch_ln_rows8<RowOut::Int8>(ld, dst, M, K, norm, stream);
     }
     if (mode == QIMG_QM_FP8_HADAMARD)
         hipLaunchKernelGGL(ln_fwht_quant_kernel<RowOut::Fp8>, dim3(M), dim3(LN_THR), lds, stream, x, shift, scale,
@@ -928,8 +1043,8 @@ hipError_t launch_ln_fwht_quant_pair(const float* xa, const float* shift_a, cons
     const PairLoader<LnLoader> ld{LnLoader{{xa, K}, shift_a, scale_a, eps}, LnLoader{{xb, K}, shift_b, scale_b, eps},
                                   Ma};
     const PairDest dst{RowDest{qa, sa}, RowDest{qb, sb}, Ma};
-    return mode == QIMG_QM_FP8_HADAMARD ? launch_wave_rows<RowOut::Fp8>(ld, dst, Ma + Mb, K, norm, stream)
-                                        : launch_wave_rows<RowOut::Int8>(ld, dst, Ma + Mb, K, norm, stream);
+    return mode == QIMG_QM_FP8_HADAMARD ? launch_ln_rows8<RowOut::Fp8>(ld, dst, Ma + Mb, K, norm, stream)
+                                        : launch_ln_rows8<RowOut::Int8>(ld, dst, Ma + Mb, K, norm, stream);
 }
 
 hipError_t launch_heads_fwht_quant_pair(const uint16_t* attn, int batch, int H, int S, int n_txt, int n_img, int hbs,
