@@ -1366,8 +1366,10 @@ def _block_summary(trace, img_rows, txt_rows, title, cmd, ops_note):
     for a, b in zip(idx, idx[1:] + [len(trace)]):
         seq = trace[a:b]
         ln = [r for r in seq if "LnLoader" in r["Kernel_Name"]]
+        # (a workgroup per row, a wave per row in fours, or in eights)
         if ln and int(ln[0]["Grid_Size_X"]) in (img_rows * 256, (img_rows + 3) // 4 * 256,
-                                                 (img_rows + txt_rows + 3) // 4 * 256):
+                                                 (img_rows + txt_rows + 3) // 4 * 256,
+                                                 (img_rows + 7) // 8 * 512, (img_rows + txt_rows + 7) // 8 * 512):
             blocks.append(seq)
     if not blocks:
         return [title, f"command: {cmd}", "no block found in the trace"]
