@@ -110,8 +110,8 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
 /* Kernel selection for qimg_linear_prequantized / qimg_linear when K is a
  * multiple of 64. No counterpart in the reference (cuBLAS picks its own
  * algorithm); it exists for tests and tuning, which compare the kernels on
- * one shape. AUTO (the default) takes the vector-ALU GEMV for int8 with
- * M <= 4, 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
+ * one shape. AUTO (the default) takes the vector-ALU GEMV for M <= 4
+ * (int8, and e4m3 with fp32 accumulation), 32x32 tiles for M <= 32, 64x64 tiles when fewer than 64 tiles of
  * 256x256 would cover the output (int8 of 128 rows or more: fewer than 32),
  * and the large-tile kernel otherwise: 256 rows of 256, 224 or 192 columns,
  * or int8 128x128 tiles (two per CU), whichever's rounds of tiles on the
@@ -122,7 +122,7 @@ int qimg_linear_prequantized(const void* act_q, const float* act_scales, int M, 
  * columns. LARGE_192, LARGE_224 and LARGE_128 force those tiles (e4m3 runs
  * 224 and 128 as 256x256); qimg_linear_bf16's large-tile path follows
  * LARGE_TILE and LARGE_192 too.
- * GEMV with e4m3 or M > 4 runs the 32x32 tiles. Process-wide; returns
+ * GEMV with M > 4 runs the 32x32 tiles. Process-wide; returns
  * QIMG_OK, or QIMG_ERR_INVALID_ARG for an unknown value. All choices give
  * identical int8 results. */
 enum {

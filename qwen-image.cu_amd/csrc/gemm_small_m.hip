@@ -30,6 +30,7 @@
 //
 // Rows past M and columns past N read as zero and are never stored. The
 // byte sizes M*K and N*K must be below 2^31 (buffer offsets are 32-bit).
+#include <type_traits>
 #include <utility>
 
 #include "qimg_device.h"
@@ -549,14 +550,19 @@ hipError_t launch_small_dma(const void* a, const float* as, int M, int K, const 
     return hipGetLastError();
 }
 
-// int8 rows of A at most GV_MAXM: a weight-streaming GEMV on the vector ALU.
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// Rows of A at most GV_MAXM: a weight-streaming GEMV on the vector ALU.
 // Each wave owns RW consecutive weight rows and reads them front to back,
 // 1 KB per load instruction (lane i takes bytes 16i.. of each 1 KB piece),
 // so the wave streams one contiguous RW*K-byte range of W; every lane also
 // loads the matching 16 bytes of the MR activation rows (cache hits after
-// the first wave). v_dot4_i32_i8 accumulates per lane, a wave reduction
-// gives each (m, n) dot product, exact in int32. Out-of-range rows and
-// chunks read as zero through buffer loads, as in the MFMA kernel.
+// the first wave). int8: v_dot4_i32_i8 accumulates per lane, a wave
+// reduction gives each (m, n) dot product, exact in int32. e4m3 (FP8): the
+// bytes are converted to fp32 (v_cvt_pk_f32_fp8; each product of two e4m3
+// values is exact in fp32) and accumulated with fp32 FMAs per lane, then
+// summed over the wave. Out-of-range rows and chunks read as zero through
+// buffer loads, as in the MFMA kernel.
 constexpr int GV_MAXM = 4;
 
 // The weight-side operands of one GEMV of a launch.
@@ -573,7 +579,7 @@ struct GemvOut {
 // ONE: the whole row fits in IU chunks per lane (K <= IU*1024): all loads
 // are issued at once and nothing is loaded past K; otherwise steps of IU
 // chunks alternate between two register sets.
-template <int MR, int RW, int IU, bool ONE, int OUT_DT, bool GELU>
+template <int MR, int RW, int IU, bool ONE, int OUT_DT, bool GELU, bool FP8 = false>
 __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(const uint8_t* __restrict__ A, const float* __restrict__ as,
                                                          int M, int K, GemvOut g0, GemvOut g1, int split) {
     const bool second = static_cast<int>(blockIdx.x) >= split;
@@ -612,7 +618,8 @@ __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(const uint8_t* __restri
     const float e_ws = ws[e_nc];
     const uint16_t e_b = (has_bias ? bias : reinterpret_cast<const uint16_t*>(ws))[e_nc];
 
-    int acc[MR][RW];
+    typedef typename std::conditional<FP8, float, int>::type acc_t;
+    acc_t acc[MR][RW];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
@@ -638,20 +645,51 @@ __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(const uint8_t* __restri
     };
     auto compute = [&](int set) {
 #pragma unroll
-        for (int u = 0; u < IU; ++u)
+        for (int u = 0; u < IU; ++u) {
+            if constexpr (FP8) {
+                // 16 e4m3 bytes -> 16 fp32, in byte order
+                auto widen = [](const v4i& c, float (&f)[16]) {
 #pragma unroll
-            for (int m = 0; m < MR; ++m)
+                    for (int d = 0; d < 4; ++d) {
+                        const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(c[d], false);
+                        const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(c[d], true);
+                        f[4 * d] = lo.x;
+                        f[4 * d + 1] = lo.y;
+                        f[4 * d + 2] = hi.x;
+                        f[4 * d + 3] = hi.y;
+                    }
+                };
+                float af[MR][16];
+#pragma unroll
+                for (int m = 0; m < MR; ++m) widen(fa[set][u][m], af[m]);
 #pragma unroll
                 for (int q = 0; q < RW; ++q) {
-                    const v4i a = fa[set][u][m];
-                    const v4i w = fw[set][u][q];
-                    int t = acc[m][q];
-                    t = __builtin_amdgcn_sdot4(a.x, w.x, t, false);
-                    t = __builtin_amdgcn_sdot4(a.y, w.y, t, false);
-                    t = __builtin_amdgcn_sdot4(a.z, w.z, t, false);
-                    t = __builtin_amdgcn_sdot4(a.w, w.w, t, false);
-                    acc[m][q] = t;
+                    float wf[16];
+                    widen(fw[set][u][q], wf);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        float t = acc[m][q];
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) t = __builtin_fmaf(af[m][e], wf[e], t);
+                        acc[m][q] = t;
+                    }
                 }
+            } else {
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int q = 0; q < RW; ++q) {
+                        const v4i a = fa[set][u][m];
+                        const v4i w = fw[set][u][q];
+                        int t = acc[m][q];
+                        t = __builtin_amdgcn_sdot4(a.x, w.x, t, false);
+                        t = __builtin_amdgcn_sdot4(a.y, w.y, t, false);
+                        t = __builtin_amdgcn_sdot4(a.z, w.z, t, false);
+                        t = __builtin_amdgcn_sdot4(a.w, w.w, t, false);
+                        acc[m][q] = t;
+                    }
+            }
+        }
     };
     load(0, 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -669,12 +707,12 @@ __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(const uint8_t* __restri
     }
 
     // wave reductions; lane m*RW + q keeps the (m, q) total
-    int mine = 0;
+    acc_t mine = 0;
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int q = 0; q < RW; ++q) {
-            const int tot = wave_sum_dpp(acc[m][q]);
+            const acc_t tot = wave_sum_dpp(acc[m][q]);
             mine = lane == m * RW + q ? tot : mine;
         }
     if (lane < MR * RW && e_m < M && e_n < N) {
@@ -686,7 +724,7 @@ __global__ __launch_bounds__(SM_THR) void gemv_i8_kernel(const uint8_t* __restri
     }
 }
 
-template <int MR, int RW, int IU, bool ONE>
+template <int MR, int RW, int IU, bool ONE, bool FP8>
 hipError_t launch_gemv(const void* a, const float* as, int M, int K, const GemvOut& g0, const GemvOut& g1,
                        int out_dt, int gelu, hipStream_t stream) {
     auto blocks_of = [](int N) {
@@ -697,7 +735,7 @@ hipError_t launch_gemv(const void* a, const float* as, int M, int K, const GemvO
     const int blocks = split + (g1.N > 0 ? blocks_of(g1.N) : 0);
     const uint8_t* A = static_cast<const uint8_t*>(a);
 #define QIMG_GEMV_LAUNCH(ODT, GL)                                                                              \
-    hipLaunchKernelGGL((gemv_i8_kernel<MR, RW, IU, ONE, ODT, GL>), dim3(blocks), dim3(SM_THR), 0, stream, A, as, M, \
+    hipLaunchKernelGGL((gemv_i8_kernel<MR, RW, IU, ONE, ODT, GL, FP8>), dim3(blocks), dim3(SM_THR), 0, stream, A, as, M, \
                        K, g0, g1, split)
     if (out_dt == QIMG_FP32) {
         if (gelu)
@@ -714,11 +752,12 @@ hipError_t launch_gemv(const void* a, const float* as, int M, int K, const GemvO
     return hipGetLastError();
 }
 
+template <bool FP8>
 hipError_t dispatch_gemv(const void* a, const float* as, int M, int K, const GemvOut& g0, const GemvOut& g1,
                          int out_dt, int gelu, hipStream_t stream) {
     const int chunks = ((K >> 4) + 63) >> 6;  // 16-byte chunks per lane
 #define QIMG_GEMV(MR_, RW_, IU_, ONE_) \
-    return launch_gemv<MR_, RW_, IU_, ONE_>(a, as, M, K, g0, g1, out_dt, gelu, stream)
+    return launch_gemv<MR_, RW_, IU_, ONE_, FP8>(a, as, M, K, g0, g1, out_dt, gelu, stream)
     if (M <= 2 && chunks <= 4) {
         if (M == 1) {
             if (chunks == 1) QIMG_GEMV(1, 8, 1, true);
@@ -743,18 +782,19 @@ bool small_m_fits(int M, int N, int K) {
            static_cast<int64_t>(N) * K < (int64_t{1} << 31);
 }
 
-// Two int8 linears of the same M <= GV_MAXM activation in one GEMV launch
-// (false: not that case; the caller then runs them one at a time).
+// Two linears of the same M <= GV_MAXM activation and mode in one GEMV
+// launch (false: not that case; the caller then runs them one at a time).
 bool launch_gemv_pair(const void* act_q, const float* act_scales, int M, int K, const LinearArgs& a,
-                      const LinearArgs& b, int out_dtype, hipStream_t stream, hipError_t* err) {
+                      const LinearArgs& b, int mode, int out_dtype, hipStream_t stream, hipError_t* err) {
     if (!(get_linear_kernel() == QIMG_LINEAR_AUTO && M >= 1 && M <= GV_MAXM && small_m_fits(M, a.N, K) &&
           small_m_fits(M, b.N, K) && a.K == K && b.K == K &&
           small_m_variant(M, a.N, K) == 3 && small_m_variant(M, b.N, K) == 3))
         return false;
-    *err = dispatch_gemv(act_q, act_scales, M, K,
-                         GemvOut{static_cast<const uint8_t*>(a.w_q), a.w_scales, a.bias, a.out, a.N},
-                         GemvOut{static_cast<const uint8_t*>(b.w_q), b.w_scales, b.bias, b.out, b.N}, out_dtype, 0,
-                         stream);
+    const GemvOut ga{static_cast<const uint8_t*>(a.w_q), a.w_scales, a.bias, a.out, a.N};
+    const GemvOut gb{static_cast<const uint8_t*>(b.w_q), b.w_scales, b.bias, b.out, b.N};
+    *err = mode == QIMG_QM_FP8_HADAMARD
+               ? dispatch_gemv<true>(act_q, act_scales, M, K, ga, gb, out_dtype, 0, stream)
+               : dispatch_gemv<false>(act_q, act_scales, M, K, ga, gb, out_dtype, 0, stream);
     return true;
 }
 
@@ -777,11 +817,12 @@ hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int
     // us at M = 256, in-process A/B, output identical); at K = 3072 they
     // measured equal.
     const bool whole_lines = (K % (128 * (SM_THR / 64))) == 0 && K >= 8192;
-    if (variant == 3 && !fp8 && M <= GV_MAXM)
-        return dispatch_gemv(act_q, act_scales, M, K,
-                             GemvOut{static_cast<const uint8_t*>(w_q), w_scales, bias, out, N}, GemvOut{}, out_dtype,
-                             gelu, stream);
-    if (variant == 3) variant = 1;  // e4m3, or more rows than the GEMV takes
+    if (variant == 3 && M <= GV_MAXM) {
+        const GemvOut g{static_cast<const uint8_t*>(w_q), w_scales, bias, out, N};
+        return fp8 ? dispatch_gemv<true>(act_q, act_scales, M, K, g, GemvOut{}, out_dtype, gelu, stream)
+                   : dispatch_gemv<false>(act_q, act_scales, M, K, g, GemvOut{}, out_dtype, gelu, stream);
+    }
+    if (variant == 3) variant = 1;  // more rows than the GEMV takes
     if (variant == 1 && lds_staged)
         return fp8 ? launch_small_dma<true, 1, 1, 4>(act_q, act_scales, M, K, w_q, w_scales, N, bias, out,
                                                      out_dtype, gelu, stream)

@@ -198,12 +198,14 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // both modulation linears in one GEMV launch where they share the
         // activation quantization (int8, the reference's weights)
         bool mods_done = false;
-        if (same_quant(b.img_mod, b.txt_mod) && b.img_mod.mode == QIMG_QM_INT8_HADAMARD) {
+        if (same_quant(b.img_mod, b.txt_mod) &&
+            (b.img_mod.mode == QIMG_QM_INT8_HADAMARD || b.img_mod.mode == QIMG_QM_FP8_HADAMARD)) {
             const LinearArgs mi{w.mod_q, w.mod_scale, 1, b.img_mod.K, b.img_mod.w, b.img_mod.scales, b.img_mod.N,
                                 b.img_mod.bias, w.img_mods, nullptr, nullptr};
             const LinearArgs mt{w.mod_q, w.mod_scale, 1, b.txt_mod.K, b.txt_mod.w, b.txt_mod.scales, b.txt_mod.N,
                                 b.txt_mod.bias, w.txt_mods, nullptr, nullptr};
-            mods_done = launch_gemv_pair(w.mod_q, w.mod_scale, 1, b.img_mod.K, mi, mt, QIMG_FP32, s, &e);
+            mods_done =
+                launch_gemv_pair(w.mod_q, w.mod_scale, 1, b.img_mod.K, mi, mt, b.img_mod.mode, QIMG_FP32, s, &e);
             if (mods_done && e != hipSuccess) goto done;
         }
         if (!mods_done) {

@@ -186,13 +186,13 @@ constexpr int kSmallMTileLimit = 64;
 // 16.4 against 15.2 us, kept on 64x64)
 constexpr int kMidTileMin = 32;
 int small_m_variant(int M, int N, int K);
-// Two int8 linears of one M <= 4 activation (act_q, act_scales, K) as one
-// GEMV launch into a.out and b.out (a.act_q / b.act_q are not read). Returns
-// false, launching nothing, when the pair is not that case (or a kernel
-// choice other than AUTO is set); otherwise true with the launch status in
-// *err.
+// Two int8 or two e4m3 (mode) linears of one M <= 4 activation (act_q,
+// act_scales, K) as one GEMV launch into a.out and b.out (a.act_q / b.act_q
+// are not read). Returns false, launching nothing, when the pair is not
+// that case (or a kernel choice other than AUTO is set); otherwise true with
+// the launch status in *err.
 bool launch_gemv_pair(const void* act_q, const float* act_scales, int M, int K, const LinearArgs& a,
-                      const LinearArgs& b, int out_dtype, hipStream_t stream, hipError_t* err);
+                      const LinearArgs& b, int mode, int out_dtype, hipStream_t stream, hipError_t* err);
 bool small_m_fits(int M, int N, int K);  // sizes the small-tile kernels can address
 hipError_t launch_linear_small_m(const void* act_q, const float* act_scales, int M, int K, const void* w_q,
                                  const float* w_scales, int N, int mode, const uint16_t* bias, void* out,

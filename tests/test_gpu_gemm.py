@@ -368,11 +368,14 @@ def test_small_m_linear_matches_oracle(qimg, oracle, M, N, K, gelu):
                                   oracle.bf16_bits_to_f32(oracle.bf16_bits_from_f32(got)).reshape(M, N))
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 18432, 3072), (256, 3072, 3072), (9, 100, 12288)])
+@pytest.mark.parametrize("M,N,K", [(1, 18432, 3072), (2, 5000, 12288), (3, 1000, 3072), (4, 130, 1024),
+                                   (256, 3072, 3072), (9, 100, 12288)])
 def test_small_m_fp8(qimg, oracle, M, N, K):
-    """e4m3 at small M: the oracle's float64 sum of the exact e4m3 products,
-    within the fp32 accumulation-order bound; the small and large kernels
-    agree to the same bound."""
+    """e4m3 at small M (M <= 4: the vector-ALU GEMV, fp32 FMAs of the
+    widened bytes; longer K in two alternating register sets): the oracle's
+    float64 sum of the exact e4m3 products, within the fp32
+    accumulation-order bound; the small and large kernels agree to the
+    same bound."""
     rng = np.random.default_rng(M + N + K + 5)
     x = rng.standard_normal((M, K)).astype(np.float32)
     w_bits = oracle.bf16_bits_from_f32((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
