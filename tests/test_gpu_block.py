@@ -292,21 +292,24 @@ def test_mmdit_block_within_oracle_noise_floor(qimg, oracle, blk, request, n_img
         assert 1 - cos <= max(1e-5, 2.5 * (1 - cos_self)), (cos, cos_self)
 
 
-def test_mmdit_blocks_batched_equals_sequential(qimg, oracle, int8_block):
+@pytest.mark.parametrize("n_img,n_txt,hw", [(64, 16, (16, 16)), (1029, 35, (42, 98))])
+def test_mmdit_blocks_batched_equals_sequential(qimg, oracle, int8_block, n_img, n_txt, hw):
     """Two blocks over two sequences batched (the CFG pair as one forward)
     reproduce, bit for bit, each sequence run alone through the same two
     blocks: every row of a linear and every head of the attention computes
-    the same thing at either batch, and int8 accumulation is exact."""
+    the same thing at either batch, and int8 accumulation is exact. At
+    1029 + 35 tokens the LayerNorms run eight rows per workgroup with a
+    workgroup straddling the image and text rows (image rows 1029 and 2058:
+    at different rows in the two runs)."""
     W, B, N, _ = int8_block
     W2 = {k: qimg.QuantizedWeight(v.data.flip(0).contiguous(), v.scales.flip(0).contiguous(), v.had_block_size,
                                   v.mode) for k, v in W.items()}
     table = qimg.BlockTable([(W, B, N), (W2, B, N)])
     rng = np.random.default_rng(11)
-    n_img, n_txt = 64, 16
     img = rng.standard_normal((2, n_img, 3072)).astype(np.float32)
     txt = rng.standard_normal((2, n_txt, 3072)).astype(np.float32)
     t_emb = _dev(rng.standard_normal(3072).astype(np.float32))
-    pe = _dev(qimg.qwen_image_pe(16, 16, 2, n_txt))
+    pe = _dev(qimg.qwen_image_pe(hw[0], hw[1], 2, n_txt))
     ib, tb = _dev(img), _dev(txt)
     prof = qimg.mmdit_blocks_forward(table, ib, tb, t_emb, pe, profile=True)
     assert set(prof) == set(qimg.PROF_CATEGORIES) and sum(prof.values()) > 0
