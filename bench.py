@@ -771,10 +771,12 @@ def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
     weights and N(0, 0.01) biases, RMSNorm weights 1, the Qwen-Image RoPE
     table for a 64x64 latent grid, SageAttention. `copies` weight sets
     (340 MB each) alternate so weights stream from HBM as in a 60-block
-    forward. ms/block: the median over 21 replays of a HIP graph of `blocks`
-    consecutive blocks; the 13-category split from events around each
-    category (no synchronisation between categories), averaged over
-    `profiled` eager blocks."""
+    forward. ms/block: the median over 21 replays of a HIP graph of one
+    qimg_mmdit_blocks_forward call over `blocks` consecutive blocks, divided
+    by `blocks` (block_c4_single_call_ms: the same blocks as single-block
+    calls); the 13-category split from events around each category (no
+    synchronisation between categories), averaged over the blocks of eager
+    multi-block calls (`profiled` blocks or more)."""
     n_img, n_txt, D, MLPD = 4096, 256, 3072, 12288
     shapes = {"img_mod": (6 * D, D), "txt_mod": (6 * D, D)}
     for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
@@ -800,25 +802,32 @@ def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
     scratch = torch.empty(q.mmdit_block_scratch_bytes(n_img, n_txt), dtype=torch.uint8, device=dev)
     img0, txt0 = img.clone(), txt.clone()
 
+    # The blocks as a forward runs them: one qimg_mmdit_blocks_forward call
+    # over `blocks` blocks (silu(t_emb) and its quantization once per call,
+    # as in the 60-block step); the single-block entry point, which redoes
+    # them in every call as transformer.cu:506-512 does per block, is timed
+    # beside it.
+    table = q.BlockTable([(sets[i % copies][0], sets[i % copies][1], norms) for i in range(blocks)])
+
     def block(i):
         W, B = sets[i % copies]
         return lambda: q.mmdit_block_forward(W, B, norms, img, txt, t_emb, pe, scratch=scratch)
 
+    ms_graph = _time_cycle(torch, [lambda: q.mmdit_blocks_forward(table, img, txt, t_emb, pe, scratch=scratch)],
+                           iters=21, min_calls=1, ramp_s=0.5) / blocks
     fns = [block(i) for i in range(blocks)]
-    ms_graph = _time_cycle(torch, fns, iters=21, min_calls=blocks, ramp_s=0.5)
+    ms_single = _time_cycle(torch, fns, iters=21, min_calls=blocks, ramp_s=0.5)
     img.copy_(img0)
     txt.copy_(txt0)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for f in fns:
-        f()
+    q.mmdit_blocks_forward(table, img, txt, t_emb, pe, scratch=scratch)
     torch.cuda.synchronize()
     ms_eager = (time.perf_counter() - t0) * 1e3 / blocks
     cats = {}
-    for i in range(profiled):
-        W, B = sets[i % copies]
-        for k, v in q.mmdit_block_forward(W, B, norms, img, txt, t_emb, pe, scratch=scratch, profile=True).items():
-            cats[k] = cats.get(k, 0.0) + v / profiled
+    for _ in range(max(1, profiled // blocks)):
+        for k, v in q.mmdit_blocks_forward(table, img, txt, t_emb, pe, scratch=scratch, profile=True).items():
+            cats[k] = cats.get(k, 0.0) + v / (blocks * max(1, profiled // blocks))
     finite = bool(torch.isfinite(img).all().item() and torch.isfinite(txt).all().item())
     S = n_img + n_txt
     lin_ops = sum(2.0 * (n_img if not n.startswith(("txt", "add_")) and n != "to_add_out" else n_txt) * N * K
@@ -826,6 +835,7 @@ def _block_c4(q, torch, dev, g, copies=2, blocks=8, profiled=10):
     lin_ops += 2 * 2.0 * shapes["img_mod"][0] * D
     att_ops = 4.0 * 24 * S * S * 128
     return {"block_c4_ms": round(ms_graph, 4), "block_c4_eager_ms": round(ms_eager, 4),
+            "block_c4_single_call_ms": round(ms_single, 4),
             "block_c4_gop": round((lin_ops + att_ops) / 1e9, 2),
             "block_c4_tflops": round((lin_ops + att_ops) / ms_graph / 1e9, 1),
             "block_c4_categories_ms": {k: round(v, 4) for k, v in cats.items()},
