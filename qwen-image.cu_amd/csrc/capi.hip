@@ -514,16 +514,23 @@ int qimg_mmdit_blocks_forward(const qimg_mmdit_block* blocks, int n_blocks, floa
     qimg::mmdit_block_scratch_layout(n_img, n_txt, batch, scratch, &ws);
     if (prof_ms)
         for (int c = 0; c < QIMG_PROF_COUNT; ++c) prof_ms[c] = 0.0f;
+    // (a block's modulation chunks may have been computed by the block
+    // before it, into the chunk set the block reads)
+    bool mods_ready = false;
     for (int i = 0; i < n_blocks; ++i) {
         // silu(t_emb) and its quantization carry over from the previous block
         // when its img_mod quantizes the same way
         const qimg_qlinear& m = blocks[i].img_mod;
         const bool t_ready = i > 0 && blocks[i - 1].img_mod.K == m.K && blocks[i - 1].img_mod.hbs == m.hbs &&
                              blocks[i - 1].img_mod.mode == m.mode;
-        const int st = hip_status(qimg::run_mmdit_block(blocks[i], img, txt, t_emb, pe, n_img, n_txt, batch, ws,
-                                                        prof_ms, static_cast<hipStream_t>(stream), t_ready),
-                                  fn);
+        bool next_ready = false;
+        const int st = hip_status(
+            qimg::run_mmdit_block(blocks[i], img, txt, t_emb, pe, n_img, n_txt, batch, ws, prof_ms,
+                                  static_cast<hipStream_t>(stream), t_ready, i & 1, mods_ready,
+                                  i + 1 < n_blocks ? blocks + i + 1 : nullptr, &next_ready),
+            fn);
         if (st) return st;
+        mods_ready = next_ready;
     }
     return QIMG_OK;
 }

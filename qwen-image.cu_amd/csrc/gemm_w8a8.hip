@@ -1456,7 +1456,7 @@ hipError_t dispatch_tiled(const TileProblems& P, int out_dt, int gelu, hipStream
 static std::atomic<int> g_linear_kernel{QIMG_LINEAR_AUTO};
 
 // Compute units of the current device (queried once per device).
-static int device_cu_count() {
+int device_cu_count() {
     constexpr int kMaxDev = 64;
     static std::atomic<int> cache[kMaxDev];
     int dev = 0;

@@ -89,8 +89,10 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
     w.t_silu = reinterpret_cast<float*>(take(4 * DIM));
     w.mod_q = take(DIM);
     w.mod_scale = reinterpret_cast<float*>(take(4));
-    w.img_mods = reinterpret_cast<float*>(take(4 * 6 * DIM));
-    w.txt_mods = reinterpret_cast<float*>(take(4 * 6 * DIM));
+    for (int i = 0; i < 2; ++i) {
+        w.img_mods[i] = reinterpret_cast<float*>(take(4 * 6 * DIM));
+        w.txt_mods[i] = reinterpret_cast<float*>(take(4 * 6 * DIM));
+    }
     w.img_norm = reinterpret_cast<float*>(take(4 * ri * DIM));
     w.txt_norm = reinterpret_cast<float*>(take(4 * rt * DIM));
     w.act_q = take(mmax * MLP);
@@ -116,7 +118,9 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
 
 hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
                            int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s,
-                           bool t_ready) {
+                           bool t_ready, int mods_set, bool mods_ready, const qimg_mmdit_block* next,
+                           bool* next_ready) {
+    if (next_ready) *next_ready = false;
     const int S = n_img + n_txt;
     // row counts of the img / txt streams over all sequences
     const int Mi = batch * n_img;
@@ -190,35 +194,41 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         // silu(t_emb) and its quantization are the same for every block of a
         // call: computed by the first block (and again where img_mod's
         // quantization changes), then kept in their own buffers
-        if (!t_ready) {
-            QIMG_TRY(launch_silu(t_emb, w.t_silu, DIM, s));
-            QIMG_TRY(launch_fwht_quant(w.t_silu, QIMG_FP32, 1, b.img_mod.K, b.img_mod.hbs, b.img_mod.mode, w.mod_q,
-                                       w.mod_scale, s));
-        }
+        float* const imods = w.img_mods[mods_set];
+        float* const tmods = w.txt_mods[mods_set];
         // both modulation linears in one GEMV launch where they share the
-        // activation quantization (int8, the reference's weights)
-        bool mods_done = false;
-        if (same_quant(b.img_mod, b.txt_mod) &&
-            (b.img_mod.mode == QIMG_QM_INT8_HADAMARD || b.img_mod.mode == QIMG_QM_FP8_HADAMARD)) {
-            const LinearArgs mi{w.mod_q, w.mod_scale, 1, b.img_mod.K, b.img_mod.w, b.img_mod.scales, b.img_mod.N,
-                                b.img_mod.bias, w.img_mods, nullptr, nullptr};
-            const LinearArgs mt{w.mod_q, w.mod_scale, 1, b.txt_mod.K, b.txt_mod.w, b.txt_mod.scales, b.txt_mod.N,
-                                b.txt_mod.bias, w.txt_mods, nullptr, nullptr};
-            mods_done =
-                launch_gemv_pair(w.mod_q, w.mod_scale, 1, b.img_mod.K, mi, mt, b.img_mod.mode, QIMG_FP32, s, &e);
+        // activation quantization (int8 or e4m3; the reference's weights)
+        auto mods_pair = [&](const qimg_mmdit_block& mb, float* io, float* to, hipStream_t st) -> bool {
+            if (!same_quant(mb.img_mod, mb.txt_mod) ||
+                (mb.img_mod.mode != QIMG_QM_INT8_HADAMARD && mb.img_mod.mode != QIMG_QM_FP8_HADAMARD))
+                return false;
+            const LinearArgs mi{w.mod_q, w.mod_scale, 1, mb.img_mod.K, mb.img_mod.w, mb.img_mod.scales,
+                                mb.img_mod.N, mb.img_mod.bias, io, nullptr, nullptr};
+            const LinearArgs mt{w.mod_q, w.mod_scale, 1, mb.txt_mod.K, mb.txt_mod.w, mb.txt_mod.scales,
+                                mb.txt_mod.N, mb.txt_mod.bias, to, nullptr, nullptr};
+            return launch_gemv_pair(w.mod_q, w.mod_scale, 1, mb.img_mod.K, mi, mt, mb.img_mod.mode, QIMG_FP32, st,
+                                    &e);
+        };
+        if (!mods_ready) {
+            if (!t_ready) {
+                QIMG_TRY(launch_silu(t_emb, w.t_silu, DIM, s));
+                QIMG_TRY(launch_fwht_quant(w.t_silu, QIMG_FP32, 1, b.img_mod.K, b.img_mod.hbs, b.img_mod.mode,
+                                           w.mod_q, w.mod_scale, s));
+            }
+            const bool mods_done = mods_pair(b, imods, tmods, s);
             if (mods_done && e != hipSuccess) goto done;
-        }
-        if (!mods_done) {
-            QIMG_TRY(gemm(w.mod_q, w.mod_scale, 1, b.img_mod, w.img_mods, 0, s));
-            if (same_quant(b.img_mod, b.txt_mod)) {
-                QIMG_TRY(gemm(w.mod_q, w.mod_scale, 1, b.txt_mod, w.txt_mods, 0, s));
-            } else {
-                QIMG_TRY(linear(w.t_silu, 1, b.txt_mod, w.txt_mods, 0));
+            if (!mods_done) {
+                QIMG_TRY(gemm(w.mod_q, w.mod_scale, 1, b.img_mod, imods, 0, s));
+                if (same_quant(b.img_mod, b.txt_mod)) {
+                    QIMG_TRY(gemm(w.mod_q, w.mod_scale, 1, b.txt_mod, tmods, 0, s));
+                } else {
+                    QIMG_TRY(linear(w.t_silu, 1, b.txt_mod, tmods, 0));
+                }
             }
         }
         // chunks: shift1, scale1, gate1, shift2, scale2, gate2
-        const float* im = w.img_mods;
-        const float* tm = w.txt_mods;
+        const float* im = imods;
+        const float* tm = tmods;
 
         // LayerNorm + modulate (transformer.cu:526-540), then QKV with one
         // activation quant per stream (transformer.cu:557-606). When the
@@ -375,6 +385,26 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(join(side));
         QIMG_TRY(launch_sage_attn_vt(ss.q_i8, ss.k_i8, ss.v_t, ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, s));
+        // The next block's modulation GEMV pair (the same quantized
+        // silu(t_emb) row when its img_mod quantizes alike) on the side
+        // stream beside the attention, when the attention has at least two
+        // rounds of workgroups: its workgroups then take CUs as attention
+        // workgroups retire, and the attention left to run absorbs them
+        // (6889 + 512 tokens, 2.7 and 5.4 rounds: 0.6-0.9% per step; 4096 +
+        // 256 tokens, 1.6 rounds: the GEMV outlasted the attention and
+        // slowed the out-projection, 1% per block). It writes the other
+        // chunk set, which no work of this block reads; the side stream's
+        // next join, at the latest the one at the end of this block, orders
+        // it before the next block.
+        const int cus = device_cu_count();
+        if (next && next_ready && same_quant(next->img_mod, b.img_mod) && cus > 0 &&
+            sage_attn_workgroups(HEADS * batch, S) >= 2 * static_cast<int64_t>(cus)) {
+            QIMG_TRY(fork(side));
+            const bool next_done = mods_pair(*next, w.img_mods[mods_set ^ 1], w.txt_mods[mods_set ^ 1], side->stream);
+            if (next_done && e != hipSuccess) goto done;
+            QIMG_TRY(hipEventRecord(side->join, side->stream));
+            *next_ready = next_done;
+        }
 
         // transpose + split back to the streams (transformer.cu:693-703),
         // read by the out-projection quantization straight from the fp16
@@ -469,6 +499,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(gemm_pair(Mi, b.img_mlp_fc2, img, im + 5 * DIM, w.img_qkv[2], Mt, b.txt_mlp_fc2, txt, tm + 5 * DIM,
                            w.txt_qkv[2], 0));
         QIMG_TRY(mark(QIMG_PROF_GATE_MLP));
+        if (forked != nullptr) QIMG_TRY(join(forked));
         QIMG_TRY(mark(QIMG_PROF_COUNT));
 
         if (prof) {

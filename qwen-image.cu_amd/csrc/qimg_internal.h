@@ -219,6 +219,8 @@ hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
                             const float* q_scale, const float* k_scale, void* out, int out_dtype,
                             int BH, int S, int D, float sm_scale, int causal, uint16_t* v_t,
                             hipStream_t stream);
+// Workgroups of one launch_sage_attn_vt call.
+int64_t sage_attn_workgroups(int BH, int S);
 // launch_sage_attn with V already in the Vt layout (no re-layout pass).
 hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t* v_t, const float* q_scale,
                                const float* k_scale, void* out, int out_dtype, int BH, int S, int D, float sm_scale,
@@ -251,13 +253,18 @@ hipError_t launch_split_heads(const uint16_t* in, float* txt, float* img, int n_
 hipError_t launch_gate_add(const float* x, const float* gate, const float* y, float* out, int rows, int dim,
                            hipStream_t stream);
 
+// Compute units of the current device (0 if the query fails).
+int device_cu_count();
+
 // mmdit_block.hip
 struct BlockScratch {
     float* t_silu;
     uint8_t* mod_q;    // quantized silu(t_emb), the modulation linears' input,
     float* mod_scale;  // kept across the blocks of one call
-    float* img_mods;
-    float* txt_mods;
+    // two sets of modulation chunks: a block reads its own set while the
+    // next block's are computed into the other
+    float* img_mods[2];
+    float* txt_mods[2];
     float* img_norm;
     float* txt_norm;
     uint8_t* act_q;  // image stream (and the modulation input)
@@ -281,8 +288,14 @@ int64_t mmdit_block_scratch_layout(int n_img, int n_txt, int batch, void* base, 
 // t_ready: silu(t_emb) and its quantization for b.img_mod are already in
 // w.t_silu / w.mod_q (left by the previous block of the same call, whose
 // img_mod has the same K, Hadamard block and mode).
+// mods_set: the modulation chunk set (w.img_mods / w.txt_mods index) the
+// block reads; mods_ready: the previous block has already computed it.
+// next != nullptr: the next block of the call, whose modulation chunks this
+// block may compute into the other set (beside its attention); *next_ready
+// says whether it did.
 hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, const float* t_emb, const float* pe,
                            int n_img, int n_txt, int batch, const BlockScratch& w, float* prof_ms, hipStream_t s,
-                           bool t_ready = false);
+                           bool t_ready = false, int mods_set = 0, bool mods_ready = false,
+                           const qimg_mmdit_block* next = nullptr, bool* next_ready = nullptr);
 
 }  // namespace qimg

@@ -1128,6 +1128,8 @@ hipError_t launch_sage_attn(const int8_t* q, const int8_t* k, const uint16_t* v,
     return launch_sage_attn_vt(q, k, v_t, q_scale, k_scale, out, out_dtype, BH, S, D, sm_scale, causal, stream);
 }
 
+int64_t sage_attn_workgroups(int BH, int S) { return static_cast<int64_t>(div_up(S, AQ)) * BH; }
+
 hipError_t launch_sage_attn_vt(const int8_t* q, const int8_t* k, const uint16_t* v_t, const float* q_scale,
                                const float* k_scale, void* out, int out_dtype, int BH, int S, int D, float sm_scale,
                                int causal, hipStream_t stream) {

@@ -759,6 +759,25 @@ class BlockTable:
             _block_struct(w, b, nr, self.array[i])
 
 
+def _check_block_operands(fn: str, img: torch.Tensor, txt: torch.Tensor, t_emb: torch.Tensor, pe: torch.Tensor,
+                          n_img: int, n_txt: int, batch: int) -> None:
+    """The block entry points take bare pointers and read every operand at
+    the sizes the token counts imply (the RoPE table for all n_img + n_txt
+    positions): a tensor of another size would be read out of bounds, so it
+    is refused here."""
+    want = {"img": (img, batch * n_img * 3072), "txt": (txt, batch * n_txt * 3072), "t_emb": (t_emb, 3072),
+            "pe": (pe, (n_img + n_txt) * 64 * 4)}
+    for name, (t, n) in want.items():
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be a contiguous float32 tensor")
+        if t.numel() != n:
+            raise ValueError(f"{fn}: {name} has {t.numel()} elements, {n} expected"
+                             + (f" (a RoPE table of {n_img + n_txt} positions x 64 x 4, qwen_image_pe)"
+                                if name == "pe" else ""))
+        if t.device != img.device:
+            raise ValueError(f"{fn}: {name} is on {t.device}, img on {img.device}")
+
+
 def mmdit_blocks_forward(table: "BlockTable", img: torch.Tensor, txt: torch.Tensor, t_emb: torch.Tensor,
                          pe: torch.Tensor, scratch: torch.Tensor | None = None, profile: bool = False):
     """The block loop (transformer.cu:497-836) over every block of `table`.
@@ -770,6 +789,7 @@ def mmdit_blocks_forward(table: "BlockTable", img: torch.Tensor, txt: torch.Tens
     n_txt = txt.shape[-2]
     if txt.dim() == 3 and txt.shape[0] != batch:
         raise ValueError("img and txt batch differ")
+    _check_block_operands("mmdit_blocks_forward", img, txt, t_emb, pe, n_img, n_txt, batch)
     if scratch is None:
         scratch = torch.empty((mmdit_block_scratch_bytes(n_img, n_txt, batch),), dtype=torch.uint8,
                               device=img.device)
@@ -791,8 +811,9 @@ def mmdit_block_forward(weights: dict, biases: dict, norms: dict, img: torch.Ten
     QuantizedWeight, `biases` the same names to bf16 [N] tensors, `norms`
     norm_q / norm_k / norm_added_q / norm_added_k to bf16 [128]. With
     profile=True returns {category: ms} (the stream is synchronised)."""
-    b = _block_struct(weights, biases, norms)
     n_img, n_txt = img.shape[0], txt.shape[0]
+    _check_block_operands("mmdit_block_forward", img, txt, t_emb, pe, n_img, n_txt, 1)
+    b = _block_struct(weights, biases, norms)
     if scratch is None:
         scratch = torch.empty((mmdit_block_scratch_bytes(n_img, n_txt),), dtype=torch.uint8, device=img.device)
     prof = (ctypes.c_float * len(PROF_CATEGORIES))() if profile else None

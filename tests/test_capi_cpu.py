@@ -117,3 +117,27 @@ def test_sage_rejects_bad_arguments(qimg):
                                       FAKE, 10, None) == 3
     assert L.qimg_sage_quant_q(None, FAKE, FAKE, 1, 64, 128, None) == 1
     assert L.qimg_sage_k_mean(FAKE, FAKE, 1, 64, 32, None) == 2
+
+
+def test_block_wrappers_refuse_operands_of_other_sizes(qimg):
+    """The block entry points read the RoPE table at all n_img + n_txt
+    positions (and img / txt / t_emb at the sizes the token counts give):
+    the Python wrappers refuse a table made for another grid before any call
+    into the library. 64 image tokens are an 8 x 8 latent grid, i.e.
+    qwen_image_pe(16, 16, 2, n_txt); (8, 8) gives 16 positions."""
+    import torch
+
+    img = torch.zeros((2, 64, 3072))
+    txt = torch.zeros((2, 16, 3072))
+    t_emb = torch.zeros(3072)
+    short = torch.from_numpy(qimg.qwen_image_pe(8, 8, 2, 16))
+    good = torch.from_numpy(qimg.qwen_image_pe(16, 16, 2, 16))
+    assert good.shape[0] == 80 and short.shape[0] == 32
+    with pytest.raises(ValueError, match="pe has 8192 elements, 20480 expected"):
+        qimg.mmdit_blocks_forward(None, img, txt, t_emb, short)
+    with pytest.raises(ValueError, match="pe has"):
+        qimg.mmdit_block_forward({}, {}, {}, img[0], txt[0], t_emb, short)
+    with pytest.raises(ValueError, match="t_emb has"):
+        qimg.mmdit_blocks_forward(None, img, txt, torch.zeros(3071), good)
+    with pytest.raises(ValueError, match="float32"):
+        qimg.mmdit_blocks_forward(None, img, txt, t_emb, good.double())

@@ -292,7 +292,7 @@ def test_mmdit_block_within_oracle_noise_floor(qimg, oracle, blk, request, n_img
         assert 1 - cos <= max(1e-5, 2.5 * (1 - cos_self)), (cos, cos_self)
 
 
-@pytest.mark.parametrize("n_img,n_txt,hw", [(64, 16, (16, 16)), (1029, 35, (42, 98))])
+@pytest.mark.parametrize("n_img,n_txt,hw", [(64, 16, (16, 16)), (1029, 35, (42, 98)), (2500, 77, (100, 100))])
 def test_mmdit_blocks_batched_equals_sequential(qimg, oracle, int8_block, n_img, n_txt, hw):
     """Two blocks over two sequences batched (the CFG pair as one forward)
     reproduce, bit for bit, each sequence run alone through the same two
@@ -300,7 +300,11 @@ def test_mmdit_blocks_batched_equals_sequential(qimg, oracle, int8_block, n_img,
     the same thing at either batch, and int8 accumulation is exact. At
     1029 + 35 tokens the LayerNorms run eight rows per workgroup with a
     workgroup straddling the image and text rows (image rows 1029 and 2058:
-    at different rows in the two runs)."""
+    at different rows in the two runs). At 2500 + 77 tokens the batched
+    attention has 528 workgroups, two rounds of 256 CUs, so the two-block
+    call computes the second block's modulation beside the first block's
+    attention on the side stream; the single-block calls compute it in
+    the block."""
     W, B, N, _ = int8_block
     W2 = {k: qimg.QuantizedWeight(v.data.flip(0).contiguous(), v.scales.flip(0).contiguous(), v.had_block_size,
                                   v.mode) for k, v in W.items()}
