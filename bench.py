@@ -1408,8 +1408,10 @@ def _block_summary(trace, img_rows, txt_rows, title, cmd, ops_note):
         lines.append(f" {j:3d} {dur:11.2f}  {k[1]:12d} x {int(r['Workgroup_Size_X']):3d}  {_short_kernel(r['Kernel_Name'])}")
     span = statistics.median((int(b[-1]["End_Timestamp"]) - int(b[0]["Start_Timestamp"])) / 1e3 for b in blocks)
     lines += ["", f"sum of kernel durations per block: {tot:.1f} us; first start to last end: {span:.1f} us",
-              "(the side stream's kernels (the K mean and quantization, the text fc1 and its fc2-input quantization) "
-              "overlap the main stream's; the span is the block time)"]
+              "(the side stream's kernels (the K mean and quantization, the text fc1 and its fc2-input quantization; "
+              "where the attention has two or more rounds of workgroups also the next block's modulation GEMV, "
+              "launched beside the attention, which then heads the list) overlap the main stream's; the span is "
+              "the block time)"]
     return lines
 
 
