@@ -271,6 +271,32 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         };
         SideStream* side = nullptr;
         QIMG_TRY(side_stream(&side));
+        // The next block's modulation GEMV pair (the same quantized
+        // silu(t_emb) row when its img_mod quantizes alike) runs on the side
+        // stream into the other chunk set, which no work of this block reads;
+        // the side stream's next join, at the latest the one at the end of
+        // this block, orders it before the next block. It goes where CUs
+        // would otherwise idle: beside the attention when that has at least
+        // two rounds of workgroups (its workgroups then take CUs as attention
+        // workgroups retire, and the attention left to run absorbs them;
+        // 6889 + 512 tokens, 2.7 and 5.4 rounds: 0.6-0.9% per step), else
+        // beside the K linears' launch, whose last round leaves CUs free
+        // (4096 + 256 tokens: 204 tiles on 256 CUs; beside that shape's
+        // 1.6-round attention the GEMV outlasted it and slowed the
+        // out-projection).
+        const bool pre_next = next && next_ready && same_quant(next->img_mod, b.img_mod);
+        const int cus = device_cu_count();
+        const bool next_beside_attn =
+            pre_next && cus > 0 && sage_attn_workgroups(HEADS * batch, S) >= 2 * static_cast<int64_t>(cus);
+        auto next_mods = [&]() -> hipError_t {
+            hipError_t r = fork(side);
+            if (r != hipSuccess) return r;
+            const bool done_ = mods_pair(*next, w.img_mods[mods_set ^ 1], w.txt_mods[mods_set ^ 1], side->stream);
+            if (done_ && e != hipSuccess) return e;
+            r = hipEventRecord(side->join, side->stream);
+            if (r == hipSuccess) *next_ready = done_;
+            return r;
+        };
         SageScratch ss;
         sage_scratch_layout(HEADS * batch, S, HEAD_DIM, w.sage, &ss);
         // When both streams' three linears share their input quantization and
@@ -336,6 +362,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
                 if (r == hipSuccess) {
                     QIMG_TRY(launch_linear_multi(ks, 2, il[0]->mode, QIMG_FP32, 0, s));
                     merged = true;
+                    if (pre_next && !next_beside_attn) QIMG_TRY(next_mods());
                     QIMG_TRY(fork(side));
                     QIMG_TRY(launch_sage_k_mean(w.k16, ss.k_mean, HEADS * batch, S, HEAD_DIM, side->stream));
                     QIMG_TRY(launch_sage_quant_k(w.k16, ss.k_mean, ss.k_i8, ss.k_scale, HEADS * batch, S, HEAD_DIM,
@@ -385,26 +412,7 @@ hipError_t run_mmdit_block(const qimg_mmdit_block& b, float* img, float* txt, co
         QIMG_TRY(join(side));
         QIMG_TRY(launch_sage_attn_vt(ss.q_i8, ss.k_i8, ss.v_t, ss.q_scale, ss.k_scale, w.attn16, QIMG_FP16,
                                      HEADS * batch, S, HEAD_DIM, 1.0f / sqrtf(128.0f), 0, s));
-        // The next block's modulation GEMV pair (the same quantized
-        // silu(t_emb) row when its img_mod quantizes alike) on the side
-        // stream beside the attention, when the attention has at least two
-        // rounds of workgroups: its workgroups then take CUs as attention
-        // workgroups retire, and the attention left to run absorbs them
-        // (6889 + 512 tokens, 2.7 and 5.4 rounds: 0.6-0.9% per step; 4096 +
-        // 256 tokens, 1.6 rounds: the GEMV outlasted the attention and
-        // slowed the out-projection, 1% per block). It writes the other
-        // chunk set, which no work of this block reads; the side stream's
-        // next join, at the latest the one at the end of this block, orders
-        // it before the next block.
-        const int cus = device_cu_count();
-        if (next && next_ready && same_quant(next->img_mod, b.img_mod) && cus > 0 &&
-            sage_attn_workgroups(HEADS * batch, S) >= 2 * static_cast<int64_t>(cus)) {
-            QIMG_TRY(fork(side));
-            const bool next_done = mods_pair(*next, w.img_mods[mods_set ^ 1], w.txt_mods[mods_set ^ 1], side->stream);
-            if (next_done && e != hipSuccess) goto done;
-            QIMG_TRY(hipEventRecord(side->join, side->stream));
-            *next_ready = next_done;
-        }
+        if (next_beside_attn) QIMG_TRY(next_mods());
 
         // transpose + split back to the streams (transformer.cu:693-703),
         // read by the out-projection quantization straight from the fp16
