@@ -1409,9 +1409,9 @@ def _block_summary(trace, img_rows, txt_rows, title, cmd, ops_note):
     span = statistics.median((int(b[-1]["End_Timestamp"]) - int(b[0]["Start_Timestamp"])) / 1e3 for b in blocks)
     lines += ["", f"sum of kernel durations per block: {tot:.1f} us; first start to last end: {span:.1f} us",
               "(the side stream's kernels (the K mean and quantization, the text fc1 and its fc2-input quantization; "
-              "where the attention has two or more rounds of workgroups also the next block's modulation GEMV, "
-              "launched beside the attention, which then heads the list) overlap the main stream's; the span is "
-              "the block time)"]
+              "in multi-block calls also the next block's modulation GEMV, beside the attention where that has two "
+              "or more rounds of workgroups, which then heads the list, else beside the K linears' launch) overlap "
+              "the main stream's; the span is the block time)"]
     return lines
 
 
