@@ -475,19 +475,24 @@ def test_mmdit_block_full_size_sampled(qimg, oracle, blk):
     assert torch.equal(txt_d, final["txt"])
 
 
-def test_mmdit_block_graph_replays_match_eager(qimg):
-    """The block (with its side-stream fork/join) captured in a HIP graph:
-    every replay, with eager work and synchronisations between replays,
-    gives the eager result bit for bit."""
+@pytest.mark.parametrize("n_blocks,n_img,n_txt,batch,hw", [(1, 1024, 128, 1, (64, 64)), (2, 1024, 128, 1, (64, 64)),
+                                                             (2, 2500, 77, 2, (100, 100))])
+def test_mmdit_block_graph_replays_match_eager(qimg, n_blocks, n_img, n_txt, batch, hw):
+    """The blocks (with their side-stream forks and joins) captured in a HIP
+    graph: every replay, with eager work and synchronisations between
+    replays, gives the eager result bit for bit. With two blocks the second
+    block's modulation GEMV runs on the side stream: beside the first
+    block's K linears at 1024 + 128 tokens (120 attention workgroups),
+    beside its attention at 2500 + 77 tokens x 2 (528 workgroups)."""
     W, B, nr = _gpu_block(qimg, 8)
-    table = qimg.BlockTable([(W, B, nr)])
+    table = qimg.BlockTable([(W, B, nr)] * n_blocks)
     g = torch.Generator(device=DEV).manual_seed(9)
-    n_img, n_txt = 1024, 128
-    img0 = torch.randn(n_img, 3072, generator=g, device=DEV)
-    txt0 = torch.randn(n_txt, 3072, generator=g, device=DEV)
+    img0 = torch.randn(batch, n_img, 3072, generator=g, device=DEV)
+    txt0 = torch.randn(batch, n_txt, 3072, generator=g, device=DEV)
     t_emb = torch.randn(3072, generator=g, device=DEV)
-    pe = _dev(qimg.qwen_image_pe(64, 64, 2, n_txt))
-    scratch = torch.empty(qimg.mmdit_block_scratch_bytes(n_img, n_txt), dtype=torch.uint8, device=DEV)
+    pe = _dev(qimg.qwen_image_pe(hw[0], hw[1], 2, n_txt))
+    assert pe.shape[0] == n_img + n_txt
+    scratch = torch.empty(qimg.mmdit_block_scratch_bytes(n_img, n_txt, batch), dtype=torch.uint8, device=DEV)
     ri, rt = img0.clone(), txt0.clone()
     qimg.mmdit_blocks_forward(table, ri, rt, t_emb, pe, scratch=scratch)
     torch.cuda.synchronize()
